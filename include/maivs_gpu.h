@@ -1,0 +1,170 @@
+/*
+ * maivs_gpu.h - C ABI of libmaivs_gpu.so, the MI355X (gfx950) batched cell-major search.
+ *
+ * This is the surface a Rust `build.rs` + `extern "C"` block binds, and what the C++
+ * `FlatCellIndex` host mirror calls. Plain pointers and sizes only; no C++ types cross it
+ * and no exceptions escape it. Every function returns 0 on success or a negative
+ * maivs_status; the message of the last failure on a context is kept per context.
+ *
+ * Reference interfaces replaced (file:line in V47VANSH/MAIVS):
+ *   maivs_gpu_search_batch   FlatCellIndex::search_batch_cellmajor, src/index.rs:1999-2311
+ *                            (route_batch :1873-1980, rerank_exact :1309-1378), reached from
+ *                            the pyo3 FlatCellIndex.search_batch, src/index.rs:3316-3362
+ *   maivs_gpu_upload_arena   the compacted arena fields read by that path, src/index.rs:431-566
+ *                            in the state compact_arena (:929-1112) leaves
+ *   maivs_gpu_query_prep     rotate + pack_signs_trunc + FsQuery::new, src/quantize.rs:57-313
+ *   maivs_gpu_block_sums     FsQuery::block_sums, src/quantize.rs:323-386
+ *   maivs_gpu_route          route_batch, src/index.rs:1873-1980
+ */
+#ifndef MAIVS_GPU_H
+#define MAIVS_GPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum maivs_status {
+    MAIVS_OK = 0,
+    MAIVS_ERR_ARG = -1,          /* bad argument (null pointer, size mismatch, k == 0 ...) */
+    MAIVS_ERR_NOT_UPLOADED = -2, /* search before maivs_gpu_upload_arena */
+    MAIVS_ERR_HIP = -3,          /* a HIP runtime call failed */
+    MAIVS_ERR_OOM = -4,          /* device allocation failed */
+    MAIVS_ERR_UNSUPPORTED = -5,  /* configuration this library does not run */
+} maivs_status;
+
+/* Rerank stores (src/index.rs:1309-1378). */
+enum {
+    MAIVS_RERANK_F32 = 0,   /* `quality`: f32 rows, dot_f32 */
+    MAIVS_RERANK_SQ8 = 1,   /* `memory`: per-dimension SQ8 rows, base + dot_f32_u8 */
+};
+
+/*
+ * The compacted index, as host pointers. Caller-owned; maivs_gpu_upload_arena copies every
+ * array to HBM and keeps nothing of the caller's. Shapes use d = dim, P = dim_pad,
+ * W = n_words, M = n_cells, N = n_slots, E = mem_off[M], B = fs_off[M].
+ */
+typedef struct maivs_arena_desc {
+    uint32_t dim;          /* d, a multiple of 8 is not required */
+    uint32_t dim_pad;      /* P = next power of two >= d, >= 64 (src/quantize.rs:38-40) */
+    uint32_t n_words;      /* W = 64-bit words per sign code (8 at d = 384) */
+    uint32_t n_cells;      /* M */
+    uint32_t n_slots;      /* N, length of the per-slot arrays */
+    uint32_t max_assign;   /* homes per slot (2 with orthogonal polysemy) */
+    uint32_t rerank_mode;  /* MAIVS_RERANK_* */
+    uint32_t reserved0;
+    /* FastScan blocks: 32 vectors x W*64 bytes each, cell-major in member order */
+    const uint8_t* fs_codes;    /* B * W * 256 bytes */
+    const uint32_t* fs_off;     /* M + 1, in blocks */
+    /* member lists: cell c owns members[mem_off[c] .. mem_off[c+1]), primaries then replicas */
+    const uint32_t* mem_off;    /* M + 1 */
+    const uint32_t* members;    /* E slots */
+    const uint32_t* slot_cells; /* N * max_assign, UINT32_MAX = unused */
+    /* routing */
+    const uint64_t* cent_bits;  /* M * W */
+    const uint8_t* cent_sq8;    /* M * d, or NULL to score the f32 centroids */
+    const float* centroids;     /* M * d (used when cent_sq8 is NULL) */
+    const float* csq_min;       /* d */
+    const float* csq_step;      /* d */
+    const float* r_bound;       /* M, p99 member angle per cell */
+    const float* rot_signs;     /* 2 * P, the +-1 rotation signs */
+    /* rerank */
+    const float* vecs_f32;      /* N * d (MAIVS_RERANK_F32) */
+    const uint8_t* sq8_codes;   /* N * d (MAIVS_RERANK_SQ8) */
+    const float* sq_min;        /* d (MAIVS_RERANK_SQ8) */
+    const float* sq_step;       /* d (MAIVS_RERANK_SQ8) */
+} maivs_arena_desc;
+
+/* Query-time settings of search_batch (src/index.rs:3316-3326 and the index setters). */
+typedef struct maivs_search_params {
+    uint32_t k;
+    uint32_t nprobe;
+    float target_confidence;  /* >= 1 probes all nprobe; < 1 nucleus over exp(beta*(s-max)) */
+    float beta;
+    uint32_t rerank_factor;   /* survivors reranked = k * rerank_factor */
+    uint32_t shortlist_mult;  /* two-stage shortlist = nprobe * max(mult, 2) */
+    uint32_t adaptive;        /* adaptive probe cut (set_adaptive) */
+    float at_margin;          /* its margin */
+} maivs_search_params;
+
+/* Per-call measurements (filled when a non-NULL pointer is passed). */
+typedef struct maivs_gpu_stats {
+    float ms_total;       /* device time of the whole pipeline (hipEvents) */
+    float ms_prep;        /* rotation, sign codes, FastScan tables */
+    float ms_route;       /* Hamming shortlist + SQ8 rescore + probe-list sort */
+    float ms_seed;        /* seed-cell scan + seed cut-off + adaptive cut */
+    float ms_invert;      /* query -> cell inversion */
+    float ms_scan;        /* the cell-major scan kernel */
+    float ms_select;      /* tie-inclusive cut at k * rerank_factor */
+    float ms_rerank;      /* exact rerank + top-k */
+    uint64_t scan_pairs;      /* (query, cell) pairs in the rest scan */
+    uint64_t scan_blocks;     /* sum over those pairs of the cell's 32-vector blocks */
+    uint64_t seed_blocks;     /* same for the seed scan */
+    uint64_t survivors;       /* candidates the rest scan emitted */
+    uint64_t rerank_rows;     /* rows the rerank read */
+    uint32_t host_checks;     /* queries whose libm-sensitive decision the host re-evaluated */
+    uint32_t host_fixes;      /* of those, how many changed the device's decision */
+    uint32_t reruns;          /* pipeline re-runs (buffer growth or host fixes) */
+    uint32_t reserved;
+} maivs_gpu_stats;
+
+typedef struct maivs_gpu_ctx maivs_gpu_ctx;
+
+/* One context per (device, arena). Creates a HIP stream on `device`. */
+int maivs_gpu_create(int device, maivs_gpu_ctx** out);
+void maivs_gpu_destroy(maivs_gpu_ctx* ctx);
+const char* maivs_gpu_last_error(const maivs_gpu_ctx* ctx);
+
+/* Copy the compacted arena to HBM (replaces any previous one). */
+int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* arena);
+
+/*
+ * Batched cell-major search. Host buffers: queries nq x dim (f32, row-major), outputs nq x k.
+ * out_slots[q*k + i] is the arena slot of the i-th best result of query q, best first, ties by
+ * ascending slot; rows with fewer than k results are padded with UINT32_MAX / -inf.
+ */
+int maivs_gpu_search_batch(maivs_gpu_ctx* ctx, const float* queries, uint32_t nq,
+                           const maivs_search_params* params, uint32_t* out_slots,
+                           float* out_scores, maivs_gpu_stats* stats);
+
+/* Same, with queries and outputs already in device memory (HBM-resident inputs). */
+int maivs_gpu_search_batch_device(maivs_gpu_ctx* ctx, const float* d_queries, uint32_t nq,
+                                  const maivs_search_params* params, uint32_t* d_out_slots,
+                                  float* d_out_scores, maivs_gpu_stats* stats);
+
+/* ---- stage entry points for parity tests (host buffers) ---- */
+
+/* Rotation, sign code and FastScan table of nq queries: bits nq x W, lut nq x (W*256),
+ * delta nq, bias nq. Needs an uploaded arena (for the rotation signs). */
+int maivs_gpu_query_prep(maivs_gpu_ctx* ctx, const float* queries, uint32_t nq,
+                         uint64_t* out_bits, uint8_t* out_lut, float* out_delta,
+                         float* out_bias);
+
+/* FastScan sums of nb blocks against one table each: blocks nb x (W*256) bytes, luts
+ * nb x (W*256) bytes, out nb x 32 u16. Needs a context (arena not required); n_words = W. */
+int maivs_gpu_block_sums(maivs_gpu_ctx* ctx, uint32_t n_words, const uint8_t* blocks,
+                         const uint8_t* luts, uint32_t nb, uint16_t* out);
+
+/* Routing of nq queries: chosen nq x nprobe cell ids (best first), cscore nq x nprobe,
+ * nchosen nq. Unused tail entries are UINT32_MAX / NaN. */
+int maivs_gpu_route(maivs_gpu_ctx* ctx, const float* queries, uint32_t nq,
+                    const maivs_search_params* params, uint32_t* out_chosen,
+                    float* out_cscore, uint32_t* out_nchosen);
+
+/*
+ * Intermediates of the last maivs_gpu_search_batch* call (host buffers, NULL to skip):
+ * tau nq (seed cut-off), rest_end nq (probe-list index where the scan stopped),
+ * cut nq (final tie-inclusive cut-off G), ncand nq (candidates reranked),
+ * cand_slots / cand_d: for each query its candidates, sorted by (d, slot), packed
+ * back to back in query order; cap = capacity of those two arrays (entries).
+ */
+int maivs_gpu_last_candidates(maivs_gpu_ctx* ctx, uint32_t* tau, uint32_t* rest_end,
+                              uint32_t* cut, uint32_t* ncand, uint32_t* cand_slots,
+                              uint32_t* cand_d, uint64_t cap);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MAIVS_GPU_H */

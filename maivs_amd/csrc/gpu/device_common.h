@@ -1,0 +1,146 @@
+// Device-side helpers shared by the search kernels: wave64 reductions, block scans, bitonic
+// sort of 64-bit keys, and the exact f32 arithmetic the reference's CPU path uses.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace maivs_dev {
+
+constexpr int kWave = 64;
+constexpr uint32_t kNone = 0xFFFFFFFFu;
+constexpr uint64_t kKeyMax = ~0ull;
+
+__device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
+
+// Number of set lanes of `mask` below this lane.
+__device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
+    return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
+}
+
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+    for (int o = 32; o > 0; o >>= 1) v = min(v, static_cast<uint32_t>(__shfl_xor(v, o, kWave)));
+    return v;
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    for (int o = 32; o > 0; o >>= 1) v = max(v, static_cast<uint32_t>(__shfl_xor(v, o, kWave)));
+    return v;
+}
+__device__ __forceinline__ float wave_max_f32(float v) {
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+
+// Block-wide reductions through LDS `scratch` (>= blockDim/64 entries). All threads get the result.
+__device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, uint32_t* scratch) {
+    v = wave_sum_u32(v);
+    const uint32_t w = threadIdx.x / kWave, nw = (blockDim.x + kWave - 1) / kWave;
+    __syncthreads();
+    if (lane_id() == 0) scratch[w] = v;
+    __syncthreads();
+    uint32_t s = 0;
+    for (uint32_t i = 0; i < nw; ++i) s += scratch[i];
+    __syncthreads();
+    return s;
+}
+__device__ __forceinline__ uint32_t block_min_u32(uint32_t v, uint32_t* scratch) {
+    v = wave_min_u32(v);
+    const uint32_t w = threadIdx.x / kWave, nw = (blockDim.x + kWave - 1) / kWave;
+    __syncthreads();
+    if (lane_id() == 0) scratch[w] = v;
+    __syncthreads();
+    uint32_t s = kNone;
+    for (uint32_t i = 0; i < nw; ++i) s = min(s, scratch[i]);
+    __syncthreads();
+    return s;
+}
+__device__ __forceinline__ float block_max_f32(float v, float* scratch) {
+    v = wave_max_f32(v);
+    const uint32_t w = threadIdx.x / kWave, nw = (blockDim.x + kWave - 1) / kWave;
+    __syncthreads();
+    if (lane_id() == 0) scratch[w] = v;
+    __syncthreads();
+    float s = -INFINITY;
+    for (uint32_t i = 0; i < nw; ++i) s = fmaxf(s, scratch[i]);
+    __syncthreads();
+    return s;
+}
+
+// Exclusive prefix sum of one value per thread, block-wide; returns the total in *total.
+__device__ __forceinline__ uint32_t block_excl_scan_u32(uint32_t v, uint32_t* scratch, uint32_t* total) {
+    const uint32_t lane = lane_id(), w = threadIdx.x / kWave, nw = (blockDim.x + kWave - 1) / kWave;
+    uint32_t x = v;
+    for (int o = 1; o < kWave; o <<= 1) {
+        uint32_t y = __shfl_up(x, o, kWave);
+        if (lane >= static_cast<uint32_t>(o)) x += y;
+    }
+    __syncthreads();
+    if (lane == kWave - 1) scratch[w] = x;
+    __syncthreads();
+    uint32_t before = 0, all = 0;
+    for (uint32_t i = 0; i < nw; ++i) {
+        if (i < w) before += scratch[i];
+        all += scratch[i];
+    }
+    __syncthreads();
+    *total = all;
+    return before + x - v;
+}
+
+// Ascending bitonic sort of n = power-of-two 64-bit keys (LDS or global), block-wide.
+__device__ __forceinline__ void bitonic_sort_u64(uint64_t* keys, uint32_t n) {
+    for (uint32_t size = 2; size <= n; size <<= 1) {
+        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+            __syncthreads();
+            for (uint32_t t = threadIdx.x; t < n / 2; t += blockDim.x) {
+                uint32_t lo = 2 * t - (t & (stride - 1));
+                uint32_t hi = lo + stride;
+                bool up = (lo & size) == 0;
+                uint64_t a = keys[lo], b = keys[hi];
+                if ((a > b) == up) {
+                    keys[lo] = b;
+                    keys[hi] = a;
+                }
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// Order-preserving key of an f32 for DESCENDING score, ties broken by the low 32 bits
+// (the id, ascending). -0.0 and +0.0 compare equal in the reference, so they share a key.
+__device__ __forceinline__ uint64_t desc_score_key(float s, uint32_t id) {
+    uint32_t b = __float_as_uint(s == 0.0f ? 0.0f : s);
+    uint32_t asc = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return (static_cast<uint64_t>(~asc) << 32) | id;
+}
+__device__ __forceinline__ float key_score(uint64_t key) {
+    uint32_t asc = ~static_cast<uint32_t>(key >> 32);
+    uint32_t b = (asc & 0x80000000u) ? (asc & 0x7FFFFFFFu) : ~asc;
+    return __uint_as_float(b);
+}
+
+// 8-lane FMA dot with the hsum order ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) and a sequential
+// tail, computed by the 8 consecutive lanes of a group (lane l of the group owns acc_l).
+// Every lane of the group returns the full result. `a` is indexed by element, `b` likewise.
+template <class LoadA, class LoadB>
+__device__ __forceinline__ float dot8_group(uint32_t n, uint32_t l, LoadA la, LoadB lb) {
+    float acc = 0.0f;
+    uint32_t n8 = n & ~7u;
+    for (uint32_t i = l; i < n8; i += 8) acc = __builtin_fmaf(la(i), lb(i), acc);
+    float a4 = __shfl_xor(acc, 4, 8);     // partner l^4
+    float s = acc + a4;                   // lanes 0..3: a_l + a_{l+4}
+    float s2 = __shfl_xor(s, 2, 8);       // partner l^2
+    float t = (l & 2) ? (s2 + s) : (s + s2);  // lanes 0,1: (a0+a4)+(a2+a6), (a1+a5)+(a3+a7)
+    float t1 = __shfl_xor(t, 1, 8);
+    float r = (l & 1) ? (t1 + t) : (t + t1);
+    for (uint32_t i = n8; i < n; ++i) r += la(i) * lb(i);
+    return r;
+}
+
+}  // namespace maivs_dev

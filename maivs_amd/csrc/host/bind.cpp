@@ -1,0 +1,222 @@
+// Python module maivs_amd._maivs: the FlatCellIndex class with the reference's Python
+// signatures (src/index.rs:2670-3603, pyo3) so callers of `maivs.FlatCellIndex` switch by import.
+#include <pybind11/numpy.h>
+#include <pybind11/pybind11.h>
+#include <pybind11/stl.h>
+
+#include <cstring>
+
+#include "index.h"
+
+namespace py = pybind11;
+using maivs::FlatCellIndex;
+
+namespace {
+
+// A float32 (n, d) C-contiguous view, with the reference's error messages.
+struct F32Rows {
+    const float* ptr;
+    size_t rows, cols;
+};
+
+F32Rows as_rows(const py::array& a, const char* what, const char* contig_msg) {
+    if (!py::dtype::of<float>().is(a.dtype()))
+        throw py::type_error(std::string(what) + " must be a float32 array, got dtype " +
+                             py::str(a.dtype()).cast<std::string>());
+    if (a.ndim() != 2) throw py::value_error(std::string(what) + " must be 2-dimensional");
+    if (!(a.flags() & py::array::c_style)) throw py::value_error(contig_msg);
+    return {static_cast<const float*>(a.data()), static_cast<size_t>(a.shape(0)), static_cast<size_t>(a.shape(1))};
+}
+
+template <class F>
+auto translate(F&& f) -> decltype(f()) {
+    try {
+        return f();
+    } catch (const maivs::ValueError& e) {
+        throw py::value_error(e.what());
+    } catch (const maivs::Unsupported& e) {
+        PyErr_SetString(PyExc_NotImplementedError, e.what());
+        throw py::error_already_set();
+    }
+}
+
+py::dict stats_dict(const maivs_gpu_stats& s) {
+    py::dict d;
+    d["ms_total"] = s.ms_total;
+    d["ms_prep"] = s.ms_prep;
+    d["ms_route"] = s.ms_route;
+    d["ms_seed"] = s.ms_seed;
+    d["ms_invert"] = s.ms_invert;
+    d["ms_scan"] = s.ms_scan;
+    d["ms_select"] = s.ms_select;
+    d["ms_rerank"] = s.ms_rerank;
+    d["scan_pairs"] = s.scan_pairs;
+    d["scan_blocks"] = s.scan_blocks;
+    d["seed_blocks"] = s.seed_blocks;
+    d["survivors"] = s.survivors;
+    d["rerank_rows"] = s.rerank_rows;
+    d["host_checks"] = s.host_checks;
+    d["host_fixes"] = s.host_fixes;
+    d["reruns"] = s.reruns;
+    return d;
+}
+
+struct PyIndex {
+    FlatCellIndex ix;
+    maivs_gpu_stats last{};
+    PyIndex(size_t dim, const std::string& mode, size_t rf, uint64_t seed, size_t code_bits)
+        : ix(dim, mode, rf, seed, code_bits) {}
+};
+
+}  // namespace
+
+PYBIND11_MODULE(_maivs, m) {
+    m.doc() = "MI355X-native batched cell-major search behind the MAIVS FlatCellIndex API";
+
+    py::class_<PyIndex>(m, "FlatCellIndex")
+        .def(py::init([](size_t dim, const std::string& scan_mode, size_t rerank_factor, uint64_t seed,
+                         size_t code_bits) {
+                 return translate([&] { return new PyIndex(dim, scan_mode, rerank_factor, seed, code_bits); });
+             }),
+             py::arg("dim"), py::arg("scan_mode") = "f32", py::arg("rerank_factor") = 4,
+             py::arg("seed") = 0x5EEDull, py::arg("code_bits") = 0)
+        .def(
+            "train_centroids",
+            [](PyIndex& s, const py::array& vectors, size_t n_cells, size_t sample, uint64_t seed) {
+                F32Rows r = as_rows(vectors, "vectors", "vectors must be C-contiguous");
+                if (r.cols != s.ix.dim()) throw py::value_error("dim mismatch");
+                py::gil_scoped_release nogil;
+                translate([&] { s.ix.train_centroids(r.ptr, r.rows, n_cells, sample, seed); });
+            },
+            py::arg("vectors"), py::arg("n_cells"), py::arg("sample") = 262144, py::arg("seed") = 0x5EEDull)
+        .def("set_centroids",
+             [](PyIndex& s, const py::array& c) {
+                 F32Rows r = as_rows(c, "centroids", "centroids must be C-contiguous");
+                 if (r.cols != s.ix.dim()) throw py::value_error("centroid dim mismatch");
+                 translate([&] { s.ix.set_centroids(r.ptr, r.rows); });
+             })
+        .def("set_i8_rerank", [](PyIndex& s, bool on) { s.ix.set_i8_rerank(on); })
+        .def(
+            "set_tree_route",
+            [](PyIndex& s, bool on, size_t min_cells, size_t fanout, float beam_frac) {
+                py::gil_scoped_release nogil;
+                s.ix.set_tree_route(on, min_cells, fanout, beam_frac);
+            },
+            py::arg("on"), py::arg("min_cells") = 0, py::arg("fanout") = 0, py::arg("beam_frac") = 0.0f)
+        .def(
+            "set_graph_route", [](PyIndex& s, bool on, size_t min_cells) { s.ix.set_graph_route(on, min_cells); },
+            py::arg("on"), py::arg("min_cells") = 0)
+        .def("set_centroid_sq8", [](PyIndex& s, bool on) { s.ix.set_centroid_sq8(on); })
+        .def("set_two_stage", [](PyIndex& s, bool on, size_t mult) { s.ix.set_two_stage(on, mult); })
+        .def("set_adaptive", [](PyIndex& s, bool on, float margin) { s.ix.set_adaptive(on, margin); })
+        .def("set_per_dim_sq", [](PyIndex& s, bool on) { s.ix.set_per_dim_sq(on); })
+        .def("set_f16_rerank", [](PyIndex& s, bool on) { translate([&] { s.ix.set_f16_rerank(on); }); })
+        .def("set_quant_scale", [](PyIndex& s, float v) { s.ix.set_quant_scale(v); })
+        .def("set_rerank_factor", [](PyIndex& s, size_t rf) { s.ix.set_rerank_factor(rf); })
+        .def("set_asym_cascade", [](PyIndex& s, size_t f) { s.ix.set_asym_cascade(f); })
+        .def("set_fastscan", [](PyIndex& s, bool on) { s.ix.set_fastscan(on); })
+        .def("set_replication", [](PyIndex& s, size_t ma, float margin) { s.ix.set_replication(ma, margin); })
+        .def(
+            "set_orthogonal_polysemy", [](PyIndex& s, size_t homes, float lam) { s.ix.set_orthogonal_polysemy(homes, lam); },
+            py::arg("homes") = 2, py::arg("lam") = 1.0f)
+        .def("set_parallel_scan", [](PyIndex& s, bool on) { s.ix.set_parallel_scan(on); })
+        .def("set_tags",
+             [](PyIndex& s, std::vector<uint64_t> ids, std::vector<uint32_t> tags) {
+                 translate([&] { s.ix.set_tags(ids, tags); });
+             })
+        .def(
+            "set_filter",
+            [](PyIndex& s, std::optional<uint32_t> lo, std::optional<uint32_t> hi) { s.ix.set_filter(lo, hi); },
+            py::arg("lo") = py::none(), py::arg("hi") = py::none())
+        .def("rebuild_tree",
+             [](PyIndex& s) {
+                 py::gil_scoped_release nogil;
+                 s.ix.rebuild_tree();
+             })
+        .def("add_batch",
+             [](PyIndex& s, std::vector<uint64_t> ids, const py::array& vectors) {
+                 F32Rows r = as_rows(vectors, "vectors", "vectors must be C-contiguous (use np.ascontiguousarray)");
+                 if (r.rows != ids.size() || r.cols != s.ix.dim()) throw py::value_error("shape mismatch");
+                 py::gil_scoped_release nogil;
+                 translate([&] { s.ix.add_batch(ids, r.ptr, r.rows); });
+             })
+        .def("remove", [](PyIndex& s, uint64_t id) { return s.ix.remove(id); })
+        .def("compact",
+             [](PyIndex& s) {
+                 py::gil_scoped_release nogil;
+                 s.ix.compact();
+             })
+        .def(
+            "search",
+            [](PyIndex&, const py::array&, size_t, size_t, float, float) -> py::tuple {
+                PyErr_SetString(PyExc_NotImplementedError,
+                                "the single-query path (search) is not part of this build; use search_batch");
+                throw py::error_already_set();
+            },
+            py::arg("query"), py::arg("k"), py::arg("nprobe") = 16, py::arg("target_confidence") = 0.95f,
+            py::arg("beta") = 8.0f)
+        .def(
+            "search_batch",
+            [](PyIndex& s, const py::array& queries, size_t k, size_t nprobe, float tc, float beta,
+               bool cell_major) {
+                if (!py::dtype::of<float>().is(queries.dtype()))
+                    throw py::type_error("queries must be a float32 array");
+                if (queries.ndim() != 2) throw py::value_error("queries must be 2-dimensional");
+                if (static_cast<size_t>(queries.shape(1)) != s.ix.dim()) throw py::value_error("query dim mismatch");
+                if (!(queries.flags() & py::array::c_style))
+                    throw py::value_error("queries must be C-contiguous (use np.ascontiguousarray)");
+                size_t nq = static_cast<size_t>(queries.shape(0));
+                const float* q = static_cast<const float*>(queries.data());
+                std::vector<uint64_t> ids;
+                std::vector<float> scores;
+                {
+                    py::gil_scoped_release nogil;
+                    translate([&] { s.ix.search_batch(q, nq, k, nprobe, tc, beta, cell_major, ids, scores, &s.last); });
+                }
+                return py::make_tuple(py::cast(ids), py::cast(scores));
+            },
+            py::arg("queries"), py::arg("k"), py::arg("nprobe") = 16, py::arg("target_confidence") = 0.95f,
+            py::arg("beta") = 8.0f, py::arg("cell_major") = true)
+        .def("stats", [](PyIndex& s) { return s.ix.stats(); })
+        .def("__len__", [](PyIndex& s) { return s.ix.len(); })
+        .def("recommend", [](PyIndex& s) { return s.ix.recommend(); })
+        // ---- not in the reference: hooks for the C-ABI tests and the benchmark ----
+        .def("last_search_stats", [](PyIndex& s) { return stats_dict(s.last); },
+             "Device timings and work counters of the last search_batch call.")
+        .def("cellmajor_blocker", [](PyIndex& s, bool cell_major) { return s.ix.cellmajor_blocker(cell_major); },
+             py::arg("cell_major") = true)
+        .def("_arena_desc",
+             [](PyIndex& s) -> uintptr_t {
+                 const maivs_arena_desc* d = s.ix.arena_desc();
+                 if (!d) throw py::value_error("index is not compacted");
+                 return reinterpret_cast<uintptr_t>(d);
+             },
+             "Address of the maivs_arena_desc of the compacted arena (valid until the next mutation).")
+        .def("_search_params",
+             [](PyIndex& s, size_t k, size_t nprobe, float tc, float beta) {
+                 maivs_search_params p = s.ix.search_params(k, nprobe, tc, beta);
+                 return py::bytes(reinterpret_cast<const char*>(&p), sizeof(p));
+             },
+             py::arg("k"), py::arg("nprobe"), py::arg("target_confidence") = 1.0f, py::arg("beta") = 8.0f,
+             "The maivs_search_params struct search_batch would pass, as raw bytes.")
+        .def("_ext_ids",
+             [](PyIndex& s) {
+                 const auto& e = s.ix.ext_ids();
+                 py::array_t<uint64_t> a(static_cast<py::ssize_t>(e.size()));
+                 std::memcpy(a.mutable_data(), e.data(), e.size() * sizeof(uint64_t));
+                 return a;
+             })
+        .def("_codes",
+             [](PyIndex& s) {
+                 const auto& b = s.ix.bits();
+                 py::array_t<uint64_t> a(static_cast<py::ssize_t>(b.size()));
+                 std::memcpy(a.mutable_data(), b.data(), b.size() * sizeof(uint64_t));
+                 return a;
+             })
+        .def("_rot_signs", [](PyIndex& s) {
+            const auto& r = s.ix.rot_signs();
+            py::array_t<float> a(static_cast<py::ssize_t>(r.size()));
+            std::memcpy(a.mutable_data(), r.data(), r.size() * sizeof(float));
+            return a;
+        });
+}

@@ -1,0 +1,168 @@
+// FlatCellIndex: the host side of the drop-in. Builds the partitioned index exactly as the
+// reference's CPU build does (train_centroids -> add_batch -> compact), and runs
+// search_batch through libmaivs_gpu.so's C ABI on the MI355X.
+//
+// Reference: the pyo3 class FlatCellIndex, src/index.rs:431-566 (state) and :2670-3603
+// (methods). Only the state the batched cell-major search and its build need is kept; the
+// per-query path, HNSW routing, split/merge and persistence are not part of this build.
+#pragma once
+
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <optional>
+#include <stdexcept>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../../include/maivs_gpu.h"
+#include "tree.h"
+
+namespace maivs {
+
+struct ValueError : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+struct Unsupported : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+enum class ScanMode { F32, I8, Binary };
+
+struct Cell {
+    std::vector<uint32_t> members;
+    std::vector<float> sum, centroid;
+    float r_bound = 0.0f, r_max = 0.0f;
+};
+
+class GpuSession;  // owns a maivs_gpu_ctx (index.cpp)
+
+class FlatCellIndex {
+public:
+    FlatCellIndex(size_t dim, const std::string& scan_mode, size_t rerank_factor, uint64_t seed,
+                  size_t code_bits);
+    ~FlatCellIndex();
+
+    // ---- configuration (src/index.rs:2806-2984, 3520-3558) ----
+    void train_centroids(const float* data, size_t n_all, size_t n_cells, size_t sample, uint64_t seed);
+    void set_centroids(const float* cents, size_t n);
+    void set_i8_rerank(bool on);
+    void set_tree_route(bool on, size_t min_cells, size_t fanout, float beam_frac);
+    void set_graph_route(bool on, size_t min_cells);
+    void set_centroid_sq8(bool on);
+    void set_two_stage(bool on, size_t mult);
+    void set_adaptive(bool on, float margin);
+    void set_per_dim_sq(bool on);
+    void set_f16_rerank(bool on);
+    void set_quant_scale(float s) { quant_scale_ = s; }
+    void set_rerank_factor(size_t rf) { rerank_factor_ = std::max<size_t>(rf, 1); }
+    void set_asym_cascade(size_t f) { asym_cascade_ = f; }
+    void set_fastscan(bool on);
+    void set_replication(size_t max_assign, float spill_margin);
+    void set_orthogonal_polysemy(size_t homes, float lam);
+    void set_parallel_scan(bool on) { par_scan_ = on; }
+    void set_tags(const std::vector<uint64_t>& ids, const std::vector<uint32_t>& tags);
+    void set_filter(std::optional<uint32_t> lo, std::optional<uint32_t> hi);
+    void rebuild_tree() { rebuild_centroid_tree(); }
+
+    // ---- mutation ----
+    void add_batch(const std::vector<uint64_t>& ids, const float* data, size_t n);
+    bool remove(uint64_t id);
+    void compact();
+
+    // ---- search ----
+    // Batched cell-major search on the GPU. Fills ids/scores (nq*k), padded u64::MAX / -inf.
+    void search_batch(const float* q, size_t nq, size_t k, size_t nprobe, float tc, float beta,
+                      bool cell_major, std::vector<uint64_t>& ids, std::vector<float>& scores,
+                      maivs_gpu_stats* stats = nullptr);
+    // Why the batched cell-major path cannot run right now (empty string when it can).
+    std::string cellmajor_blocker(bool cell_major) const;
+
+    // ---- introspection ----
+    std::map<std::string, double> stats() const;
+    size_t len() const { return n_live_; }
+    size_t dim() const { return dim_; }
+    std::pair<size_t, bool> recommend() const;
+    // The compacted arena as a C descriptor (valid until the next mutation).
+    const maivs_arena_desc* arena_desc();
+    maivs_search_params search_params(size_t k, size_t nprobe, float tc, float beta) const;
+    const std::vector<uint64_t>& ext_ids() const { return ext_ids_; }
+    const std::vector<uint64_t>& bits() const { return bits_; }
+    const std::vector<float>& rot_signs() const { return rot_signs_; }
+    uint64_t generation() const { return generation_; }
+
+private:
+    void refresh_derived();
+    void recompute_radii();
+    void rebuild_centroid_codes();
+    void rebuild_centroid_sq8();
+    void maybe_rebuild_centroid_tree();
+    void rebuild_centroid_tree();
+    size_t live_cell_count() const;
+    std::vector<uint32_t> assign_cells(const float* v) const;
+    std::vector<uint32_t> assign_cells_routed(const float* v, std::vector<float>& rot, std::vector<uint64_t>& bits,
+                                              TreeScratch& ts, std::vector<uint32_t>& out) const;
+    std::vector<uint32_t> pick_orthogonal(std::vector<std::pair<uint32_t, float>>& scored) const;
+    void encode_slot(const float* v, uint64_t* bits_out, int8_t* i8_out) const;
+    void compact_arena();
+    void recompute_centroid(Cell& c);
+    void touch() { ++generation_; compacted_ = false; }
+
+    size_t dim_, rerank_factor_, dim_pad_, n_words_;
+    ScanMode scan_mode_;
+    uint64_t seed_;
+    std::vector<float> rot_signs_;
+
+    std::vector<uint64_t> bits_;
+    std::vector<int8_t> scan_i8_;
+    std::vector<float> vecs_f32_;
+    std::vector<uint64_t> ext_ids_;
+    std::vector<uint32_t> slot_cell_;
+    std::vector<uint32_t> free_slots_;
+    std::unordered_map<uint64_t, uint32_t> id_to_slot_;
+
+    std::vector<Cell> cells_;
+    std::vector<uint64_t> cent_bits_;
+    std::vector<uint8_t> cent_sq8_;
+    std::vector<float> csq_min_, csq_step_;
+    bool centroid_sq8_ = true;
+    std::unique_ptr<CentroidTree> tree_;
+    bool tree_route_ = true;
+    size_t tree_min_cells_ = CentroidTree::kMinCellsForTree;
+    size_t tree_fanout_ = CentroidTree::kDefaultFanout;
+    float tree_beam_frac_ = CentroidTree::kDefaultBeamFrac;
+    size_t tree_cells_ = 0;
+    bool par_scan_ = false;
+    bool graph_route_ = true;
+    size_t graph_min_cells_ = 65536;
+    bool two_stage_ = false;
+    size_t shortlist_mult_ = 4;
+    float quant_scale_ = 0.0f;
+    size_t n_live_ = 0;
+
+    size_t max_assign_ = 1;
+    float spill_margin_ = 0.0f, spill_lambda_ = 0.0f;
+    bool compacted_ = false;
+    size_t asym_cascade_ = 0;
+    bool fastscan_ = false;
+    std::vector<uint8_t> fs_codes_;
+    std::vector<uint32_t> fs_off_;
+    std::vector<uint32_t> prim_len_, rep_off_;
+    std::vector<uint32_t> slot_cells_;
+    std::vector<uint32_t> tags_;
+    std::optional<std::pair<uint32_t, uint32_t>> tag_filter_;
+    bool i8_rerank_ = false, per_dim_sq_ = false, f16_rerank_ = false, keep_f32_ = true;
+    std::vector<float> sq_min_, sq_step_;
+    bool adaptive_ = false;
+    float at_margin_ = 0.02f;
+
+    // flattened member CSR of the compacted arena (built by compact_arena)
+    std::vector<uint32_t> mem_off_, members_flat_;
+    std::vector<float> cents_flat_, r_bound_flat_;
+    maivs_arena_desc desc_{};
+    uint64_t generation_ = 0;
+    std::unique_ptr<GpuSession> gpu_;
+};
+
+}  // namespace maivs

@@ -1,0 +1,61 @@
+// Centroid training and the dynamic-depth centroid tree used to place vectors at ingest
+// (restated from src/tree.rs). Build-side support only: the batched search routes with the
+// flat two-stage router, not the tree (src/index.rs:2105-2107).
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <vector>
+
+namespace maivs {
+
+// Spherical Lloyd k-means over unit vectors, src/tree.rs:179-248. Returns (assign, centroids).
+void kmeans_spherical(const float* x, size_t n, size_t dim, size_t k, size_t iters, uint64_t seed,
+                      std::vector<uint32_t>& assign, std::vector<float>& cents, bool parallel);
+
+// Two-level balanced k-means, src/tree.rs:257-348. Returns k x dim centroids.
+std::vector<float> hierarchical_kmeans(const float* x, size_t n, size_t dim, size_t k, uint64_t seed);
+
+struct TreeLevel {
+    size_t n = 0;
+    std::vector<float> cents;
+    std::vector<uint64_t> codes;
+    std::vector<uint32_t> child_start, child_len, child_idx;
+};
+
+struct TreeScratch {
+    std::vector<uint32_t> frontier, expand, hist;
+    std::vector<std::pair<uint32_t, uint32_t>> scored;  // (hamming, node)
+};
+
+class CentroidTree {
+public:
+    static constexpr size_t kDefaultFanout = 64;   // src/tree.rs:37
+    static constexpr size_t kTopMax = 256;         // src/tree.rs:41
+    static constexpr size_t kMinBeam = 32;         // src/tree.rs:45
+    static constexpr float kDefaultBeamFrac = 0.5f;  // src/tree.rs:66
+    static constexpr size_t kMinCellsForTree = 2048;  // src/tree.rs:70
+
+    // Build over live cells (cell_cents row i belongs to cell_ids[i]); false if degenerate.
+    bool build(const float* cell_cents, const std::vector<uint32_t>& cell_ids, size_t dim,
+               const float* rot_signs, size_t dim_pad, size_t n_words, size_t fanout, float beam_frac);
+    // Up to `want` leaf cell ids, best first by Hamming (ties in encounter order).
+    void search(const uint64_t* q_bits, size_t want, TreeScratch& s, std::vector<uint32_t>& out) const;
+    size_t depth() const { return levels_.size(); }
+    size_t n_leaf() const { return n_leaf_; }
+    size_t top_width() const { return levels_.empty() ? 0 : levels_.front().n; }
+    size_t bytes() const;
+
+private:
+    std::vector<size_t> beams(size_t want) const;
+    void compact_layout();
+
+    size_t dim_ = 0, n_words_ = 0, fanout_ = 0;
+    float beam_frac_ = kDefaultBeamFrac;
+    std::vector<TreeLevel> levels_;  // coarsest first
+    std::vector<uint64_t> leaf_codes_;
+    std::vector<uint32_t> leaf_ids_;
+    size_t n_leaf_ = 0;
+};
+
+}  // namespace maivs

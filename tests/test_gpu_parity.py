@@ -1,0 +1,138 @@
+"""GPU parity through the C ABI (libmaivs_gpu.so) against the oracle, on the same seeded
+inputs and the same arena: FastScan tables and sums, routed cell lists, seed cut-offs,
+adaptive cuts, candidate sets and final top-k must be bit-exact; recall identical.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from maivs_amd import capi, mixture
+
+pytestmark = pytest.mark.gpu
+
+
+def _params(ix, k, nprobe, tc=1.0, beta=8.0):
+    return capi.params_from_bytes(ix._search_params(k, nprobe, tc, beta))
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = capi.Context(0)
+    yield c
+    c.close()
+
+
+def _upload(ctx, ix):
+    ctx.upload(ix._arena_desc())
+
+
+def test_query_prep_matches_oracle(ctx, quality50k, mix50k):
+    _, queries, _ = mix50k
+    ix = quality50k
+    _upload(ctx, ix)
+    q = queries[:257]
+    bits, lut, delta, bias = ctx.query_prep(q, 8)
+    signs = ix._rot_signs()
+    for i in range(len(q)):
+        rq = oracle.rotate(q[i], signs, 512)
+        ob = oracle.pack_signs(rq, 8)
+        olut, od, obias = oracle.fs_query(rq, 8)
+        assert np.array_equal(bits[i], ob), i
+        assert np.array_equal(lut[i], olut), i
+        assert delta[i].tobytes() == od.tobytes(), i
+        assert bias[i].tobytes() == obias.tobytes(), i
+
+
+def test_block_sums_match_oracle(ctx):
+    rs = np.random.RandomState(7)
+    nb = 64
+    blocks = rs.randint(0, 256, size=(nb, 2048)).astype(np.uint8)
+    luts = rs.randint(0, 256, size=(nb, 2048)).astype(np.uint8)
+    luts[0] = 255  # the maximum sum, 32640
+    blocks[1] = 0
+    out = ctx.block_sums(blocks, luts, 8)
+    for b in range(nb):
+        assert np.array_equal(out[b], oracle.fs_block_sums(blocks[b], luts[b])), b
+    assert out[0].max() == 32640
+
+
+@pytest.mark.parametrize("nprobe,tc", [(1, 1.0), (8, 1.0), (16, 1.0), (64, 1.0), (390, 1.0), (16, 0.95), (64, 0.5)])
+def test_route_matches_oracle(ctx, quality50k, mix50k, nprobe, tc):
+    _, queries, _ = mix50k
+    ix = quality50k
+    _upload(ctx, ix)
+    p = _params(ix, 10, nprobe, tc)
+    ch, cs, nch = ctx.route(queries, p)
+    _, och, ocs, onch = oracle.route_batch(ix._arena_desc(), queries, p, 8)
+    assert np.array_equal(nch, onch)
+    for i in range(len(queries)):
+        n = onch[i]
+        assert np.array_equal(ch[i, :n], och[i, :n]), i
+        assert cs[i, :n].tobytes() == ocs[i, :n].tobytes(), i
+
+
+def _compare_search(ctx, ix, queries, p, gt=None):
+    _upload(ctx, ix)
+    st = capi.GpuStats()
+    slots, scores = ctx.search(queries, p, st)
+    desc = ix._arena_desc()
+    oslots, oscores = oracle.search_batch(desc, queries, p, 8)
+    nq = len(queries)
+    otau, ore, ocut, onc, ocs, ocd = oracle.last_candidates(nq)
+    tau, re, cut, nc, cs, cd = ctx.last_candidates(nq, int(onc.sum()) + 1024)
+    assert np.array_equal(tau, otau)
+    assert np.array_equal(re, ore)
+    assert np.array_equal(cut, ocut)
+    assert np.array_equal(nc, onc)
+    n = int(onc.sum())
+    assert np.array_equal(cs[:n], ocs) and np.array_equal(cd[:n], ocd)
+    assert np.array_equal(slots, oslots)
+    assert scores.tobytes() == oscores.tobytes()
+    if gt is not None:
+        ext = ix._ext_ids()
+        ids = np.where(slots == 0xFFFFFFFF, -1, ext[np.minimum(slots, len(ext) - 1)].astype(np.int64))
+        oids = np.where(oslots == 0xFFFFFFFF, -1, ext[np.minimum(oslots, len(ext) - 1)].astype(np.int64))
+        assert mixture.recall_at(ids, gt) == mixture.recall_at(oids, gt)
+    return st
+
+
+@pytest.mark.parametrize("nprobe,rf", [(1, 8), (8, 8), (16, 32), (64, 16), (390, 4)])
+def test_search_quality_matches_oracle(ctx, quality50k, mix50k, nprobe, rf):
+    _, queries, gt = mix50k
+    ix = quality50k
+    ix.set_rerank_factor(rf)
+    try:
+        _compare_search(ctx, ix, queries, _params(ix, 10, nprobe), gt)
+    finally:
+        ix.set_rerank_factor(32)
+
+
+@pytest.mark.parametrize("nprobe", [8, 32])
+def test_search_memory_matches_oracle(ctx, memory50k, mix50k, nprobe):
+    _, queries, gt = mix50k
+    _compare_search(ctx, memory50k, queries, _params(memory50k, 10, nprobe), gt)
+
+
+def test_search_nucleus_matches_oracle(ctx, quality50k, mix50k):
+    _, queries, gt = mix50k
+    _compare_search(ctx, quality50k, queries, _params(quality50k, 10, 32, tc=0.95), gt)
+
+
+def test_search_small_batches_and_k(ctx, quality50k, mix50k):
+    _, queries, _ = mix50k
+    ix = quality50k
+    for nq, k in [(1, 10), (3, 1), (17, 100)]:
+        _compare_search(ctx, ix, queries[:nq], _params(ix, k, 16))
+
+
+def test_binding_search_batch(quality50k, mix50k):
+    """The Python drop-in (FlatCellIndex.search_batch) returns the oracle's answer as ids."""
+    _, queries, gt = mix50k
+    ix = quality50k
+    ids, scores = ix.search_batch(queries, 10, 16, 1.0, 8.0, True)
+    p = _params(ix, 10, 16)
+    oslots, oscores = oracle.search_batch(ix._arena_desc(), queries, p, 8)
+    ext = ix._ext_ids()
+    oids = np.where(oslots == 0xFFFFFFFF, np.iinfo(np.uint64).max, ext[np.minimum(oslots, len(ext) - 1)])
+    assert np.array_equal(np.array(ids, dtype=np.uint64).reshape(oids.shape), oids)
+    assert np.array(scores, np.float32).tobytes() == oscores.tobytes()
