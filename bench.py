@@ -1,0 +1,283 @@
+#!/usr/bin/env python3
+"""Batched cell-major search on one MI355X: batch QPS at matched R@10, plus the scan's
+achieved bandwidth against the HBM roofline.
+
+Workload (default): 500k x 384 f32 unit vectors from the seeded 4,096-component anisotropic
+mixture, 1,000 held-out queries, the `quality` preset (orthogonal polysemy + FastScan +
+two-stage routing + adaptive probing, 3,906 cells, f32 rerank), k = 10.
+
+A step is one search_batch pass over the 1,000-query batch, queries already resident in HBM,
+through libmaivs_gpu.so's C ABI. The operating point is the cheapest (nprobe, rerank_factor)
+of the sweep whose R@10 reaches --target (0.99); K steps are timed there. The CPU baseline is
+the oracle (the C++ restatement of the reference CPU path) on the host cores, same index, same
+grid, bounded to one pass per grid point.
+
+Prints ONE JSON line on stdout; progress goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "batch QPS at R@10 0.95/0.99, 500k×384 f32, 1 MI355X; scan HBM GB/s"
+HBM_PEAK_GBS = 8000.0
+NPROBE_GRID = (1, 2, 3, 4, 6, 8, 10, 12, 16, 20, 24, 32, 48, 64, 96, 128)
+RF_GRID = (8, 16, 32)
+TARGETS = (0.95, 0.99, 0.995)
+
+
+def log(msg: str) -> None:
+    print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
+
+
+def frontier(pts, rk, vk):
+    """Points not dominated in (recall up, value up), bench/fair/summarise.py:28-37."""
+    s = sorted(pts, key=lambda p: (-p[rk], -p[vk]))
+    out, best = [], None
+    for p in s:
+        if best is None or p[vk] > best:
+            out.append(p)
+            best = p[vk]
+    return sorted(out, key=lambda p: p[rk])
+
+
+def interp(front, rk, vk, t):
+    """Log-interpolated value at recall t, never extrapolated (summarise.py:40-46)."""
+    for a, b in zip(front, front[1:]):
+        if a[rk] <= t <= b[rk]:
+            f = (t - a[rk]) / max(b[rk] - a[rk], 1e-12)
+            return math.exp(math.log(a[vk]) + f * (math.log(b[vk]) - math.log(a[vk])))
+    if front and abs(front[-1][rk] - t) < 1e-9:
+        return front[-1][vk]
+    return float("nan")
+
+
+def at_or_above(pts, rk, vk, t):
+    ok = [p for p in pts if p[rk] >= t]
+    return max(ok, key=lambda p: p[vk]) if ok else None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="mix500k")
+    ap.add_argument("--profile", default="quality", choices=("quality", "memory"))
+    ap.add_argument("--target", type=float, default=0.99)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-threads", type=int, default=0, help="0 = all host cores")
+    ap.add_argument("--only", default="", help="time only this point, e.g. 12:8 (nprobe:rf)")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU; --gpus {args.gpus} is not supported by this build "
+              f"(the multi-GPU sharding is a design, see the design notes)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import maivs_amd as M
+    from maivs_amd import capi, mixture
+
+    dev = torch.device("cuda:0")
+    torch.cuda.init()
+    k = 10
+    t0 = time.time()
+    base, queries = mixture.workload(args.workload)
+    nq = len(queries)
+    log(f"workload {args.workload}: base {base.shape}, queries {queries.shape} ({time.time() - t0:.1f}s)")
+    t0 = time.time()
+    gt = mixture.exact_topk(base, queries, k, device="cuda:0")
+    log(f"exact ground truth ({time.time() - t0:.1f}s)")
+    t0 = time.time()
+    ix = M.build_preset(base, args.profile)
+    st = ix.stats()
+    log(f"index built: {int(st['n_cells'])} cells, {st['member_entries']:.0f} entries ({time.time() - t0:.1f}s)")
+    ext = ix._ext_ids()
+
+    ctx = capi.Context(0)
+    t0 = time.time()
+    ctx.upload(ix._arena_desc())
+    log(f"arena uploaded ({time.time() - t0:.2f}s)")
+    dq = torch.from_numpy(queries).to(dev)
+    d_slots = torch.empty((nq, k), dtype=torch.int32, device=dev)
+    d_scores = torch.empty((nq, k), dtype=torch.float32, device=dev)
+
+    def params(nprobe, rf):
+        ix.set_rerank_factor(rf)
+        return capi.params_from_bytes(ix._search_params(k, nprobe, 1.0, 8.0))
+
+    def gpu_call(p, stats=None):
+        ctx.search_device(dq.data_ptr(), nq, p, d_slots.data_ptr(), d_scores.data_ptr(), stats)
+
+    def recall_of(slots):
+        slots = slots.astype(np.uint32)
+        ids = np.where(slots == 0xFFFFFFFF, -1, ext[np.minimum(slots, len(ext) - 1)].astype(np.int64))
+        return mixture.recall_at(ids, gt, k)
+
+    # ---- sweep (GPU), recall per point
+    grid = [(npb, rf) for rf in RF_GRID for npb in NPROBE_GRID if npb <= st["n_cells"]]
+    if args.only:
+        a, b = args.only.split(":")
+        grid = [(int(a), int(b))]
+    pts = []
+    for npb, rf in grid:
+        p = params(npb, rf)
+        gpu_call(p)
+        torch.cuda.synchronize()
+        r = recall_of(d_slots.cpu().numpy())
+        best = float("inf")
+        for _ in range(5):
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            gpu_call(p)
+            torch.cuda.synchronize()
+            best = min(best, time.perf_counter() - t)
+        pts.append({"nprobe": npb, "rf": rf, "recall": r, "qps": nq / best})
+    log("sweep: " + " ".join(f"np{p['nprobe']}/rf{p['rf']}:{p['recall']:.4f}@{p['qps']:.0f}" for p in pts))
+
+    op = at_or_above(pts, "recall", "qps", args.target) or max(pts, key=lambda p: p["recall"])
+    npb, rf = op["nprobe"], op["rf"]
+    p = params(npb, rf)
+    log(f"operating point nprobe={npb} rf={rf} R@10={op['recall']:.4f}")
+
+    # ---- timed region: K steps, per-step stage timings from the library's HIP events
+    for _ in range(args.warmup):
+        gpu_call(p)
+    stats = capi.GpuStats()
+    acc = {}
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    for _ in range(args.steps):
+        gpu_call(p, stats)
+        for kk, v in stats.as_dict().items():
+            acc[kk] = acc.get(kk, 0.0) + float(v)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t_start
+    value = nq * args.steps / elapsed
+    ms_per_step = 1e3 * elapsed / args.steps
+    avg = {kk: v / args.steps for kk, v in acc.items()}
+    r_final = recall_of(d_slots.cpu().numpy())
+    log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step, {value:.0f} QPS, R@10 {r_final:.4f}")
+
+    # ---- roofline of the dominant kernel (algorithmic bytes / its average duration)
+    d = base.shape[1]
+    row_bytes = d * 4 if args.profile == "quality" else d
+    blk = 2048  # one 32-vector FastScan block of 64-byte codes
+    stages = {
+        # name: (avg ms, algorithmic bytes per launch, what the bytes are)
+        "prep_route_kernel": (avg["ms_prep"],
+                              nq * (d * 4 + int(st["n_cells"]) * 64 + 2048),
+                              "query f32 + every centroid code + the FastScan table written"),
+        "seed_kernel": (avg["ms_seed"], avg["seed_blocks"] * blk + nq * 2048,
+                        "seed cells' FastScan blocks + the query table"),
+        "cell_scan_kernel": (avg["ms_scan"], avg["scan_blocks"] * blk + nq * 2048,
+                             "probed cells' FastScan blocks per (query, cell) + the query table"),
+        "finish_kernel": (avg["ms_rerank"], avg["rerank_rows"] * row_bytes,
+                          "rerank rows gathered"),
+    }
+    dom = max(stages, key=lambda s_: stages[s_][0])
+    ms_dom, bytes_dom, what = stages[dom]
+    achieved = bytes_dom / (ms_dom * 1e-3) / 1e9 if ms_dom > 0 else 0.0
+    scan_ms = avg["ms_seed"] + avg["ms_scan"]
+    scan_bytes = (avg["seed_blocks"] + avg["scan_blocks"]) * blk + nq * 2048
+    scan_gbs = scan_bytes / (scan_ms * 1e-3) / 1e9 if scan_ms > 0 else 0.0
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dom,
+                "kernel_ms": round(ms_dom, 4), "bytes_per_launch": int(bytes_dom), "bytes_are": what}
+    log(f"stages (avg ms): " + ", ".join(f"{s_}={stages[s_][0]:.4f}" for s_ in stages))
+
+    # ---- CPU baseline: the oracle on the host cores, same index, same grid
+    cpu = None
+    cpu_pts = []
+    if not args.no_cpu:
+        import oracle
+        threads = args.cpu_threads or (os.cpu_count() or 1)
+        desc = ix._arena_desc()
+        t_all = time.time()
+        for pt in pts:
+            pp = params(pt["nprobe"], pt["rf"])
+            dt = float("inf")
+            for _ in range(3):  # best of 3, as bench/fair/fairbench.py:52-58
+                t = time.perf_counter()
+                oracle.search_batch(desc, queries, pp, threads)
+                dt = min(dt, time.perf_counter() - t)
+            cpu_pts.append({**pt, "qps": nq / dt})
+            if time.time() - t_all > 40:
+                log("cpu baseline: time budget reached, stopping the grid early")
+                break
+        cop = at_or_above(cpu_pts, "recall", "qps", args.target) or max(cpu_pts, key=lambda q: q["recall"])
+        cpu = {"value": round(cop["qps"], 1), "unit": "queries/s", "cores": threads, "kind": "port",
+               "sample": (f"oracle (C++ restatement of route_batch + search_batch_cellmajor + rerank_exact), "
+                          f"best of 3 1,000-query search_batch calls per grid point over {len(cpu_pts)} points; value = "
+                          f"best point with R@10 >= {args.target}: nprobe={cop['nprobe']} rf={cop['rf']} "
+                          f"R@10={cop['recall']:.4f}"),
+               "cpu_model": _cpu_model()}
+        log(f"cpu baseline: {cop['qps']:.0f} QPS at np{cop['nprobe']}/rf{cop['rf']} on {threads} threads "
+            f"({time.time() - t_all:.1f}s)")
+
+    gfront = frontier(pts, "recall", "qps")
+    matched = {str(t): {"gpu_interp": _r(interp(gfront, "recall", "qps", t)),
+                        "gpu_at_or_above": _r((at_or_above(pts, "recall", "qps", t) or {}).get("qps"))}
+               for t in TARGETS}
+    if cpu_pts:
+        cfront = frontier(cpu_pts, "recall", "qps")
+        for t in TARGETS:
+            matched[str(t)]["cpu_interp"] = _r(interp(cfront, "recall", "qps", t))
+            matched[str(t)]["cpu_at_or_above"] = _r((at_or_above(cpu_pts, "recall", "qps", t) or {}).get("qps"))
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "queries/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8+f32",
+        "data": "synthetic (seeded Gaussian mixture, no external data)",
+        "config": {"workload": f"{args.workload} {args.profile}: {base.shape[0]}x{d} f32, {nq} queries, "
+                               f"k={k}, {int(st['n_cells'])} cells",
+                   "batch": nq, "k": k, "nprobe": npb, "rerank_factor": rf, "recall_at_10": round(r_final, 4),
+                   "target_recall": args.target, "parallelism": "1 GPU",
+                   "scan_gbs": round(scan_gbs, 1), "scan_frac_of_hbm": round(scan_gbs / HBM_PEAK_GBS, 4),
+                   "stage_ms": {s_: round(stages[s_][0], 4) for s_ in stages},
+                   "matched_recall_qps": matched},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    ctx.close()
+    return 0
+
+
+def _r(x):
+    return None if x is None or (isinstance(x, float) and math.isnan(x)) else round(float(x), 1)
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+if __name__ == "__main__":
+    sys.exit(main())

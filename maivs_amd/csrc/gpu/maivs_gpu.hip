@@ -79,6 +79,11 @@ struct Ctl {
     uint32_t err_shortlist;   // a shortlist exceeded the sort capacity
     uint32_t max_shortlist;
     uint32_t pad[3];
+    unsigned long long seed_blocks;  // 32-vector blocks the seed scan read (work counter)
+    unsigned long long scan_blocks;  // 32-vector blocks the cell-major scan scored, per query
+    unsigned long long scan_pairs;   // (query, cell) pairs of the cell-major scan
+    unsigned long long survivors;    // candidates the cell-major scan emitted
+    unsigned long long rerank_rows;  // rows the rerank read
 };
 
 struct Work {
@@ -533,6 +538,10 @@ seed_kernel(DevArena A, Work Wk, KParams K) {
     // ---- seed: every canonical member of the first ns probed cells (src/index.rs:2150-2154)
     const uint32_t ns = min(kSeedCells, nch);
     uint2* seed = Wk.seed + static_cast<uint64_t>(qi) * K.seed_cap;
+    if (tid < ns) {
+        const uint32_t c = chosen[tid];
+        atomicAdd(&Wk.ctl->seed_blocks, static_cast<unsigned long long>((A.mem_off[c + 1] - A.mem_off[c] + 31) / 32));
+    }
     for (uint32_t si = 0; si < ns; ++si) {
         const uint32_t c = chosen[si];
         const uint32_t e0 = A.mem_off[c], len = A.mem_off[c + 1] - e0;
@@ -614,12 +623,22 @@ seed_kernel(DevArena A, Work Wk, KParams K) {
 
 // ---------------------------------------------------------------- inversion: cell -> queries
 
-__global__ void invert_count_kernel(Work Wk, KParams K) {
+__global__ void invert_count_kernel(Work Wk, KParams K, const uint32_t* __restrict__ mem_off) {
     uint32_t qi = blockIdx.x;
     if (qi >= K.nq) return;
     uint32_t ns = min(kSeedCells, Wk.nchosen[qi]), re = Wk.rest_end[qi];
     const uint32_t* chosen = Wk.chosen + static_cast<uint64_t>(qi) * K.nprobe;
-    for (uint32_t i = ns + threadIdx.x; i < re; i += blockDim.x) atomicAdd(&Wk.cell_cnt[chosen[i]], 1u);
+    uint32_t blocks = 0;
+    for (uint32_t i = ns + threadIdx.x; i < re; i += blockDim.x) {
+        uint32_t c = chosen[i];
+        atomicAdd(&Wk.cell_cnt[c], 1u);
+        blocks += (mem_off[c + 1] - mem_off[c] + 31) / 32;
+    }
+    blocks = wave_sum_u32(blocks);
+    if (threadIdx.x == 0 && blocks) {
+        atomicAdd(&Wk.ctl->scan_blocks, static_cast<unsigned long long>(blocks));
+        atomicAdd(&Wk.ctl->scan_pairs, static_cast<unsigned long long>(re - ns));
+    }
 }
 
 // Single workgroup: exclusive scan of cell_cnt[0..M) -> cell_off[0..M], cell_cur = cell_off.
@@ -828,6 +847,8 @@ finish_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries,
         Wk.cut[qi] = cutv;
         Wk.ncand[qi] = n;
         atomicMax(&Wk.ctl->max_cand, Wk.cand_cnt[qi]);
+        atomicAdd(&Wk.ctl->survivors, static_cast<unsigned long long>(Wk.cand_cnt[qi]));
+        atomicAdd(&Wk.ctl->rerank_rows, static_cast<unsigned long long>(n));
     }
 }
 
@@ -1093,7 +1114,7 @@ int launch_scan(maivs_gpu_ctx* ctx, const KParams& K) {
     Work& W = ctx->Wk;
     HIP_TRY(ctx, hipMemsetAsync(W.cell_cnt, 0, (A.M + 1) * sizeof(uint32_t), ctx->stream));
     HIP_TRY(ctx, hipMemsetAsync(W.cand_cnt, 0, K.nq * sizeof(uint32_t), ctx->stream));
-    hipLaunchKernelGGL(invert_count_kernel, dim3(K.nq), dim3(64), 0, ctx->stream, W, K);
+    hipLaunchKernelGGL(invert_count_kernel, dim3(K.nq), dim3(64), 0, ctx->stream, W, K, A.mem_off);
     hipLaunchKernelGGL(invert_scan_kernel, dim3(1), dim3(1024), 0, ctx->stream, W, A.M);
     hipLaunchKernelGGL(invert_fill_kernel, dim3(K.nq), dim3(64), 0, ctx->stream, W, K);
     HIP_TRY(ctx, hipGetLastError());
@@ -1187,6 +1208,8 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
     if (hipEventElapsedTime(&ms, ctx->ev[2], ctx->ev[4]) == hipSuccess) S.ms_invert = ms;
     if (hipEventElapsedTime(&ms, ctx->ev[4], ctx->ev[5]) == hipSuccess) S.ms_scan = ms;
     if (hipEventElapsedTime(&ms, ctx->ev[5], ctx->ev[6]) == hipSuccess) S.ms_rerank = ms;
+    S.seed_blocks = ctl.seed_blocks;
+    S.scan_blocks = ctl.scan_blocks;
 
     std::vector<float> cs;
     std::vector<uint32_t> ch;
@@ -1216,6 +1239,8 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
             if ((rc = launch_scan(ctx, K))) return rc;
             if ((rc = launch_finish(ctx, K, d_q, d_slots, d_scores))) return rc;
             if ((rc = read_ctl(ctx, &ctl))) return rc;
+            S.seed_blocks = ctl.seed_blocks;
+            S.scan_blocks = ctl.scan_blocks;
         }
     }
     // (2) adaptive cuts near their threshold
@@ -1255,25 +1280,17 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
     if (rerun_scan) {
         S.reruns++;
         HIP_TRY(ctx, hipMemsetAsync(W.ctl, 0, sizeof(Ctl), ctx->stream));
+        // the seed stage is not re-run: keep its counter
         if ((rc = launch_scan(ctx, K))) return rc;
         if ((rc = launch_finish(ctx, K, d_q, d_slots, d_scores))) return rc;
         if ((rc = read_ctl(ctx, &ctl))) return rc;
         if (ctl.max_cand > ctx->cap_cand) return fail(ctx, MAIVS_ERR_HIP, "candidate count changed between passes");
+        S.scan_blocks = ctl.scan_blocks;
     }
-    // work counters
-    {
-        std::vector<uint32_t> nch(nq), re(nq), cc(nq), nc(nq);
-        HIP_TRY(ctx, hipMemcpy(nch.data(), W.nchosen, nq * 4, hipMemcpyDeviceToHost));
-        HIP_TRY(ctx, hipMemcpy(re.data(), W.rest_end, nq * 4, hipMemcpyDeviceToHost));
-        HIP_TRY(ctx, hipMemcpy(cc.data(), W.cand_cnt, nq * 4, hipMemcpyDeviceToHost));
-        HIP_TRY(ctx, hipMemcpy(nc.data(), W.ncand, nq * 4, hipMemcpyDeviceToHost));
-        for (uint32_t i = 0; i < nq; ++i) {
-            uint32_t ns = std::min(kSeedCells, nch[i]);
-            S.scan_pairs += re[i] > ns ? re[i] - ns : 0;
-            S.survivors += cc[i];
-            S.rerank_rows += nc[i];
-        }
-    }
+    // work counters of the pass that produced the results
+    S.scan_pairs = ctl.scan_pairs;
+    S.survivors = ctl.survivors;
+    S.rerank_rows = ctl.rerank_rows;
     ctx->last_nq = nq;
     return 0;
 }
