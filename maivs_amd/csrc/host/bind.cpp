@@ -5,6 +5,7 @@
 #include <pybind11/stl.h>
 
 #include <cstring>
+#include <type_traits>
 
 #include "index.h"
 
@@ -28,16 +29,11 @@ F32Rows as_rows(const py::array& a, const char* what, const char* contig_msg) {
     return {static_cast<const float*>(a.data()), static_cast<size_t>(a.shape(0)), static_cast<size_t>(a.shape(1))};
 }
 
+// Index errors cross into Python through a registered translator (it runs with the GIL held,
+// so C++ code may throw them from regions that released the GIL).
 template <class F>
 auto translate(F&& f) -> decltype(f()) {
-    try {
-        return f();
-    } catch (const maivs::ValueError& e) {
-        throw py::value_error(e.what());
-    } catch (const maivs::Unsupported& e) {
-        PyErr_SetString(PyExc_NotImplementedError, e.what());
-        throw py::error_already_set();
-    }
+    return f();
 }
 
 py::dict stats_dict(const maivs_gpu_stats& s) {
@@ -72,6 +68,15 @@ struct PyIndex {
 
 PYBIND11_MODULE(_maivs, m) {
     m.doc() = "MI355X-native batched cell-major search behind the MAIVS FlatCellIndex API";
+    py::register_exception_translator([](std::exception_ptr p) {
+        try {
+            if (p) std::rethrow_exception(p);
+        } catch (const maivs::ValueError& e) {
+            PyErr_SetString(PyExc_ValueError, e.what());
+        } catch (const maivs::Unsupported& e) {
+            PyErr_SetString(PyExc_NotImplementedError, e.what());
+        }
+    });
 
     py::class_<PyIndex>(m, "FlatCellIndex")
         .def(py::init([](size_t dim, const std::string& scan_mode, size_t rerank_factor, uint64_t seed,
@@ -213,6 +218,45 @@ PYBIND11_MODULE(_maivs, m) {
                  std::memcpy(a.mutable_data(), b.data(), b.size() * sizeof(uint64_t));
                  return a;
              })
+        .def("_arena_arrays",
+             [](PyIndex& s) {
+                 const maivs_arena_desc* a = s.ix.arena_desc();
+                 if (!a) throw py::value_error("index is not compacted");
+                 auto copy = [](const auto* p, size_t n) {
+                     using T = std::remove_cv_t<std::remove_pointer_t<decltype(p)>>;
+                     py::array_t<T> out(static_cast<py::ssize_t>(p ? n : 0));
+                     if (p && n) std::memcpy(out.mutable_data(), p, n * sizeof(T));
+                     return out;
+                 };
+                 const size_t M = a->n_cells, N = a->n_slots, d = a->dim, W = a->n_words;
+                 const size_t E = a->mem_off[M], B = a->fs_off ? a->fs_off[M] : 0;
+                 py::dict r;
+                 r["dim"] = a->dim;
+                 r["dim_pad"] = a->dim_pad;
+                 r["n_words"] = a->n_words;
+                 r["n_cells"] = a->n_cells;
+                 r["n_slots"] = a->n_slots;
+                 r["max_assign"] = a->max_assign;
+                 r["rerank_mode"] = a->rerank_mode;
+                 r["fs_codes"] = copy(a->fs_codes, B * W * 256);
+                 r["fs_off"] = copy(a->fs_off, a->fs_off ? M + 1 : 0);
+                 r["mem_off"] = copy(a->mem_off, M + 1);
+                 r["members"] = copy(a->members, E);
+                 r["slot_cells"] = copy(a->slot_cells, N * a->max_assign);
+                 r["cent_bits"] = copy(a->cent_bits, M * W);
+                 r["cent_sq8"] = copy(a->cent_sq8, M * d);
+                 r["centroids"] = copy(a->centroids, M * d);
+                 r["csq_min"] = copy(a->csq_min, d);
+                 r["csq_step"] = copy(a->csq_step, d);
+                 r["r_bound"] = copy(a->r_bound, M);
+                 r["rot_signs"] = copy(a->rot_signs, 2 * static_cast<size_t>(a->dim_pad));
+                 r["vecs_f32"] = copy(a->vecs_f32, N * d);
+                 r["sq8_codes"] = copy(a->sq8_codes, N * d);
+                 r["sq_min"] = copy(a->sq_min, d);
+                 r["sq_step"] = copy(a->sq_step, d);
+                 return r;
+             },
+             "Copies of the compacted arena arrays (for brute-force checks).")
         .def("_rot_signs", [](PyIndex& s) {
             const auto& r = s.ix.rot_signs();
             py::array_t<float> a(static_cast<py::ssize_t>(r.size()));
