@@ -167,6 +167,9 @@ def main() -> int:
     value = nq * args.steps / elapsed
     ms_per_step = 1e3 * elapsed / args.steps
     avg = {kk: v / args.steps for kk, v in acc.items()}
+    ctx.last_counters(stats)  # work counters of a batch (identical every step)
+    for kk in ("seed_blocks", "scan_blocks", "scan_pairs", "survivors", "rerank_rows"):
+        avg[kk] = float(getattr(stats, kk))
     r_final = recall_of(d_slots.cpu().numpy())
     log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step, {value:.0f} QPS, R@10 {r_final:.4f}")
 

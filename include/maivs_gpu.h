@@ -89,7 +89,9 @@ typedef struct maivs_search_params {
     float at_margin;          /* its margin */
 } maivs_search_params;
 
-/* Per-call measurements (filled when a non-NULL pointer is passed). */
+/* Per-call measurements. maivs_gpu_search_batch* fills the times and host_* / reruns fields
+ * (HIP events on the context's stream; no extra device work); the work counters (the *_blocks,
+ * scan_pairs, survivors, rerank_rows fields) are filled on demand by maivs_gpu_last_counters. */
 typedef struct maivs_gpu_stats {
     float ms_total;       /* device time of the whole pipeline (hipEvents) */
     float ms_prep;        /* rotation, sign codes, FastScan tables */
@@ -152,6 +154,12 @@ int maivs_gpu_block_sums(maivs_gpu_ctx* ctx, uint32_t n_words, const uint8_t* bl
 int maivs_gpu_route(maivs_gpu_ctx* ctx, const float* queries, uint32_t nq,
                     const maivs_search_params* params, uint32_t* out_chosen,
                     float* out_cscore, uint32_t* out_nchosen);
+
+/* Work counters of the last maivs_gpu_search_batch* call into `stats` (other fields untouched):
+ * seed_blocks / scan_blocks = 32-vector FastScan blocks scored by the seed and cell-major scans
+ * (one per (query, block) pair), scan_pairs = (query, cell) pairs of the cell-major scan,
+ * survivors = candidates it emitted, rerank_rows = rows the rerank read. */
+int maivs_gpu_last_counters(maivs_gpu_ctx* ctx, maivs_gpu_stats* stats);
 
 /*
  * Intermediates of the last maivs_gpu_search_batch* call (host buffers, NULL to skip):

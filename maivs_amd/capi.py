@@ -68,6 +68,7 @@ SIGNATURES = {
     "maivs_gpu_block_sums": (I32, [P, U32, P, P, U32, P]),
     "maivs_gpu_route": (I32, [P, P, U32, C.POINTER(SearchParams), P, P, P]),
     "maivs_gpu_last_candidates": (I32, [P, P, P, P, P, P, P, U64]),
+    "maivs_gpu_last_counters": (I32, [P, C.POINTER(GpuStats)]),
 }
 
 _lib = None
@@ -173,6 +174,10 @@ class Context:
         self._check(self.lib.maivs_gpu_route(self.h, ptr(q), nq, C.byref(params), ptr(chosen), ptr(cscore),
                                              ptr(nchosen)), "maivs_gpu_route")
         return chosen, cscore, nchosen
+
+    def last_counters(self, stats: GpuStats) -> GpuStats:
+        self._check(self.lib.maivs_gpu_last_counters(self.h, C.byref(stats)), "maivs_gpu_last_counters")
+        return stats
 
     def last_candidates(self, nq: int, cap: int):
         tau, rest_end, cut, ncand = (np.empty(nq, np.uint32) for _ in range(4))

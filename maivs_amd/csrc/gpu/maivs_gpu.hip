@@ -2,23 +2,21 @@
 // include/maivs_gpu.h. Restates MAIVS's FlatCellIndex::search_batch_cellmajor
 // (src/index.rs:1999-2311) with route_batch (:1873-1980) and rerank_exact (:1309-1378).
 //
-// Pipeline of one batch (one HIP stream, no host round trip until the end):
+// Pipeline of one batch (one HIP stream; the host syncs once, at the end, on a small control block):
+//   reset        zero the per-call counters
 //   prep_route   one workgroup per query: rotation (2 x sign flip + FWHT), 1-bit code,
 //                FastScan table, Hamming against every centroid code, tie-inclusive
 //                shortlist, exact SQ8 rescore, probe list sorted (score desc, cell asc)
-//   seed         one workgroup per query: scan of the first 8 probed cells, seed cut-off
-//                tau, adaptive probe cut
-//   invert       count / scan / fill: cell -> probing queries
-//   cell_scan    one workgroup per probed cell: each lane holds one member's code in
-//                registers; groups of 4 probing queries' tables are interleaved in LDS so one
-//                ds_read_b32 looks up a nibble for 4 queries; survivors d <= tau appended
+//   seed         one workgroup per query: every member of the first 8 probed cells scored at
+//                once, seed cut-off tau (only d <= tau kept), adaptive probe cut, probe counts
+//   invert       scan / fill: cell -> probing queries
+//   cell_scan    one workgroup per probed cell: each lane holds one member's code; groups of 4
+//                probing queries' tables are interleaved in LDS so one ds_read_b32 looks up a
+//                nibble for 4 queries; survivors d <= tau appended per query
 //   finish       one workgroup per query: exact tie-inclusive cut at k*rerank_factor, exact
-//                f32 / SQ8 rerank, top-k (score desc, slot asc)
-// The host reads a small control block at the end; rare events (candidate buffer overflow,
-// libm-sensitive decisions near their threshold) re-run the affected stages.
-//
-// Compiled with -ffp-contract=off: every FMA below is an explicit __builtin_fmaf standing
-// for one of the reference's _mm256_fmadd_ps.
+//                f32 / SQ8 rerank over chain-major rows, top-k (score desc, slot asc)
+// Rare events (candidate buffer overflow, libm-sensitive decisions near their threshold) re-run
+// the affected stages after the host has read the control block.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -28,830 +26,19 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "../../../include/maivs_gpu.h"
-#include "device_common.h"
+#include "kernels.h"
 
 using namespace maivs_dev;
 
 namespace {
-
-constexpr uint32_t kSeedCells = 8;       // SEED_CELLS, src/index.rs:2018
-constexpr uint32_t kRouteThreads = 256;
-constexpr uint32_t kScanThreads = 256;
-constexpr uint32_t kG = 4;               // queries interleaved per cell_scan table pass
-constexpr uint32_t kHistBins = 256;
-constexpr uint32_t kFinishSortCap = 2048;  // final candidates sorted in LDS up to this many
-constexpr size_t kLdsBudget = 160 * 1024;
-// Host re-evaluation bands around libm-sensitive thresholds (see host_check_* below).
+// Host re-evaluation bands around libm-sensitive thresholds (see host_nucleus / host_rest_end).
 constexpr float kPruneBand = 4e-6f;
 constexpr float kNucleusBand = 2e-3f;
-
-// ---------------------------------------------------------------- arena / params on device
-
-struct DevArena {
-    uint32_t d, P, W, M, N, ma, rerank_mode, npos, maxk, n_live, max_cell_len, MW;
-    uint64_t E;
-    float fht_scale;
-    const uint32_t* codes;      // E x (2W) dwords, entry-major 1-bit codes
-    const uint32_t* members;    // E
-    const uint32_t* mem_off;    // M + 1
-    const uint32_t* slot_cells; // N x ma
-    const uint64_t* cent_bits;  // M x W
-    const uint8_t* cent_sq8;    // M x d or null
-    const float* centroids;     // M x d (used when cent_sq8 is null)
-    const float* csq_min;
-    const float* csq_step;
-    const float* r_bound;       // M
-    const float* rot_signs;     // 2P
-    const float* vecs;          // N x d (f32 rerank)
-    const uint8_t* sq8;         // N x d (SQ8 rerank)
-    const float* sq_min;
-    const float* sq_step;
-    const uint8_t* live;        // M
-};
-
-struct Ctl {
-    uint32_t nflag_route;
-    uint32_t nflag_prune;
-    uint32_t max_cand;
-    uint32_t err_shortlist;   // a shortlist exceeded the sort capacity
-    uint32_t max_shortlist;
-    uint32_t pad[3];
-    unsigned long long seed_blocks;  // 32-vector blocks the seed scan read (work counter)
-    unsigned long long scan_blocks;  // 32-vector blocks the cell-major scan scored, per query
-    unsigned long long scan_pairs;   // (query, cell) pairs of the cell-major scan
-    unsigned long long survivors;    // candidates the cell-major scan emitted
-    unsigned long long rerank_rows;  // rows the rerank read
-};
-
-struct Work {
-    // per query
-    float* q;              // nq x d (host-input calls)
-    uint64_t* qbits;       // nq x W
-    uint8_t* lut;          // nq x npos*16
-    float* delta;          // nq
-    float* bias;           // nq
-    uint32_t* chosen;      // nq x nprobe
-    float* cscore;         // nq x nprobe
-    uint32_t* nchosen;     // nq
-    uint32_t* probed;      // nq x MW
-    uint2* seed;           // nq x seed_cap (d, slot)
-    uint32_t* seed_cnt;    // nq
-    uint32_t* tau;         // nq
-    uint32_t* rest_end;    // nq
-    uint2* cand;           // nq x cand_cap
-    uint32_t* cand_cnt;    // nq
-    uint2* fin;            // nq x fin_cap (d, slot) final candidates
-    uint64_t* keys;        // nq x key_cap (global sort fallback)
-    uint32_t* cut;         // nq
-    uint32_t* ncand;       // nq
-    uint32_t* out_slots;   // nq x k (host-output calls)
-    float* out_scores;     // nq x k
-    // per cell
-    uint32_t* cell_cnt;    // M + 1
-    uint32_t* cell_off;    // M + 1
-    uint32_t* cell_cur;    // M
-    uint32_t* qof;         // nq x nprobe
-    uint32_t* flag_route;  // nq
-    uint32_t* flag_prune;  // nq
-    Ctl* ctl;
-};
-
-struct KParams {
-    uint32_t nq, k, nprobe, want_c, target, adaptive, sort_cap, use_nucleus;
-    uint32_t seed_cap, cand_cap, fin_cap, key_cap, fin_sort_cap;
-    float tc, beta, at_margin, norm, prune_band, nucleus_band;
-};
-
-// ---------------------------------------------------------------- small device pieces
-
-// One member's nibble sums against a FastScan table of G interleaved queries in LDS.
-// `code` = the member's entry-major code (2*NW dwords; nibble j at dword j/8, bits 4*(j%8)),
-// streamed 16 bytes (32 positions) at a time with the next chunk prefetched. Table byte
-// [(j*16 + e)*G + g] = query g's entry e of position j.
-template <int G>
-__device__ __forceinline__ void lut_chunk(uint32_t dw0, uint32_t dw1, uint32_t dw2, uint32_t dw3, int npos,
-                                          const uint8_t* tk, uint32_t& S, uint32_t& T) {
-#pragma unroll
-    for (int t = 0; t < 32; ++t) {
-        if (t < npos) {
-            const uint32_t dw = t < 8 ? dw0 : t < 16 ? dw1 : t < 24 ? dw2 : dw3;
-            const uint32_t nib = (dw >> (4 * (t & 7))) & 0xFu;
-            if constexpr (G == 1) {
-                S += tk[t * 16 + nib];
-            } else {
-                const uint32_t v = reinterpret_cast<const uint32_t*>(tk)[t * 16 + nib];
-                S += v;
-                T += __builtin_amdgcn_perm(0u, v, 0x0c030c01u);  // bytes 1,3 -> u16 lanes
-            }
-        }
-    }
-}
-
-template <int NW, int G>
-__device__ __forceinline__ void lut_sums(const uint32_t* __restrict__ code, const uint8_t* table, uint32_t (&sum)[G]) {
-    static_assert(G == 1 || G == 4, "G is 1 or 4");
-    // S accumulates table words; for G = 4 it is b0 + 256 b1 + 65536 b2 + 2^24 b3 (mod 2^32) and T
-    // the odd bytes as u16 lanes (b1 + 65536 b3). Every per-query sum is at most 255 * 16 * NW
-    // < 65536, so both un-mix exactly at the end.
-    uint32_t S = 0, T = 0;
-    if constexpr (NW == 1) {
-        uint2 v = *reinterpret_cast<const uint2*>(code);
-        lut_chunk<G>(v.x, v.y, 0u, 0u, 16, table, S, T);
-    } else {
-        constexpr int NCH = NW / 2;  // 16-byte chunks of 32 positions
-        const uint4* p = reinterpret_cast<const uint4*>(code);
-        uint4 v = p[0];
-#pragma unroll 1
-        for (int k = 0; k < NCH; ++k) {
-            uint4 vn = (k + 1 < NCH) ? p[k + 1] : v;
-            lut_chunk<G>(v.x, v.y, v.z, v.w, 32, table + static_cast<uint32_t>(k) * 32 * 16 * G, S, T);
-            v = vn;
-        }
-    }
-    if constexpr (G == 1) {
-        sum[0] = S;
-    } else {
-        uint32_t b1 = T & 0xFFFFu, b3 = T >> 16;
-        uint32_t r = S - (b1 << 8) - (b3 << 24);
-        sum[0] = r & 0xFFFFu;
-        sum[1] = b1;
-        sum[2] = r >> 16;
-        sum[3] = b3;
-    }
-}
-
-// canonical(slot, c, probed) of src/index.rs:2036-2045: false when another home h < c of the
-// slot was probed by the query.
-__device__ __forceinline__ bool canonical(const DevArena& A, uint32_t slot, uint32_t c, const uint32_t* probed) {
-    if (A.ma <= 1) return true;
-    const uint32_t* h = A.slot_cells + static_cast<uint64_t>(slot) * A.ma;
-    for (uint32_t j = 0; j < A.ma; ++j) {
-        uint32_t hc = h[j];
-        if (hc != kNone && hc < c && ((probed[hc >> 5] >> (hc & 31)) & 1u)) return false;
-    }
-    return true;
-}
-
-// Exact target-th smallest of d values (1-based `want`) supplied by get(i), i < n, d < 65536.
-// Two 256-bin LDS histogram passes; every thread returns the value.
-template <class Get>
-__device__ uint32_t select_kth(uint32_t n, uint32_t want, Get get, uint32_t* hist, uint32_t* scratch) {
-    for (uint32_t i = threadIdx.x; i < kHistBins; i += blockDim.x) hist[i] = 0;
-    __syncthreads();
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) atomicAdd(&hist[get(i) >> 8], 1u);
-    __syncthreads();
-    // find the high byte: first bin where the inclusive prefix reaches want
-    uint32_t hb = 0, below = 0;
-    {
-        uint32_t v = threadIdx.x < kHistBins ? hist[threadIdx.x] : 0u;
-        uint32_t total;
-        uint32_t ex = block_excl_scan_u32(v, scratch, &total);
-        uint32_t cand = (threadIdx.x < kHistBins && ex < want && ex + v >= want) ? threadIdx.x : kNone;
-        hb = block_min_u32(cand, scratch);
-        // exclusive prefix at hb
-        uint32_t exb = (threadIdx.x == hb) ? ex : 0u;
-        below = block_sum_u32(exb, scratch);
-    }
-    for (uint32_t i = threadIdx.x; i < kHistBins; i += blockDim.x) hist[i] = 0;
-    __syncthreads();
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
-        uint32_t d = get(i);
-        if ((d >> 8) == hb) atomicAdd(&hist[d & 0xFFu], 1u);
-    }
-    __syncthreads();
-    uint32_t need = want - below;
-    uint32_t v = threadIdx.x < kHistBins ? hist[threadIdx.x] : 0u;
-    uint32_t total;
-    uint32_t ex = block_excl_scan_u32(v, scratch, &total);
-    uint32_t cand = (threadIdx.x < kHistBins && ex < need && ex + v >= need) ? threadIdx.x : kNone;
-    uint32_t lb = block_min_u32(cand, scratch);
-    return (hb << 8) | lb;
-}
-
-// f32 acos / cos / exp evaluated in f64 and rounded once. glibc's acosf / cosf / expf (what the
-// reference's f32::acos / cos / exp call) are not correctly rounded, so a decision that lands
-// within a small band of its threshold is flagged and re-evaluated on the host with libm.
-__device__ __forceinline__ float acos_f(float x) { return static_cast<float>(acos(static_cast<double>(x))); }
-__device__ __forceinline__ float cos_f(float x) { return static_cast<float>(cos(static_cast<double>(x))); }
-__device__ __forceinline__ float exp_f(float x) { return static_cast<float>(exp(static_cast<double>(x))); }
-
-// ---------------------------------------------------------------- upload: FastScan -> entry-major
-
-// Entry e of cell c (member position i) lives in block fs_off[c] + i/32, lane i%32; nibble j
-// is byte [(j/2)*32 + (j%2)*16 + lane%16], low half for lanes < 16 (src/quantize.rs:238-265).
-__global__ void fs_to_codes_kernel(const uint8_t* __restrict__ fs, const uint32_t* __restrict__ fs_off,
-                                   const uint32_t* __restrict__ mem_off, uint32_t M, uint32_t W,
-                                   uint32_t* __restrict__ codes) {
-    uint32_t c = blockIdx.x;
-    if (c >= M) return;
-    uint32_t e0 = mem_off[c], len = mem_off[c + 1] - e0;
-    const uint32_t bb = W * 256, nd = 2 * W;
-    for (uint32_t i = threadIdx.x; i < len; i += blockDim.x) {
-        const uint8_t* blk = fs + static_cast<uint64_t>(fs_off[c] + i / 32) * bb;
-        uint32_t lane = i % 32, li = lane % 16;
-        bool hi = lane >= 16;
-        for (uint32_t w = 0; w < nd; ++w) {
-            uint32_t dw = 0;
-            for (uint32_t t = 0; t < 8; ++t) {
-                uint32_t j = w * 8 + t;
-                uint8_t byte = blk[(j / 2) * 32 + (j % 2) * 16 + li];
-                uint32_t nib = hi ? (byte >> 4) : (byte & 0xFu);
-                dw |= nib << (4 * t);
-            }
-            codes[(static_cast<uint64_t>(e0) + i) * nd + w] = dw;
-        }
-    }
-}
-
-// Test entry point: nibble sums of nb entry-major codes (32 per block) against per-block tables.
-template <int NW>
-__global__ void entry_sums_kernel(const uint32_t* __restrict__ codes, const uint8_t* __restrict__ luts,
-                                  uint32_t n_entries, uint16_t* __restrict__ out) {
-    extern __shared__ uint8_t smem[];
-    constexpr uint32_t TB = NW * 256;
-    uint32_t b = blockIdx.x;  // one FastScan block = 32 entries
-    for (uint32_t i = threadIdx.x; i < TB; i += blockDim.x) smem[i] = luts[static_cast<uint64_t>(b) * TB + i];
-    __syncthreads();
-    uint32_t e = b * 32 + threadIdx.x;
-    if (threadIdx.x < 32 && e < n_entries) {
-        uint32_t s[1];
-        lut_sums<NW, 1>(codes + static_cast<uint64_t>(e) * (2 * NW), smem, s);
-        out[e] = static_cast<uint16_t>(s[0]);
-    }
-}
-
-// ---------------------------------------------------------------- prep + route
-
-// LDS layout of prep_route (dynamic): x[P] f32 | cqs[d] f32 | hs[M] u16 (padded) | keys[sort_cap] u64
-// | mins[npos] f32 | hist[P/ ... 513] u32 | scratch[16] u32
-template <int NW>
-__global__ void __launch_bounds__(kRouteThreads)
-prep_route_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries, uint32_t route_only) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    const uint32_t qi = blockIdx.x;
-    if (qi >= K.nq) return;
-    const uint32_t tid = threadIdx.x, nt = blockDim.x;
-    const uint32_t d = A.d, P = A.P, M = A.M, npos = A.npos;
-    constexpr uint32_t W = NW;
-    float* x = reinterpret_cast<float*>(smem);
-    float* cqs = x + P;
-    uint16_t* hs = reinterpret_cast<uint16_t*>(cqs + ((d + 3) & ~3u));
-    uint64_t* keys = reinterpret_cast<uint64_t*>(hs + ((M + 7) & ~7u));
-    float* mins = reinterpret_cast<float*>(keys + K.sort_cap);
-    uint32_t* hist = reinterpret_cast<uint32_t*>(mins + npos);
-    const uint32_t nbins = W * 64 + 1;
-    uint32_t* scratch = hist + ((nbins + 3) & ~3u);
-    __shared__ float s_cqbase;
-    __shared__ uint32_t s_cut, s_nsl;
-
-    const float* q = queries + static_cast<uint64_t>(qi) * d;
-    // ---- rotation: copy, zero-pad, 2 x (sign flip, FWHT, x 1/sqrt(P)) (src/quantize.rs:152-163)
-    for (uint32_t i = tid; i < P; i += nt) x[i] = i < d ? q[i] : 0.0f;
-    for (int r = 0; r < 2; ++r) {
-        __syncthreads();
-        for (uint32_t i = tid; i < P; i += nt) x[i] *= A.rot_signs[r * P + i];
-        for (uint32_t h = 1; h < P; h <<= 1) {
-            __syncthreads();
-            for (uint32_t t = tid; t < P / 2; t += nt) {
-                uint32_t j = (t / h) * 2 * h + (t % h);
-                float u = x[j], v = x[j + h];
-                x[j] = u + v;
-                x[j + h] = u - v;
-            }
-        }
-        __syncthreads();
-        for (uint32_t i = tid; i < P; i += nt) x[i] *= A.fht_scale;
-    }
-    __syncthreads();
-    // ---- 1-bit code: bit i = x[i] < 0 over the first W*64 coordinates (src/quantize.rs:57-67)
-    uint64_t* qb_out = Wk.qbits + static_cast<uint64_t>(qi) * W;
-    for (uint32_t base = 0; base < W * 64; base += nt) {
-        uint32_t i = base + tid;
-        bool neg = i < W * 64 && i < P && x[i] < 0.0f;
-        uint64_t m = __ballot(neg);
-        if (lane_id() == 0 && i < W * 64) qb_out[i >> 6] = m;
-    }
-    // ---- FastScan table (src/quantize.rs:279-313): position j uses x[4j .. 4j+3]
-    float lo = INFINITY, hi = -INFINITY;
-    float raw[16];
-    const bool own = tid < npos;
-    if (own) {
-        float xs[4];
-        for (int t = 0; t < 4; ++t) {
-            uint32_t dd = 4 * tid + t;
-            xs[t] = dd < P ? x[dd] : 0.0f;
-        }
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            float v = 0.0f;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) v += ((e >> t) & 1) ? -xs[t] : xs[t];
-            raw[e] = v;
-            lo = fminf(lo, v);
-            hi = fmaxf(hi, v);
-        }
-        mins[tid] = lo;
-    }
-    float range = block_max_f32(own ? hi - lo : 0.0f, reinterpret_cast<float*>(scratch));
-    range = fmaxf(range, 0.0f);
-    const float delta = fmaxf(range / 255.0f, 1e-12f);
-    if (own) {
-        uint8_t* lut = Wk.lut + static_cast<uint64_t>(qi) * npos * 16 + tid * 16;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            float qv = roundf((raw[e] - lo) / delta);
-            qv = fminf(fmaxf(qv, 0.0f), 255.0f);
-            lut[e] = static_cast<uint8_t>(qv);
-        }
-    }
-    __syncthreads();
-    if (tid == 0) {
-        float b = -0.0f;  // Rust's f32 Sum folds from -0.0
-        for (uint32_t j = 0; j < npos; ++j) b += mins[j];
-        Wk.bias[qi] = b;
-        Wk.delta[qi] = delta;
-    }
-    if (route_only == 2) return;  // query_prep test entry point
-    // ---- SQ8 rescore prep: cqs = q * csq_step, cqbase = sum q * csq_min (src/index.rs:1934-1942)
-    const bool sq8 = A.cent_sq8 != nullptr;
-    if (sq8) {
-        for (uint32_t j = tid; j < d; j += nt) cqs[j] = q[j] * A.csq_step[j];
-        if (tid == 0) {
-            float b = 0.0f;
-            for (uint32_t j = 0; j < d; ++j) b += q[j] * A.csq_min[j];
-            s_cqbase = b;
-        }
-    }
-    // ---- Hamming against every centroid code + live histogram (src/index.rs:1901-1923)
-    for (uint32_t i = tid; i < nbins; i += nt) hist[i] = 0;
-    __syncthreads();
-    uint64_t qw[W];
-#pragma unroll
-    for (int w = 0; w < (int)W; ++w) qw[w] = qb_out[w];
-    for (uint32_t c = tid; c < M; c += nt) {
-        const uint64_t* cb = A.cent_bits + static_cast<uint64_t>(c) * W;
-        uint32_t h = 0;
-#pragma unroll
-        for (int w = 0; w < (int)W; ++w) h += __popcll(qw[w] ^ cb[w]);
-        hs[c] = static_cast<uint16_t>(h);
-        if (A.live[c]) atomicAdd(&hist[h], 1u);
-    }
-    __syncthreads();
-    // cut = smallest t whose cumulative live count reaches want_c (hamming_cutoff, :86-104)
-    {
-        uint32_t per = (nbins + nt - 1) / nt, b0 = tid * per, loc = 0;
-        for (uint32_t i = b0; i < min(b0 + per, nbins); ++i) loc += hist[i];
-        uint32_t total;
-        uint32_t ex = block_excl_scan_u32(loc, scratch, &total);
-        uint32_t cand = kNone, cum = ex;
-        for (uint32_t i = b0; i < min(b0 + per, nbins); ++i) {
-            cum += hist[i];
-            if (cum >= K.want_c) {
-                cand = i;
-                break;
-            }
-        }
-        uint32_t cut = block_min_u32(cand, scratch);
-        if (tid == 0) s_cut = cut == kNone ? W * 64 : cut;
-    }
-    __syncthreads();
-    const uint32_t cut = s_cut;
-    // ---- shortlist: live cells with h <= cut, ascending id, via a block-wide compaction
-    {
-        uint32_t per = (M + nt - 1) / nt, c0 = tid * per, c1 = min(c0 + per, M), cnt = 0;
-        for (uint32_t c = c0; c < c1; ++c) cnt += (A.live[c] && hs[c] <= cut);
-        uint32_t total;
-        uint32_t pos = block_excl_scan_u32(cnt, scratch, &total);
-        if (tid == 0) {
-            s_nsl = total;
-            atomicMax(&Wk.ctl->max_shortlist, total);
-        }
-        if (total <= K.sort_cap) {
-            for (uint32_t c = c0; c < c1; ++c)
-                if (A.live[c] && hs[c] <= cut) keys[pos++] = c;  // id for now; score below
-        }
-    }
-    __syncthreads();
-    const uint32_t nsl = s_nsl;
-    uint32_t* chosen = Wk.chosen + static_cast<uint64_t>(qi) * K.nprobe;
-    float* cscore = Wk.cscore + static_cast<uint64_t>(qi) * K.nprobe;
-    if (nsl > K.sort_cap) {
-        if (tid == 0) {
-            atomicAdd(&Wk.ctl->err_shortlist, 1u);
-            Wk.nchosen[qi] = 0;
-        }
-        return;
-    }
-    // ---- exact rescore: 8 lanes per cell, the reference's 8-lane FMA order (:777-800)
-    const float cqbase = sq8 ? s_cqbase : 0.0f;
-    {
-        const uint32_t l = tid & 7, grp = tid >> 3, ngrp = nt >> 3;
-        const uint32_t rounds = (nsl + ngrp - 1) / ngrp;
-        for (uint32_t rr = 0; rr < rounds; ++rr) {
-            uint32_t i = rr * ngrp + grp;
-            uint32_t c = i < nsl ? static_cast<uint32_t>(keys[i]) : 0u;
-            float s;
-            if (sq8) {
-                const uint8_t* code = A.cent_sq8 + static_cast<uint64_t>(c) * d;
-                s = dot8_group(d, l, [&](uint32_t j) { return cqs[j]; },
-                               [&](uint32_t j) { return static_cast<float>(code[j]); }) + cqbase;
-            } else {
-                const float* cen = A.centroids + static_cast<uint64_t>(c) * d;
-                s = dot8_group(d, l, [&](uint32_t j) { return q[j]; }, [&](uint32_t j) { return cen[j]; });
-            }
-            __syncthreads();  // all reads of keys[] in this round happen before the writes
-            if (i < nsl && l == 0) keys[i] = desc_score_key(s, c);
-        }
-    }
-    // pad to a power of two with max keys, sort ascending = (score desc, id asc)
-    uint32_t n2 = 1;
-    while (n2 < nsl) n2 <<= 1;
-    __syncthreads();
-    for (uint32_t i = nsl + tid; i < n2; i += nt) keys[i] = kKeyMax;
-    bitonic_sort_u64(keys, n2);
-    const uint32_t cap = min(K.nprobe, nsl);
-    for (uint32_t i = tid; i < K.nprobe; i += nt) {
-        bool ok = i < cap;
-        chosen[i] = ok ? static_cast<uint32_t>(keys[i]) : kNone;
-        cscore[i] = ok ? key_score(keys[i]) : __uint_as_float(0x7fc00000u);
-    }
-    // ---- nucleus over the capped list (:1960-1973); tc >= 1 keeps all cap cells
-    if (tid == 0) {
-        uint32_t nch = cap;
-        if (K.use_nucleus && cap > 0) {
-            float max_s = key_score(keys[0]);
-            float z = -0.0f;
-            for (uint32_t i = 0; i < cap; ++i) z += exp_f((key_score(keys[i]) - max_s) * K.beta);
-            float cum = 0.0f;
-            bool near = false;
-            nch = cap;
-            for (uint32_t i = 0; i < cap; ++i) {
-                cum += exp_f((key_score(keys[i]) - max_s) * K.beta) / (z + 1e-9f);
-                if (fabsf(cum - K.tc) <= K.nucleus_band) near = true;
-                if (cum >= K.tc) {
-                    nch = i + 1;
-                    break;
-                }
-            }
-            if (near) {
-                uint32_t slot = atomicAdd(&Wk.ctl->nflag_route, 1u);
-                Wk.flag_route[slot] = qi;
-            }
-        }
-        Wk.nchosen[qi] = nch;
-    }
-}
-
-// ---------------------------------------------------------------- seed scan + tau + adaptive cut
-
-template <int NW>
-__global__ void __launch_bounds__(kScanThreads)
-seed_kernel(DevArena A, Work Wk, KParams K) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    const uint32_t qi = blockIdx.x;
-    if (qi >= K.nq) return;
-    const uint32_t tid = threadIdx.x, nt = blockDim.x;
-    constexpr uint32_t TB = NW * 256;
-    uint8_t* table = smem;
-    uint32_t* probed = reinterpret_cast<uint32_t*>(smem + TB);
-    uint32_t* hist = probed + ((A.MW + 3) & ~3u);
-    uint32_t* scratch = hist + kHistBins;
-    float* fsc = reinterpret_cast<float*>(scratch + 16);
-    __shared__ uint32_t s_cnt;
-
-    const uint32_t nch = Wk.nchosen[qi];
-    const uint32_t* chosen = Wk.chosen + static_cast<uint64_t>(qi) * K.nprobe;
-    const float* cscore = Wk.cscore + static_cast<uint64_t>(qi) * K.nprobe;
-    const uint8_t* lut = Wk.lut + static_cast<uint64_t>(qi) * TB;
-    for (uint32_t i = tid; i < TB / 4; i += nt) reinterpret_cast<uint32_t*>(table)[i] = reinterpret_cast<const uint32_t*>(lut)[i];
-    for (uint32_t i = tid; i < A.MW; i += nt) probed[i] = 0;
-    if (tid == 0) s_cnt = 0;
-    __syncthreads();
-    for (uint32_t i = tid; i < nch; i += nt) atomicOr(&probed[chosen[i] >> 5], 1u << (chosen[i] & 31));
-    __syncthreads();
-    uint32_t* gprobed = Wk.probed + static_cast<uint64_t>(qi) * A.MW;
-    for (uint32_t i = tid; i < A.MW; i += nt) gprobed[i] = probed[i];
-
-    // ---- seed: every canonical member of the first ns probed cells (src/index.rs:2150-2154)
-    const uint32_t ns = min(kSeedCells, nch);
-    uint2* seed = Wk.seed + static_cast<uint64_t>(qi) * K.seed_cap;
-    if (tid < ns) {
-        const uint32_t c = chosen[tid];
-        atomicAdd(&Wk.ctl->seed_blocks, static_cast<unsigned long long>((A.mem_off[c + 1] - A.mem_off[c] + 31) / 32));
-    }
-    for (uint32_t si = 0; si < ns; ++si) {
-        const uint32_t c = chosen[si];
-        const uint32_t e0 = A.mem_off[c], len = A.mem_off[c + 1] - e0;
-        for (uint32_t base = 0; base < len; base += nt) {
-            uint32_t i = base + tid;
-            bool pass = false;
-            uint32_t dv = 0, slot = 0;
-            if (i < len) {
-                uint32_t s[1];
-                lut_sums<NW, 1>(A.codes + (static_cast<uint64_t>(e0) + i) * (2 * NW), table, s);
-                dv = A.maxk - s[0];
-                slot = A.members[e0 + i];
-                pass = canonical(A, slot, c, probed);
-            }
-            uint64_t m = __ballot(pass);
-            uint32_t wbase = 0;
-            if (lane_id() == 0 && m) wbase = atomicAdd(&s_cnt, static_cast<uint32_t>(__popcll(m)));
-            wbase = __shfl(wbase, 0, kWave);
-            if (pass) seed[wbase + lanes_below(m)] = make_uint2(dv, slot);
-        }
-    }
-    __syncthreads();
-    const uint32_t cnt = s_cnt;
-    __threadfence_block();
-    // ---- tau = target-th smallest seed d (src/index.rs:2155-2160)
-    uint32_t tau = A.maxk;
-    if (cnt >= K.target) tau = select_kth(cnt, K.target, [&](uint32_t i) { return seed[i].x; }, hist, scratch);
-    // ---- adaptive cut (src/index.rs:2166-2188): b_i = cos(max(acos(clamp(cs_i)) - r_c, 0)),
-    // suffix max from the end, rest_end = first i >= ns with suffix_i < thr - margin
-    uint32_t rest_end = nch;
-    if (K.adaptive && cnt >= K.target && ns < nch) {
-        const float delta = Wk.delta[qi], bias = Wk.bias[qi];
-        const float est = delta * static_cast<float>(A.maxk - tau) + bias;
-        const float thr = fminf(fmaxf(est / K.norm, -1.0f), 1.0f);
-        const float T = thr - K.at_margin;
-        // suffix max over [i, nch): chunked, each thread owns a contiguous run
-        const uint32_t m = nch - ns, per = (m + nt - 1) / nt;
-        const uint32_t i0 = ns + tid * per, i1 = min(i0 + per, nch);
-        float run_max = -INFINITY;
-        for (uint32_t i = i1; i-- > i0;) {
-            float cs = fminf(fmaxf(cscore[i], -1.0f), 1.0f);
-            float b = cos_f(fmaxf(acos_f(cs) - A.r_bound[chosen[i]], 0.0f));
-            run_max = fmaxf(run_max, b);
-        }
-        // exclusive suffix of the run maxima of later threads
-        fsc[tid] = run_max;
-        __syncthreads();
-        float later = -INFINITY;
-        for (uint32_t t = tid + 1; t < nt; ++t) later = fmaxf(later, fsc[t]);
-        // walk own run forward: suffix_i = max(b_i.., later)
-        uint32_t first = kNone;
-        bool near = false;
-        {
-            // recompute suffix values from the end of the run
-            float sfx = later;
-            // need forward order of the first crossing: collect in reverse, remember the smallest i
-            for (uint32_t i = i1; i-- > i0;) {
-                float cs = fminf(fmaxf(cscore[i], -1.0f), 1.0f);
-                float b = cos_f(fmaxf(acos_f(cs) - A.r_bound[chosen[i]], 0.0f));
-                sfx = fmaxf(sfx, b);
-                if (sfx < T) first = i;
-                if (fabsf(sfx - T) <= K.prune_band) near = true;
-            }
-        }
-        uint32_t fe = block_min_u32(first, scratch);
-        uint32_t any_near = block_sum_u32(near ? 1u : 0u, scratch);
-        if (fe != kNone) rest_end = fe;
-        if (tid == 0 && any_near) {
-            uint32_t slot = atomicAdd(&Wk.ctl->nflag_prune, 1u);
-            Wk.flag_prune[slot] = qi;
-        }
-    }
-    if (tid == 0) {
-        Wk.seed_cnt[qi] = cnt;
-        Wk.tau[qi] = tau;
-        Wk.rest_end[qi] = rest_end;
-    }
-}
-
-// ---------------------------------------------------------------- inversion: cell -> queries
-
-__global__ void invert_count_kernel(Work Wk, KParams K, const uint32_t* __restrict__ mem_off) {
-    uint32_t qi = blockIdx.x;
-    if (qi >= K.nq) return;
-    uint32_t ns = min(kSeedCells, Wk.nchosen[qi]), re = Wk.rest_end[qi];
-    const uint32_t* chosen = Wk.chosen + static_cast<uint64_t>(qi) * K.nprobe;
-    uint32_t blocks = 0;
-    for (uint32_t i = ns + threadIdx.x; i < re; i += blockDim.x) {
-        uint32_t c = chosen[i];
-        atomicAdd(&Wk.cell_cnt[c], 1u);
-        blocks += (mem_off[c + 1] - mem_off[c] + 31) / 32;
-    }
-    blocks = wave_sum_u32(blocks);
-    if (threadIdx.x == 0 && blocks) {
-        atomicAdd(&Wk.ctl->scan_blocks, static_cast<unsigned long long>(blocks));
-        atomicAdd(&Wk.ctl->scan_pairs, static_cast<unsigned long long>(re - ns));
-    }
-}
-
-// Single workgroup: exclusive scan of cell_cnt[0..M) -> cell_off[0..M], cell_cur = cell_off.
-__global__ void invert_scan_kernel(Work Wk, uint32_t M) {
-    __shared__ uint32_t scratch[32];
-    __shared__ uint32_t carry;
-    if (threadIdx.x == 0) carry = 0;
-    __syncthreads();
-    for (uint32_t base = 0; base < M; base += blockDim.x) {
-        uint32_t i = base + threadIdx.x;
-        uint32_t v = i < M ? Wk.cell_cnt[i] : 0u;
-        uint32_t total;
-        uint32_t ex = block_excl_scan_u32(v, scratch, &total);
-        uint32_t c0 = carry;
-        if (i < M) {
-            Wk.cell_off[i] = c0 + ex;
-            Wk.cell_cur[i] = c0 + ex;
-        }
-        __syncthreads();
-        if (threadIdx.x == 0) carry = c0 + total;
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) Wk.cell_off[M] = carry;
-}
-
-__global__ void invert_fill_kernel(Work Wk, KParams K) {
-    uint32_t qi = blockIdx.x;
-    if (qi >= K.nq) return;
-    uint32_t ns = min(kSeedCells, Wk.nchosen[qi]), re = Wk.rest_end[qi];
-    const uint32_t* chosen = Wk.chosen + static_cast<uint64_t>(qi) * K.nprobe;
-    for (uint32_t i = ns + threadIdx.x; i < re; i += blockDim.x) {
-        uint32_t c = chosen[i];
-        uint32_t pos = atomicAdd(&Wk.cell_cur[c], 1u);
-        Wk.qof[pos] = qi;
-    }
-}
-
-// ---------------------------------------------------------------- the cell-major scan
-
-// One workgroup per cell (src/index.rs:2231-2275 is the CPU loop this replaces). Lanes own
-// members; their codes stay in registers while groups of kG probing queries stream through.
-template <int NW>
-__global__ void __launch_bounds__(kScanThreads)
-cell_scan_kernel(DevArena A, Work Wk, KParams K) {
-    constexpr uint32_t TB = NW * 256;
-    __shared__ __align__(16) uint8_t table[kG * TB];
-    __shared__ uint32_t s_q[kG], s_t[kG];
-    const uint32_t c = blockIdx.x;
-    if (c >= A.M) return;
-    const uint32_t q0 = Wk.cell_off[c], nqc = Wk.cell_off[c + 1] - q0;
-    const uint32_t e0 = A.mem_off[c], len = A.mem_off[c + 1] - e0;
-    if (nqc == 0 || len == 0) return;
-    const uint32_t tid = threadIdx.x, nt = blockDim.x;
-    for (uint32_t ebase = 0; ebase < len; ebase += nt) {
-        const uint32_t i = ebase + tid;
-        const bool have = i < len;
-        // lanes past the end read the cell's first member (in bounds) and emit nothing
-        const uint32_t* code = A.codes + (static_cast<uint64_t>(e0) + (have ? i : 0u)) * (2 * NW);
-        const uint32_t slot = have ? A.members[e0 + i] : 0u;
-        for (uint32_t g0 = 0; g0 < nqc; g0 += kG) {
-            const uint32_t ng = min(kG, nqc - g0);
-            __syncthreads();
-            if (tid < kG) {
-                uint32_t qq = tid < ng ? Wk.qof[q0 + g0 + tid] : kNone;
-                s_q[tid] = qq;
-                s_t[tid] = qq != kNone ? Wk.tau[qq] : 0u;
-            }
-            // interleave the group's tables: table[x*4 + g] = lut_g[x]
-            for (uint32_t x4 = tid; x4 < TB / 4; x4 += nt) {
-                uint32_t v[kG];
-#pragma unroll
-                for (uint32_t g = 0; g < kG; ++g) {
-                    uint32_t qq = g < ng ? Wk.qof[q0 + g0 + g] : kNone;
-                    v[g] = qq != kNone ? reinterpret_cast<const uint32_t*>(Wk.lut + static_cast<uint64_t>(qq) * TB)[x4] : 0u;
-                }
-                // 4x4 byte transpose: out[b] = (v0.b, v1.b, v2.b, v3.b)
-                uint32_t lo01 = __builtin_amdgcn_perm(v[1], v[0], 0x05010400u);  // v0.b0 v1.b0 v0.b1 v1.b1
-                uint32_t hi01 = __builtin_amdgcn_perm(v[1], v[0], 0x07030602u);  // v0.b2 v1.b2 v0.b3 v1.b3
-                uint32_t lo23 = __builtin_amdgcn_perm(v[3], v[2], 0x05010400u);
-                uint32_t hi23 = __builtin_amdgcn_perm(v[3], v[2], 0x07030602u);
-                uint4 o;
-                o.x = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
-                o.y = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);
-                o.z = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
-                o.w = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
-                reinterpret_cast<uint4*>(table)[x4] = o;
-            }
-            __syncthreads();
-            uint32_t sums[kG];
-            lut_sums<NW, kG>(code, table, sums);
-#pragma unroll
-            for (uint32_t g = 0; g < kG; ++g) {
-                const uint32_t qq = s_q[g];
-                bool pass = false;
-                uint32_t dv = 0;
-                if (have && qq != kNone) {
-                    dv = A.maxk - sums[g];
-                    if (dv <= s_t[g]) pass = canonical(A, slot, c, Wk.probed + static_cast<uint64_t>(qq) * A.MW);
-                }
-                uint64_t m = __ballot(pass);
-                if (m) {
-                    uint32_t wbase = 0;
-                    if (lane_id() == 0) wbase = atomicAdd(&Wk.cand_cnt[qq], static_cast<uint32_t>(__popcll(m)));
-                    wbase = __shfl(wbase, 0, kWave);
-                    uint32_t pos = wbase + lanes_below(m);
-                    if (pass && pos < K.cand_cap) Wk.cand[static_cast<uint64_t>(qq) * K.cand_cap + pos] = make_uint2(dv, slot);
-                }
-            }
-        }
-    }
-}
-
-// ---------------------------------------------------------------- finish: cut + rerank + top-k
-
-__global__ void __launch_bounds__(kScanThreads)
-finish_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries, uint32_t* __restrict__ out_slots,
-              float* __restrict__ out_scores) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    const uint32_t qi = blockIdx.x;
-    if (qi >= K.nq) return;
-    const uint32_t tid = threadIdx.x, nt = blockDim.x, d = A.d;
-    uint32_t* hist = reinterpret_cast<uint32_t*>(smem);
-    uint32_t* scratch = hist + kHistBins;
-    float* qs = reinterpret_cast<float*>(scratch + 32);
-    uint64_t* keys = reinterpret_cast<uint64_t*>(qs + ((d + 3) & ~3u));
-    __shared__ uint32_t s_n;
-    __shared__ float s_base;
-
-    const uint32_t ns_cnt = Wk.seed_cnt[qi];
-    const uint32_t nc = min(Wk.cand_cnt[qi], K.cand_cap);
-    const uint2* seed = Wk.seed + static_cast<uint64_t>(qi) * K.seed_cap;
-    const uint2* cand = Wk.cand + static_cast<uint64_t>(qi) * K.cand_cap;
-    const uint32_t total = ns_cnt + nc;
-    auto get_d = [&](uint32_t i) { return i < ns_cnt ? seed[i].x : cand[i - ns_cnt].x; };
-    // ---- exact cut at target, every tie kept (src/index.rs:2281-2293)
-    // G = target-th smallest d; with fewer than target candidates every one is kept
-    uint32_t cutv = A.maxk;
-    if (total >= K.target) cutv = select_kth(total, K.target, get_d, hist, scratch);
-    // ---- compact the survivors into fin[]
-    uint2* fin = Wk.fin + static_cast<uint64_t>(qi) * K.fin_cap;
-    if (tid == 0) s_n = 0;
-    __syncthreads();
-    for (uint32_t base = 0; base < total; base += nt) {
-        uint32_t i = base + tid;
-        uint2 e = make_uint2(0, 0);
-        bool pass = false;
-        if (i < total) {
-            e = i < ns_cnt ? seed[i] : cand[i - ns_cnt];
-            pass = e.x <= cutv;
-        }
-        uint64_t m = __ballot(pass);
-        uint32_t wbase = 0;
-        if (lane_id() == 0 && m) wbase = atomicAdd(&s_n, static_cast<uint32_t>(__popcll(m)));
-        wbase = __shfl(wbase, 0, kWave);
-        if (pass) fin[wbase + lanes_below(m)] = e;
-    }
-    __syncthreads();
-    const uint32_t n = s_n;
-    __threadfence_block();
-    // ---- exact rerank (src/index.rs:1309-1378): f32 dot_f32, or SQ8 base + dot_f32_u8
-    const float* q = queries + static_cast<uint64_t>(qi) * d;
-    const bool sq8 = A.rerank_mode == MAIVS_RERANK_SQ8;
-    if (sq8) {
-        for (uint32_t j = tid; j < d; j += nt) qs[j] = q[j] * A.sq_step[j];
-        if (tid == 0) {
-            float b = 0.0f;
-            for (uint32_t j = 0; j < d; ++j) b += q[j] * A.sq_min[j];
-            s_base = b;
-        }
-    } else {
-        for (uint32_t j = tid; j < d; j += nt) qs[j] = q[j];
-    }
-    __syncthreads();
-    uint32_t n2 = 1;
-    while (n2 < n) n2 <<= 1;
-    const bool in_lds = n2 <= K.fin_sort_cap;
-    uint64_t* kk = in_lds ? keys : (Wk.keys + static_cast<uint64_t>(qi) * K.key_cap);
-    {
-        const uint32_t l = tid & 7, grp = tid >> 3, ngrp = nt >> 3;
-        const uint32_t rounds = (n + ngrp - 1) / ngrp;
-        const float base = sq8 ? s_base : 0.0f;
-        for (uint32_t rr = 0; rr < rounds; ++rr) {
-            uint32_t i = rr * ngrp + grp;
-            uint32_t slot = i < n ? fin[i].y : 0u;
-            float s;
-            if (sq8) {
-                const uint8_t* code = A.sq8 + static_cast<uint64_t>(slot) * d;
-                s = base + dot8_group(d, l, [&](uint32_t j) { return qs[j]; },
-                                      [&](uint32_t j) { return static_cast<float>(code[j]); });
-            } else {
-                const float* row = A.vecs + static_cast<uint64_t>(slot) * d;
-                s = dot8_group(d, l, [&](uint32_t j) { return qs[j]; }, [&](uint32_t j) { return row[j]; });
-            }
-            if (i < n && l == 0) kk[i] = desc_score_key(s, slot);
-        }
-    }
-    __syncthreads();
-    for (uint32_t i = n + tid; i < n2; i += nt) kk[i] = kKeyMax;
-    bitonic_sort_u64(kk, n2);
-    for (uint32_t i = tid; i < K.k; i += nt) {
-        bool ok = i < n;
-        out_slots[static_cast<uint64_t>(qi) * K.k + i] = ok ? static_cast<uint32_t>(kk[i]) : kNone;
-        out_scores[static_cast<uint64_t>(qi) * K.k + i] = ok ? key_score(kk[i]) : -INFINITY;
-    }
-    if (tid == 0) {
-        Wk.cut[qi] = cutv;
-        Wk.ncand[qi] = n;
-        atomicMax(&Wk.ctl->max_cand, Wk.cand_cnt[qi]);
-        atomicAdd(&Wk.ctl->survivors, static_cast<unsigned long long>(Wk.cand_cnt[qi]));
-        atomicAdd(&Wk.ctl->rerank_rows, static_cast<unsigned long long>(n));
-    }
-}
-
+constexpr size_t kLdsBudget = 160 * 1024;
 }  // namespace
 
 // ================================================================ host side
@@ -935,10 +122,30 @@ bool supported_nw(uint32_t w) { return w == 1 || w == 2 || w == 4 || w == 8 || w
         default: { constexpr int NW = 16; __VA_ARGS__; break; } \
     }
 
+// LDS of prep_route: x[P] | cqs[d4] | cqp[d4] | hs[M8] u16 | keys[sort_cap] u64 | mins[npos4] |
+// hist[nbins4] | scratch[16]
 size_t route_lds(const DevArena& A, uint32_t sort_cap) {
-    size_t b = A.P * 4 + ((A.d + 3) & ~3u) * 4 + ((A.M + 7) & ~7u) * 2 + static_cast<size_t>(sort_cap) * 8 +
-               A.npos * 4 + (((A.W * 64 + 1) + 3) & ~3u) * 4 + 16 * 4;
-    return b;
+    const size_t d4 = (A.d + 3) & ~3u;
+    return A.P * 4 + d4 * 8 + ((A.M + 7) & ~7u) * 2 + static_cast<size_t>(sort_cap) * 8 + ((A.npos + 3) & ~3u) * 4 +
+           (((A.W * 64 + 1) + 3) & ~3u) * 4 + 16 * 4;
+}
+
+// LDS of seed: table | probed[MW4] | sbuf[seed_cap4] | hist[256] | scratch[32] | suffix maxima[nt]
+size_t seed_lds(const DevArena& A, uint32_t seed_cap) {
+    return A.W * 256 + ((A.MW + 3) & ~3u) * 4 + ((seed_cap + 3) & ~3u) * 4 + kHistBins * 4 + 32 * 4 + kSeedThreads * 4;
+}
+
+size_t finish_lds(const DevArena& A) {
+    return kHistBins * 4 + 32 * 4 + ((A.d + 3) & ~3u) * 4 + static_cast<size_t>(kFinishLdsCap) * 8;
+}
+
+Chain make_chain(uint32_t d, uint32_t vec) {
+    Chain c{};
+    c.T = d / 8;
+    c.Tp = (c.T + vec - 1) / vec * vec;
+    c.tail = d - 8 * c.T;
+    c.stride = 8 * c.Tp + (c.tail + vec - 1) / vec * vec;
+    return c;
 }
 
 // Per-query and per-cell work buffers for (nq, nprobe, k); grows only. Candidate buffers are
@@ -971,6 +178,7 @@ int ensure_work(maivs_gpu_ctx* ctx, uint32_t nq, uint32_t nprobe, uint32_t k) {
     rc |= dalloc(ctx, o, &W.seed_cnt, nql);
     rc |= dalloc(ctx, o, &W.tau, nql);
     rc |= dalloc(ctx, o, &W.rest_end, nql);
+    rc |= dalloc(ctx, o, &W.qstat, nql * 3);
     rc |= dalloc(ctx, o, &W.cand_cnt, nql);
     rc |= dalloc(ctx, o, &W.cut, nql);
     rc |= dalloc(ctx, o, &W.ncand, nql);
@@ -1048,7 +256,6 @@ KParams make_params(maivs_gpu_ctx* ctx, uint32_t nq, const maivs_search_params* 
     K.cand_cap = ctx->cap_cand;
     K.fin_cap = ctx->cap_fin;
     K.key_cap = ctx->cap_key;
-    K.fin_sort_cap = kFinishSortCap;
     K.tc = p->target_confidence;
     K.beta = p->beta;
     K.at_margin = p->at_margin;
@@ -1092,9 +299,17 @@ uint32_t host_rest_end(const float* cscore, const uint32_t* chosen, uint32_t nch
 
 // ---- pipeline stages ----
 
+int launch_reset(maivs_gpu_ctx* ctx, uint32_t nq) {
+    const uint32_t n = std::max(ctx->A.M + 1, nq);
+    const uint32_t blocks = std::min<uint32_t>((n + 255) / 256, 1024);
+    hipLaunchKernelGGL(reset_kernel, dim3(std::max(blocks, 1u)), dim3(256), 0, ctx->stream, ctx->Wk, ctx->A.M, nq);
+    HIP_TRY(ctx, hipGetLastError());
+    return 0;
+}
+
 int launch_route(maivs_gpu_ctx* ctx, const KParams& K, const float* d_q, uint32_t mode) {
     const DevArena& A = ctx->A;
-    const size_t lds = ctx->lds_route_fixed + static_cast<size_t>(K.sort_cap) * 8;
+    const size_t lds = route_lds(A, K.sort_cap);
     DISPATCH_NW(A.W, hipLaunchKernelGGL(prep_route_kernel<NW>, dim3(K.nq), dim3(kRouteThreads), lds, ctx->stream, A,
                                         ctx->Wk, K, d_q, mode));
     HIP_TRY(ctx, hipGetLastError());
@@ -1103,18 +318,22 @@ int launch_route(maivs_gpu_ctx* ctx, const KParams& K, const float* d_q, uint32_
 
 int launch_seed(maivs_gpu_ctx* ctx, const KParams& K) {
     const DevArena& A = ctx->A;
-    DISPATCH_NW(A.W, hipLaunchKernelGGL(seed_kernel<NW>, dim3(K.nq), dim3(kScanThreads), ctx->lds_seed,
+    DISPATCH_NW(A.W, hipLaunchKernelGGL(seed_kernel<NW>, dim3(K.nq), dim3(kSeedThreads), ctx->lds_seed,
                                         ctx->stream, A, ctx->Wk, K));
     HIP_TRY(ctx, hipGetLastError());
     return 0;
 }
 
-int launch_scan(maivs_gpu_ctx* ctx, const KParams& K) {
+// Inversion and the cell-major scan. The probe counts come from the seed kernel, or from
+// invert_count when a host fix changed a cut afterwards (recount = true, counts reset first).
+int launch_scan(maivs_gpu_ctx* ctx, const KParams& K, bool recount) {
     const DevArena& A = ctx->A;
     Work& W = ctx->Wk;
-    HIP_TRY(ctx, hipMemsetAsync(W.cell_cnt, 0, (A.M + 1) * sizeof(uint32_t), ctx->stream));
-    HIP_TRY(ctx, hipMemsetAsync(W.cand_cnt, 0, K.nq * sizeof(uint32_t), ctx->stream));
-    hipLaunchKernelGGL(invert_count_kernel, dim3(K.nq), dim3(64), 0, ctx->stream, W, K, A.mem_off);
+    if (recount) {
+        int rc = launch_reset(ctx, K.nq);
+        if (rc) return rc;
+        hipLaunchKernelGGL(invert_count_kernel, dim3(K.nq), dim3(64), 0, ctx->stream, W, K);
+    }
     hipLaunchKernelGGL(invert_scan_kernel, dim3(1), dim3(1024), 0, ctx->stream, W, A.M);
     hipLaunchKernelGGL(invert_fill_kernel, dim3(K.nq), dim3(64), 0, ctx->stream, W, K);
     HIP_TRY(ctx, hipGetLastError());
@@ -1126,7 +345,7 @@ int launch_scan(maivs_gpu_ctx* ctx, const KParams& K) {
 }
 
 int launch_finish(maivs_gpu_ctx* ctx, const KParams& K, const float* d_q, uint32_t* d_slots, float* d_scores) {
-    hipLaunchKernelGGL(finish_kernel, dim3(K.nq), dim3(kScanThreads), ctx->lds_finish, ctx->stream, ctx->A, ctx->Wk,
+    hipLaunchKernelGGL(finish_kernel, dim3(K.nq), dim3(kFinishThreads), ctx->lds_finish, ctx->stream, ctx->A, ctx->Wk,
                        K, d_q, d_slots, d_scores);
     HIP_TRY(ctx, hipGetLastError());
     return 0;
@@ -1179,13 +398,13 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
     }
     Ctl ctl{};
     for (;;) {
-        HIP_TRY(ctx, hipMemsetAsync(W.ctl, 0, sizeof(Ctl), ctx->stream));
         HIP_TRY(ctx, hipEventRecord(ctx->ev[0], ctx->stream));
+        if ((rc = launch_reset(ctx, nq))) return rc;
         if ((rc = launch_route(ctx, K, d_q, 0))) return rc;
         HIP_TRY(ctx, hipEventRecord(ctx->ev[1], ctx->stream));
         if ((rc = launch_seed(ctx, K))) return rc;
         HIP_TRY(ctx, hipEventRecord(ctx->ev[2], ctx->stream));
-        if ((rc = launch_scan(ctx, K))) return rc;
+        if ((rc = launch_scan(ctx, K, false))) return rc;
         HIP_TRY(ctx, hipEventRecord(ctx->ev[5], ctx->stream));
         if ((rc = launch_finish(ctx, K, d_q, d_slots, d_scores))) return rc;
         HIP_TRY(ctx, hipEventRecord(ctx->ev[6], ctx->stream));
@@ -1201,6 +420,7 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
         return fail(ctx, MAIVS_ERR_UNSUPPORTED,
                     "a routing shortlist of %u cells exceeds the on-chip sort capacity %u (lower nprobe)",
                     ctl.max_shortlist, ctx->max_sort_cap_route);
+    if (ctl.err_seed) return fail(ctx, MAIVS_ERR_UNSUPPORTED, "a seed set exceeds its on-chip capacity");
     float ms;
     if (hipEventElapsedTime(&ms, ctx->ev[0], ctx->ev[6]) == hipSuccess) S.ms_total = ms;
     if (hipEventElapsedTime(&ms, ctx->ev[0], ctx->ev[1]) == hipSuccess) S.ms_prep = S.ms_route = ms;
@@ -1208,8 +428,6 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
     if (hipEventElapsedTime(&ms, ctx->ev[2], ctx->ev[4]) == hipSuccess) S.ms_invert = ms;
     if (hipEventElapsedTime(&ms, ctx->ev[4], ctx->ev[5]) == hipSuccess) S.ms_scan = ms;
     if (hipEventElapsedTime(&ms, ctx->ev[5], ctx->ev[6]) == hipSuccess) S.ms_rerank = ms;
-    S.seed_blocks = ctl.seed_blocks;
-    S.scan_blocks = ctl.scan_blocks;
 
     std::vector<float> cs;
     std::vector<uint32_t> ch;
@@ -1234,13 +452,12 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
         }
         if (fixed) {
             S.reruns++;
-            HIP_TRY(ctx, hipMemsetAsync(W.ctl, 0, sizeof(Ctl), ctx->stream));
+            if ((rc = launch_reset(ctx, nq))) return rc;
             if ((rc = launch_seed(ctx, K))) return rc;
-            if ((rc = launch_scan(ctx, K))) return rc;
+            if ((rc = launch_scan(ctx, K, false))) return rc;
             if ((rc = launch_finish(ctx, K, d_q, d_slots, d_scores))) return rc;
             if ((rc = read_ctl(ctx, &ctl))) return rc;
-            S.seed_blocks = ctl.seed_blocks;
-            S.scan_blocks = ctl.scan_blocks;
+            if (ctl.err_seed) return fail(ctx, MAIVS_ERR_UNSUPPORTED, "a seed set exceeds its on-chip capacity");
         }
     }
     // (2) adaptive cuts near their threshold
@@ -1274,23 +491,18 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
         uint32_t need = ctl.max_cand + ctl.max_cand / 4 + 64;
         ctx->initial_cand_cap = std::max(ctx->initial_cand_cap, need);
         if ((rc = ensure_cand(ctx, need))) return rc;
+        const uint32_t sc = K.sort_cap;
         K = make_params(ctx, nq, p);
+        K.sort_cap = sc;
         rerun_scan = true;
     }
     if (rerun_scan) {
         S.reruns++;
-        HIP_TRY(ctx, hipMemsetAsync(W.ctl, 0, sizeof(Ctl), ctx->stream));
-        // the seed stage is not re-run: keep its counter
-        if ((rc = launch_scan(ctx, K))) return rc;
+        if ((rc = launch_scan(ctx, K, true))) return rc;
         if ((rc = launch_finish(ctx, K, d_q, d_slots, d_scores))) return rc;
         if ((rc = read_ctl(ctx, &ctl))) return rc;
         if (ctl.max_cand > ctx->cap_cand) return fail(ctx, MAIVS_ERR_HIP, "candidate count changed between passes");
-        S.scan_blocks = ctl.scan_blocks;
     }
-    // work counters of the pass that produced the results
-    S.scan_pairs = ctl.scan_pairs;
-    S.survivors = ctl.survivors;
-    S.rerank_rows = ctl.rerank_rows;
     ctx->last_nq = nq;
     return 0;
 }
@@ -1361,6 +573,7 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
     free_all(ctx->arena_allocs);
     ctx->cap_nq = ctx->cap_nprobe = ctx->cap_k = ctx->cap_cand = ctx->cap_seed = ctx->cand_nq = 0;
     ctx->uploaded = false;
+    ctx->last_nq = 0;
 
     DevArena& A = ctx->A;
     A = DevArena{};
@@ -1376,6 +589,8 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
     A.MW = (A.M + 31) / 32;
     A.E = a->mem_off[A.M];
     A.fht_scale = 1.0f / std::sqrt(static_cast<float>(A.P));
+    A.cf = make_chain(A.d, 4);
+    A.cu = make_chain(A.d, 16);
     std::vector<uint8_t> live(A.M);
     uint32_t max_len = 0, n_live = 0;
     for (uint32_t c = 0; c < A.M; ++c) {
@@ -1389,64 +604,102 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
     A.n_live = n_live;
     A.max_cell_len = max_len;
     if (A.M * 2 > 96 * 1024) return fail(ctx, MAIVS_ERR_UNSUPPORTED, "%u cells exceed the on-chip routing table", A.M);
+    const uint32_t seed_cap = kSeedCells * std::max<uint32_t>(max_len, 1);
+    if (seed_cap > 65536 || seed_lds(A, seed_cap) > kLdsBudget)
+        return fail(ctx, MAIVS_ERR_UNSUPPORTED, "a cell of %u members is too large for the on-chip seed set", max_len);
 
-    int rc = 0;
-    uint8_t* fs = nullptr;
-    uint32_t* fs_off = nullptr;
-    uint32_t *codes = nullptr, *members = nullptr, *mem_off = nullptr, *slot_cells = nullptr;
-    uint64_t* cent_bits = nullptr;
-    uint8_t *cent_sq8 = nullptr, *sq8 = nullptr, *dlive = nullptr;
-    float *cents = nullptr, *csq_min = nullptr, *csq_step = nullptr, *r_bound = nullptr, *signs = nullptr,
-          *vecs = nullptr, *sq_min = nullptr, *sq_step = nullptr;
-    const uint64_t nblocks = a->fs_off[A.M];
-    rc |= dupload(ctx, a->fs_codes, nblocks * A.W * 256, &fs);
-    rc |= dupload(ctx, a->fs_off, static_cast<uint64_t>(A.M) + 1, &fs_off);
-    rc |= dalloc(ctx, ctx->arena_allocs, &codes, A.E * 2 * A.W);
-    rc |= dupload(ctx, a->members, A.E, &members);
-    rc |= dupload(ctx, a->mem_off, static_cast<uint64_t>(A.M) + 1, &mem_off);
-    if (A.ma > 1) rc |= dupload(ctx, a->slot_cells, static_cast<uint64_t>(A.N) * A.ma, &slot_cells);
-    rc |= dupload(ctx, a->cent_bits, static_cast<uint64_t>(A.M) * A.W, &cent_bits);
-    if (a->cent_sq8) {
-        rc |= dupload(ctx, a->cent_sq8, static_cast<uint64_t>(A.M) * A.d, &cent_sq8);
-        rc |= dupload(ctx, a->csq_min, A.d, &csq_min);
-        rc |= dupload(ctx, a->csq_step, A.d, &csq_step);
-    } else {
-        rc |= dupload(ctx, a->centroids, static_cast<uint64_t>(A.M) * A.d, &cents);
-    }
-    rc |= dupload(ctx, a->r_bound, A.M, &r_bound);
-    rc |= dupload(ctx, a->rot_signs, 2ull * A.P, &signs);
-    if (A.rerank_mode == MAIVS_RERANK_F32) {
-        rc |= dupload(ctx, a->vecs_f32, static_cast<uint64_t>(A.N) * A.d, &vecs);
-    } else {
-        rc |= dupload(ctx, a->sq8_codes, static_cast<uint64_t>(A.N) * A.d, &sq8);
-        rc |= dupload(ctx, a->sq_min, A.d, &sq_min);
-        rc |= dupload(ctx, a->sq_step, A.d, &sq_step);
-    }
-    rc |= dupload(ctx, live.data(), A.M, &dlive);
+    std::vector<void*> tmp;  // row-major staging, freed once the chain-major copies exist
+    auto stage = [&](auto* src, size_t count, auto** out) -> int {
+        int r = dalloc(ctx, tmp, out, count);
+        if (r) return r;
+        HIP_TRY(ctx, hipMemcpyAsync(*out, src, count * sizeof(**out), hipMemcpyHostToDevice, ctx->stream));
+        return 0;
+    };
+    auto run = [&]() -> int {
+        int rc = 0;
+        uint8_t *fs = nullptr, *dlive = nullptr;
+        uint32_t *fs_off = nullptr, *codes = nullptr, *members = nullptr, *mem_off = nullptr, *slot_cells = nullptr,
+                 *alt = nullptr;
+        uint64_t* cent_bits = nullptr;
+        float *csq_min = nullptr, *csq_step = nullptr, *r_bound = nullptr, *signs = nullptr, *sq_min = nullptr,
+              *sq_step = nullptr;
+        const uint64_t nblocks = a->fs_off[A.M];
+        if ((rc = stage(a->fs_codes, nblocks * A.W * 256, &fs))) return rc;
+        if ((rc = stage(a->fs_off, static_cast<uint64_t>(A.M) + 1, &fs_off))) return rc;
+        if ((rc = dalloc(ctx, ctx->arena_allocs, &codes, A.E * 2 * A.W))) return rc;
+        if ((rc = dupload(ctx, a->members, A.E, &members))) return rc;
+        if ((rc = dupload(ctx, a->mem_off, static_cast<uint64_t>(A.M) + 1, &mem_off))) return rc;
+        if ((rc = dalloc(ctx, ctx->arena_allocs, &alt, A.E))) return rc;
+        if (A.ma > 1 && (rc = dupload(ctx, a->slot_cells, static_cast<uint64_t>(A.N) * A.ma, &slot_cells))) return rc;
+        if ((rc = dupload(ctx, a->cent_bits, static_cast<uint64_t>(A.M) * A.W, &cent_bits))) return rc;
+        if ((rc = dupload(ctx, a->r_bound, A.M, &r_bound))) return rc;
+        if ((rc = dupload(ctx, a->rot_signs, 2ull * A.P, &signs))) return rc;
+        if ((rc = dupload(ctx, live.data(), A.M, &dlive))) return rc;
+        hipLaunchKernelGGL(fs_to_codes_kernel, dim3(std::max<uint32_t>(A.M, 1)), dim3(256), 0, ctx->stream, fs, fs_off,
+                           mem_off, A.M, A.W, codes);
+        if (A.ma == 2)
+            hipLaunchKernelGGL(entry_alt_kernel, dim3(std::max<uint32_t>(A.M, 1)), dim3(256), 0, ctx->stream, mem_off,
+                               members, slot_cells, A.M, alt);
+        HIP_TRY(ctx, hipGetLastError());
+        // chain-major copies of the rows the 8-lane dots read
+        auto chain_f32 = [&](const float* src, uint64_t rows, const float** out) -> int {
+            float *raw = nullptr, *cm = nullptr;
+            int r;
+            if ((r = stage(src, rows * A.d, &raw))) return r;
+            if ((r = dalloc(ctx, ctx->arena_allocs, &cm, rows * A.cf.stride))) return r;
+            hipLaunchKernelGGL(to_chain_kernel<float>, dim3(static_cast<uint32_t>(std::min<uint64_t>(rows, 65535))),
+                               dim3(256), 0, ctx->stream, raw, rows, A.d, A.cf, cm);
+            *out = cm;
+            return 0;
+        };
+        auto chain_u8 = [&](const uint8_t* src, uint64_t rows, const uint8_t** out) -> int {
+            uint8_t *raw = nullptr, *cm = nullptr;
+            int r;
+            if ((r = stage(src, rows * A.d, &raw))) return r;
+            if ((r = dalloc(ctx, ctx->arena_allocs, &cm, rows * A.cu.stride))) return r;
+            hipLaunchKernelGGL(to_chain_kernel<uint8_t>, dim3(static_cast<uint32_t>(std::min<uint64_t>(rows, 65535))),
+                               dim3(256), 0, ctx->stream, raw, rows, A.d, A.cu, cm);
+            *out = cm;
+            return 0;
+        };
+        if (a->cent_sq8) {
+            if ((rc = chain_u8(a->cent_sq8, A.M, &A.cent_sq8))) return rc;
+            if ((rc = dupload(ctx, a->csq_min, A.d, &csq_min))) return rc;
+            if ((rc = dupload(ctx, a->csq_step, A.d, &csq_step))) return rc;
+        } else {
+            if ((rc = chain_f32(a->centroids, A.M, &A.cents))) return rc;
+        }
+        if (A.rerank_mode == MAIVS_RERANK_F32) {
+            if ((rc = chain_f32(a->vecs_f32, A.N, &A.vecs))) return rc;
+        } else {
+            if ((rc = chain_u8(a->sq8_codes, A.N, &A.sq8))) return rc;
+            if ((rc = dupload(ctx, a->sq_min, A.d, &sq_min))) return rc;
+            if ((rc = dupload(ctx, a->sq_step, A.d, &sq_step))) return rc;
+        }
+        HIP_TRY(ctx, hipGetLastError());
+        HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+        A.codes = codes;
+        A.members = members;
+        A.entry_alt = alt;
+        A.mem_off = mem_off;
+        A.slot_cells = slot_cells;
+        A.cent_bits = cent_bits;
+        A.csq_min = csq_min;
+        A.csq_step = csq_step;
+        A.r_bound = r_bound;
+        A.rot_signs = signs;
+        A.sq_min = sq_min;
+        A.sq_step = sq_step;
+        A.live = dlive;
+        return 0;
+    };
+    int rc = run();
+    (void)hipStreamSynchronize(ctx->stream);
+    free_all(tmp);
     if (rc) {
         free_all(ctx->arena_allocs);
         return rc;
     }
-    hipLaunchKernelGGL(fs_to_codes_kernel, dim3(std::max<uint32_t>(A.M, 1)), dim3(256), 0, ctx->stream, fs, fs_off,
-                       mem_off, A.M, A.W, codes);
-    HIP_TRY(ctx, hipGetLastError());
-    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
-    A.codes = codes;
-    A.members = members;
-    A.mem_off = mem_off;
-    A.slot_cells = slot_cells;
-    A.cent_bits = cent_bits;
-    A.cent_sq8 = cent_sq8;
-    A.centroids = cents;
-    A.csq_min = csq_min;
-    A.csq_step = csq_step;
-    A.r_bound = r_bound;
-    A.rot_signs = signs;
-    A.vecs = vecs;
-    A.sq8 = sq8;
-    A.sq_min = sq_min;
-    A.sq_step = sq_step;
-    A.live = dlive;
     ctx->h_r_bound.assign(a->r_bound, a->r_bound + A.M);
     // LDS plan: route keeps hs[M] and the shortlist sort on chip (the sort size is per call)
     ctx->lds_route_fixed = route_lds(A, 0);
@@ -1455,15 +708,13 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
     uint32_t sc = 1024;
     while (static_cast<size_t>(sc) * 2 <= room && sc < 16384) sc <<= 1;
     ctx->max_sort_cap_route = sc;
-    ctx->lds_seed = A.W * 256 + ((A.MW + 3) & ~3u) * 4 + kHistBins * 4 + 16 * 4 + kScanThreads * 4;
-    ctx->lds_finish = kHistBins * 4 + 32 * 4 + ((A.d + 3) & ~3u) * 4 + static_cast<size_t>(kFinishSortCap) * 8;
-    if (ctx->lds_finish > kLdsBudget || ctx->lds_seed > kLdsBudget)
-        return fail(ctx, MAIVS_ERR_UNSUPPORTED, "LDS plan exceeds 160 KB");
+    ctx->lds_seed = seed_lds(A, seed_cap);
+    ctx->lds_finish = finish_lds(A);
     hipFuncSetAttribute(reinterpret_cast<const void*>(finish_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                         static_cast<int>(ctx->lds_finish));
     DISPATCH_NW(A.W, {
         hipFuncSetAttribute(reinterpret_cast<const void*>(prep_route_kernel<NW>), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            static_cast<int>(ctx->lds_route_fixed + static_cast<size_t>(sc) * 8));
+                            static_cast<int>(route_lds(A, sc)));
         hipFuncSetAttribute(reinterpret_cast<const void*>(seed_kernel<NW>), hipFuncAttributeMaxDynamicSharedMemorySize,
                             static_cast<int>(ctx->lds_seed));
     });
@@ -1588,7 +839,7 @@ int maivs_gpu_route(maivs_gpu_ctx* ctx, const float* q, uint32_t nq, const maivs
         return 0;
     }
     HIP_TRY(ctx, hipMemcpyAsync(W.q, q, static_cast<size_t>(nq) * ctx->A.d * 4, hipMemcpyHostToDevice, ctx->stream));
-    HIP_TRY(ctx, hipMemsetAsync(W.ctl, 0, sizeof(Ctl), ctx->stream));
+    if ((rc = launch_reset(ctx, nq))) return rc;
     if ((rc = launch_route(ctx, K, W.q, 1))) return rc;
     Ctl ctl{};
     HIP_TRY(ctx, hipMemcpyAsync(&ctl, W.ctl, sizeof(Ctl), hipMemcpyDeviceToHost, ctx->stream));
@@ -1610,6 +861,25 @@ int maivs_gpu_route(maivs_gpu_ctx* ctx, const float* q, uint32_t nq, const maivs
             out_nchosen[qi] = host_nucleus(cs, cap, p->target_confidence, p->beta);
         }
     }
+    return 0;
+}
+
+int maivs_gpu_last_counters(maivs_gpu_ctx* ctx, maivs_gpu_stats* stats) {
+    if (!ctx || !stats) return MAIVS_ERR_ARG;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    stats->seed_blocks = stats->scan_blocks = stats->scan_pairs = stats->survivors = stats->rerank_rows = 0;
+    if (ctx->last_nq == 0) return 0;
+    hipLaunchKernelGGL(counters_kernel, dim3(1), dim3(1024), 0, ctx->stream, ctx->Wk, ctx->last_nq);
+    HIP_TRY(ctx, hipGetLastError());
+    Ctl ctl{};
+    int rc = read_ctl(ctx, &ctl);
+    if (rc) return rc;
+    stats->seed_blocks = ctl.seed_blocks;
+    stats->scan_blocks = ctl.scan_blocks;
+    stats->scan_pairs = ctl.scan_pairs;
+    stats->survivors = ctl.survivors;
+    stats->rerank_rows = ctl.rerank_rows;
     return 0;
 }
 

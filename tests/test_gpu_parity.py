@@ -88,6 +88,18 @@ def _compare_search(ctx, ix, queries, p, gt=None):
     assert np.array_equal(cs[:n], ocs) and np.array_equal(cd[:n], ocd)
     assert np.array_equal(slots, oslots)
     assert scores.tobytes() == oscores.tobytes()
+    # work counters agree with the oracle's routed lists
+    ctx.last_counters(st)
+    arr = ix._arena_arrays()
+    blocks = (np.diff(arr["mem_off"]) + 31) // 32
+    _, och, _, onch = oracle.route_batch(desc, queries, p, arr["n_words"])
+    seed_b = scan_b = pairs = 0
+    for i in range(nq):
+        ns = min(8, int(onch[i]))
+        seed_b += int(blocks[och[i, :ns]].sum())
+        scan_b += int(blocks[och[i, ns:ore[i]]].sum())
+        pairs += max(int(ore[i]) - ns, 0)
+    assert (st.seed_blocks, st.scan_blocks, st.scan_pairs, st.rerank_rows) == (seed_b, scan_b, pairs, n)
     if gt is not None:
         ext = ix._ext_ids()
         ids = np.where(slots == 0xFFFFFFFF, -1, ext[np.minimum(slots, len(ext) - 1)].astype(np.int64))
