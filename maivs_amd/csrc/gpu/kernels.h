@@ -17,8 +17,11 @@
 namespace maivs_dev {
 
 constexpr uint32_t kSeedCells = 8;       // SEED_CELLS, src/index.rs:2018
+constexpr uint32_t kPrepWaves = 4;       // queries per prep workgroup, one wave each
+constexpr uint32_t kHamThreads = 256;    // cells per Hamming tile
+constexpr uint32_t kHamQ = 16;           // queries per Hamming tile
 constexpr uint32_t kRouteThreads = 256;
-constexpr uint32_t kSeedThreads = 1024;
+constexpr uint32_t kSeedThreads = 256;
 constexpr uint32_t kScanThreads = 256;
 constexpr uint32_t kFinishThreads = 512;
 constexpr uint32_t kG = 4;               // queries interleaved per cell_scan table pass
@@ -34,7 +37,7 @@ struct Chain {
 };
 
 struct DevArena {
-    uint32_t d, P, W, M, N, ma, rerank_mode, npos, maxk, n_live, max_cell_len, MW;
+    uint32_t d, P, W, M, N, ma, rerank_mode, npos, maxk, n_live, max_cell_len, MW, Mp;
     uint64_t E;
     float fht_scale;
     Chain cf, cu;               // f32 and u8 chain layouts
@@ -74,6 +77,10 @@ struct Work {
     uint8_t* lut;          // nq x npos*16
     float* delta;          // nq
     float* bias;           // nq
+    float* cqs;            // nq x d: rescore operand q * csq_step (q itself for f32 centroids)
+    float* cqbase;         // nq: sum(q * csq_min), sequential
+    uint16_t* hs;          // nq x Mp: Hamming distance to every cell, 0xFFFF for dead cells
+    float* bnd;            // nq x nprobe: adaptive-cut bounds of the probe list (i >= SEED_CELLS)
     uint32_t* chosen;      // nq x nprobe
     float* cscore;         // nq x nprobe
     uint32_t* nchosen;     // nq
@@ -82,7 +89,6 @@ struct Work {
     uint32_t* seed_cnt;    // nq
     uint32_t* tau;         // nq
     uint32_t* rest_end;    // nq
-    uint32_t* qstat;       // nq x 3: seed blocks, scan blocks, scan pairs
     uint2* cand;           // nq x cand_cap
     uint32_t* cand_cnt;    // nq
     uint2* fin;            // nq x fin_cap (d, slot) final candidates
@@ -483,180 +489,281 @@ __global__ void reset_kernel(Work Wk, uint32_t M, uint32_t nq) {
     for (uint32_t j = i; j < nq; j += stride) Wk.cand_cnt[j] = 0;
 }
 
-// ---------------------------------------------------------------- prep + route (one WG per query)
+// ---------------------------------------------------------------- prep (one wave per query)
 
+// Rotation, sign code, FastScan table and the two sequential sums of one query per wave
+// (src/quantize.rs:57-67,152-163,279-313; src/index.rs:1934-1942). Lane l holds rotated
+// coordinates [l*EPL, (l+1)*EPL) in registers: FWHT levels below EPL run inside the lane, the
+// others across lanes (partner l ^ (h / EPL)), in the reference's ascending level order, so every
+// butterfly sees the reference's operands. With `reset` set the grid also clears the per-call
+// counters (control block, probe counts, candidate counts).
+// LDS per wave: x[P] | mins[npos4] | cqp[d4].
+template <int EPL>
+__global__ void __launch_bounds__(kPrepWaves * kWave)
+prep_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries, uint32_t reset) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    if (reset) {
+        const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x, stride = gridDim.x * blockDim.x;
+        if (i < sizeof(Ctl) / 4) reinterpret_cast<uint32_t*>(Wk.ctl)[i] = 0;
+        for (uint32_t j = i; j <= A.M; j += stride) Wk.cell_cnt[j] = 0;
+        for (uint32_t j = i; j < K.nq; j += stride) Wk.cand_cnt[j] = 0;
+    }
+    const uint32_t lane = lane_id(), wv = threadIdx.x / kWave;
+    const uint32_t qi = blockIdx.x * kPrepWaves + wv;
+    if (qi >= K.nq) return;
+    const uint32_t P = A.P, d = A.d, npos = A.npos;
+    const uint32_t d4 = (d + 3) & ~3u, np4 = (npos + 3) & ~3u;
+    float* xs = reinterpret_cast<float*>(smem) + wv * (P + np4 + d4);
+    float* mins = xs + P;
+    float* cqp = mins + np4;
+    const float* q = queries + static_cast<uint64_t>(qi) * d;
+    const bool sq8 = A.cent_sq8 != nullptr;
+    const uint32_t base = lane * EPL;
+    float x[EPL], sg[2][EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+        const uint32_t i = base + e;
+        x[e] = i < d ? q[i] : 0.0f;
+        sg[0][e] = A.rot_signs[i];
+        sg[1][e] = A.rot_signs[P + i];
+    }
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+        const uint32_t i = base + e;
+        if (i < d) {
+            // rescore operands: cqs = q * step and q * min, each rounded once (src/index.rs:1937-1941)
+            const float v = x[e];
+            Wk.cqs[static_cast<uint64_t>(qi) * d + i] = sq8 ? v * A.csq_step[i] : v;
+            cqp[i] = sq8 ? v * A.csq_min[i] : 0.0f;
+        }
+    }
+    for (int r = 0; r < 2; ++r) {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) x[e] *= sg[r][e];
+#pragma unroll
+        for (int h = 1; h < EPL; h <<= 1) {
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+                if ((e & h) == 0) {
+                    const float u = x[e], v = x[e + h];
+                    x[e] = u + v;
+                    x[e + h] = u - v;
+                }
+            }
+        }
+#pragma unroll
+        for (uint32_t m = 1; m < kWave; m <<= 1) {
+            const bool upper = (lane & m) != 0;
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+                const float v = __shfl_xor(x[e], static_cast<int>(m), kWave);
+                x[e] = upper ? v - x[e] : x[e] + v;
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) x[e] *= A.fht_scale;
+    }
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) xs[base + e] = x[e];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // ---- 1-bit code over the first 64*W coordinates: bit i = x[i] < 0
+    {
+        uint64_t mine = 0;
+        for (uint32_t w = 0; w < A.W; ++w) {
+            const uint64_t m = __ballot(xs[64 * w + lane] < 0.0f);
+            if (lane == w) mine = m;
+        }
+        if (lane < A.W) Wk.qbits[static_cast<uint64_t>(qi) * A.W + lane] = mine;
+    }
+    // ---- FastScan table: position j from x[4j .. 4j+3], 16 sums accumulated from 0 in order t = 0..3
+    auto raw_of = [&](const float4& v, int e) {
+        float s = 0.0f;
+        s += (e & 1) ? -v.x : v.x;
+        s += (e & 2) ? -v.y : v.y;
+        s += (e & 4) ? -v.z : v.z;
+        s += (e & 8) ? -v.w : v.w;
+        return s;
+    };
+    float range = 0.0f;
+    for (uint32_t j = lane; j < npos; j += kWave) {
+        const float4 v = reinterpret_cast<const float4*>(xs)[j];
+        float lo = INFINITY, hi = -INFINITY;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const float s = raw_of(v, e);
+            lo = fminf(lo, s);
+            hi = fmaxf(hi, s);
+        }
+        mins[j] = lo;
+        range = fmaxf(range, hi - lo);
+    }
+    range = wave_max_f32(range);
+    const float delta = fmaxf(range / 255.0f, 1e-12f);
+    uint4* lut = reinterpret_cast<uint4*>(Wk.lut + static_cast<uint64_t>(qi) * npos * 16);
+    for (uint32_t j = lane; j < npos; j += kWave) {
+        const float4 v = reinterpret_cast<const float4*>(xs)[j];
+        const float lo = mins[j];
+        uint32_t pk[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const float qv = fminf(fmaxf(roundf((raw_of(v, e) - lo) / delta), 0.0f), 255.0f);
+            pk[e >> 2] |= static_cast<uint32_t>(qv) << (8 * (e & 3));
+        }
+        lut[j] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // ---- sequential sums in index order: lane 0 the table bias (Rust's f32 Sum folds from -0.0),
+    // lane 1 the rescore base sum(q * csq_min) from 0.0
+    if (lane < 2) {
+        // both arrays are padded to a multiple of 4 in LDS, so whole float4s are read 16 at a
+        // time ahead of the dependent adds
+        const uint32_t n = lane == 0 ? npos : (sq8 ? d : 0u);
+        const float4* src = reinterpret_cast<const float4*>(lane == 0 ? mins : cqp);
+        float s = lane == 0 ? -0.0f : 0.0f;
+        for (uint32_t i = 0; i < n; i += 16) {
+            float4 v[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] = i + 4 * j < n ? src[i / 4 + j] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t b = i + 4 * j;
+                if (b < n) s += v[j].x;
+                if (b + 1 < n) s += v[j].y;
+                if (b + 2 < n) s += v[j].z;
+                if (b + 3 < n) s += v[j].w;
+            }
+        }
+        if (lane == 0) {
+            Wk.bias[qi] = s;
+            Wk.delta[qi] = delta;
+        } else {
+            Wk.cqbase[qi] = s;
+        }
+    }
+}
+
+// ---------------------------------------------------------------- Hamming (query tile x cell tile)
+
+// h[q][c] = popcount(qbits[q] ^ cent_bits[c]) for every query and cell (src/index.rs:1896-1915),
+// 0xFFFF for dead cells and the padding up to Mp. Each thread holds one centroid code in
+// registers and runs it against kHamQ query codes broadcast from LDS.
+template <int NW>
+__global__ void __launch_bounds__(kHamThreads)
+hamming_kernel(DevArena A, Work Wk, KParams K) {
+    __shared__ uint64_t qb[kHamQ * NW];
+    const uint32_t q0 = blockIdx.y * kHamQ;
+    const uint32_t nqt = min(kHamQ, K.nq - q0);
+    for (uint32_t i = threadIdx.x; i < nqt * NW; i += blockDim.x) qb[i] = Wk.qbits[static_cast<uint64_t>(q0) * NW + i];
+    const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t Mp = A.Mp;
+    uint64_t cw[NW];
+    bool live = false;
+    if (c < A.M) {
+#pragma unroll
+        for (int w = 0; w < NW; ++w) cw[w] = A.cent_bits[static_cast<uint64_t>(c) * NW + w];
+        live = A.live[c] != 0;
+    }
+    __syncthreads();
+    if (c >= Mp) return;
+    uint16_t* out = Wk.hs + static_cast<uint64_t>(q0) * Mp + c;
+    for (uint32_t j = 0; j < nqt; ++j) {
+        uint32_t h = 0;
+        if (live) {
+#pragma unroll
+            for (int w = 0; w < NW; ++w) h += __popcll(qb[j * NW + w] ^ cw[w]);
+        }
+        out[static_cast<uint64_t>(j) * Mp] = live ? static_cast<uint16_t>(h) : static_cast<uint16_t>(0xFFFFu);
+    }
+}
+
+// ---------------------------------------------------------------- route (one WG per query)
+
+// route_batch (src/index.rs:1873-1980) from the query's Hamming row: cut-off (hamming_cutoff,
+// :86-104), shortlist of live cells with h <= cut in ascending id, exact rescore, probe list
+// sorted by (score desc, cell asc), nucleus. Also the adaptive-cut bounds of the probe list
+// b_i = cos(max(acos(clamp(s_i)) - r_bound_c, 0)) for i >= SEED_CELLS (:2171-2176), which
+// depend on routing alone.
+// LDS: cqs[d4] | ex[np4] | keys[sort_cap] u64 | hist[nbins4] | scratch[16].
 template <int NW>
 __global__ void __launch_bounds__(kRouteThreads)
-prep_route_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries, uint32_t mode) {
+route_kernel(DevArena A, Work Wk, KParams K) {
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t qi = blockIdx.x;
     if (qi >= K.nq) return;
     const uint32_t tid = threadIdx.x, nt = blockDim.x;
-    const uint32_t d = A.d, P = A.P, M = A.M, npos = A.npos;
-    constexpr uint32_t W = NW;
-    const uint32_t d4 = (d + 3) & ~3u;
-    float* x = reinterpret_cast<float*>(smem);
-    float* cqs = x + P;
-    float* cqp = cqs + d4;
-    uint16_t* hs = reinterpret_cast<uint16_t*>(cqp + d4);
-    uint64_t* keys = reinterpret_cast<uint64_t*>(hs + ((M + 7) & ~7u));
-    float* mins = reinterpret_cast<float*>(keys + K.sort_cap);
-    uint32_t* hist = reinterpret_cast<uint32_t*>(mins + ((npos + 3) & ~3u));
-    const uint32_t nbins = W * 64 + 1;
+    const uint32_t d = A.d, M = A.M, Mp = A.Mp;
+    const uint32_t d4 = (d + 3) & ~3u, np4 = min((K.nprobe + 3) & ~3u, K.sort_cap);
+    const uint32_t nbins = NW * 64 + 1;
+    float* cqs = reinterpret_cast<float*>(smem);
+    float* ex = cqs + d4;
+    uint64_t* keys = reinterpret_cast<uint64_t*>(ex + np4);
+    uint32_t* hist = reinterpret_cast<uint32_t*>(keys + K.sort_cap);
     uint32_t* scratch = hist + ((nbins + 3) & ~3u);
-    __shared__ float s_cqbase;
-    __shared__ uint32_t s_cut, s_nsl;
-    __shared__ uint64_t s_qw[16];
+    __shared__ uint32_t s_cut;
+    (void)M;
 
-    const float* q = queries + static_cast<uint64_t>(qi) * d;
-    const bool sq8 = A.cent_sq8 != nullptr;
-    // ---- load: query, and the SQ8 rescore operands cqs = q*step, q*min (src/index.rs:1934-1942)
-    for (uint32_t i = tid; i < P; i += nt) {
-        float v = i < d ? q[i] : 0.0f;
-        x[i] = v;
-        if (i < d) {
-            cqs[i] = sq8 ? v * A.csq_step[i] : v;
-            cqp[i] = sq8 ? v * A.csq_min[i] : 0.0f;
-        }
-    }
-    // ---- rotation: 2 x (sign flip, FWHT, x 1/sqrt(P)), src/quantize.rs:152-163
-    for (int r = 0; r < 2; ++r) {
-        __syncthreads();
-        for (uint32_t i = tid; i < P; i += nt) x[i] *= A.rot_signs[r * P + i];
-        for (uint32_t h = 1; h < P; h <<= 1) {
-            __syncthreads();
-            for (uint32_t t = tid; t < P / 2; t += nt) {
-                uint32_t j = (t / h) * 2 * h + (t % h);
-                float u = x[j], v = x[j + h];
-                x[j] = u + v;
-                x[j + h] = u - v;
-            }
-        }
-        __syncthreads();
-        for (uint32_t i = tid; i < P; i += nt) x[i] *= A.fht_scale;
-    }
-    __syncthreads();
-    // ---- 1-bit code: bit i = x[i] < 0 (src/quantize.rs:57-67)
-    uint64_t* qb_out = Wk.qbits + static_cast<uint64_t>(qi) * W;
-    for (uint32_t base = 0; base < W * 64; base += nt) {
-        uint32_t i = base + tid;
-        bool neg = i < W * 64 && x[i] < 0.0f;
-        uint64_t m = __ballot(neg);
-        if (lane_id() == 0 && i < W * 64) {
-            qb_out[i >> 6] = m;
-            s_qw[i >> 6] = m;
-        }
-    }
-    // ---- FastScan table (src/quantize.rs:279-313): position j uses x[4j .. 4j+3]
-    float lo = INFINITY, hi = -INFINITY;
-    float raw[16];
-    const bool own = tid < npos;
-    if (own) {
-        float xs[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) xs[t] = x[4 * tid + t];
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            float v = 0.0f;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) v += ((e >> t) & 1) ? -xs[t] : xs[t];
-            raw[e] = v;
-            lo = fminf(lo, v);
-            hi = fmaxf(hi, v);
-        }
-        mins[tid] = lo;
-    }
-    const float range = fmaxf(block_max_f32(own ? hi - lo : 0.0f, reinterpret_cast<float*>(scratch)), 0.0f);
-    const float delta = fmaxf(range / 255.0f, 1e-12f);
-    if (own) {
-        uint32_t pk[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            float qv = fminf(fmaxf(roundf((raw[e] - lo) / delta), 0.0f), 255.0f);
-            pk[e >> 2] |= static_cast<uint32_t>(qv) << (8 * (e & 3));
-        }
-        reinterpret_cast<uint4*>(Wk.lut + static_cast<uint64_t>(qi) * npos * 16)[tid] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-    }
-    __syncthreads();
-    if (mode == 2) {  // query_prep test entry point
-        if (tid == 0) {
-            Wk.bias[qi] = seq_sum_lds(mins, npos, -0.0f);  // Rust's f32 Sum folds from -0.0
-            Wk.delta[qi] = delta;
-        }
-        return;
-    }
-    // ---- wave 0 lane 0: the two sequential sums (bias, cqbase) while the other waves run the
-    // Hamming pass; everything else: Hamming against every centroid code + live histogram
     for (uint32_t i = tid; i < nbins; i += nt) hist[i] = 0;
+    for (uint32_t i = tid; i < d; i += nt) cqs[i] = Wk.cqs[static_cast<uint64_t>(qi) * d + i];
     __syncthreads();
-    if (tid == 0) {
-        Wk.bias[qi] = seq_sum_lds(mins, npos, -0.0f);
-        Wk.delta[qi] = delta;
-        s_cqbase = sq8 ? seq_sum_lds(cqp, d, 0.0f) : 0.0f;
-    }
-    {
-        uint64_t qw[W];
+    const uint4* hrow = reinterpret_cast<const uint4*>(Wk.hs + static_cast<uint64_t>(qi) * Mp);
+    const uint32_t nch8 = Mp / 8;
+    auto h_at = [](const uint4& v, int k) -> uint32_t {
+        const uint32_t w = k < 2 ? v.x : k < 4 ? v.y : k < 6 ? v.z : v.w;
+        return (k & 1) ? (w >> 16) : (w & 0xFFFFu);
+    };
+    uint4 first = make_uint4(~0u, ~0u, ~0u, ~0u);
+    for (uint32_t ch = tid; ch < nch8; ch += nt) {
+        const uint4 v = hrow[ch];
+        if (ch == tid) first = v;
 #pragma unroll
-        for (int w = 0; w < (int)W; ++w) qw[w] = s_qw[w];
-        const uint32_t h0 = nt > 64 ? 64u : 0u;  // wave 0 is busy with the sums
-        for (uint32_t c = tid - h0; tid >= h0 && c < M; c += 2 * (nt - h0)) {
-            const uint32_t c2 = c + (nt - h0);
-            uint64_t a[W], b[W];
-#pragma unroll
-            for (int w = 0; w < (int)W; ++w) a[w] = A.cent_bits[static_cast<uint64_t>(c) * W + w];
-            const bool two = c2 < M;
-            if (two) {
-#pragma unroll
-                for (int w = 0; w < (int)W; ++w) b[w] = A.cent_bits[static_cast<uint64_t>(c2) * W + w];
-            }
-            const uint8_t l1 = A.live[c];
-            const uint8_t l2 = two ? A.live[c2] : 0;
-            uint32_t h1 = 0, h2 = 0;
-#pragma unroll
-            for (int w = 0; w < (int)W; ++w) h1 += __popcll(qw[w] ^ a[w]);
-            hs[c] = l1 ? static_cast<uint16_t>(h1) : 0xFFFFu;
-            if (l1) atomicAdd(&hist[h1], 1u);
-            if (two) {
-#pragma unroll
-                for (int w = 0; w < (int)W; ++w) h2 += __popcll(qw[w] ^ b[w]);
-                hs[c2] = l2 ? static_cast<uint16_t>(h2) : 0xFFFFu;
-                if (l2) atomicAdd(&hist[h2], 1u);
-            }
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t h = h_at(v, k);
+            if (h != 0xFFFFu) atomicAdd(&hist[h], 1u);
         }
     }
     __syncthreads();
-    // cut = smallest t whose cumulative live count reaches want_c (hamming_cutoff, :86-104)
+    // cut = smallest t whose cumulative live count reaches want_c
     {
-        uint32_t per = (nbins + nt - 1) / nt, b0 = tid * per, loc = 0;
-        for (uint32_t i = b0; i < min(b0 + per, nbins); ++i) loc += hist[i];
+        const uint32_t per = (nbins + nt - 1) / nt, b0 = tid * per, b1 = min(b0 + per, nbins);
+        uint32_t loc = 0;
+        for (uint32_t i = b0; i < b1; ++i) loc += hist[i];
         uint32_t total;
-        uint32_t ex = block_excl_scan_u32(loc, scratch, &total);
-        uint32_t cand = kNone, cum = ex;
-        for (uint32_t i = b0; i < min(b0 + per, nbins); ++i) {
+        const uint32_t ex0 = block_excl_scan_u32(loc, scratch, &total);
+        uint32_t cand = kNone, cum = ex0;
+        for (uint32_t i = b0; i < b1; ++i) {
             cum += hist[i];
             if (cum >= K.want_c) {
                 cand = i;
                 break;
             }
         }
-        uint32_t cut = block_min_u32(cand, scratch);
-        if (tid == 0) s_cut = cut == kNone ? W * 64 : cut;
+        const uint32_t cut = block_min_u32(cand, scratch);
+        if (tid == 0) s_cut = cut == kNone ? NW * 64 : cut;
     }
     __syncthreads();
     const uint32_t cut = s_cut;
-    // ---- shortlist: live cells with h <= cut, ascending id (dead cells hold 0xFFFF)
-    {
-        uint32_t per = (M + nt - 1) / nt, c0 = tid * per, c1 = min(c0 + per, M), cnt = 0;
-        for (uint32_t c = c0; c < c1; ++c) cnt += hs[c] <= cut;
-        uint32_t total;
-        uint32_t pos = block_excl_scan_u32(cnt, scratch, &total);
-        if (tid == 0) s_nsl = total;
-        if (total <= K.sort_cap)
-            for (uint32_t c = c0; c < c1; ++c)
-                if (hs[c] <= cut) keys[pos++] = c;
+    // ---- shortlist: live cells with h <= cut, ascending id (dead cells and padding hold 0xFFFF)
+    uint32_t nsl = 0;
+    for (uint32_t r0 = 0; r0 < nch8; r0 += nt) {
+        const uint32_t ch = r0 + tid;
+        uint4 v = make_uint4(~0u, ~0u, ~0u, ~0u);
+        if (ch < nch8) v = r0 == 0 ? first : hrow[ch];
+        uint32_t cnt = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) cnt += h_at(v, k) <= cut;
+        uint32_t tot;
+        uint32_t pos = nsl + block_excl_scan_u32(cnt, scratch, &tot);
+        if (nsl + tot <= K.sort_cap) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                if (h_at(v, k) <= cut) keys[pos++] = ch * 8 + k;
+        }
+        nsl += tot;
     }
-    __syncthreads();
-    const uint32_t nsl = s_nsl;
     uint32_t* chosen = Wk.chosen + static_cast<uint64_t>(qi) * K.nprobe;
     float* cscore = Wk.cscore + static_cast<uint64_t>(qi) * K.nprobe;
     if (nsl > K.sort_cap) {
@@ -667,8 +774,10 @@ prep_route_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ quer
         }
         return;
     }
+    __syncthreads();
     // ---- exact rescore, 8 lanes per cell in the reference's FMA order (:777-800)
-    const float cqbase = sq8 ? s_cqbase : 0.0f;
+    const bool sq8 = A.cent_sq8 != nullptr;
+    const float cqbase = sq8 ? Wk.cqbase[qi] : 0.0f;
     {
         const uint32_t l = tid & 7, grp = tid >> 3, ngrp = nt >> 3;
         const uint32_t rounds = (nsl + ngrp - 1) / ngrp;
@@ -699,21 +808,28 @@ prep_route_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ quer
     }
     __syncthreads();
     for (uint32_t i = tid; i < K.nprobe; i += nt) {
-        bool ok = i < cap;
-        chosen[i] = ok ? static_cast<uint32_t>(keys[i]) : kNone;
-        cscore[i] = ok ? key_score(keys[i]) : __uint_as_float(0x7fc00000u);
+        const bool ok = i < cap;
+        const uint32_t c = ok ? static_cast<uint32_t>(keys[i]) : kNone;
+        const float s = ok ? key_score(keys[i]) : __uint_as_float(0x7fc00000u);
+        chosen[i] = c;
+        cscore[i] = s;
+        if (K.adaptive && ok && i >= kSeedCells)
+            Wk.bnd[static_cast<uint64_t>(qi) * K.nprobe + i] =
+                cos_f(fmaxf(acos_f(fminf(fmaxf(s, -1.0f), 1.0f)) - A.r_bound[c], 0.0f));
     }
     // ---- nucleus over the capped list (:1960-1973); tc >= 1 keeps all cap cells
-    if (tid == 0) {
-        uint32_t nch = cap;
-        if (K.use_nucleus && cap > 0) {
-            const float max_s = key_score(keys[0]);
+    uint32_t nch = cap;
+    if (K.use_nucleus && cap > 0) {
+        const float max_s = key_score(keys[0]);
+        for (uint32_t i = tid; i < cap; i += nt) ex[i] = exp_f((key_score(keys[i]) - max_s) * K.beta);
+        __syncthreads();
+        if (tid == 0) {
             float z = -0.0f;
-            for (uint32_t i = 0; i < cap; ++i) z += exp_f((key_score(keys[i]) - max_s) * K.beta);
+            for (uint32_t i = 0; i < cap; ++i) z += ex[i];
             float cum = 0.0f;
             bool near = false;
             for (uint32_t i = 0; i < cap; ++i) {
-                cum += exp_f((key_score(keys[i]) - max_s) * K.beta) / (z + 1e-9f);
+                cum += ex[i] / (z + 1e-9f);
                 if (fabsf(cum - K.tc) <= K.nucleus_band) near = true;
                 if (cum >= K.tc) {
                     nch = i + 1;
@@ -722,168 +838,260 @@ prep_route_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ quer
             }
             if (near) Wk.flag_route[atomicAdd(&Wk.ctl->nflag_route, 1u)] = qi;
         }
-        Wk.nchosen[qi] = nch;
     }
+    if (tid == 0) Wk.nchosen[qi] = nch;
 }
 
 // ---------------------------------------------------------------- seed (one WG per query)
 
-// All canonical members of the first 8 probed cells are scored at once (src/index.rs:2150-2154);
-// tau is their exact target-th smallest d (:2155-2160) and only d <= tau is kept; then the
-// adaptive cut (:2166-2188) and the per-cell probe counts for the inversion.
+// One member's nibble sums against a single query's FastScan table at LDS offset 0: the
+// position offsets are immediates of the LDS reads, so each lookup costs one bit-field
+// extract and half an add.
 template <int NW>
-__global__ void __launch_bounds__(kSeedThreads)
+__device__ __forceinline__ uint32_t lut_sum1(const Code<NW>& c, const uint8_t* __restrict__ table) {
+    uint32_t S = 0;
+#pragma unroll
+    for (int k = 0; k < Code<NW>::NCH; ++k) {
+        const uint32_t dw[4] = {c.v[k].x, c.v[k].y, c.v[k].z, c.v[k].w};
+        constexpr int npos = NW == 1 ? 16 : 32;
+#pragma unroll
+        for (int t = 0; t < npos; ++t) {
+            const uint32_t nib = (dw[t >> 3] >> (4 * (t & 7))) & 0xFu;
+            S += table[(k * 32 + t) * 16 + nib];
+            // keep the running sum in order per 16 lookups: without this the compiler re-associates
+            // all 16*NW terms into one tree and holds every looked-up byte live at once
+            if ((t & 15) == 15) asm volatile("" : "+v"(S));
+        }
+    }
+    return S;
+}
+
+// All canonical members of the first SEED_CELLS probed cells are scored
+// (src/index.rs:2150-2154); tau is their exact target-th smallest d (:2155-2160) and only
+// d <= tau is kept; then the adaptive cut (:2166-2188) from the route's bounds, and the per-cell
+// probe counts for the inversion.
+// LDS: static table[TB] at offset 0; dynamic probed[MW4] | coarse[256] | fine[256] | misc[32] |
+// sbuf[seed_cap4] (d << 16 | item, item < 65536).
+template <int NW>
+__global__ void __launch_bounds__(kSeedThreads, 4)
 seed_kernel(DevArena A, Work Wk, KParams K) {
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t qi = blockIdx.x;
     if (qi >= K.nq) return;
-    const uint32_t tid = threadIdx.x, nt = blockDim.x;
+    const uint32_t tid = threadIdx.x, nt = blockDim.x, lane = lane_id();
     constexpr uint32_t TB = NW * 256;
-    uint8_t* table = smem;
-    uint32_t* probed = reinterpret_cast<uint32_t*>(smem + TB);
-    uint32_t* sbuf = probed + ((A.MW + 3) & ~3u);              // seed_cap: d << 16 | item (item < 65536)
-    uint32_t* hist = sbuf + ((K.seed_cap + 3) & ~3u);
-    uint32_t* scratch = hist + kHistBins;
-    float* fsc = reinterpret_cast<float*>(scratch + 32);       // nt floats
-    __shared__ uint32_t s_off[kSeedCells + 1], s_cell[kSeedCells], s_cnt, s_keep;
+    constexpr uint32_t kOff = 0, kCell = 9, kE0 = 17, kCnt = 25, kKeep = 26, kTau = 27, kRe = 28, kHb = 29, kBelow = 30;
+    // the kernel's only static LDS: its address is the constant 0, so the table lookups need no base add
+    __shared__ __align__(16) uint8_t table[TB];
+    uint32_t* probed = reinterpret_cast<uint32_t*>(smem);
+    uint32_t* coarse = probed + ((A.MW + 3) & ~3u);
+    uint32_t* fine = coarse + 256;
+    uint32_t* misc = fine + 256;
+    uint32_t* sbuf = misc + 32;
 
     const uint32_t nch = Wk.nchosen[qi];
     const uint32_t* chosen = Wk.chosen + static_cast<uint64_t>(qi) * K.nprobe;
-    const float* cscore = Wk.cscore + static_cast<uint64_t>(qi) * K.nprobe;
     const uint32_t ns = min(kSeedCells, nch);
     {
-        const uint32_t* lut = reinterpret_cast<const uint32_t*>(Wk.lut + static_cast<uint64_t>(qi) * TB);
-        for (uint32_t i = tid; i < TB / 4; i += nt) reinterpret_cast<uint32_t*>(table)[i] = lut[i];
+        const uint4* src = reinterpret_cast<const uint4*>(Wk.lut + static_cast<uint64_t>(qi) * TB);
+        for (uint32_t i = tid; i < TB / 16; i += nt) reinterpret_cast<uint4*>(table)[i] = src[i];
     }
     for (uint32_t i = tid; i < A.MW; i += nt) probed[i] = 0;
-    if (tid == 0) {
-        s_cnt = 0;
-        s_keep = 0;
-        uint32_t o = 0;
-        for (uint32_t s = 0; s < ns; ++s) {
-            uint32_t c = chosen[s];
-            s_cell[s] = c;
-            s_off[s] = o;
-            o += A.mem_off[c + 1] - A.mem_off[c];
+    for (uint32_t i = tid; i < 512; i += nt) coarse[i] = 0;  // coarse and fine
+    if (tid < kWave) {
+        uint32_t c = 0, e0 = 0, len = 0;
+        if (tid < ns) {
+            c = chosen[tid];
+            e0 = A.mem_off[c];
+            len = A.mem_off[c + 1] - e0;
         }
-        s_off[ns] = o;
+        uint32_t x = len;
+#pragma unroll
+        for (int o = 1; o < static_cast<int>(kSeedCells); o <<= 1) {
+            const uint32_t y = __shfl_up(x, o, kWave);
+            if (tid >= static_cast<uint32_t>(o)) x += y;
+        }
+        if (tid < ns) {
+            misc[kOff + tid + 1] = x;
+            misc[kCell + tid] = c;
+            misc[kE0 + tid] = e0;
+        }
+        if (tid == 0) {
+            misc[kOff] = 0;
+            misc[kCnt] = 0;
+            misc[kKeep] = 0;
+        }
     }
     __syncthreads();
     for (uint32_t i = tid; i < nch; i += nt) atomicOr(&probed[chosen[i] >> 5], 1u << (chosen[i] & 31));
     __syncthreads();
     {
-        uint32_t* gprobed = Wk.probed + static_cast<uint64_t>(qi) * A.MW;
-        for (uint32_t i = tid; i < A.MW; i += nt) gprobed[i] = probed[i];
+        uint32_t* gp = Wk.probed + static_cast<uint64_t>(qi) * A.MW;
+        for (uint32_t i = tid; i < A.MW; i += nt) gp[i] = probed[i];
     }
-    const uint32_t total = s_off[ns];
-    if (total > K.seed_cap) {  // cannot happen for an arena whose largest cell fits (checked at upload)
+    const uint32_t total = misc[kOff + ns];
+    if (total > K.seed_cap) {  // cannot happen: seed_cap bounds the SEED_CELLS largest cells
         if (tid == 0) atomicAdd(&Wk.ctl->err_seed, 1u);
         return;
     }
-    // ---- score every seed member, all cells at once
-    for (uint32_t base = 0; base < total; base += nt) {
-        const uint32_t it = base + tid;
-        bool pass = false;
-        uint32_t dv = 0;
-        if (it < total) {
-            uint32_t s = 0;
+    auto seed_cell = [&](uint32_t it) {
+        uint32_t s = 0;
 #pragma unroll
-            for (uint32_t k = 1; k < kSeedCells; ++k) s += (k < ns && it >= s_off[k]);
-            const uint32_t c = s_cell[s];
-            const uint64_t e = static_cast<uint64_t>(A.mem_off[c]) + (it - s_off[s]);
-            Code<NW> code;
-            code.load(A.codes + e * (2 * NW));
-            const uint32_t slot = A.members[e];
-            pass = canonical(A, e, slot, c, probed);
-            uint32_t sm[1];
-            lut_sums<NW, 1>(code, table, sm);
-            dv = A.maxk - sm[0];
+        for (uint32_t k = 1; k < kSeedCells; ++k) s += (k < ns && it >= misc[kOff + k]);
+        return s;
+    };
+    // ---- score every seed member, all cells at once; coarse histogram of d >> 8 on the fly.
+    // Software pipeline: the next round's code (and other home) is in flight during this round's
+    // lookups.
+    if (total > 0) {
+        auto locate = [&](uint32_t it, uint32_t& c) -> uint64_t {
+            const uint32_t j = min(it, total - 1);
+            const uint32_t s = seed_cell(j);
+            c = misc[kCell + s];
+            return static_cast<uint64_t>(misc[kE0 + s]) + (j - misc[kOff + s]);
+        };
+        uint32_t c_cur;
+        uint64_t e_cur = locate(tid, c_cur);
+        Code<NW> cur;
+        cur.load(A.codes + e_cur * (2 * NW));
+        uint32_t alt_cur = A.ma == 2 ? A.entry_alt[e_cur] : kNoAlt;
+        for (uint32_t b = 0; b < total; b += nt) {
+            const uint32_t it = b + tid;
+            const bool have = it < total;
+            const bool more = b + nt < total;
+            uint32_t c_nxt = 0, alt_nxt = kNoAlt;
+            uint64_t e_nxt = 0;
+            Code<NW> nxt;
+            if (more) {
+                e_nxt = locate(it + nt, c_nxt);
+                nxt.load(A.codes + e_nxt * (2 * NW));
+                if (A.ma == 2) alt_nxt = A.entry_alt[e_nxt];
+            }
+            bool pass = false;
+            uint32_t dv = 0;
+            if (have) {
+                if (A.ma == 2)
+                    pass = !(alt_cur < c_cur && ((probed[alt_cur >> 5] >> (alt_cur & 31)) & 1u));
+                else
+                    pass = canonical(A, e_cur, A.ma > 2 ? A.members[e_cur] : 0u, c_cur, probed);
+                dv = A.maxk - lut_sum1<NW>(cur, table);
+                if (pass) atomicAdd(&coarse[dv >> 8], 1u);
+            }
+            const uint64_t m = __ballot(pass);
+            uint32_t wb = 0;
+            if (lane == 0 && m) wb = atomicAdd(&misc[kCnt], static_cast<uint32_t>(__popcll(m)));
+            wb = __shfl(wb, 0, kWave);
+            if (pass) sbuf[wb + lanes_below(m)] = (dv << 16) | it;
+            if (more) {
+                cur = nxt;
+                e_cur = e_nxt;
+                c_cur = c_nxt;
+                alt_cur = alt_nxt;
+            }
         }
-        uint64_t m = __ballot(pass);
-        uint32_t wb = 0;
-        if (lane_id() == 0 && m) wb = atomicAdd(&s_cnt, static_cast<uint32_t>(__popcll(m)));
-        wb = __shfl(wb, 0, kWave);
-        if (pass) sbuf[wb + lanes_below(m)] = (dv << 16) | it;
     }
     __syncthreads();
-    const uint32_t cnt = s_cnt;
-    // ---- tau = target-th smallest seed d; keep d <= tau (src/index.rs:2155-2160)
+    const uint32_t cnt = misc[kCnt];
+    // ---- tau = target-th smallest seed d (two 256-bin passes, scanned by wave 0)
     uint32_t tau = A.maxk;
-    if (cnt >= K.target) tau = select_kth(cnt, K.target, [&](uint32_t i) { return sbuf[i] >> 16; }, hist, scratch);
+    if (cnt >= K.target) {
+        auto find_bin = [&](const uint32_t* h, uint32_t want, uint32_t* bin, uint32_t* below) {
+            uint32_t v[4], s4 = 0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                v[k] = h[4 * lane + k];
+                s4 += v[k];
+            }
+            uint32_t x = s4;
+#pragma unroll
+            for (int o = 1; o < kWave; o <<= 1) {
+                const uint32_t y = __shfl_up(x, o, kWave);
+                if (lane >= static_cast<uint32_t>(o)) x += y;
+            }
+            uint32_t cum = x - s4;
+            if (cum < want && x >= want) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    if (cum + v[k] >= want) {
+                        *bin = 4 * lane + k;
+                        *below = cum;
+                        break;
+                    }
+                    cum += v[k];
+                }
+            }
+        };
+        if (tid < kWave) find_bin(coarse, K.target, &misc[kHb], &misc[kBelow]);
+        __syncthreads();
+        const uint32_t hb = misc[kHb], need = K.target - misc[kBelow];
+        for (uint32_t i = tid; i < cnt; i += nt) {
+            const uint32_t dd = sbuf[i] >> 16;
+            if ((dd >> 8) == hb) atomicAdd(&fine[dd & 0xFFu], 1u);
+        }
+        __syncthreads();
+        if (tid < kWave) find_bin(fine, need, &misc[kTau], &misc[kBelow]);
+        __syncthreads();
+        tau = (hb << 8) | misc[kTau];
+    }
+    // ---- keep d <= tau, with the member's slot
     uint2* seed = Wk.seed + static_cast<uint64_t>(qi) * K.seed_cap;
-    for (uint32_t base = 0; base < cnt; base += nt) {
-        const uint32_t i = base + tid;
-        uint32_t v = i < cnt ? sbuf[i] : 0u;
+    for (uint32_t b = 0; b < cnt; b += nt) {
+        const uint32_t i = b + tid;
+        const uint32_t v = i < cnt ? sbuf[i] : 0u;
         const bool keep = i < cnt && (v >> 16) <= tau;
-        uint64_t m = __ballot(keep);
+        const uint64_t m = __ballot(keep);
         uint32_t wb = 0;
-        if (lane_id() == 0 && m) wb = atomicAdd(&s_keep, static_cast<uint32_t>(__popcll(m)));
+        if (lane == 0 && m) wb = atomicAdd(&misc[kKeep], static_cast<uint32_t>(__popcll(m)));
         wb = __shfl(wb, 0, kWave);
         if (keep) {
             const uint32_t it = v & 0xFFFFu;
-            uint32_t s = 0;
-#pragma unroll
-            for (uint32_t k = 1; k < kSeedCells; ++k) s += (k < ns && it >= s_off[k]);
-            const uint32_t slot = A.members[A.mem_off[s_cell[s]] + (it - s_off[s])];
+            const uint32_t s = seed_cell(it);
+            const uint32_t slot = A.members[misc[kE0 + s] + (it - misc[kOff + s])];
             seed[wb + lanes_below(m)] = make_uint2(v >> 16, slot);
         }
     }
-    // ---- adaptive cut: b_i = cos(max(acos(clamp(cs_i)) - r_c, 0)), suffix max, first i >= ns
-    // with suffix_i < thr - margin
+    __syncthreads();  // every wave's kept count is in misc[kKeep]
+    // ---- adaptive cut: suffix maxima of the route's bounds, first i >= ns below thr - margin
     uint32_t rest_end = nch;
     if (K.adaptive && cnt >= K.target && ns < nch) {
-        const float est = Wk.delta[qi] * static_cast<float>(A.maxk - tau) + Wk.bias[qi];
-        const float thr = fminf(fmaxf(est / K.norm, -1.0f), 1.0f);
-        const float T = thr - K.at_margin;
-        const uint32_t m = nch - ns, per = (m + nt - 1) / nt;
-        const uint32_t i0 = ns + tid * per, i1 = min(i0 + per, nch);
-        float run_max = -INFINITY;
-        for (uint32_t i = i1; i-- > i0;)
-            run_max = fmaxf(run_max, cos_f(fmaxf(acos_f(fminf(fmaxf(cscore[i], -1.0f), 1.0f)) - A.r_bound[chosen[i]], 0.0f)));
-        // inclusive suffix max of the run maxima (Hillis-Steele over the block, from the right)
-        fsc[tid] = run_max;
+        if (tid < kWave) {
+            const float est = Wk.delta[qi] * static_cast<float>(A.maxk - tau) + Wk.bias[qi];
+            const float thr = fminf(fmaxf(est / K.norm, -1.0f), 1.0f);
+            const float T = thr - K.at_margin;
+            const float* bnd = Wk.bnd + static_cast<uint64_t>(qi) * K.nprobe;
+            float carry = -INFINITY;
+            uint32_t firstb = kNone;
+            bool near = false;
+            for (int32_t hi = static_cast<int32_t>(nch); hi > static_cast<int32_t>(ns); hi -= kWave) {
+                const int32_t lo = max(hi - kWave, static_cast<int32_t>(ns));
+                const int32_t i = lo + static_cast<int32_t>(lane);
+                const bool valid = i < hi;
+                float x = valid ? bnd[i] : -INFINITY;
+#pragma unroll
+                for (int o = 1; o < kWave; o <<= 1) {
+                    const float y = __shfl_down(x, o, kWave);
+                    if (lane + o < static_cast<uint32_t>(kWave)) x = fmaxf(x, y);
+                }
+                x = fmaxf(x, carry);
+                carry = __shfl(x, 0, kWave);
+                const uint64_t below = __ballot(valid && x < T);
+                if (below) firstb = static_cast<uint32_t>(lo) + static_cast<uint32_t>(__ffsll(static_cast<long long>(below)) - 1);
+                if (__ballot(valid && fabsf(x - T) <= K.prune_band)) near = true;
+            }
+            if (lane == 0) {
+                misc[kRe] = firstb != kNone ? firstb : nch;
+                if (near) Wk.flag_prune[atomicAdd(&Wk.ctl->nflag_prune, 1u)] = qi;
+            }
+        }
         __syncthreads();
-        for (uint32_t off = 1; off < nt; off <<= 1) {
-            float o = tid + off < nt ? fsc[tid + off] : -INFINITY;
-            __syncthreads();
-            fsc[tid] = fmaxf(fsc[tid], o);
-            __syncthreads();
-        }
-        float later = tid + 1 < nt ? fsc[tid + 1] : -INFINITY;
-        uint32_t first = kNone;
-        bool near = false;
-        float sfx = later;
-        for (uint32_t i = i1; i-- > i0;) {
-            sfx = fmaxf(sfx, cos_f(fmaxf(acos_f(fminf(fmaxf(cscore[i], -1.0f), 1.0f)) - A.r_bound[chosen[i]], 0.0f)));
-            if (sfx < T) first = i;
-            if (fabsf(sfx - T) <= K.prune_band) near = true;
-        }
-        const uint32_t fe = block_min_u32(first, scratch);
-        const uint32_t any_near = block_sum_u32(near ? 1u : 0u, scratch);
-        if (fe != kNone) rest_end = fe;
-        if (tid == 0 && any_near) Wk.flag_prune[atomicAdd(&Wk.ctl->nflag_prune, 1u)] = qi;
+        rest_end = misc[kRe];
     }
-    // ---- probe counts for the inversion, and this query's work counters
-    uint32_t sb = 0, rb = 0;
-    for (uint32_t i = tid; i < rest_end; i += nt) {
-        const uint32_t c = chosen[i];
-        const uint32_t nb = (A.mem_off[c + 1] - A.mem_off[c] + 31) / 32;
-        if (i < ns) {
-            sb += nb;
-        } else {
-            rb += nb;
-            atomicAdd(&Wk.cell_cnt[c], 1u);
-        }
-    }
-    sb = block_sum_u32(sb, scratch);
-    rb = block_sum_u32(rb, scratch);
+    // ---- probe counts for the inversion
+    for (uint32_t i = ns + tid; i < rest_end; i += nt) atomicAdd(&Wk.cell_cnt[chosen[i]], 1u);
     if (tid == 0) {
-        Wk.seed_cnt[qi] = s_keep;
+        Wk.seed_cnt[qi] = misc[kKeep];
         Wk.tau[qi] = tau;
         Wk.rest_end[qi] = rest_end;
-        Wk.qstat[3ull * qi] = sb;
-        Wk.qstat[3ull * qi + 1] = rb;
-        Wk.qstat[3ull * qi + 2] = rest_end > ns ? rest_end - ns : 0u;
     }
 }
 
@@ -1117,16 +1325,23 @@ finish_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries,
     }
 }
 
-// Work counters of the last batch (on demand, one workgroup).
-__global__ void counters_kernel(Work Wk, uint32_t nq) {
+// Work counters of the last batch (on demand, one workgroup), from the routed lists: seed and
+// scan blocks (32-vector FastScan blocks per (query, cell) pair), scan pairs, survivors, reranked
+// rows.
+__global__ void counters_kernel(DevArena A, Work Wk, KParams K) {
     __shared__ uint32_t scratch[32];
     unsigned long long v[5] = {0, 0, 0, 0, 0};
-    for (uint32_t i = threadIdx.x; i < nq; i += blockDim.x) {
-        v[0] += Wk.qstat[3ull * i];
-        v[1] += Wk.qstat[3ull * i + 1];
-        v[2] += Wk.qstat[3ull * i + 2];
-        v[3] += Wk.cand_cnt[i];
-        v[4] += Wk.ncand[i];
+    for (uint32_t q = threadIdx.x; q < K.nq; q += blockDim.x) {
+        const uint32_t* ch = Wk.chosen + static_cast<uint64_t>(q) * K.nprobe;
+        const uint32_t nch = Wk.nchosen[q], ns = min(kSeedCells, nch), re = Wk.rest_end[q];
+        for (uint32_t i = 0; i < max(ns, re); ++i) {
+            const uint32_t c = ch[i];
+            const uint32_t nb = (A.mem_off[c + 1] - A.mem_off[c] + 31) / 32;
+            v[i < ns ? 0 : 1] += nb;
+        }
+        v[2] += re > ns ? re - ns : 0u;
+        v[3] += Wk.cand_cnt[q];
+        v[4] += Wk.ncand[q];
     }
     for (int k = 0; k < 5; ++k) {
         // per-thread partials are < 2^32 for any batch the buffers can hold

@@ -22,8 +22,10 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdarg>
+#include <cstdlib>
 #include <cstdio>
 #include <cstring>
+#include <functional>
 #include <mutex>
 #include <string>
 #include <type_traits>
@@ -60,11 +62,25 @@ struct maivs_gpu_ctx {
     uint32_t cap_nq = 0, cap_nprobe = 0, cap_k = 0, cap_cand = 0, cap_seed = 0, cap_fin = 0, cap_key = 0;
     uint32_t cand_nq = 0;
     uint32_t max_sort_cap_route = 0;  // largest shortlist sort the route kernel's LDS can hold
-    size_t lds_route_fixed = 0, lds_seed = 0, lds_finish = 0;
+    uint32_t seed_cap = 0;            // sum of the SEED_CELLS largest cells: bound of one seed set
+    size_t lds_prep = 0, lds_seed = 0, lds_finish = 0;
     hipEvent_t ev[8] = {};
-    // last call, for maivs_gpu_last_candidates
+    // last call, for maivs_gpu_last_candidates / maivs_gpu_last_counters
     uint32_t last_nq = 0, last_fin_cap = 0;
+    KParams last_K{};
     uint32_t initial_cand_cap = 4096;
+    // the main pass captured as one HIP graph, replayed while its key matches
+    struct GraphKey {
+        KParams K;
+        const float* q;
+        uint32_t* slots;
+        float* scores;
+        uint64_t gen;
+    };
+    bool use_graph = true;
+    uint64_t buf_gen = 0;  // bumped whenever a buffer the graph references is reallocated
+    hipGraphExec_t gexec = nullptr;
+    GraphKey gkey{};
 };
 
 namespace {
@@ -111,7 +127,24 @@ void free_all(std::vector<void*>& v) {
     v.clear();
 }
 
+void drop_graph(maivs_gpu_ctx* ctx) {
+    if (ctx->gexec) (void)hipGraphExecDestroy(ctx->gexec);
+    ctx->gexec = nullptr;
+    ctx->buf_gen++;
+}
+
 bool supported_nw(uint32_t w) { return w == 1 || w == 2 || w == 4 || w == 8 || w == 16; }
+
+#define DISPATCH_EPL(E, ...)                              \
+    switch (E) {                                          \
+        case 1: { constexpr int EPL = 1; __VA_ARGS__; break; } \
+        case 2: { constexpr int EPL = 2; __VA_ARGS__; break; } \
+        case 4: { constexpr int EPL = 4; __VA_ARGS__; break; } \
+        case 8: { constexpr int EPL = 8; __VA_ARGS__; break; } \
+        case 16: { constexpr int EPL = 16; __VA_ARGS__; break; } \
+        case 32: { constexpr int EPL = 32; __VA_ARGS__; break; } \
+        default: { constexpr int EPL = 64; __VA_ARGS__; break; } \
+    }
 
 #define DISPATCH_NW(W, ...)                              \
     switch (W) {                                         \
@@ -122,17 +155,23 @@ bool supported_nw(uint32_t w) { return w == 1 || w == 2 || w == 4 || w == 8 || w
         default: { constexpr int NW = 16; __VA_ARGS__; break; } \
     }
 
-// LDS of prep_route: x[P] | cqs[d4] | cqp[d4] | hs[M8] u16 | keys[sort_cap] u64 | mins[npos4] |
-// hist[nbins4] | scratch[16]
-size_t route_lds(const DevArena& A, uint32_t sort_cap) {
-    const size_t d4 = (A.d + 3) & ~3u;
-    return A.P * 4 + d4 * 8 + ((A.M + 7) & ~7u) * 2 + static_cast<size_t>(sort_cap) * 8 + ((A.npos + 3) & ~3u) * 4 +
+// LDS of prep: per wave x[P] | mins[npos4] | cqp[d4]
+size_t prep_lds(const DevArena& A) {
+    return static_cast<size_t>(kPrepWaves) * (A.P + ((A.npos + 3) & ~3u) + ((A.d + 3) & ~3u)) * 4;
+}
+
+// LDS of route: cqs[d4] | ex[np4] | keys[sort_cap] u64 | hist[nbins4] | scratch[16]
+// (ex holds the nucleus weights of the capped list, at most min(nprobe, sort_cap) of them)
+size_t route_lds(const DevArena& A, uint32_t sort_cap, uint32_t nprobe) {
+    const size_t np4 = std::min<size_t>((nprobe + 3) & ~3u, sort_cap);
+    return ((A.d + 3) & ~3u) * 4 + np4 * 4 + static_cast<size_t>(sort_cap) * 8 +
            (((A.W * 64 + 1) + 3) & ~3u) * 4 + 16 * 4;
 }
 
-// LDS of seed: table | probed[MW4] | sbuf[seed_cap4] | hist[256] | scratch[32] | suffix maxima[nt]
+// Dynamic LDS of seed: probed[MW4] | coarse[256] | fine[256] | misc[32] | sbuf[seed_cap4]
+// (plus its static table of W*256 bytes)
 size_t seed_lds(const DevArena& A, uint32_t seed_cap) {
-    return A.W * 256 + ((A.MW + 3) & ~3u) * 4 + ((seed_cap + 3) & ~3u) * 4 + kHistBins * 4 + 32 * 4 + kSeedThreads * 4;
+    return ((A.MW + 3) & ~3u) * 4 + 512 * 4 + 32 * 4 + static_cast<size_t>((seed_cap + 3) & ~3u) * 4;
 }
 
 size_t finish_lds(const DevArena& A) {
@@ -152,9 +191,10 @@ Chain make_chain(uint32_t d, uint32_t vec) {
 // separate (ensure_cand) so that growing them never moves the staged queries or outputs.
 int ensure_work(maivs_gpu_ctx* ctx, uint32_t nq, uint32_t nprobe, uint32_t k) {
     const DevArena& A = ctx->A;
-    uint32_t seed_cap = kSeedCells * std::max<uint32_t>(A.max_cell_len, 1);
+    const uint32_t seed_cap = ctx->seed_cap;
     if (nq <= ctx->cap_nq && nprobe <= ctx->cap_nprobe && k <= ctx->cap_k && seed_cap <= ctx->cap_seed) return 0;
     HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    drop_graph(ctx);
     free_all(ctx->work_allocs);
     free_all(ctx->cand_allocs);
     ctx->cand_nq = 0;
@@ -170,6 +210,10 @@ int ensure_work(maivs_gpu_ctx* ctx, uint32_t nq, uint32_t nprobe, uint32_t k) {
     rc |= dalloc(ctx, o, &W.lut, nql * A.npos * 16);
     rc |= dalloc(ctx, o, &W.delta, nql);
     rc |= dalloc(ctx, o, &W.bias, nql);
+    rc |= dalloc(ctx, o, &W.cqs, nql * A.d);
+    rc |= dalloc(ctx, o, &W.cqbase, nql);
+    rc |= dalloc(ctx, o, &W.hs, nql * A.Mp);
+    rc |= dalloc(ctx, o, &W.bnd, nql * nprobe);
     rc |= dalloc(ctx, o, &W.chosen, nql * nprobe);
     rc |= dalloc(ctx, o, &W.cscore, nql * nprobe);
     rc |= dalloc(ctx, o, &W.nchosen, nql);
@@ -178,7 +222,6 @@ int ensure_work(maivs_gpu_ctx* ctx, uint32_t nq, uint32_t nprobe, uint32_t k) {
     rc |= dalloc(ctx, o, &W.seed_cnt, nql);
     rc |= dalloc(ctx, o, &W.tau, nql);
     rc |= dalloc(ctx, o, &W.rest_end, nql);
-    rc |= dalloc(ctx, o, &W.qstat, nql * 3);
     rc |= dalloc(ctx, o, &W.cand_cnt, nql);
     rc |= dalloc(ctx, o, &W.cut, nql);
     rc |= dalloc(ctx, o, &W.ncand, nql);
@@ -207,6 +250,7 @@ int ensure_work(maivs_gpu_ctx* ctx, uint32_t nq, uint32_t nprobe, uint32_t k) {
 int ensure_cand(maivs_gpu_ctx* ctx, uint32_t cand_cap) {
     if (ctx->cand_nq >= ctx->cap_nq && cand_cap <= ctx->cap_cand && ctx->cand_nq) return 0;
     HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    drop_graph(ctx);
     free_all(ctx->cand_allocs);
     cand_cap = std::max(cand_cap, ctx->cap_cand);
     uint32_t fin_cap = ctx->cap_seed + cand_cap;
@@ -307,11 +351,23 @@ int launch_reset(maivs_gpu_ctx* ctx, uint32_t nq) {
     return 0;
 }
 
-int launch_route(maivs_gpu_ctx* ctx, const KParams& K, const float* d_q, uint32_t mode) {
+int launch_prep(maivs_gpu_ctx* ctx, const KParams& K, const float* d_q, bool reset) {
     const DevArena& A = ctx->A;
-    const size_t lds = route_lds(A, K.sort_cap);
-    DISPATCH_NW(A.W, hipLaunchKernelGGL(prep_route_kernel<NW>, dim3(K.nq), dim3(kRouteThreads), lds, ctx->stream, A,
-                                        ctx->Wk, K, d_q, mode));
+    const uint32_t blocks = (K.nq + kPrepWaves - 1) / kPrepWaves;
+    DISPATCH_EPL(A.P / 64, hipLaunchKernelGGL(prep_kernel<EPL>, dim3(blocks), dim3(kPrepWaves * kWave), ctx->lds_prep,
+                                              ctx->stream, A, ctx->Wk, K, d_q, reset ? 1u : 0u));
+    HIP_TRY(ctx, hipGetLastError());
+    return 0;
+}
+
+// Hamming distances of every query to every cell, then the per-query route.
+int launch_route(maivs_gpu_ctx* ctx, const KParams& K) {
+    const DevArena& A = ctx->A;
+    const dim3 hg((A.Mp + kHamThreads - 1) / kHamThreads, (K.nq + kHamQ - 1) / kHamQ);
+    DISPATCH_NW(A.W, hipLaunchKernelGGL(hamming_kernel<NW>, hg, dim3(kHamThreads), 0, ctx->stream, A, ctx->Wk, K));
+    const size_t lds = route_lds(A, K.sort_cap, K.nprobe);
+    DISPATCH_NW(A.W, hipLaunchKernelGGL(route_kernel<NW>, dim3(K.nq), dim3(kRouteThreads), lds, ctx->stream, A,
+                                        ctx->Wk, K));
     HIP_TRY(ctx, hipGetLastError());
     return 0;
 }
@@ -326,7 +382,7 @@ int launch_seed(maivs_gpu_ctx* ctx, const KParams& K) {
 
 // Inversion and the cell-major scan. The probe counts come from the seed kernel, or from
 // invert_count when a host fix changed a cut afterwards (recount = true, counts reset first).
-int launch_scan(maivs_gpu_ctx* ctx, const KParams& K, bool recount) {
+int launch_scan(maivs_gpu_ctx* ctx, const KParams& K, bool recount, bool events = false) {
     const DevArena& A = ctx->A;
     Work& W = ctx->Wk;
     if (recount) {
@@ -337,7 +393,7 @@ int launch_scan(maivs_gpu_ctx* ctx, const KParams& K, bool recount) {
     hipLaunchKernelGGL(invert_scan_kernel, dim3(1), dim3(1024), 0, ctx->stream, W, A.M);
     hipLaunchKernelGGL(invert_fill_kernel, dim3(K.nq), dim3(64), 0, ctx->stream, W, K);
     HIP_TRY(ctx, hipGetLastError());
-    HIP_TRY(ctx, hipEventRecord(ctx->ev[4], ctx->stream));
+    if (events) HIP_TRY(ctx, hipEventRecord(ctx->ev[4], ctx->stream));
     DISPATCH_NW(A.W, hipLaunchKernelGGL(cell_scan_kernel<NW>, dim3(A.M), dim3(kScanThreads), 0, ctx->stream, A,
                                         W, K));
     HIP_TRY(ctx, hipGetLastError());
@@ -397,17 +453,61 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
         return 0;
     }
     Ctl ctl{};
+    // the main pass; run eagerly it has an event between stages (the per-stage device times)
+    auto enqueue_main = [&](bool events) -> int {
+        int r;
+        auto mark = [&](int i) -> int {
+            if (events) HIP_TRY(ctx, hipEventRecord(ctx->ev[i], ctx->stream));
+            return 0;
+        };
+        if ((r = mark(0)) || (r = launch_prep(ctx, K, d_q, true)) || (r = mark(3))) return r;
+        if ((r = launch_route(ctx, K)) || (r = mark(1))) return r;
+        if ((r = launch_seed(ctx, K)) || (r = mark(2))) return r;
+        if ((r = launch_scan(ctx, K, false, events)) || (r = mark(5))) return r;
+        if ((r = launch_finish(ctx, K, d_q, d_slots, d_scores)) || (r = mark(6))) return r;
+        return 0;
+    };
+    bool staged = true;  // per-stage events recorded (eager pass)
+    // replayed as one captured graph when possible (one launch instead of a dozen); the capture
+    // is keyed by the parameters and every buffer address it bakes in
+    auto run_main = [&]() -> int {
+        if (ctx->use_graph) {
+            maivs_gpu_ctx::GraphKey key{};
+            key.K = K;
+            key.q = d_q;
+            key.slots = d_slots;
+            key.scores = d_scores;
+            key.gen = ctx->buf_gen;
+            if (!ctx->gexec || std::memcmp(&key, &ctx->gkey, sizeof key) != 0) {
+                if (ctx->gexec) (void)hipGraphExecDestroy(ctx->gexec);
+                ctx->gexec = nullptr;
+                hipGraph_t g = nullptr;
+                bool ok = hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeRelaxed) == hipSuccess;
+                int r = ok ? enqueue_main(false) : 0;
+                if (ok) ok = hipStreamEndCapture(ctx->stream, &g) == hipSuccess && r == 0 && g;
+                if (ok) ok = hipGraphInstantiate(&ctx->gexec, g, nullptr, nullptr, 0) == hipSuccess;
+                if (g) (void)hipGraphDestroy(g);
+                (void)hipGetLastError();
+                if (!ok) {  // capture is unavailable: run the stages eagerly from now on
+                    if (ctx->gexec) (void)hipGraphExecDestroy(ctx->gexec);
+                    ctx->gexec = nullptr;
+                    ctx->use_graph = false;
+                    return enqueue_main(true);
+                }
+                ctx->gkey = key;
+            }
+            // whole-pass time only: events recorded inside a graph do not time stages
+            staged = false;
+            HIP_TRY(ctx, hipEventRecord(ctx->ev[0], ctx->stream));
+            HIP_TRY(ctx, hipGraphLaunch(ctx->gexec, ctx->stream));
+            HIP_TRY(ctx, hipEventRecord(ctx->ev[6], ctx->stream));
+            return 0;
+        }
+        staged = true;
+        return enqueue_main(true);
+    };
     for (;;) {
-        HIP_TRY(ctx, hipEventRecord(ctx->ev[0], ctx->stream));
-        if ((rc = launch_reset(ctx, nq))) return rc;
-        if ((rc = launch_route(ctx, K, d_q, 0))) return rc;
-        HIP_TRY(ctx, hipEventRecord(ctx->ev[1], ctx->stream));
-        if ((rc = launch_seed(ctx, K))) return rc;
-        HIP_TRY(ctx, hipEventRecord(ctx->ev[2], ctx->stream));
-        if ((rc = launch_scan(ctx, K, false))) return rc;
-        HIP_TRY(ctx, hipEventRecord(ctx->ev[5], ctx->stream));
-        if ((rc = launch_finish(ctx, K, d_q, d_slots, d_scores))) return rc;
-        HIP_TRY(ctx, hipEventRecord(ctx->ev[6], ctx->stream));
+        if ((rc = run_main())) return rc;
         if ((rc = read_ctl(ctx, &ctl))) return rc;
         if (ctl.err_shortlist && K.sort_cap < ctx->max_sort_cap_route) {
             K.sort_cap = ctx->max_sort_cap_route;  // ties at the Hamming cut: retry with the largest sort
@@ -423,11 +523,15 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
     if (ctl.err_seed) return fail(ctx, MAIVS_ERR_UNSUPPORTED, "a seed set exceeds its on-chip capacity");
     float ms;
     if (hipEventElapsedTime(&ms, ctx->ev[0], ctx->ev[6]) == hipSuccess) S.ms_total = ms;
-    if (hipEventElapsedTime(&ms, ctx->ev[0], ctx->ev[1]) == hipSuccess) S.ms_prep = S.ms_route = ms;
-    if (hipEventElapsedTime(&ms, ctx->ev[1], ctx->ev[2]) == hipSuccess) S.ms_seed = ms;
-    if (hipEventElapsedTime(&ms, ctx->ev[2], ctx->ev[4]) == hipSuccess) S.ms_invert = ms;
-    if (hipEventElapsedTime(&ms, ctx->ev[4], ctx->ev[5]) == hipSuccess) S.ms_scan = ms;
-    if (hipEventElapsedTime(&ms, ctx->ev[5], ctx->ev[6]) == hipSuccess) S.ms_rerank = ms;
+    if (staged) {
+        if (hipEventElapsedTime(&ms, ctx->ev[0], ctx->ev[3]) == hipSuccess) S.ms_prep = ms;
+        if (hipEventElapsedTime(&ms, ctx->ev[3], ctx->ev[1]) == hipSuccess) S.ms_route = ms;
+        if (hipEventElapsedTime(&ms, ctx->ev[1], ctx->ev[2]) == hipSuccess) S.ms_seed = ms;
+        if (hipEventElapsedTime(&ms, ctx->ev[2], ctx->ev[4]) == hipSuccess) S.ms_invert = ms;
+        if (hipEventElapsedTime(&ms, ctx->ev[4], ctx->ev[5]) == hipSuccess) S.ms_scan = ms;
+        if (hipEventElapsedTime(&ms, ctx->ev[5], ctx->ev[6]) == hipSuccess) S.ms_rerank = ms;
+    }
+    (void)hipGetLastError();  // a failed timing query must not surface as a later call's error
 
     std::vector<float> cs;
     std::vector<uint32_t> ch;
@@ -504,6 +608,7 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
         if (ctl.max_cand > ctx->cap_cand) return fail(ctx, MAIVS_ERR_HIP, "candidate count changed between passes");
     }
     ctx->last_nq = nq;
+    ctx->last_K = K;
     return 0;
 }
 
@@ -521,6 +626,7 @@ int maivs_gpu_create(int device, maivs_gpu_ctx** out) {
     auto* ctx = new (std::nothrow) maivs_gpu_ctx();
     if (!ctx) return MAIVS_ERR_OOM;
     ctx->device = device;
+    if (const char* g = std::getenv("MAIVS_GPU_GRAPH")) ctx->use_graph = std::strcmp(g, "0") != 0;
     if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
         delete ctx;
         return MAIVS_ERR_HIP;
@@ -539,6 +645,7 @@ void maivs_gpu_destroy(maivs_gpu_ctx* ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->gexec) (void)hipGraphExecDestroy(ctx->gexec);
     free_all(ctx->work_allocs);
     free_all(ctx->cand_allocs);
     free_all(ctx->arena_allocs);
@@ -568,6 +675,7 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
         return fail(ctx, MAIVS_ERR_UNSUPPORTED, "dim %u / dim_pad %u", a->dim, a->dim_pad);
     if (a->n_words * 64 > a->dim_pad) return fail(ctx, MAIVS_ERR_ARG, "n_words exceeds dim_pad");
     HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    drop_graph(ctx);
     free_all(ctx->work_allocs);
     free_all(ctx->cand_allocs);
     free_all(ctx->arena_allocs);
@@ -587,6 +695,7 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
     A.npos = A.W * 16;
     A.maxk = 255 * A.npos;
     A.MW = (A.M + 31) / 32;
+    A.Mp = (A.M + 7) & ~7u;
     A.E = a->mem_off[A.M];
     A.fht_scale = 1.0f / std::sqrt(static_cast<float>(A.P));
     A.cf = make_chain(A.d, 4);
@@ -603,10 +712,21 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
     }
     A.n_live = n_live;
     A.max_cell_len = max_len;
-    if (A.M * 2 > 96 * 1024) return fail(ctx, MAIVS_ERR_UNSUPPORTED, "%u cells exceed the on-chip routing table", A.M);
-    const uint32_t seed_cap = kSeedCells * std::max<uint32_t>(max_len, 1);
-    if (seed_cap > 65536 || seed_lds(A, seed_cap) > kLdsBudget)
-        return fail(ctx, MAIVS_ERR_UNSUPPORTED, "a cell of %u members is too large for the on-chip seed set", max_len);
+    // a seed set holds the members of at most SEED_CELLS cells: bound it by the largest ones
+    uint32_t seed_cap = 0;
+    {
+        std::vector<uint32_t> lens(A.M);
+        for (uint32_t c = 0; c < A.M; ++c) lens[c] = a->mem_off[c + 1] - a->mem_off[c];
+        const uint32_t top = std::min<uint32_t>(kSeedCells, A.M);
+        std::partial_sort(lens.begin(), lens.begin() + top, lens.end(), std::greater<uint32_t>());
+        uint64_t sum = 0;
+        for (uint32_t i = 0; i < top; ++i) sum += lens[i];
+        seed_cap = static_cast<uint32_t>(std::min<uint64_t>(std::max<uint64_t>(sum, 1), 1ull << 20));
+    }
+    if (seed_cap > 65536 || seed_lds(A, seed_cap) + A.W * 256 > kLdsBudget)
+        return fail(ctx, MAIVS_ERR_UNSUPPORTED, "the %u largest cells (%u members) exceed the on-chip seed set", kSeedCells,
+                    seed_cap);
+    if (prep_lds(A) > kLdsBudget) return fail(ctx, MAIVS_ERR_UNSUPPORTED, "dim_pad %u too large for query prep", A.P);
 
     std::vector<void*> tmp;  // row-major staging, freed once the chain-major copies exist
     auto stage = [&](auto* src, size_t count, auto** out) -> int {
@@ -701,20 +821,25 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
         return rc;
     }
     ctx->h_r_bound.assign(a->r_bound, a->r_bound + A.M);
-    // LDS plan: route keeps hs[M] and the shortlist sort on chip (the sort size is per call)
-    ctx->lds_route_fixed = route_lds(A, 0);
-    size_t room = kLdsBudget - 4096 > ctx->lds_route_fixed ? (kLdsBudget - 4096 - ctx->lds_route_fixed) / 8 : 0;
+    // LDS plan: the route's shortlist sort size is per call (12 bytes per entry: key + weight)
+    const size_t route_fixed = route_lds(A, 0, 0);
+    size_t room = kLdsBudget - 4096 > route_fixed ? (kLdsBudget - 4096 - route_fixed) / 12 : 0;
     if (room < 1024) return fail(ctx, MAIVS_ERR_UNSUPPORTED, "routing tables do not fit in LDS");
     uint32_t sc = 1024;
     while (static_cast<size_t>(sc) * 2 <= room && sc < 16384) sc <<= 1;
     ctx->max_sort_cap_route = sc;
+    ctx->seed_cap = seed_cap;
+    ctx->lds_prep = prep_lds(A);
     ctx->lds_seed = seed_lds(A, seed_cap);
     ctx->lds_finish = finish_lds(A);
     hipFuncSetAttribute(reinterpret_cast<const void*>(finish_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                         static_cast<int>(ctx->lds_finish));
+    DISPATCH_EPL(A.P / 64, hipFuncSetAttribute(reinterpret_cast<const void*>(prep_kernel<EPL>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               static_cast<int>(ctx->lds_prep)));
     DISPATCH_NW(A.W, {
-        hipFuncSetAttribute(reinterpret_cast<const void*>(prep_route_kernel<NW>), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            static_cast<int>(route_lds(A, sc)));
+        hipFuncSetAttribute(reinterpret_cast<const void*>(route_kernel<NW>), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(route_lds(A, sc, sc)));
         hipFuncSetAttribute(reinterpret_cast<const void*>(seed_kernel<NW>), hipFuncAttributeMaxDynamicSharedMemorySize,
                             static_cast<int>(ctx->lds_seed));
     });
@@ -766,7 +891,7 @@ int maivs_gpu_query_prep(maivs_gpu_ctx* ctx, const float* q, uint32_t nq, uint64
     p.target_confidence = 1.0f;
     KParams K = make_params(ctx, nq, &p);
     HIP_TRY(ctx, hipMemcpyAsync(ctx->Wk.q, q, static_cast<size_t>(nq) * A.d * 4, hipMemcpyHostToDevice, ctx->stream));
-    if ((rc = launch_route(ctx, K, ctx->Wk.q, 2))) return rc;
+    if ((rc = launch_prep(ctx, K, ctx->Wk.q, false))) return rc;
     HIP_TRY(ctx, hipMemcpyAsync(out_bits, ctx->Wk.qbits, static_cast<size_t>(nq) * A.W * 8, hipMemcpyDeviceToHost, ctx->stream));
     HIP_TRY(ctx, hipMemcpyAsync(out_lut, ctx->Wk.lut, static_cast<size_t>(nq) * A.npos * 16, hipMemcpyDeviceToHost, ctx->stream));
     HIP_TRY(ctx, hipMemcpyAsync(out_delta, ctx->Wk.delta, nq * 4, hipMemcpyDeviceToHost, ctx->stream));
@@ -839,8 +964,8 @@ int maivs_gpu_route(maivs_gpu_ctx* ctx, const float* q, uint32_t nq, const maivs
         return 0;
     }
     HIP_TRY(ctx, hipMemcpyAsync(W.q, q, static_cast<size_t>(nq) * ctx->A.d * 4, hipMemcpyHostToDevice, ctx->stream));
-    if ((rc = launch_reset(ctx, nq))) return rc;
-    if ((rc = launch_route(ctx, K, W.q, 1))) return rc;
+    if ((rc = launch_prep(ctx, K, W.q, true))) return rc;
+    if ((rc = launch_route(ctx, K))) return rc;
     Ctl ctl{};
     HIP_TRY(ctx, hipMemcpyAsync(&ctl, W.ctl, sizeof(Ctl), hipMemcpyDeviceToHost, ctx->stream));
     HIP_TRY(ctx, hipMemcpyAsync(out_chosen, W.chosen, static_cast<size_t>(nq) * p->nprobe * 4, hipMemcpyDeviceToHost, ctx->stream));
@@ -870,7 +995,7 @@ int maivs_gpu_last_counters(maivs_gpu_ctx* ctx, maivs_gpu_stats* stats) {
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     stats->seed_blocks = stats->scan_blocks = stats->scan_pairs = stats->survivors = stats->rerank_rows = 0;
     if (ctx->last_nq == 0) return 0;
-    hipLaunchKernelGGL(counters_kernel, dim3(1), dim3(1024), 0, ctx->stream, ctx->Wk, ctx->last_nq);
+    hipLaunchKernelGGL(counters_kernel, dim3(1), dim3(1024), 0, ctx->stream, ctx->A, ctx->Wk, ctx->last_K);
     HIP_TRY(ctx, hipGetLastError());
     Ctl ctl{};
     int rc = read_ctl(ctx, &ctl);

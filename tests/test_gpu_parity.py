@@ -148,3 +148,34 @@ def test_binding_search_batch(quality50k, mix50k):
     oids = np.where(oslots == 0xFFFFFFFF, np.iinfo(np.uint64).max, ext[np.minimum(oslots, len(ext) - 1)])
     assert np.array_equal(np.array(ids, dtype=np.uint64).reshape(oids.shape), oids)
     assert np.array(scores, np.float32).tobytes() == oscores.tobytes()
+
+
+def test_graph_replays_match_eager(quality50k, mix50k, monkeypatch):
+    """The main pass replayed as one captured HIP graph returns the eager result on every replay,
+    with other eager GPU work and synchronisations between the replays, and after re-captures."""
+    _, queries, _ = mix50k
+    ix = quality50k
+    monkeypatch.setenv("MAIVS_GPU_GRAPH", "0")
+    eager = capi.Context(0)
+    monkeypatch.setenv("MAIVS_GPU_GRAPH", "1")
+    graph = capi.Context(0)
+    try:
+        eager.upload(ix._arena_desc())
+        graph.upload(ix._arena_desc())
+        for npb in (16, 48, 16):
+            p = _params(ix, 10, npb)
+            ref_s, ref_v = eager.search(queries, p)
+            for rep in range(4):
+                st = capi.GpuStats()
+                s, v = graph.search(queries, p, st)
+                assert np.array_equal(s, ref_s), (npb, rep)
+                assert v.tobytes() == ref_v.tobytes(), (npb, rep)
+                assert st.ms_total > 0
+                eager.search(queries[: 97 + rep], p)  # unrelated eager work between replays
+            # a different batch size re-captures; the original shape then re-captures again
+            s2, _ = graph.search(queries[:33], p)
+            e2, _ = eager.search(queries[:33], p)
+            assert np.array_equal(s2, e2)
+    finally:
+        eager.close()
+        graph.close()
