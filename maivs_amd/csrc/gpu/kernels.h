@@ -18,8 +18,7 @@ namespace maivs_dev {
 
 constexpr uint32_t kSeedCells = 8;       // SEED_CELLS, src/index.rs:2018
 constexpr uint32_t kPrepWaves = 4;       // queries per prep workgroup, one wave each
-constexpr uint32_t kHamThreads = 256;    // cells per Hamming tile
-constexpr uint32_t kHamQ = 16;           // queries per Hamming tile
+constexpr uint32_t kPrepReset = 1, kPrepHamming = 2;
 constexpr uint32_t kRouteThreads = 256;
 constexpr uint32_t kSeedThreads = 256;
 constexpr uint32_t kScanThreads = 256;
@@ -67,7 +66,8 @@ struct Ctl {
     uint32_t err_shortlist;   // a shortlist exceeded the sort capacity
     uint32_t max_shortlist;
     uint32_t err_seed;        // a seed set exceeded its on-chip capacity
-    uint32_t pad[2];
+    uint32_t bucket_overflow; // a cell's query bucket was full (the pass falls back to the counting sort)
+    uint32_t pad;
     unsigned long long seed_blocks, scan_blocks, scan_pairs, survivors, rerank_rows;
 };
 
@@ -101,6 +101,7 @@ struct Work {
     uint32_t* cell_off;    // M + 1
     uint32_t* cell_cur;    // M
     uint32_t* qof;         // nq x nprobe
+    uint32_t* qbuck;       // M x bucket_cap: the queries probing each cell (bucket mode)
     uint32_t* flag_route;  // nq
     uint32_t* flag_prune;  // nq
     Ctl* ctl;
@@ -108,7 +109,7 @@ struct Work {
 
 struct KParams {
     uint32_t nq, k, nprobe, want_c, target, adaptive, sort_cap, use_nucleus;
-    uint32_t seed_cap, cand_cap, fin_cap, key_cap;
+    uint32_t seed_cap, cand_cap, fin_cap, key_cap, bucket_cap;
     float tc, beta, at_margin, norm, prune_band, nucleus_band;
 };
 
@@ -489,52 +490,92 @@ __global__ void reset_kernel(Work Wk, uint32_t M, uint32_t nq) {
     for (uint32_t j = i; j < nq; j += stride) Wk.cand_cnt[j] = 0;
 }
 
-// ---------------------------------------------------------------- prep (one wave per query)
+// ---------------------------------------------------------------- prep + Hamming (one wave per query)
 
-// Rotation, sign code, FastScan table and the two sequential sums of one query per wave
+// Rotation, sign code, FastScan table and the two sequential sums of one query, by one wave
 // (src/quantize.rs:57-67,152-163,279-313; src/index.rs:1934-1942). Lane l holds rotated
 // coordinates [l*EPL, (l+1)*EPL) in registers: FWHT levels below EPL run inside the lane, the
 // others across lanes (partner l ^ (h / EPL)), in the reference's ascending level order, so every
-// butterfly sees the reference's operands. With `reset` set the grid also clears the per-call
-// counters (control block, probe counts, candidate counts).
-// LDS per wave: x[P] | mins[npos4] | cqp[d4].
+// butterfly sees the reference's operands. `xs` is the wave's LDS region (x[P] | mins[npos4] |
+// cqp[d4]); `qw` receives the code words.
 template <int EPL>
-__global__ void __launch_bounds__(kPrepWaves * kWave)
-prep_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries, uint32_t reset) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    if (reset) {
-        const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x, stride = gridDim.x * blockDim.x;
-        if (i < sizeof(Ctl) / 4) reinterpret_cast<uint32_t*>(Wk.ctl)[i] = 0;
-        for (uint32_t j = i; j <= A.M; j += stride) Wk.cell_cnt[j] = 0;
-        for (uint32_t j = i; j < K.nq; j += stride) Wk.cand_cnt[j] = 0;
-    }
-    const uint32_t lane = lane_id(), wv = threadIdx.x / kWave;
-    const uint32_t qi = blockIdx.x * kPrepWaves + wv;
-    if (qi >= K.nq) return;
+__device__ __forceinline__ void prep_wave(const DevArena& A, const Work& Wk, const float* __restrict__ queries,
+                                          uint32_t qi, uint32_t lane, float* xs, uint64_t* qw) {
     const uint32_t P = A.P, d = A.d, npos = A.npos;
-    const uint32_t d4 = (d + 3) & ~3u, np4 = (npos + 3) & ~3u;
-    float* xs = reinterpret_cast<float*>(smem) + wv * (P + np4 + d4);
+    const uint32_t np4 = (npos + 3) & ~3u;
     float* mins = xs + P;
     float* cqp = mins + np4;
     const float* q = queries + static_cast<uint64_t>(qi) * d;
     const bool sq8 = A.cent_sq8 != nullptr;
     const uint32_t base = lane * EPL;
     float x[EPL], sg[2][EPL];
+    // whole float4s where the lane's coordinates are all inside the query (the common case)
+    const bool vec = EPL >= 4 && (d & 3u) == 0 && base + EPL <= d;
+    if (vec) {
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-        const uint32_t i = base + e;
-        x[e] = i < d ? q[i] : 0.0f;
-        sg[0][e] = A.rot_signs[i];
-        sg[1][e] = A.rot_signs[P + i];
+        for (int e = 0; e < EPL; e += 4) {
+            const float4 v = *reinterpret_cast<const float4*>(q + base + e);
+            x[e] = v.x;
+            x[e + 1] = v.y;
+            x[e + 2] = v.z;
+            x[e + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) x[e] = base + e < d ? q[base + e] : 0.0f;
     }
+    // signs, steps and mins are 16-byte aligned device arrays; base is a multiple of EPL
+    auto ld4 = [](const float* p, float* o) {
+        const float4 v = *reinterpret_cast<const float4*>(p);
+        o[0] = v.x;
+        o[1] = v.y;
+        o[2] = v.z;
+        o[3] = v.w;
+    };
+    if constexpr (EPL >= 4) {
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-        const uint32_t i = base + e;
-        if (i < d) {
-            // rescore operands: cqs = q * step and q * min, each rounded once (src/index.rs:1937-1941)
-            const float v = x[e];
-            Wk.cqs[static_cast<uint64_t>(qi) * d + i] = sq8 ? v * A.csq_step[i] : v;
-            cqp[i] = sq8 ? v * A.csq_min[i] : 0.0f;
+        for (int e = 0; e < EPL; e += 4) {
+            ld4(A.rot_signs + base + e, &sg[0][e]);
+            ld4(A.rot_signs + P + base + e, &sg[1][e]);
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+            sg[0][e] = A.rot_signs[base + e];
+            sg[1][e] = A.rot_signs[P + base + e];
+        }
+    }
+    float* cqs_out = Wk.cqs + static_cast<uint64_t>(qi) * d;
+    if (vec) {
+        // rescore operands: cqs = q * step and q * min, each rounded once (src/index.rs:1937-1941)
+#pragma unroll
+        for (int e = 0; e < EPL; e += 4) {
+            float st[4] = {1.f, 1.f, 1.f, 1.f}, mn[4] = {0.f, 0.f, 0.f, 0.f};
+            if (sq8) {
+                ld4(A.csq_step + base + e, st);
+                ld4(A.csq_min + base + e, mn);
+            }
+            float4 o, m;
+            o.x = sq8 ? x[e] * st[0] : x[e];
+            o.y = sq8 ? x[e + 1] * st[1] : x[e + 1];
+            o.z = sq8 ? x[e + 2] * st[2] : x[e + 2];
+            o.w = sq8 ? x[e + 3] * st[3] : x[e + 3];
+            m.x = sq8 ? x[e] * mn[0] : 0.0f;
+            m.y = sq8 ? x[e + 1] * mn[1] : 0.0f;
+            m.z = sq8 ? x[e + 2] * mn[2] : 0.0f;
+            m.w = sq8 ? x[e + 3] * mn[3] : 0.0f;
+            *reinterpret_cast<float4*>(cqs_out + base + e) = o;
+            *reinterpret_cast<float4*>(cqp + base + e) = m;
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+            const uint32_t i = base + e;
+            if (i < d) {
+                const float v = x[e];
+                cqs_out[i] = sq8 ? v * A.csq_step[i] : v;
+                cqp[i] = sq8 ? v * A.csq_min[i] : 0.0f;
+            }
         }
     }
     for (int r = 0; r < 2; ++r) {
@@ -575,7 +616,10 @@ prep_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries, u
             const uint64_t m = __ballot(xs[64 * w + lane] < 0.0f);
             if (lane == w) mine = m;
         }
-        if (lane < A.W) Wk.qbits[static_cast<uint64_t>(qi) * A.W + lane] = mine;
+        if (lane < A.W) {
+            Wk.qbits[static_cast<uint64_t>(qi) * A.W + lane] = mine;
+            qw[lane] = mine;
+        }
     }
     // ---- FastScan table: position j from x[4j .. 4j+3], 16 sums accumulated from 0 in order t = 0..3
     auto raw_of = [&](const float4& v, int e) {
@@ -619,24 +663,33 @@ prep_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries, u
     // ---- sequential sums in index order: lane 0 the table bias (Rust's f32 Sum folds from -0.0),
     // lane 1 the rescore base sum(q * csq_min) from 0.0
     if (lane < 2) {
-        // both arrays are padded to a multiple of 4 in LDS, so whole float4s are read 16 at a
-        // time ahead of the dependent adds
+        // whole 16-element chunks with the next chunk's LDS reads in flight, then the tail
         const uint32_t n = lane == 0 ? npos : (sq8 ? d : 0u);
-        const float4* src = reinterpret_cast<const float4*>(lane == 0 ? mins : cqp);
+        const float* src = lane == 0 ? mins : cqp;
+        const float4* src4 = reinterpret_cast<const float4*>(src);
         float s = lane == 0 ? -0.0f : 0.0f;
-        for (uint32_t i = 0; i < n; i += 16) {
-            float4 v[4];
+        const uint32_t nfull = n / 16;
+        float4 cur[4], nxt[4];
+        if (nfull > 0) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) v[j] = i + 4 * j < n ? src[i / 4 + j] : make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int j = 0; j < 4; ++j) cur[j] = src4[j];
+        }
+        for (uint32_t c = 0; c < nfull; ++c) {
+            if (c + 1 < nfull) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) nxt[j] = src4[4 * (c + 1) + j];
+            }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const uint32_t b = i + 4 * j;
-                if (b < n) s += v[j].x;
-                if (b + 1 < n) s += v[j].y;
-                if (b + 2 < n) s += v[j].z;
-                if (b + 3 < n) s += v[j].w;
+                s += cur[j].x;
+                s += cur[j].y;
+                s += cur[j].z;
+                s += cur[j].w;
             }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) cur[j] = nxt[j];
         }
+        for (uint32_t i = nfull * 16; i < n; ++i) s += src[i];
         if (lane == 0) {
             Wk.bias[qi] = s;
             Wk.delta[qi] = delta;
@@ -646,39 +699,70 @@ prep_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries, u
     }
 }
 
-// ---------------------------------------------------------------- Hamming (query tile x cell tile)
-
-// h[q][c] = popcount(qbits[q] ^ cent_bits[c]) for every query and cell (src/index.rs:1896-1915),
-// 0xFFFF for dead cells and the padding up to Mp. Each thread holds one centroid code in
-// registers and runs it against kHamQ query codes broadcast from LDS.
+// The block's nqb query codes (LDS) against every cell code: h = popcount(q ^ c) per word
+// (src/index.rs:1896-1915), 0xFFFF for dead cells and the padding up to Mp. Each thread takes
+// cells tid, tid + nt, ... four at a time so that four codes are in flight together.
 template <int NW>
-__global__ void __launch_bounds__(kHamThreads)
-hamming_kernel(DevArena A, Work Wk, KParams K) {
-    __shared__ uint64_t qb[kHamQ * NW];
-    const uint32_t q0 = blockIdx.y * kHamQ;
-    const uint32_t nqt = min(kHamQ, K.nq - q0);
-    for (uint32_t i = threadIdx.x; i < nqt * NW; i += blockDim.x) qb[i] = Wk.qbits[static_cast<uint64_t>(q0) * NW + i];
-    const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
-    const uint32_t Mp = A.Mp;
-    uint64_t cw[NW];
-    bool live = false;
-    if (c < A.M) {
+__device__ __forceinline__ void hamming_tile(const DevArena& A, const Work& Wk, const uint64_t* qb, uint32_t q0,
+                                             uint32_t nqb) {
+    const uint32_t Mp = A.Mp, nt = blockDim.x;
+    uint16_t* out = Wk.hs + static_cast<uint64_t>(q0) * Mp;
+    for (uint32_t c0 = threadIdx.x; c0 < Mp; c0 += 4 * nt) {
+        uint64_t cw[4][NW];
+        bool live[4];
 #pragma unroll
-        for (int w = 0; w < NW; ++w) cw[w] = A.cent_bits[static_cast<uint64_t>(c) * NW + w];
-        live = A.live[c] != 0;
-    }
-    __syncthreads();
-    if (c >= Mp) return;
-    uint16_t* out = Wk.hs + static_cast<uint64_t>(q0) * Mp + c;
-    for (uint32_t j = 0; j < nqt; ++j) {
-        uint32_t h = 0;
-        if (live) {
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t c = c0 + u * nt;
+            live[u] = c < A.M && A.live[c] != 0;
 #pragma unroll
-            for (int w = 0; w < NW; ++w) h += __popcll(qb[j * NW + w] ^ cw[w]);
+            for (int w = 0; w < NW; ++w) cw[u][w] = c < A.M ? A.cent_bits[static_cast<uint64_t>(c) * NW + w] : 0ull;
         }
-        out[static_cast<uint64_t>(j) * Mp] = live ? static_cast<uint16_t>(h) : static_cast<uint16_t>(0xFFFFu);
+        for (uint32_t j = 0; j < nqb; ++j) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t c = c0 + u * nt;
+                uint32_t h = 0;
+#pragma unroll
+                for (int w = 0; w < NW; ++w) h += __popcll(qb[j * 16 + w] ^ cw[u][w]);
+                if (c < Mp) out[static_cast<uint64_t>(j) * Mp + c] = live[u] ? static_cast<uint16_t>(h) : static_cast<uint16_t>(0xFFFFu);
+            }
+        }
     }
 }
+
+// kPrepWaves queries per workgroup, one wave each (prep_wave). Flags: kPrepReset also clears the
+// per-call counters (control block, probe counts, candidate counts); kPrepHamming then runs the
+// block's queries against every cell code (hamming_tile).
+// LDS: codes[kPrepWaves * 16] u64 | per wave x[P] | mins[npos4] | cqp[d4].
+template <int EPL>
+__global__ void __launch_bounds__(kPrepWaves * kWave)
+prep_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries, uint32_t flags) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    if (flags & kPrepReset) {
+        const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x, stride = gridDim.x * blockDim.x;
+        if (i < sizeof(Ctl) / 4) reinterpret_cast<uint32_t*>(Wk.ctl)[i] = 0;
+        for (uint32_t j = i; j <= A.M; j += stride) Wk.cell_cnt[j] = 0;
+        for (uint32_t j = i; j < K.nq; j += stride) Wk.cand_cnt[j] = 0;
+    }
+    const uint32_t lane = lane_id(), wv = threadIdx.x / kWave;
+    const uint32_t qi = blockIdx.x * kPrepWaves + wv;
+    uint64_t* qbl = reinterpret_cast<uint64_t*>(smem);
+    if (qi < K.nq) prep_wave<EPL>(A, Wk, queries, qi, lane, reinterpret_cast<float*>(qbl + kPrepWaves * 16) +
+                                  wv * (A.P + ((A.npos + 3) & ~3u) + ((A.d + 3) & ~3u)), qbl + wv * 16);
+    if (flags & kPrepHamming) {
+        __syncthreads();
+        const uint32_t q0 = blockIdx.x * kPrepWaves;
+        const uint32_t nqb = min(kPrepWaves, K.nq - q0);
+        switch (A.W) {
+            case 1: hamming_tile<1>(A, Wk, qbl, q0, nqb); break;
+            case 2: hamming_tile<2>(A, Wk, qbl, q0, nqb); break;
+            case 4: hamming_tile<4>(A, Wk, qbl, q0, nqb); break;
+            case 8: hamming_tile<8>(A, Wk, qbl, q0, nqb); break;
+            default: hamming_tile<16>(A, Wk, qbl, q0, nqb); break;
+        }
+    }
+}
+
 
 // ---------------------------------------------------------------- route (one WG per query)
 
@@ -689,11 +773,8 @@ hamming_kernel(DevArena A, Work Wk, KParams K) {
 // depend on routing alone.
 // LDS: cqs[d4] | ex[np4] | keys[sort_cap] u64 | hist[nbins4] | scratch[16].
 template <int NW>
-__global__ void __launch_bounds__(kRouteThreads)
-route_kernel(DevArena A, Work Wk, KParams K) {
+__device__ __forceinline__ void route_phase(const DevArena& A, const Work& Wk, const KParams& K, uint32_t qi) {
     extern __shared__ __align__(16) uint8_t smem[];
-    const uint32_t qi = blockIdx.x;
-    if (qi >= K.nq) return;
     const uint32_t tid = threadIdx.x, nt = blockDim.x;
     const uint32_t d = A.d, M = A.M, Mp = A.Mp;
     const uint32_t d4 = (d + 3) & ~3u, np4 = min((K.nprobe + 3) & ~3u, K.sort_cap);
@@ -842,6 +923,12 @@ route_kernel(DevArena A, Work Wk, KParams K) {
     if (tid == 0) Wk.nchosen[qi] = nch;
 }
 
+template <int NW>
+__global__ void __launch_bounds__(kRouteThreads)
+route_kernel(DevArena A, Work Wk, KParams K) {
+    if (blockIdx.x < K.nq) route_phase<NW>(A, Wk, K, blockIdx.x);
+}
+
 // ---------------------------------------------------------------- seed (one WG per query)
 
 // One member's nibble sums against a single query's FastScan table at LDS offset 0: the
@@ -873,11 +960,8 @@ __device__ __forceinline__ uint32_t lut_sum1(const Code<NW>& c, const uint8_t* _
 // LDS: static table[TB] at offset 0; dynamic probed[MW4] | coarse[256] | fine[256] | misc[32] |
 // sbuf[seed_cap4] (d << 16 | item, item < 65536).
 template <int NW>
-__global__ void __launch_bounds__(kSeedThreads, 4)
-seed_kernel(DevArena A, Work Wk, KParams K) {
+__device__ __forceinline__ void seed_phase(const DevArena& A, const Work& Wk, const KParams& K, uint32_t qi) {
     extern __shared__ __align__(16) uint8_t smem[];
-    const uint32_t qi = blockIdx.x;
-    if (qi >= K.nq) return;
     const uint32_t tid = threadIdx.x, nt = blockDim.x, lane = lane_id();
     constexpr uint32_t TB = NW * 256;
     constexpr uint32_t kOff = 0, kCell = 9, kE0 = 17, kCnt = 25, kKeep = 26, kTau = 27, kRe = 28, kHb = 29, kBelow = 30;
@@ -1086,13 +1170,40 @@ seed_kernel(DevArena A, Work Wk, KParams K) {
         __syncthreads();
         rest_end = misc[kRe];
     }
-    // ---- probe counts for the inversion
-    for (uint32_t i = ns + tid; i < rest_end; i += nt) atomicAdd(&Wk.cell_cnt[chosen[i]], 1u);
+    // ---- the query into each rest cell's bucket (bucket mode), else probe counts for the
+    // counting-sort inversion
+    for (uint32_t i = ns + tid; i < rest_end; i += nt) {
+        const uint32_t c = chosen[i];
+        const uint32_t slot = atomicAdd(&Wk.cell_cnt[c], 1u);
+        if (K.bucket_cap) {
+            if (slot < K.bucket_cap)
+                Wk.qbuck[static_cast<uint64_t>(c) * K.bucket_cap + slot] = qi;
+            else
+                atomicOr(&Wk.ctl->bucket_overflow, 1u);
+        }
+    }
     if (tid == 0) {
         Wk.seed_cnt[qi] = misc[kKeep];
         Wk.tau[qi] = tau;
         Wk.rest_end[qi] = rest_end;
     }
+}
+
+template <int NW>
+__global__ void __launch_bounds__(kSeedThreads, 4)
+seed_kernel(DevArena A, Work Wk, KParams K) {
+    if (blockIdx.x < K.nq) seed_phase<NW>(A, Wk, K, blockIdx.x);
+}
+
+// Route and seed of one query in one workgroup (the seed reads the probe list the route just
+// wrote; LDS is reused: the route's regions are dead once the list is written).
+template <int NW>
+__global__ void __launch_bounds__(kSeedThreads)
+route_seed_kernel(DevArena A, Work Wk, KParams K) {
+    if (blockIdx.x >= K.nq) return;
+    route_phase<NW>(A, Wk, K, blockIdx.x);
+    __syncthreads();
+    seed_phase<NW>(A, Wk, K, blockIdx.x);
 }
 
 // ---------------------------------------------------------------- inversion: cell -> queries
@@ -1154,7 +1265,17 @@ cell_scan_kernel(DevArena A, Work Wk, KParams K) {
     __shared__ uint32_t s_q[kG], s_t[kG];
     const uint32_t c = blockIdx.x;
     if (c >= A.M) return;
-    const uint32_t q0 = Wk.cell_off[c], nqc = Wk.cell_off[c + 1] - q0;
+    // the queries probing c: its bucket, or its range of the counting-sort inversion
+    uint32_t nqc;
+    const uint32_t* ql;
+    if (K.bucket_cap) {
+        nqc = min(Wk.cell_cnt[c], K.bucket_cap);
+        ql = Wk.qbuck + static_cast<uint64_t>(c) * K.bucket_cap;
+    } else {
+        const uint32_t q0 = Wk.cell_off[c];
+        nqc = Wk.cell_off[c + 1] - q0;
+        ql = Wk.qof + q0;
+    }
     const uint32_t e0 = A.mem_off[c], len = A.mem_off[c + 1] - e0;
     if (nqc == 0 || len == 0) return;
     const uint32_t tid = threadIdx.x, nt = blockDim.x;
@@ -1170,7 +1291,7 @@ cell_scan_kernel(DevArena A, Work Wk, KParams K) {
             const uint32_t ng = min(kG, nqc - g0);
             __syncthreads();
             if (tid < kG) {
-                uint32_t qq = tid < ng ? Wk.qof[q0 + g0 + tid] : kNone;
+                uint32_t qq = tid < ng ? ql[g0 + tid] : kNone;
                 s_q[tid] = qq;
                 s_t[tid] = qq != kNone ? Wk.tau[qq] : 0u;
             }
@@ -1179,7 +1300,7 @@ cell_scan_kernel(DevArena A, Work Wk, KParams K) {
                 uint32_t v[kG];
 #pragma unroll
                 for (uint32_t g = 0; g < kG; ++g) {
-                    uint32_t qq = g < ng ? Wk.qof[q0 + g0 + g] : kNone;
+                    uint32_t qq = g < ng ? ql[g0 + g] : kNone;
                     v[g] = qq != kNone ? reinterpret_cast<const uint32_t*>(Wk.lut + static_cast<uint64_t>(qq) * TB)[x4] : 0u;
                 }
                 uint32_t lo01 = __builtin_amdgcn_perm(v[1], v[0], 0x05010400u);

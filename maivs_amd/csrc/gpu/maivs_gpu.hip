@@ -59,7 +59,7 @@ struct maivs_gpu_ctx {
     Work Wk{};
     std::vector<void*> work_allocs;   // per-query / per-cell buffers, sized by (nq, nprobe, k)
     std::vector<void*> cand_allocs;   // candidate buffers, sized by (nq, cand_cap); grow on overflow
-    uint32_t cap_nq = 0, cap_nprobe = 0, cap_k = 0, cap_cand = 0, cap_seed = 0, cap_fin = 0, cap_key = 0;
+    uint32_t cap_nq = 0, cap_nprobe = 0, cap_k = 0, cap_cand = 0, cap_seed = 0, cap_fin = 0, cap_key = 0, cap_bucket = 0;
     uint32_t cand_nq = 0;
     uint32_t max_sort_cap_route = 0;  // largest shortlist sort the route kernel's LDS can hold
     uint32_t seed_cap = 0;            // sum of the SEED_CELLS largest cells: bound of one seed set
@@ -155,9 +155,9 @@ bool supported_nw(uint32_t w) { return w == 1 || w == 2 || w == 4 || w == 8 || w
         default: { constexpr int NW = 16; __VA_ARGS__; break; } \
     }
 
-// LDS of prep: per wave x[P] | mins[npos4] | cqp[d4]
+// LDS of prep: codes[kPrepWaves * 16] u64 | per wave x[P] | mins[npos4] | cqp[d4]
 size_t prep_lds(const DevArena& A) {
-    return static_cast<size_t>(kPrepWaves) * (A.P + ((A.npos + 3) & ~3u) + ((A.d + 3) & ~3u)) * 4;
+    return kPrepWaves * 16 * 8 + static_cast<size_t>(kPrepWaves) * (A.P + ((A.npos + 3) & ~3u) + ((A.d + 3) & ~3u)) * 4;
 }
 
 // LDS of route: cqs[d4] | ex[np4] | keys[sort_cap] u64 | hist[nbins4] | scratch[16]
@@ -189,10 +189,23 @@ Chain make_chain(uint32_t d, uint32_t vec) {
 
 // Per-query and per-cell work buffers for (nq, nprobe, k); grows only. Candidate buffers are
 // separate (ensure_cand) so that growing them never moves the staged queries or outputs.
+// Per-cell query buckets: room for 4x the mean number of queries per live cell in the rest scan,
+// a power of two in [32, 4096]; a fuller cell sends the pass to the counting-sort inversion.
+uint32_t bucket_cap_for(const DevArena& A, uint32_t nq, uint32_t nprobe) {
+    const uint64_t pairs = static_cast<uint64_t>(nq) * (nprobe > kSeedCells ? nprobe - kSeedCells : 0u);
+    const uint64_t mean = pairs / std::max<uint32_t>(A.n_live, 1u);
+    uint32_t cap = 32;
+    while (cap < 4 * mean + 32 && cap < 4096) cap <<= 1;
+    return cap;
+}
+
 int ensure_work(maivs_gpu_ctx* ctx, uint32_t nq, uint32_t nprobe, uint32_t k) {
     const DevArena& A = ctx->A;
     const uint32_t seed_cap = ctx->seed_cap;
-    if (nq <= ctx->cap_nq && nprobe <= ctx->cap_nprobe && k <= ctx->cap_k && seed_cap <= ctx->cap_seed) return 0;
+    const uint32_t bcap = bucket_cap_for(A, nq, nprobe);
+    if (nq <= ctx->cap_nq && nprobe <= ctx->cap_nprobe && k <= ctx->cap_k && seed_cap <= ctx->cap_seed &&
+        bcap <= ctx->cap_bucket)
+        return 0;
     HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
     drop_graph(ctx);
     free_all(ctx->work_allocs);
@@ -231,18 +244,21 @@ int ensure_work(maivs_gpu_ctx* ctx, uint32_t nq, uint32_t nprobe, uint32_t k) {
     rc |= dalloc(ctx, o, &W.cell_off, static_cast<uint64_t>(A.M) + 1);
     rc |= dalloc(ctx, o, &W.cell_cur, static_cast<uint64_t>(A.M) + 1);
     rc |= dalloc(ctx, o, &W.qof, nql * nprobe);
+    const uint32_t bcap_all = std::max(bcap, ctx->cap_bucket);
+    rc |= dalloc(ctx, o, &W.qbuck, static_cast<uint64_t>(A.M) * bcap_all);
     rc |= dalloc(ctx, o, &W.flag_route, nql);
     rc |= dalloc(ctx, o, &W.flag_prune, nql);
     rc |= dalloc(ctx, o, &W.ctl, 1);
     if (rc) {
         free_all(ctx->work_allocs);
-        ctx->cap_nq = ctx->cap_nprobe = ctx->cap_k = ctx->cap_seed = 0;
+        ctx->cap_nq = ctx->cap_nprobe = ctx->cap_k = ctx->cap_seed = ctx->cap_bucket = 0;
         return rc;
     }
     ctx->cap_nq = nq;
     ctx->cap_nprobe = nprobe;
     ctx->cap_k = k;
     ctx->cap_seed = seed_cap;
+    ctx->cap_bucket = bcap_all;
     return 0;
 }
 
@@ -297,6 +313,7 @@ KParams make_params(maivs_gpu_ctx* ctx, uint32_t nq, const maivs_search_params* 
     K.sort_cap = std::min(sc, ctx->max_sort_cap_route);
     K.use_nucleus = p->target_confidence < 1.0f;
     K.seed_cap = ctx->cap_seed;
+    K.bucket_cap = ctx->cap_bucket;
     K.cand_cap = ctx->cap_cand;
     K.fin_cap = ctx->cap_fin;
     K.key_cap = ctx->cap_key;
@@ -351,22 +368,30 @@ int launch_reset(maivs_gpu_ctx* ctx, uint32_t nq) {
     return 0;
 }
 
-int launch_prep(maivs_gpu_ctx* ctx, const KParams& K, const float* d_q, bool reset) {
+int launch_prep(maivs_gpu_ctx* ctx, const KParams& K, const float* d_q, uint32_t flags) {
     const DevArena& A = ctx->A;
     const uint32_t blocks = (K.nq + kPrepWaves - 1) / kPrepWaves;
     DISPATCH_EPL(A.P / 64, hipLaunchKernelGGL(prep_kernel<EPL>, dim3(blocks), dim3(kPrepWaves * kWave), ctx->lds_prep,
-                                              ctx->stream, A, ctx->Wk, K, d_q, reset ? 1u : 0u));
+                                              ctx->stream, A, ctx->Wk, K, d_q, flags));
     HIP_TRY(ctx, hipGetLastError());
     return 0;
 }
 
-// Hamming distances of every query to every cell, then the per-query route.
+// The per-query route alone (needs the Hamming rows of prep).
 int launch_route(maivs_gpu_ctx* ctx, const KParams& K) {
     const DevArena& A = ctx->A;
-    const dim3 hg((A.Mp + kHamThreads - 1) / kHamThreads, (K.nq + kHamQ - 1) / kHamQ);
-    DISPATCH_NW(A.W, hipLaunchKernelGGL(hamming_kernel<NW>, hg, dim3(kHamThreads), 0, ctx->stream, A, ctx->Wk, K));
     const size_t lds = route_lds(A, K.sort_cap, K.nprobe);
     DISPATCH_NW(A.W, hipLaunchKernelGGL(route_kernel<NW>, dim3(K.nq), dim3(kRouteThreads), lds, ctx->stream, A,
+                                        ctx->Wk, K));
+    HIP_TRY(ctx, hipGetLastError());
+    return 0;
+}
+
+// Route and seed fused, one workgroup per query.
+int launch_route_seed(maivs_gpu_ctx* ctx, const KParams& K) {
+    const DevArena& A = ctx->A;
+    const size_t lds = std::max(route_lds(A, K.sort_cap, K.nprobe), ctx->lds_seed);
+    DISPATCH_NW(A.W, hipLaunchKernelGGL(route_seed_kernel<NW>, dim3(K.nq), dim3(kSeedThreads), lds, ctx->stream, A,
                                         ctx->Wk, K));
     HIP_TRY(ctx, hipGetLastError());
     return 0;
@@ -380,24 +405,34 @@ int launch_seed(maivs_gpu_ctx* ctx, const KParams& K) {
     return 0;
 }
 
-// Inversion and the cell-major scan. The probe counts come from the seed kernel, or from
-// invert_count when a host fix changed a cut afterwards (recount = true, counts reset first).
+// The cell-major scan. In bucket mode (K.bucket_cap > 0) the seed stage already filed every
+// query into its cells' buckets. Otherwise the counting-sort inversion runs first, from the seed
+// stage's probe counts, or from invert_count when the cuts changed afterwards (recount = true,
+// counters reset first).
 int launch_scan(maivs_gpu_ctx* ctx, const KParams& K, bool recount, bool events = false) {
     const DevArena& A = ctx->A;
     Work& W = ctx->Wk;
-    if (recount) {
-        int rc = launch_reset(ctx, K.nq);
-        if (rc) return rc;
-        hipLaunchKernelGGL(invert_count_kernel, dim3(K.nq), dim3(64), 0, ctx->stream, W, K);
+    if (!K.bucket_cap) {
+        if (recount) {
+            int rc = launch_reset(ctx, K.nq);
+            if (rc) return rc;
+            hipLaunchKernelGGL(invert_count_kernel, dim3(K.nq), dim3(64), 0, ctx->stream, W, K);
+        }
+        hipLaunchKernelGGL(invert_scan_kernel, dim3(1), dim3(1024), 0, ctx->stream, W, A.M);
+        hipLaunchKernelGGL(invert_fill_kernel, dim3(K.nq), dim3(64), 0, ctx->stream, W, K);
+        HIP_TRY(ctx, hipGetLastError());
     }
-    hipLaunchKernelGGL(invert_scan_kernel, dim3(1), dim3(1024), 0, ctx->stream, W, A.M);
-    hipLaunchKernelGGL(invert_fill_kernel, dim3(K.nq), dim3(64), 0, ctx->stream, W, K);
-    HIP_TRY(ctx, hipGetLastError());
     if (events) HIP_TRY(ctx, hipEventRecord(ctx->ev[4], ctx->stream));
     DISPATCH_NW(A.W, hipLaunchKernelGGL(cell_scan_kernel<NW>, dim3(A.M), dim3(kScanThreads), 0, ctx->stream, A,
                                         W, K));
     HIP_TRY(ctx, hipGetLastError());
     return 0;
+}
+
+// The same parameters with the counting-sort inversion instead of the buckets (every re-run).
+KParams csr(KParams K) {
+    K.bucket_cap = 0;
+    return K;
 }
 
 int launch_finish(maivs_gpu_ctx* ctx, const KParams& K, const float* d_q, uint32_t* d_slots, float* d_scores) {
@@ -460,9 +495,8 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
             if (events) HIP_TRY(ctx, hipEventRecord(ctx->ev[i], ctx->stream));
             return 0;
         };
-        if ((r = mark(0)) || (r = launch_prep(ctx, K, d_q, true)) || (r = mark(3))) return r;
-        if ((r = launch_route(ctx, K)) || (r = mark(1))) return r;
-        if ((r = launch_seed(ctx, K)) || (r = mark(2))) return r;
+        if ((r = mark(0)) || (r = launch_prep(ctx, K, d_q, kPrepReset | kPrepHamming)) || (r = mark(3))) return r;
+        if ((r = launch_route_seed(ctx, K)) || (r = mark(2))) return r;
         if ((r = launch_scan(ctx, K, false, events)) || (r = mark(5))) return r;
         if ((r = launch_finish(ctx, K, d_q, d_slots, d_scores)) || (r = mark(6))) return r;
         return 0;
@@ -478,7 +512,10 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
             key.slots = d_slots;
             key.scores = d_scores;
             key.gen = ctx->buf_gen;
-            if (!ctx->gexec || std::memcmp(&key, &ctx->gkey, sizeof key) != 0) {
+            const auto& g0 = ctx->gkey;
+            const bool same = ctx->gexec && std::memcmp(&key.K, &g0.K, sizeof(KParams)) == 0 && key.q == g0.q &&
+                              key.slots == g0.slots && key.scores == g0.scores && key.gen == g0.gen;
+            if (!same) {
                 if (ctx->gexec) (void)hipGraphExecDestroy(ctx->gexec);
                 ctx->gexec = nullptr;
                 hipGraph_t g = nullptr;
@@ -525,8 +562,7 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
     if (hipEventElapsedTime(&ms, ctx->ev[0], ctx->ev[6]) == hipSuccess) S.ms_total = ms;
     if (staged) {
         if (hipEventElapsedTime(&ms, ctx->ev[0], ctx->ev[3]) == hipSuccess) S.ms_prep = ms;
-        if (hipEventElapsedTime(&ms, ctx->ev[3], ctx->ev[1]) == hipSuccess) S.ms_route = ms;
-        if (hipEventElapsedTime(&ms, ctx->ev[1], ctx->ev[2]) == hipSuccess) S.ms_seed = ms;
+        if (hipEventElapsedTime(&ms, ctx->ev[3], ctx->ev[2]) == hipSuccess) S.ms_route = ms;
         if (hipEventElapsedTime(&ms, ctx->ev[2], ctx->ev[4]) == hipSuccess) S.ms_invert = ms;
         if (hipEventElapsedTime(&ms, ctx->ev[4], ctx->ev[5]) == hipSuccess) S.ms_scan = ms;
         if (hipEventElapsedTime(&ms, ctx->ev[5], ctx->ev[6]) == hipSuccess) S.ms_rerank = ms;
@@ -557,15 +593,16 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
         if (fixed) {
             S.reruns++;
             if ((rc = launch_reset(ctx, nq))) return rc;
-            if ((rc = launch_seed(ctx, K))) return rc;
-            if ((rc = launch_scan(ctx, K, false))) return rc;
-            if ((rc = launch_finish(ctx, K, d_q, d_slots, d_scores))) return rc;
+            if ((rc = launch_seed(ctx, csr(K)))) return rc;
+            if ((rc = launch_scan(ctx, csr(K), false))) return rc;
+            if ((rc = launch_finish(ctx, csr(K), d_q, d_slots, d_scores))) return rc;
             if ((rc = read_ctl(ctx, &ctl))) return rc;
             if (ctl.err_seed) return fail(ctx, MAIVS_ERR_UNSUPPORTED, "a seed set exceeds its on-chip capacity");
         }
     }
-    // (2) adaptive cuts near their threshold
-    bool rerun_scan = false;
+    // (2) adaptive cuts near their threshold; a full query bucket re-runs the scan from the
+    // counting-sort inversion
+    bool rerun_scan = ctl.bucket_overflow != 0;
     if (ctl.nflag_prune) {
         std::vector<uint32_t> fl(ctl.nflag_prune);
         HIP_TRY(ctx, hipMemcpy(fl.data(), W.flag_prune, fl.size() * 4, hipMemcpyDeviceToHost));
@@ -602,8 +639,8 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
     }
     if (rerun_scan) {
         S.reruns++;
-        if ((rc = launch_scan(ctx, K, true))) return rc;
-        if ((rc = launch_finish(ctx, K, d_q, d_slots, d_scores))) return rc;
+        if ((rc = launch_scan(ctx, csr(K), true))) return rc;
+        if ((rc = launch_finish(ctx, csr(K), d_q, d_slots, d_scores))) return rc;
         if ((rc = read_ctl(ctx, &ctl))) return rc;
         if (ctl.max_cand > ctx->cap_cand) return fail(ctx, MAIVS_ERR_HIP, "candidate count changed between passes");
     }
@@ -823,7 +860,7 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
     ctx->h_r_bound.assign(a->r_bound, a->r_bound + A.M);
     // LDS plan: the route's shortlist sort size is per call (12 bytes per entry: key + weight)
     const size_t route_fixed = route_lds(A, 0, 0);
-    size_t room = kLdsBudget - 4096 > route_fixed ? (kLdsBudget - 4096 - route_fixed) / 12 : 0;
+    size_t room = kLdsBudget - 8192 > route_fixed ? (kLdsBudget - 8192 - route_fixed) / 12 : 0;
     if (room < 1024) return fail(ctx, MAIVS_ERR_UNSUPPORTED, "routing tables do not fit in LDS");
     uint32_t sc = 1024;
     while (static_cast<size_t>(sc) * 2 <= room && sc < 16384) sc <<= 1;
@@ -842,6 +879,9 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
                             static_cast<int>(route_lds(A, sc, sc)));
         hipFuncSetAttribute(reinterpret_cast<const void*>(seed_kernel<NW>), hipFuncAttributeMaxDynamicSharedMemorySize,
                             static_cast<int>(ctx->lds_seed));
+        hipFuncSetAttribute(reinterpret_cast<const void*>(route_seed_kernel<NW>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(std::max(route_lds(A, sc, sc), ctx->lds_seed)));
     });
     ctx->uploaded = true;
     return 0;
@@ -891,7 +931,7 @@ int maivs_gpu_query_prep(maivs_gpu_ctx* ctx, const float* q, uint32_t nq, uint64
     p.target_confidence = 1.0f;
     KParams K = make_params(ctx, nq, &p);
     HIP_TRY(ctx, hipMemcpyAsync(ctx->Wk.q, q, static_cast<size_t>(nq) * A.d * 4, hipMemcpyHostToDevice, ctx->stream));
-    if ((rc = launch_prep(ctx, K, ctx->Wk.q, false))) return rc;
+    if ((rc = launch_prep(ctx, K, ctx->Wk.q, 0))) return rc;
     HIP_TRY(ctx, hipMemcpyAsync(out_bits, ctx->Wk.qbits, static_cast<size_t>(nq) * A.W * 8, hipMemcpyDeviceToHost, ctx->stream));
     HIP_TRY(ctx, hipMemcpyAsync(out_lut, ctx->Wk.lut, static_cast<size_t>(nq) * A.npos * 16, hipMemcpyDeviceToHost, ctx->stream));
     HIP_TRY(ctx, hipMemcpyAsync(out_delta, ctx->Wk.delta, nq * 4, hipMemcpyDeviceToHost, ctx->stream));
@@ -964,7 +1004,7 @@ int maivs_gpu_route(maivs_gpu_ctx* ctx, const float* q, uint32_t nq, const maivs
         return 0;
     }
     HIP_TRY(ctx, hipMemcpyAsync(W.q, q, static_cast<size_t>(nq) * ctx->A.d * 4, hipMemcpyHostToDevice, ctx->stream));
-    if ((rc = launch_prep(ctx, K, W.q, true))) return rc;
+    if ((rc = launch_prep(ctx, K, W.q, kPrepReset | kPrepHamming))) return rc;
     if ((rc = launch_route(ctx, K))) return rc;
     Ctl ctl{};
     HIP_TRY(ctx, hipMemcpyAsync(&ctl, W.ctl, sizeof(Ctl), hipMemcpyDeviceToHost, ctx->stream));

@@ -179,3 +179,12 @@ def test_graph_replays_match_eager(quality50k, mix50k, monkeypatch):
     finally:
         eager.close()
         graph.close()
+
+
+def test_search_bucket_overflow_falls_back(ctx, quality50k, mix50k):
+    """Many queries probing the same cells overflow the per-cell query buckets; the pass then runs
+    the counting-sort inversion and still matches the oracle."""
+    _, queries, _ = mix50k
+    ix = quality50k
+    q = np.repeat(queries[:3], 150, axis=0)  # 450 queries, three distinct probe lists
+    _compare_search(ctx, ix, q, _params(ix, 10, 40))
