@@ -22,7 +22,7 @@ constexpr uint32_t kPrepReset = 1, kPrepHamming = 2;
 constexpr uint32_t kRouteThreads = 256;
 constexpr uint32_t kSeedThreads = 256;
 constexpr uint32_t kScanThreads = 256;
-constexpr uint32_t kFinishThreads = 512;
+constexpr uint32_t kFinishThreads = 256;
 constexpr uint32_t kG = 4;               // queries interleaved per cell_scan table pass
 constexpr uint32_t kHistBins = 256;
 constexpr uint32_t kFinishLdsCap = 2048; // final candidates kept and sorted in LDS up to this many
@@ -79,6 +79,7 @@ struct Work {
     float* bias;           // nq
     float* cqs;            // nq x d: rescore operand q * csq_step (q itself for f32 centroids)
     float* cqbase;         // nq: sum(q * csq_min), sequential
+    float* rbase;          // nq: SQ8 rerank base sum(q * sq_min), sequential (MAIVS_RERANK_SQ8)
     uint16_t* hs;          // nq x Mp: Hamming distance to every cell, 0xFFFF for dead cells
     float* bnd;            // nq x nprobe: adaptive-cut bounds of the probe list (i >= SEED_CELLS)
     uint32_t* chosen;      // nq x nprobe
@@ -497,7 +498,8 @@ __global__ void reset_kernel(Work Wk, uint32_t M, uint32_t nq) {
 // coordinates [l*EPL, (l+1)*EPL) in registers: FWHT levels below EPL run inside the lane, the
 // others across lanes (partner l ^ (h / EPL)), in the reference's ascending level order, so every
 // butterfly sees the reference's operands. `xs` is the wave's LDS region (x[P] | mins[npos4] |
-// cqp[d4]); `qw` receives the code words.
+// cqp[d4] | rqp[d4]); `qw` receives the code words. For an SQ8 rerank store it also computes the
+// rerank base sum(q * sq_min) (src/index.rs:1326-1330).
 template <int EPL>
 __device__ __forceinline__ void prep_wave(const DevArena& A, const Work& Wk, const float* __restrict__ queries,
                                           uint32_t qi, uint32_t lane, float* xs, uint64_t* qw) {
@@ -505,8 +507,10 @@ __device__ __forceinline__ void prep_wave(const DevArena& A, const Work& Wk, con
     const uint32_t np4 = (npos + 3) & ~3u;
     float* mins = xs + P;
     float* cqp = mins + np4;
+    float* rqp = cqp + ((d + 3) & ~3u);
     const float* q = queries + static_cast<uint64_t>(qi) * d;
     const bool sq8 = A.cent_sq8 != nullptr;
+    const bool rsq8 = A.rerank_mode == MAIVS_RERANK_SQ8;
     const uint32_t base = lane * EPL;
     float x[EPL], sg[2][EPL];
     // whole float4s where the lane's coordinates are all inside the query (the common case)
@@ -577,6 +581,11 @@ __device__ __forceinline__ void prep_wave(const DevArena& A, const Work& Wk, con
                 cqp[i] = sq8 ? v * A.csq_min[i] : 0.0f;
             }
         }
+    }
+    if (rsq8) {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e)
+            if (base + e < d) rqp[base + e] = x[e] * A.sq_min[base + e];
     }
     for (int r = 0; r < 2; ++r) {
 #pragma unroll
@@ -661,11 +670,12 @@ __device__ __forceinline__ void prep_wave(const DevArena& A, const Work& Wk, con
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     // ---- sequential sums in index order: lane 0 the table bias (Rust's f32 Sum folds from -0.0),
-    // lane 1 the rescore base sum(q * csq_min) from 0.0
-    if (lane < 2) {
+    // lane 1 the rescore base sum(q * csq_min) from 0.0, lane 2 the SQ8 rerank base
+    // sum(q * sq_min) from 0.0
+    if (lane < 3) {
         // whole 16-element chunks with the next chunk's LDS reads in flight, then the tail
-        const uint32_t n = lane == 0 ? npos : (sq8 ? d : 0u);
-        const float* src = lane == 0 ? mins : cqp;
+        const uint32_t n = lane == 0 ? npos : lane == 1 ? (sq8 ? d : 0u) : (rsq8 ? d : 0u);
+        const float* src = lane == 0 ? mins : lane == 1 ? cqp : rqp;
         const float4* src4 = reinterpret_cast<const float4*>(src);
         float s = lane == 0 ? -0.0f : 0.0f;
         const uint32_t nfull = n / 16;
@@ -693,8 +703,10 @@ __device__ __forceinline__ void prep_wave(const DevArena& A, const Work& Wk, con
         if (lane == 0) {
             Wk.bias[qi] = s;
             Wk.delta[qi] = delta;
-        } else {
+        } else if (lane == 1) {
             Wk.cqbase[qi] = s;
+        } else {
+            Wk.rbase[qi] = s;
         }
     }
 }
@@ -733,7 +745,7 @@ __device__ __forceinline__ void hamming_tile(const DevArena& A, const Work& Wk, 
 // kPrepWaves queries per workgroup, one wave each (prep_wave). Flags: kPrepReset also clears the
 // per-call counters (control block, probe counts, candidate counts); kPrepHamming then runs the
 // block's queries against every cell code (hamming_tile).
-// LDS: codes[kPrepWaves * 16] u64 | per wave x[P] | mins[npos4] | cqp[d4].
+// LDS: codes[kPrepWaves * 16] u64 | per wave x[P] | mins[npos4] | cqp[d4] | rqp[d4].
 template <int EPL>
 __global__ void __launch_bounds__(kPrepWaves * kWave)
 prep_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries, uint32_t flags) {
@@ -748,7 +760,7 @@ prep_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries, u
     const uint32_t qi = blockIdx.x * kPrepWaves + wv;
     uint64_t* qbl = reinterpret_cast<uint64_t*>(smem);
     if (qi < K.nq) prep_wave<EPL>(A, Wk, queries, qi, lane, reinterpret_cast<float*>(qbl + kPrepWaves * 16) +
-                                  wv * (A.P + ((A.npos + 3) & ~3u) + ((A.d + 3) & ~3u)), qbl + wv * 16);
+                                  wv * (A.P + ((A.npos + 3) & ~3u) + 2 * ((A.d + 3) & ~3u)), qbl + wv * 16);
     if (flags & kPrepHamming) {
         __syncthreads();
         const uint32_t q0 = blockIdx.x * kPrepWaves;
@@ -1361,7 +1373,6 @@ finish_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries,
     float* qs = reinterpret_cast<float*>(scratch + 32);
     uint64_t* keys = reinterpret_cast<uint64_t*>(qs + ((d + 3) & ~3u));  // kFinishLdsCap
     __shared__ uint32_t s_n;
-    __shared__ float s_base;
 
     const uint32_t ns_cnt = Wk.seed_cnt[qi];
     const uint32_t cc = Wk.cand_cnt[qi];
@@ -1378,11 +1389,6 @@ finish_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries,
     if (total >= K.target)
         cutv = select_kth(total, K.target, [&](uint32_t i) { return i < ns_cnt ? seed[i].x : cand[i - ns_cnt].x; },
                           hist, scratch);
-    if (sq8 && tid == 0) {
-        float b = 0.0f;
-        for (uint32_t j = 0; j < d; ++j) b += q[j] * A.sq_min[j];
-        s_base = b;
-    }
     __syncthreads();
     // ---- compact the survivors into fin[] (global, read back by the debug entry point)
     uint2* fin = Wk.fin + static_cast<uint64_t>(qi) * K.fin_cap;
@@ -1408,7 +1414,7 @@ finish_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries,
     {
         const uint32_t l = tid & 7, grp = tid >> 3, ngrp = nt >> 3;
         const uint32_t rounds = (n + ngrp - 1) / ngrp;
-        const float base = sq8 ? s_base : 0.0f;
+        const float base = sq8 ? Wk.rbase[qi] : 0.0f;
         for (uint32_t rr = 0; rr < rounds; ++rr) {
             const uint32_t i = rr * ngrp + grp;
             const uint32_t slot = i < n ? fin[i].y : fin[0].y;

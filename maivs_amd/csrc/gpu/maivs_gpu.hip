@@ -155,9 +155,10 @@ bool supported_nw(uint32_t w) { return w == 1 || w == 2 || w == 4 || w == 8 || w
         default: { constexpr int NW = 16; __VA_ARGS__; break; } \
     }
 
-// LDS of prep: codes[kPrepWaves * 16] u64 | per wave x[P] | mins[npos4] | cqp[d4]
+// LDS of prep: codes[kPrepWaves * 16] u64 | per wave x[P] | mins[npos4] | cqp[d4] | rqp[d4]
 size_t prep_lds(const DevArena& A) {
-    return kPrepWaves * 16 * 8 + static_cast<size_t>(kPrepWaves) * (A.P + ((A.npos + 3) & ~3u) + ((A.d + 3) & ~3u)) * 4;
+    return kPrepWaves * 16 * 8 +
+           static_cast<size_t>(kPrepWaves) * (A.P + ((A.npos + 3) & ~3u) + 2 * ((A.d + 3) & ~3u)) * 4;
 }
 
 // LDS of route: cqs[d4] | ex[np4] | keys[sort_cap] u64 | hist[nbins4] | scratch[16]
@@ -225,6 +226,7 @@ int ensure_work(maivs_gpu_ctx* ctx, uint32_t nq, uint32_t nprobe, uint32_t k) {
     rc |= dalloc(ctx, o, &W.bias, nql);
     rc |= dalloc(ctx, o, &W.cqs, nql * A.d);
     rc |= dalloc(ctx, o, &W.cqbase, nql);
+    rc |= dalloc(ctx, o, &W.rbase, nql);
     rc |= dalloc(ctx, o, &W.hs, nql * A.Mp);
     rc |= dalloc(ctx, o, &W.bnd, nql * nprobe);
     rc |= dalloc(ctx, o, &W.chosen, nql * nprobe);
