@@ -75,6 +75,8 @@ typedef struct maivs_arena_desc {
     const uint8_t* sq8_codes;   /* N * d (MAIVS_RERANK_SQ8) */
     const float* sq_min;        /* d (MAIVS_RERANK_SQ8) */
     const float* sq_step;       /* d (MAIVS_RERANK_SQ8) */
+    /* filtering: one u32 attribute per slot (src/index.rs:551-555), or NULL when unused */
+    const uint32_t* tags;       /* N */
 } maivs_arena_desc;
 
 /* Query-time settings of search_batch (src/index.rs:3316-3326 and the index setters). */
@@ -87,6 +89,14 @@ typedef struct maivs_search_params {
     uint32_t shortlist_mult;  /* two-stage shortlist = nprobe * max(mult, 2) */
     uint32_t adaptive;        /* adaptive probe cut (set_adaptive) */
     float at_margin;          /* its margin */
+    /* Inclusive tag range [tag_lo, tag_hi] (set_filter, src/index.rs:3553-3558). With filter != 0
+     * and uploaded tags, a member counts only when its slot's tag is in range: the reference's
+     * keep! predicate (:1428-1439), applied in the seed and cell-major scans beside the canonical
+     * test, before tau and the cut-offs. (The reference runs filtered searches per query,
+     * :3343-3348; this is the same predicate on the batched path.) */
+    uint32_t filter;
+    uint32_t tag_lo;
+    uint32_t tag_hi;
 } maivs_search_params;
 
 /* Per-call measurements. maivs_gpu_search_batch* fills the times and host_* / reruns fields

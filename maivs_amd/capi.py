@@ -29,7 +29,7 @@ class ArenaDesc(C.Structure):
         ("slot_cells", C.c_void_p), ("cent_bits", C.c_void_p), ("cent_sq8", C.c_void_p),
         ("centroids", C.c_void_p), ("csq_min", C.c_void_p), ("csq_step", C.c_void_p), ("r_bound", C.c_void_p),
         ("rot_signs", C.c_void_p), ("vecs_f32", C.c_void_p), ("sq8_codes", C.c_void_p), ("sq_min", C.c_void_p),
-        ("sq_step", C.c_void_p),
+        ("sq_step", C.c_void_p), ("tags", C.c_void_p),
     ]
 
 
@@ -37,7 +37,7 @@ class SearchParams(C.Structure):
     _fields_ = [
         ("k", C.c_uint32), ("nprobe", C.c_uint32), ("target_confidence", C.c_float), ("beta", C.c_float),
         ("rerank_factor", C.c_uint32), ("shortlist_mult", C.c_uint32), ("adaptive", C.c_uint32),
-        ("at_margin", C.c_float),
+        ("at_margin", C.c_float), ("filter", C.c_uint32), ("tag_lo", C.c_uint32), ("tag_hi", C.c_uint32),
     ]
 
 

@@ -57,6 +57,7 @@ struct DevArena {
     const float* sq_min;
     const float* sq_step;
     const uint8_t* live;        // M
+    const uint32_t* entry_tag;  // E: the tag of the entry's slot (null without tags)
 };
 
 struct Ctl {
@@ -111,6 +112,7 @@ struct Work {
 struct KParams {
     uint32_t nq, k, nprobe, want_c, target, adaptive, sort_cap, use_nucleus;
     uint32_t seed_cap, cand_cap, fin_cap, key_cap, bucket_cap;
+    uint32_t filter, tag_lo, tag_hi;  // keep!: tag in [tag_lo, tag_hi] (filter != 0 only with tags)
     float tc, beta, at_margin, norm, prune_band, nucleus_band;
 };
 
@@ -462,6 +464,14 @@ __global__ void to_chain_kernel(const T* __restrict__ src, uint64_t rows, uint32
             o[i] = v;
         }
     }
+}
+
+// The tag of every entry's slot (for the filter test inside the scans).
+__global__ void entry_tag_kernel(const uint32_t* __restrict__ members, const uint32_t* __restrict__ tags, uint64_t E,
+                                 uint32_t* __restrict__ out) {
+    for (uint64_t e = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x; e < E;
+         e += static_cast<uint64_t>(gridDim.x) * blockDim.x)
+        out[e] = tags[members[e]];
 }
 
 // Test entry point: nibble sums of entry-major codes (32 per block) against per-block tables.
@@ -1046,22 +1056,25 @@ __device__ __forceinline__ void seed_phase(const DevArena& A, const Work& Wk, co
             c = misc[kCell + s];
             return static_cast<uint64_t>(misc[kE0 + s]) + (j - misc[kOff + s]);
         };
+        const bool filt = K.filter != 0;
         uint32_t c_cur;
         uint64_t e_cur = locate(tid, c_cur);
         Code<NW> cur;
         cur.load(A.codes + e_cur * (2 * NW));
         uint32_t alt_cur = A.ma == 2 ? A.entry_alt[e_cur] : kNoAlt;
+        uint32_t tag_cur = filt ? A.entry_tag[e_cur] : 0u;
         for (uint32_t b = 0; b < total; b += nt) {
             const uint32_t it = b + tid;
             const bool have = it < total;
             const bool more = b + nt < total;
-            uint32_t c_nxt = 0, alt_nxt = kNoAlt;
+            uint32_t c_nxt = 0, alt_nxt = kNoAlt, tag_nxt = 0;
             uint64_t e_nxt = 0;
             Code<NW> nxt;
             if (more) {
                 e_nxt = locate(it + nt, c_nxt);
                 nxt.load(A.codes + e_nxt * (2 * NW));
                 if (A.ma == 2) alt_nxt = A.entry_alt[e_nxt];
+                if (filt) tag_nxt = A.entry_tag[e_nxt];
             }
             bool pass = false;
             uint32_t dv = 0;
@@ -1070,6 +1083,7 @@ __device__ __forceinline__ void seed_phase(const DevArena& A, const Work& Wk, co
                     pass = !(alt_cur < c_cur && ((probed[alt_cur >> 5] >> (alt_cur & 31)) & 1u));
                 else
                     pass = canonical(A, e_cur, A.ma > 2 ? A.members[e_cur] : 0u, c_cur, probed);
+                if (filt) pass = pass && tag_cur >= K.tag_lo && tag_cur <= K.tag_hi;
                 dv = A.maxk - lut_sum1<NW>(cur, table);
                 if (pass) atomicAdd(&coarse[dv >> 8], 1u);
             }
@@ -1083,6 +1097,7 @@ __device__ __forceinline__ void seed_phase(const DevArena& A, const Work& Wk, co
                 e_cur = e_nxt;
                 c_cur = c_nxt;
                 alt_cur = alt_nxt;
+                tag_cur = tag_nxt;
             }
         }
     }
@@ -1299,6 +1314,11 @@ cell_scan_kernel(DevArena A, Work Wk, KParams K) {
         code.load(A.codes + e * (2 * NW));
         const uint32_t slot = A.members[e];
         const uint32_t alt = A.ma == 2 ? A.entry_alt[e] : kNoAlt;
+        bool kept = have;
+        if (K.filter) {
+            const uint32_t tg = A.entry_tag[e];
+            kept = kept && tg >= K.tag_lo && tg <= K.tag_hi;
+        }
         for (uint32_t g0 = 0; g0 < nqc; g0 += kG) {
             const uint32_t ng = min(kG, nqc - g0);
             __syncthreads();
@@ -1334,7 +1354,7 @@ cell_scan_kernel(DevArena A, Work Wk, KParams K) {
                 const uint32_t qq = s_q[g];
                 bool pass = false;
                 uint32_t dv = 0;
-                if (have && qq != kNone) {
+                if (kept && qq != kNone) {
                     dv = A.maxk - sums[g];
                     if (dv <= s_t[g]) {
                         const uint32_t* probed = Wk.probed + static_cast<uint64_t>(qq) * A.MW;

@@ -322,6 +322,9 @@ KParams make_params(maivs_gpu_ctx* ctx, uint32_t nq, const maivs_search_params* 
     K.tc = p->target_confidence;
     K.beta = p->beta;
     K.at_margin = p->at_margin;
+    K.filter = (p->filter && A.entry_tag) ? 1u : 0u;
+    K.tag_lo = p->tag_lo;
+    K.tag_hi = p->tag_hi;
     // norm = sqrt(2 * dim_pad / pi) in f32 (src/index.rs:2169)
     K.norm = std::sqrt(2.0f * static_cast<float>(A.P) / static_cast<float>(M_PI));
     K.prune_band = kPruneBand;
@@ -799,6 +802,15 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
         if (A.ma == 2)
             hipLaunchKernelGGL(entry_alt_kernel, dim3(std::max<uint32_t>(A.M, 1)), dim3(256), 0, ctx->stream, mem_off,
                                members, slot_cells, A.M, alt);
+        uint32_t* etag = nullptr;
+        if (a->tags && A.E) {
+            uint32_t* tags = nullptr;
+            if ((rc = stage(a->tags, A.N, &tags))) return rc;
+            if ((rc = dalloc(ctx, ctx->arena_allocs, &etag, A.E))) return rc;
+            hipLaunchKernelGGL(entry_tag_kernel, dim3(static_cast<uint32_t>(std::min<uint64_t>((A.E + 255) / 256, 65535))),
+                               dim3(256), 0, ctx->stream, members, tags, A.E, etag);
+        }
+        A.entry_tag = etag;
         HIP_TRY(ctx, hipGetLastError());
         // chain-major copies of the rows the 8-lane dots read
         auto chain_f32 = [&](const float* src, uint64_t rows, const float** out) -> int {

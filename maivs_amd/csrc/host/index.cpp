@@ -196,6 +196,7 @@ void FlatCellIndex::set_tags(const std::vector<uint64_t>& ids, const std::vector
         auto it = id_to_slot_.find(ids[i]);
         if (it != id_to_slot_.end()) tags_[it->second] = tags[i];
     }
+    ++generation_;  // the uploaded arena carries the tags
 }
 
 void FlatCellIndex::set_filter(std::optional<uint32_t> lo, std::optional<uint32_t> hi) {  // :3553-3558
@@ -787,7 +788,6 @@ std::string FlatCellIndex::cellmajor_blocker(bool cell_major) const {
     if (scan_mode_ != ScanMode::Binary) return "the batched path needs scan_mode='binary'";
     if (!compacted_) return "the index is not compacted (call compact() after add_batch/remove)";
     if (!(max_assign_ == 1 || !rep_off_.empty())) return "polysemic runs are missing (compact() again)";
-    if (tag_filter_) return "a tag filter is set; the filtered path is not part of this build";
     if (!fastscan_ || fs_off_.empty()) return "the MI355X scan needs set_fastscan(True) before compact()";
     if (!two_stage_ || cent_bits_.empty()) return "the MI355X router needs set_two_stage(True, mult)";
     if (f16_rerank_) return "the f16 rerank store is not part of this build";
@@ -831,6 +831,11 @@ const maivs_arena_desc* FlatCellIndex::arena_desc() {
     a.sq8_codes = scan_i8_.empty() ? nullptr : reinterpret_cast<const uint8_t*>(scan_i8_.data());
     a.sq_min = sq_min_.empty() ? nullptr : sq_min_.data();
     a.sq_step = sq_step_.empty() ? nullptr : sq_step_.data();
+    if (!tags_.empty()) {
+        // slots added after set_tags carry tag 0 (the reference indexes past its tag array there)
+        if (tags_.size() < ext_ids_.size()) tags_.resize(ext_ids_.size(), 0);
+        a.tags = tags_.data();
+    }
     return &desc_;
 }
 
@@ -844,6 +849,12 @@ maivs_search_params FlatCellIndex::search_params(size_t k, size_t nprobe, float 
     p.shortlist_mult = static_cast<uint32_t>(shortlist_mult_);
     p.adaptive = adaptive_ ? 1u : 0u;
     p.at_margin = at_margin_;
+    // filtering = tag_filter.is_some() && !tags.is_empty() (src/index.rs:1430-1431)
+    if (tag_filter_ && !tags_.empty()) {
+        p.filter = 1;
+        p.tag_lo = tag_filter_->first;
+        p.tag_hi = tag_filter_->second;
+    }
     return p;
 }
 

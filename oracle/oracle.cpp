@@ -452,6 +452,15 @@ int orc_search_batch(const maivs_arena_desc* a, const float* data, uint32_t nq, 
             if (h[j] != UINT32_MAX && h[j] < ci && ((probed[h[j] >> 6] >> (h[j] & 63)) & 1)) return false;
         return true;
     };
+    // keep!: the tag-range predicate of src/index.rs:1428-1439 (filtering = a filter is set and
+    // tags exist, :1430-1431). The reference applies it on its per-query path only; here it sits
+    // beside the canonical test in the cell-major scan, as the GPU path applies it.
+    const bool filtering = p->filter && a->tags;
+    auto keep = [&](uint32_t slot) {
+        if (!filtering) return true;
+        const uint32_t tg = a->tags[slot];
+        return tg >= p->tag_lo && tg <= p->tag_hi;
+    };
     // scan_cell, FastScan branch, src/index.rs:2048-2074
     auto scan_cell = [&](uint32_t c, const QState& s, uint32_t t, std::vector<Cand>& out) {
         uint32_t len = A.mem_len(c);
@@ -466,7 +475,7 @@ int orc_search_batch(const maivs_arena_desc* a, const float* data, uint32_t nq, 
                 uint32_t dd = dp - sums[i];
                 if (dd <= t) {
                     uint32_t slot = mem[base + i];
-                    if (!poly || canonical(slot, c, s.probed)) out.push_back({dd, slot});
+                    if (keep(slot) && (!poly || canonical(slot, c, s.probed))) out.push_back({dd, slot});
                 }
             }
         }

@@ -52,6 +52,31 @@ def memory50k(mix50k):
     return M.build_preset(base, "memory")
 
 
+@pytest.fixture(scope="session")
+def churn50k(mix50k):
+    """The update-and-filter workload at 50k (the 400k churn + filter workload's shape): 40k initial
+    vectors, 5 rounds of (delete 2k random initial ids, insert 2k new vectors), compact(), then a
+    tag in [0, 1000) per id (bench/fair/churn.py:29,47-61; bench/fair/filtered.py:33).
+    Returns (index, tag of every id, live ids)."""
+    import maivs_amd as M
+    base, _, _ = mix50k
+    n0, nnew, rounds = 40_000, 10_000, 5
+    ix = M.build_preset(base[:n0], "quality")
+    dele = np.random.RandomState(501).choice(n0, nnew, replace=False)
+    per = nnew // rounds
+    for r in range(rounds):
+        for i in dele[r * per:(r + 1) * per]:
+            assert ix.remove(int(i))
+        lo = n0 + r * per
+        ix.add_batch(list(range(lo, lo + per)), np.ascontiguousarray(base[lo:lo + per]))
+    ix.compact()
+    gone = set(dele.tolist())
+    live = [i for i in range(n0 + nnew) if i not in gone]
+    tags = np.random.RandomState(502).randint(0, 1000, n0 + nnew).astype(np.uint32)
+    ix.set_tags(live, [int(tags[i]) for i in live])
+    return ix, tags, live
+
+
 def small_clustered(n=4000, d=64, n_clusters=40, seed=0):
     """Small clustered unit vectors (tests/test_index.py:51-95 style: Gaussian centres, noise)."""
     rs = np.random.RandomState(seed)

@@ -155,12 +155,34 @@ def test_blockers_name_the_missing_piece(quality50k):
     ix = quality50k
     assert ix.cellmajor_blocker(True) == ""
     assert "per-query" in ix.cellmajor_blocker(False)
+    # a tag filter no longer blocks the batched path: the predicate runs inside the scans
     ix.set_filter(0, 10)
     try:
-        assert "filter" in ix.cellmajor_blocker(True)
+        assert ix.cellmajor_blocker(True) == ""
     finally:
         ix.set_filter()
     assert ix.cellmajor_blocker(True) == ""
+
+
+def test_filter_params_need_tags():
+    """filtering = a filter is set and tags exist (src/index.rs:1430-1431); the range is inclusive,
+    an omitted bound is open (src/index.rs:3553-3558)."""
+    x = small_clustered(3000, 64)
+    ix = M.build_preset(x, "quality")
+    sp = lambda: capi.params_from_bytes(ix._search_params(10, 8, 1.0, 8.0))
+    ix.set_filter(3, 7)
+    assert sp().filter == 0  # no tags yet: inert
+    ix.set_tags(list(range(3000)), [i % 10 for i in range(3000)])
+    p = sp()
+    assert (p.filter, p.tag_lo, p.tag_hi) == (1, 3, 7)
+    ix.set_filter(None, 4)
+    p = sp()
+    assert (p.filter, p.tag_lo, p.tag_hi) == (1, 0, 4)
+    ix.set_filter(5)
+    p = sp()
+    assert (p.filter, p.tag_lo, p.tag_hi) == (1, 5, 2 ** 32 - 1)
+    ix.set_filter()
+    assert sp().filter == 0
 
 
 def test_recall_of_the_restated_path(quality50k, mix50k):

@@ -282,13 +282,20 @@ def _all_nibbles(codes_u64):
     return nib
 
 
-@pytest.mark.parametrize("nprobe,rf", [(16, 8), (4, 32), (64, 4)])
-def test_candidate_set_and_rerank_bruteforce(quality50k, mix50k, nprobe, rf):
-    """U(q) = canonical members of the scanned cells; candidates = {d <= G}, G the target-th
-    smallest d; top-k = best exact scores (src/index.rs:2036-2045, 2155-2160, 2277-2311)."""
+@pytest.mark.parametrize("nprobe,rf,filt", [(16, 8, None), (4, 32, None), (64, 4, None), (16, 8, (0, 99)),
+                                             (32, 8, (0, 9)), (8, 16, (250, 749))])
+def test_candidate_set_and_rerank_bruteforce(quality50k, mix50k, nprobe, rf, filt):
+    """U(q) = canonical members of the scanned cells that pass the tag filter (keep!); candidates
+    = {d <= G}, G the target-th smallest d; top-k = best exact scores (src/index.rs:1428-1439,
+    2036-2045, 2155-2160, 2277-2311)."""
     _, queries, _ = mix50k
     ix = quality50k
     ix.set_rerank_factor(rf)
+    ext = ix._ext_ids()
+    tags = np.random.RandomState(502).randint(0, 1000, len(ext)).astype(np.uint32)
+    if filt is not None:
+        ix.set_tags([int(x) for x in ext], [int(t) for t in tags])
+        ix.set_filter(*filt)
     try:
         arr = ix._arena_arrays()
         nibs = _all_nibbles(ix._codes().reshape(-1, arr["n_words"]))
@@ -314,6 +321,8 @@ def test_candidate_set_and_rerank_bruteforce(quality50k, mix50k, nprobe, rf):
                 mem = arr["members"][arr["mem_off"][c]: arr["mem_off"][c + 1]].astype(np.int64)
                 dd = maxk - tab[np.arange(npos)[None, :], nibs[mem]].sum(axis=1)
                 for slot, d in zip(mem.tolist(), dd.tolist()):
+                    if filt is not None and not (filt[0] <= tags[slot] <= filt[1]):
+                        continue  # keep!: tag outside the filter range
                     if any(h != 0xFFFFFFFF and h < c and h in probed for h in sc[slot].tolist()):
                         continue  # scored at a lower-id probed home
                     U.append((d, slot))
@@ -336,8 +345,12 @@ def test_candidate_set_and_rerank_bruteforce(quality50k, mix50k, nprobe, rf):
             clear = kk == len(ex) or ex[kk - 1][0] - ex[kk][0] > 1e-5
             if clear:
                 assert sorted(s for _, s in ex[:kk]) == sorted(int(s) for s in slots[i][:kk])
+            if filt is not None:
+                got_slots = [int(s) for s in slots[i] if s != 0xFFFFFFFF]
+                assert all(filt[0] <= tags[s] <= filt[1] for s in got_slots)
     finally:
         ix.set_rerank_factor(32)
+        ix.set_filter()
 
 
 def test_adaptive_cut_matches_double_precision(quality50k, mix50k):
