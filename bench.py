@@ -77,6 +77,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0 = all host cores")
     ap.add_argument("--only", default="", help="time only this point, e.g. 12:8 (nprobe:rf)")
+    ap.add_argument("--copy-mb", type=int, default=0,
+                    help="after the run, copy this many MiB device-to-device 5 times (the plain copy whose "
+                         "FETCH_SIZE / WRITE_SIZE calibrate the counters under rocprofv3 --pmc)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -189,6 +192,17 @@ def main() -> int:
     log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step, {value:.0f} QPS, R@10 {r_final:.4f} "
         f"(stage-by-stage launches: {staged_ms:.3f} ms/step)")
 
+    if args.copy_mb:
+        n = args.copy_mb << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy calibration: 5 x {args.copy_mb} MiB device-to-device")
+        del src, dst
+
     # ---- roofline of the dominant kernel (algorithmic bytes / its average duration)
     d = base.shape[1]
     row_bytes = d * 4 if args.profile == "quality" else d
@@ -212,8 +226,10 @@ def main() -> int:
     scan_ms = avg["ms_route"] + avg["ms_seed"] + avg["ms_scan"]  # the seed scan runs inside route_seed
     scan_bytes = (avg["seed_blocks"] + avg["scan_blocks"]) * blk + nq * 2048
     scan_gbs = scan_bytes / (scan_ms * 1e-3) / 1e9 if scan_ms > 0 else 0.0
+    traffic = _traffic(dom, args.workload, args.profile)
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dom,
+                "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": traffic["bytes_per_launch"] if traffic else None, "kernel": dom,
                 "kernel_ms": round(ms_dom, 4), "bytes_per_launch": int(bytes_dom), "bytes_are": what}
     log(f"stages (avg ms): " + ", ".join(f"{s_}={stages[s_][0]:.4f}" for s_ in stages))
 
@@ -284,6 +300,21 @@ def main() -> int:
     ctx.close()
     ctx_st.close()
     return 0
+
+
+def _traffic(kernel: str, workload: str, profile: str):
+    """Physical HBM bytes per launch of `kernel` from the committed counter summary
+    (profiles/traffic.json: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs, each scaled by the same
+    counter over a plain device copy of known size), or None when no summary covers it."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        t = json.load(f)
+    for e in t.get("kernels", []):
+        if e.get("kernel") == kernel.split(" ")[0] and e.get("workload") == f"{workload} {profile}":
+            return e
+    return None
 
 
 def _r(x):
