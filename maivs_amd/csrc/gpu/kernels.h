@@ -1379,20 +1379,44 @@ cell_scan_kernel(DevArena A, Work Wk, KParams K) {
 
 // ---------------------------------------------------------------- finish (one WG per query)
 
+// Exact `want`-th smallest (1-based) of the n <= 64 * KPL values v (d < 65536) held by one wave,
+// lane-major (value r*64 + lane in v[r]; invalid ones are 0xFFFFFFFF): a most-significant-bit-first
+// radix select with ballots, no LDS and no barriers. Every lane returns the value.
+template <int KPL>
+__device__ __forceinline__ uint32_t wave_select_kth(const uint32_t (&v)[KPL], uint32_t want) {
+    uint32_t prefix = 0;
+#pragma unroll 1
+    for (int b = 15; b >= 0; --b) {
+        const uint32_t hi = prefix >> b;  // the candidate prefix with bit b = 0
+        uint32_t cnt0 = 0;
+#pragma unroll
+        for (int r = 0; r < KPL; ++r) cnt0 += __popcll(__ballot((v[r] >> b) == hi));
+        if (cnt0 < want) {
+            want -= cnt0;
+            prefix |= 1u << b;
+        }
+    }
+    return prefix;
+}
+
 // Exact tie-inclusive cut at k*rerank_factor over the seed and scan candidates
 // (src/index.rs:2281-2293), exact rerank (rerank_exact, :1309-1378), top-k by (score desc, slot asc).
-__global__ void __launch_bounds__(kFinishThreads)
+// Up to kFinishLdsCap candidates are staged in LDS once; the cut G is then a one-wave radix
+// select, and the top k of up to 256 reranked keys come from their ranks (keys are unique).
+// LDS: hist[256] | scratch[32] | qs[d4] | ent[kFinishLdsCap] (d, slot) | keys[kFinishLdsCap] u64.
+__global__ void __launch_bounds__(kFinishThreads, 4)
 finish_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries, uint32_t* __restrict__ out_slots,
               float* __restrict__ out_scores) {
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t qi = blockIdx.x;
     if (qi >= K.nq) return;
-    const uint32_t tid = threadIdx.x, nt = blockDim.x, d = A.d;
+    const uint32_t tid = threadIdx.x, nt = blockDim.x, d = A.d, lane = lane_id();
     uint32_t* hist = reinterpret_cast<uint32_t*>(smem);
     uint32_t* scratch = hist + kHistBins;
     float* qs = reinterpret_cast<float*>(scratch + 32);
-    uint64_t* keys = reinterpret_cast<uint64_t*>(qs + ((d + 3) & ~3u));  // kFinishLdsCap
-    __shared__ uint32_t s_n;
+    uint2* ent = reinterpret_cast<uint2*>(qs + ((d + 3) & ~3u));
+    uint64_t* keys = reinterpret_cast<uint64_t*>(ent + kFinishLdsCap);
+    __shared__ uint32_t s_n, s_g;
 
     const uint32_t ns_cnt = Wk.seed_cnt[qi];
     const uint32_t cc = Wk.cand_cnt[qi];
@@ -1402,69 +1426,125 @@ finish_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries,
     const uint32_t total = ns_cnt + nc;
     const float* q = queries + static_cast<uint64_t>(qi) * d;
     const bool sq8 = A.rerank_mode == MAIVS_RERANK_SQ8;
+    const bool staged = total <= kFinishLdsCap;
     for (uint32_t j = tid; j < d; j += nt) qs[j] = sq8 ? q[j] * A.sq_step[j] : q[j];
-    if (tid == 0) s_n = 0;
+    if (staged)
+        for (uint32_t i = tid; i < total; i += nt) ent[i] = i < ns_cnt ? seed[i] : cand[i - ns_cnt];
+    if (tid == 0) {
+        s_n = 0;
+        s_g = A.maxk;
+    }
+    __syncthreads();
+    auto entry = [&](uint32_t i) -> uint2 { return staged ? ent[i] : (i < ns_cnt ? seed[i] : cand[i - ns_cnt]); };
     // ---- G = target-th smallest d; with fewer than target candidates every one is kept
     uint32_t cutv = A.maxk;
-    if (total >= K.target)
-        cutv = select_kth(total, K.target, [&](uint32_t i) { return i < ns_cnt ? seed[i].x : cand[i - ns_cnt].x; },
-                          hist, scratch);
-    __syncthreads();
-    // ---- compact the survivors into fin[] (global, read back by the debug entry point)
+    if (total >= K.target) {
+        if (total <= 64 * 16) {
+            if (tid < kWave) {
+                auto run = [&](auto kpl_tag) {
+                    constexpr int KPL = decltype(kpl_tag)::value;
+                    uint32_t v[KPL];
+#pragma unroll
+                    for (int r = 0; r < KPL; ++r) {
+                        const uint32_t i = static_cast<uint32_t>(r) * 64 + lane;
+                        v[r] = i < total ? ent[i].x : 0xFFFFFFFFu;
+                    }
+                    const uint32_t g = wave_select_kth<KPL>(v, K.target);
+                    if (lane == 0) s_g = g;
+                };
+                if (total <= 64 * 4)
+                    run(std::integral_constant<int, 4>{});
+                else
+                    run(std::integral_constant<int, 16>{});
+            }
+            __syncthreads();
+            cutv = s_g;
+        } else {
+            cutv = select_kth(total, K.target, [&](uint32_t i) { return entry(i).x; }, hist, scratch);
+        }
+    }
+    // ---- compaction, rerank and top-k over the key list `kk`: written once for each address space
+    // (an LDS list for up to kFinishLdsCap candidates, else the global key buffer) so that every
+    // access compiles to LDS or global instructions rather than generic ones
     uint2* fin = Wk.fin + static_cast<uint64_t>(qi) * K.fin_cap;
-    for (uint32_t base = 0; base < total; base += nt) {
-        const uint32_t i = base + tid;
-        uint2 e = make_uint2(0, 0);
-        bool pass = false;
-        if (i < total) {
-            e = i < ns_cnt ? seed[i] : cand[i - ns_cnt];
-            pass = e.x <= cutv;
+    auto tail = [&](uint64_t* kk) -> uint32_t {
+        // compact the survivors into fin[] (global, read back by the debug entry point); their
+        // slots go into the key list
+        for (uint32_t base = 0; base < total; base += nt) {
+            const uint32_t i = base + tid;
+            uint2 e = make_uint2(0, 0);
+            bool pass = false;
+            if (i < total) {
+                e = entry(i);
+                pass = e.x <= cutv;
+            }
+            const uint64_t m = __ballot(pass);
+            uint32_t wb = 0;
+            if (lane == 0 && m) wb = atomicAdd(&s_n, static_cast<uint32_t>(__popcll(m)));
+            wb = __shfl(wb, 0, kWave);
+            if (pass) {
+                const uint32_t pos = wb + lanes_below(m);
+                fin[pos] = e;
+                kk[pos] = e.y;
+            }
         }
-        uint64_t m = __ballot(pass);
-        uint32_t wb = 0;
-        if (lane_id() == 0 && m) wb = atomicAdd(&s_n, static_cast<uint32_t>(__popcll(m)));
-        wb = __shfl(wb, 0, kWave);
-        if (pass) fin[wb + lanes_below(m)] = e;
-    }
-    __syncthreads();
-    const uint32_t n = s_n;
-    // ---- exact rerank, 8 lanes per row
-    const bool in_lds = n <= kFinishLdsCap;
-    uint64_t* kk = in_lds ? keys : (Wk.keys + static_cast<uint64_t>(qi) * K.key_cap);
-    {
-        const uint32_t l = tid & 7, grp = tid >> 3, ngrp = nt >> 3;
-        const uint32_t rounds = (n + ngrp - 1) / ngrp;
-        const float base = sq8 ? Wk.rbase[qi] : 0.0f;
-        for (uint32_t rr = 0; rr < rounds; ++rr) {
-            const uint32_t i = rr * ngrp + grp;
-            const uint32_t slot = i < n ? fin[i].y : fin[0].y;
-            float s;
-            if (sq8)
-                s = base + dot_cm_u8(A.sq8 + static_cast<uint64_t>(slot) * A.cu.stride, A.cu, l,
-                                     [&](uint32_t j) { return qs[j]; });
-            else
-                s = dot_cm_f32(A.vecs + static_cast<uint64_t>(slot) * A.cf.stride, A.cf, l,
-                               [&](uint32_t j) { return qs[j]; });
-            if (i < n && l == 0) kk[i] = desc_score_key(s, slot);
+        __syncthreads();
+        const uint32_t n = s_n;
+        // exact rerank, 8 lanes per row
+        {
+            const uint32_t l = tid & 7, grp = tid >> 3, ngrp = nt >> 3;
+            const uint32_t rounds = (n + ngrp - 1) / ngrp;
+            const float base = sq8 ? Wk.rbase[qi] : 0.0f;
+            auto slot_of = [&](uint32_t rr) {
+                const uint32_t i = rr * ngrp + grp;
+                return static_cast<uint32_t>(kk[i < n ? i : 0]);
+            };
+            auto qf = [&](uint32_t j) { return qs[j]; };
+            for (uint32_t rr = 0; rr < rounds; ++rr) {
+                const uint32_t i = rr * ngrp + grp;
+                const uint32_t slot = slot_of(rr);
+                float sc;
+                if (sq8)
+                    sc = base + dot_cm_u8(A.sq8 + static_cast<uint64_t>(slot) * A.cu.stride, A.cu, l, qf);
+                else
+                    sc = dot_cm_f32(A.vecs + static_cast<uint64_t>(slot) * A.cf.stride, A.cf, l, qf);
+                if (i < n && l == 0) kk[i] = desc_score_key(sc, slot);
+            }
         }
-    }
-    __syncthreads();
-    const uint32_t kout = min(K.k, n);
-    if (n <= 256) {
-        wave0_sort_prefix(kk, n, kk, kout);
-    } else {
-        // n <= kFinishLdsCap (a power of two) keeps n2 in LDS; larger lists live in the global key buffer
-        uint32_t n2 = 1;
-        while (n2 < n) n2 <<= 1;
-        for (uint32_t i = n + tid; i < n2; i += nt) kk[i] = kKeyMax;
-        bitonic_sort_u64(kk, n2);
-    }
-    __syncthreads();
-    for (uint32_t i = tid; i < K.k; i += nt) {
-        const bool ok = i < kout;
-        out_slots[static_cast<uint64_t>(qi) * K.k + i] = ok ? static_cast<uint32_t>(kk[i]) : kNone;
-        out_scores[static_cast<uint64_t>(qi) * K.k + i] = ok ? key_score(kk[i]) : -INFINITY;
-    }
+        __syncthreads();
+        const uint32_t kout = min(K.k, n);
+        if (n <= nt) {
+            // the rank of each (unique) key among the n places it directly in the output
+            if (tid < n) {
+                const uint64_t mine = kk[tid];
+                uint32_t r = 0;
+#pragma unroll 8
+                for (uint32_t j = 0; j < n; ++j) r += kk[j] < mine;
+                if (r < kout) {
+                    out_slots[static_cast<uint64_t>(qi) * K.k + r] = static_cast<uint32_t>(mine);
+                    out_scores[static_cast<uint64_t>(qi) * K.k + r] = key_score(mine);
+                }
+            }
+            for (uint32_t i = kout + tid; i < K.k; i += nt) {
+                out_slots[static_cast<uint64_t>(qi) * K.k + i] = kNone;
+                out_scores[static_cast<uint64_t>(qi) * K.k + i] = -INFINITY;
+            }
+        } else {
+            // an LDS list has n <= kFinishLdsCap (a power of two), so n2 fits; longer lists sort in
+            // the global key buffer
+            uint32_t n2 = 1;
+            while (n2 < n) n2 <<= 1;
+            for (uint32_t i = n + tid; i < n2; i += nt) kk[i] = kKeyMax;
+            bitonic_sort_u64(kk, n2);
+            for (uint32_t i = tid; i < K.k; i += nt) {
+                const bool ok = i < kout;
+                out_slots[static_cast<uint64_t>(qi) * K.k + i] = ok ? static_cast<uint32_t>(kk[i]) : kNone;
+                out_scores[static_cast<uint64_t>(qi) * K.k + i] = ok ? key_score(kk[i]) : -INFINITY;
+            }
+        }
+        return n;
+    };
+    const uint32_t n = total <= kFinishLdsCap ? tail(keys) : tail(Wk.keys + static_cast<uint64_t>(qi) * K.key_cap);
     if (tid == 0) {
         Wk.cut[qi] = cutv;
         Wk.ncand[qi] = n;

@@ -175,8 +175,9 @@ size_t seed_lds(const DevArena& A, uint32_t seed_cap) {
     return ((A.MW + 3) & ~3u) * 4 + 512 * 4 + 32 * 4 + static_cast<size_t>((seed_cap + 3) & ~3u) * 4;
 }
 
+// LDS of finish: hist[256] | scratch[32] | qs[d4] | ent[kFinishLdsCap] (d, slot) | keys[kFinishLdsCap] u64
 size_t finish_lds(const DevArena& A) {
-    return kHistBins * 4 + 32 * 4 + ((A.d + 3) & ~3u) * 4 + static_cast<size_t>(kFinishLdsCap) * 8;
+    return kHistBins * 4 + 32 * 4 + ((A.d + 3) & ~3u) * 4 + static_cast<size_t>(kFinishLdsCap) * 16;
 }
 
 Chain make_chain(uint32_t d, uint32_t vec) {
