@@ -24,6 +24,7 @@ constexpr uint32_t kSeedThreads = 256;
 constexpr uint32_t kScanThreads = 256;
 constexpr uint32_t kFinishThreads = 256;
 constexpr uint32_t kG = 4;               // queries interleaved per cell_scan table pass
+constexpr uint32_t kItemGroups = 1024;   // bucket groups per cell in a scan work item id (bucket_cap <= 4096)
 constexpr uint32_t kHistBins = 256;
 constexpr uint32_t kFinishLdsCap = 2048; // final candidates kept and sorted in LDS up to this many
 constexpr uint32_t kNoAlt = 0xFFFFFFFEu; // entry_alt: the slot has no other home
@@ -68,7 +69,7 @@ struct Ctl {
     uint32_t max_shortlist;
     uint32_t err_seed;        // a seed set exceeded its on-chip capacity
     uint32_t bucket_overflow; // a cell's query bucket was full (the pass falls back to the counting sort)
-    uint32_t pad;
+    uint32_t n_active;        // scan work items: (cell, group of kG bucket entries) (bucket mode)
     unsigned long long seed_blocks, scan_blocks, scan_pairs, survivors, rerank_rows;
 };
 
@@ -104,6 +105,7 @@ struct Work {
     uint32_t* cell_cur;    // M
     uint32_t* qof;         // nq x nprobe
     uint32_t* qbuck;       // M x bucket_cap: the queries probing each cell (bucket mode)
+    uint32_t* active;      // scan work items, cell * kItemGroups + group, in arrival order (bucket mode)
     uint32_t* flag_route;  // nq
     uint32_t* flag_prune;  // nq
     Ctl* ctl;
@@ -301,6 +303,9 @@ __device__ __forceinline__ void lut_chunk(uint32_t dw0, uint32_t dw1, uint32_t d
                 const uint32_t v = reinterpret_cast<const uint32_t*>(tk)[t * 16 + nib];
                 S += v;
                 T += __builtin_amdgcn_perm(0u, v, 0x0c030c01u);  // bytes 1,3 -> u16 lanes
+                // keep both running sums in order every 8 lookups (no re-association into trees
+                // that hold every looked-up word live)
+                if ((t & 7) == 7) asm volatile("" : "+v"(S), "+v"(T));
             }
         }
     }
@@ -1203,6 +1208,9 @@ __device__ __forceinline__ void seed_phase(const DevArena& A, const Work& Wk, co
         const uint32_t c = chosen[i];
         const uint32_t slot = atomicAdd(&Wk.cell_cnt[c], 1u);
         if (K.bucket_cap) {
+            // every kG-th query of a cell opens a scan work item for that group of the bucket
+            if (slot % kG == 0 && slot < K.bucket_cap)
+                Wk.active[atomicAdd(&Wk.ctl->n_active, 1u)] = c * kItemGroups + slot / kG;
             if (slot < K.bucket_cap)
                 Wk.qbuck[static_cast<uint64_t>(c) * K.bucket_cap + slot] = qi;
             else
@@ -1284,27 +1292,13 @@ __global__ void invert_fill_kernel(Work Wk, KParams K) {
 // One workgroup per cell (the CPU loop this replaces is src/index.rs:2231-2275). Lanes own
 // members; each lane's code is loaded once per pass while groups of kG probing queries stream
 // through the LDS table; survivors d <= tau of canonical members are appended per query.
+// Members of cell c against the queries ql[g0 .. g1), kG at a time (the interleaved table).
 template <int NW>
-__global__ void __launch_bounds__(kScanThreads)
-cell_scan_kernel(DevArena A, Work Wk, KParams K) {
+__device__ __forceinline__ void scan_cell_groups(const DevArena& A, const Work& Wk, const KParams& K, uint32_t c,
+                                                 const uint32_t* ql, uint32_t g0, uint32_t g1, uint8_t* table,
+                                                 uint32_t* s_q, uint32_t* s_t) {
     constexpr uint32_t TB = NW * 256;
-    __shared__ __align__(16) uint8_t table[kG * TB];
-    __shared__ uint32_t s_q[kG], s_t[kG];
-    const uint32_t c = blockIdx.x;
-    if (c >= A.M) return;
-    // the queries probing c: its bucket, or its range of the counting-sort inversion
-    uint32_t nqc;
-    const uint32_t* ql;
-    if (K.bucket_cap) {
-        nqc = min(Wk.cell_cnt[c], K.bucket_cap);
-        ql = Wk.qbuck + static_cast<uint64_t>(c) * K.bucket_cap;
-    } else {
-        const uint32_t q0 = Wk.cell_off[c];
-        nqc = Wk.cell_off[c + 1] - q0;
-        ql = Wk.qof + q0;
-    }
     const uint32_t e0 = A.mem_off[c], len = A.mem_off[c + 1] - e0;
-    if (nqc == 0 || len == 0) return;
     const uint32_t tid = threadIdx.x, nt = blockDim.x;
     for (uint32_t ebase = 0; ebase < len; ebase += nt) {
         const uint32_t i = ebase + tid;
@@ -1319,11 +1313,11 @@ cell_scan_kernel(DevArena A, Work Wk, KParams K) {
             const uint32_t tg = A.entry_tag[e];
             kept = kept && tg >= K.tag_lo && tg <= K.tag_hi;
         }
-        for (uint32_t g0 = 0; g0 < nqc; g0 += kG) {
-            const uint32_t ng = min(kG, nqc - g0);
+        for (uint32_t gb = g0; gb < g1; gb += kG) {
+            const uint32_t ng = min(kG, g1 - gb);
             __syncthreads();
             if (tid < kG) {
-                uint32_t qq = tid < ng ? ql[g0 + tid] : kNone;
+                uint32_t qq = tid < ng ? ql[gb + tid] : kNone;
                 s_q[tid] = qq;
                 s_t[tid] = qq != kNone ? Wk.tau[qq] : 0u;
             }
@@ -1332,7 +1326,7 @@ cell_scan_kernel(DevArena A, Work Wk, KParams K) {
                 uint32_t v[kG];
 #pragma unroll
                 for (uint32_t g = 0; g < kG; ++g) {
-                    uint32_t qq = g < ng ? ql[g0 + g] : kNone;
+                    uint32_t qq = g < ng ? ql[gb + g] : kNone;
                     v[g] = qq != kNone ? reinterpret_cast<const uint32_t*>(Wk.lut + static_cast<uint64_t>(qq) * TB)[x4] : 0u;
                 }
                 uint32_t lo01 = __builtin_amdgcn_perm(v[1], v[0], 0x05010400u);
@@ -1374,6 +1368,32 @@ cell_scan_kernel(DevArena A, Work Wk, KParams K) {
                 }
             }
         }
+    }
+}
+
+// The cell-major scan (src/index.rs:2231-2275). Bucket mode: each work item is one cell and one
+// group of kG queries of its bucket, so a popular cell's groups run in parallel workgroups; the
+// grid strides over the items. Counting-sort mode: workgroup c scans cell c for all its queries.
+template <int NW>
+__global__ void __launch_bounds__(kScanThreads, NW >= 16 ? 4 : 8)
+cell_scan_kernel(DevArena A, Work Wk, KParams K) {
+    constexpr uint32_t TB = NW * 256;
+    __shared__ __align__(16) uint8_t table[kG * TB];
+    __shared__ uint32_t s_q[kG], s_t[kG];
+    if (K.bucket_cap) {
+        const uint32_t items = Wk.ctl->n_active;
+        for (uint32_t b = blockIdx.x; b < items; b += gridDim.x) {
+            const uint32_t it = Wk.active[b];
+            const uint32_t c = it / kItemGroups, g0 = (it % kItemGroups) * kG;
+            const uint32_t nqc = min(Wk.cell_cnt[c], K.bucket_cap);
+            scan_cell_groups<NW>(A, Wk, K, c, Wk.qbuck + static_cast<uint64_t>(c) * K.bucket_cap, g0,
+                                 min(g0 + kG, nqc), table, s_q, s_t);
+        }
+    } else {
+        const uint32_t c = blockIdx.x;
+        if (c >= A.M) return;
+        const uint32_t q0 = Wk.cell_off[c];
+        scan_cell_groups<NW>(A, Wk, K, c, Wk.qof + q0, 0, Wk.cell_off[c + 1] - q0, table, s_q, s_t);
     }
 }
 

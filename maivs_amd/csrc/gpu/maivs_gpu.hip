@@ -41,6 +41,7 @@ namespace {
 constexpr float kPruneBand = 4e-6f;
 constexpr float kNucleusBand = 2e-3f;
 constexpr size_t kLdsBudget = 160 * 1024;
+constexpr uint32_t kScanGridMax = 16384;  // workgroups of the bucket-mode scan (they stride over the items)
 }  // namespace
 
 // ================================================================ host side
@@ -249,6 +250,8 @@ int ensure_work(maivs_gpu_ctx* ctx, uint32_t nq, uint32_t nprobe, uint32_t k) {
     rc |= dalloc(ctx, o, &W.qof, nql * nprobe);
     const uint32_t bcap_all = std::max(bcap, ctx->cap_bucket);
     rc |= dalloc(ctx, o, &W.qbuck, static_cast<uint64_t>(A.M) * bcap_all);
+    // scan work items: at most one per kG bucket entries plus one per cell
+    rc |= dalloc(ctx, o, &W.active, static_cast<uint64_t>(A.M) + nql * nprobe / kG + 1);
     rc |= dalloc(ctx, o, &W.flag_route, nql);
     rc |= dalloc(ctx, o, &W.flag_prune, nql);
     rc |= dalloc(ctx, o, &W.ctl, 1);
@@ -429,8 +432,11 @@ int launch_scan(maivs_gpu_ctx* ctx, const KParams& K, bool recount, bool events 
         HIP_TRY(ctx, hipGetLastError());
     }
     if (events) HIP_TRY(ctx, hipEventRecord(ctx->ev[4], ctx->stream));
-    DISPATCH_NW(A.W, hipLaunchKernelGGL(cell_scan_kernel<NW>, dim3(A.M), dim3(kScanThreads), 0, ctx->stream, A,
-                                        W, K));
+    // bucket mode: a grid that strides over the work items (their count is on the device)
+    const uint64_t items = static_cast<uint64_t>(A.M) + static_cast<uint64_t>(K.nq) * K.nprobe / kG + 1;
+    const uint32_t grid = K.bucket_cap ? static_cast<uint32_t>(std::min<uint64_t>(items, kScanGridMax)) : A.M;
+    DISPATCH_NW(A.W, hipLaunchKernelGGL(cell_scan_kernel<NW>, dim3(std::max(grid, 1u)), dim3(kScanThreads), 0,
+                                        ctx->stream, A, W, K));
     HIP_TRY(ctx, hipGetLastError());
     return 0;
 }
