@@ -24,7 +24,8 @@ constexpr uint32_t kSeedThreads = 256;
 constexpr uint32_t kScanThreads = 256;
 constexpr uint32_t kFinishThreads = 256;
 constexpr uint32_t kG = 4;               // queries interleaved per cell_scan table pass
-constexpr uint32_t kItemGroups = 1024;   // bucket groups per cell in a scan work item id (bucket_cap <= 4096)
+constexpr uint32_t kItemQ = 2 * kG;      // queries per scan work item (two interleaved tables)
+constexpr uint32_t kItemGroups = 1024;   // work items per cell in a scan work item id (bucket_cap <= 4096)
 constexpr uint32_t kHistBins = 256;
 constexpr uint32_t kFinishLdsCap = 2048; // final candidates kept and sorted in LDS up to this many
 constexpr uint32_t kNoAlt = 0xFFFFFFFEu; // entry_alt: the slot has no other home
@@ -1208,9 +1209,9 @@ __device__ __forceinline__ void seed_phase(const DevArena& A, const Work& Wk, co
         const uint32_t c = chosen[i];
         const uint32_t slot = atomicAdd(&Wk.cell_cnt[c], 1u);
         if (K.bucket_cap) {
-            // every kG-th query of a cell opens a scan work item for that group of the bucket
-            if (slot % kG == 0 && slot < K.bucket_cap)
-                Wk.active[atomicAdd(&Wk.ctl->n_active, 1u)] = c * kItemGroups + slot / kG;
+            // every kItemQ-th query of a cell opens a scan work item for those bucket entries
+            if (slot % kItemQ == 0 && slot < K.bucket_cap)
+                Wk.active[atomicAdd(&Wk.ctl->n_active, 1u)] = c * kItemGroups + slot / kItemQ;
             if (slot < K.bucket_cap)
                 Wk.qbuck[static_cast<uint64_t>(c) * K.bucket_cap + slot] = qi;
             else
@@ -1292,108 +1293,141 @@ __global__ void invert_fill_kernel(Work Wk, KParams K) {
 // One workgroup per cell (the CPU loop this replaces is src/index.rs:2231-2275). Lanes own
 // members; each lane's code is loaded once per pass while groups of kG probing queries stream
 // through the LDS table; survivors d <= tau of canonical members are appended per query.
-// Members of cell c against the queries ql[g0 .. g1), kG at a time (the interleaved table).
+// One work item: the members of cell c (entries [e0, e0 + len)) against the nqi <= kItemQ queries
+// in s_q / s_t (LDS, already visible), kG per interleaved table. The member data of the first
+// chunk is loaded before the tables are built so both latencies overlap.
 template <int NW>
-__device__ __forceinline__ void scan_cell_groups(const DevArena& A, const Work& Wk, const KParams& K, uint32_t c,
-                                                 const uint32_t* ql, uint32_t g0, uint32_t g1, uint8_t* table,
-                                                 uint32_t* s_q, uint32_t* s_t) {
+__device__ __forceinline__ void scan_item(const DevArena& A, const Work& Wk, const KParams& K, uint32_t c, uint32_t e0,
+                                          uint32_t len, uint32_t nqi, uint8_t (*table)[kG * NW * 256],
+                                          const uint32_t* s_q, const uint32_t* s_t) {
     constexpr uint32_t TB = NW * 256;
-    const uint32_t e0 = A.mem_off[c], len = A.mem_off[c + 1] - e0;
     const uint32_t tid = threadIdx.x, nt = blockDim.x;
-    for (uint32_t ebase = 0; ebase < len; ebase += nt) {
+    const uint32_t ngroups = (nqi + kG - 1) / kG;
+    struct Member {
+        Code<NW> code;
+        uint32_t slot, alt;
+        bool kept;
+    };
+    auto load_member = [&](uint32_t ebase, Member& m) {
         const uint32_t i = ebase + tid;
         const bool have = i < len;
         const uint64_t e = static_cast<uint64_t>(e0) + (have ? i : 0u);  // past the end: member 0, no output
-        Code<NW> code;
-        code.load(A.codes + e * (2 * NW));
-        const uint32_t slot = A.members[e];
-        const uint32_t alt = A.ma == 2 ? A.entry_alt[e] : kNoAlt;
-        bool kept = have;
+        m.code.load(A.codes + e * (2 * NW));
+        m.slot = A.members[e];
+        m.alt = A.ma == 2 ? A.entry_alt[e] : kNoAlt;
+        m.kept = have;
         if (K.filter) {
             const uint32_t tg = A.entry_tag[e];
-            kept = kept && tg >= K.tag_lo && tg <= K.tag_hi;
+            m.kept = m.kept && tg >= K.tag_lo && tg <= K.tag_hi;
         }
-        for (uint32_t gb = g0; gb < g1; gb += kG) {
-            const uint32_t ng = min(kG, g1 - gb);
-            __syncthreads();
-            if (tid < kG) {
-                uint32_t qq = tid < ng ? ql[gb + tid] : kNone;
-                s_q[tid] = qq;
-                s_t[tid] = qq != kNone ? Wk.tau[qq] : 0u;
-            }
-            // interleave the group's tables: table[x*4 + g] = lut_g[x] (4x4 byte transpose)
-            for (uint32_t x4 = tid; x4 < TB / 4; x4 += nt) {
-                uint32_t v[kG];
-#pragma unroll
-                for (uint32_t g = 0; g < kG; ++g) {
-                    uint32_t qq = g < ng ? ql[gb + g] : kNone;
-                    v[g] = qq != kNone ? reinterpret_cast<const uint32_t*>(Wk.lut + static_cast<uint64_t>(qq) * TB)[x4] : 0u;
-                }
-                uint32_t lo01 = __builtin_amdgcn_perm(v[1], v[0], 0x05010400u);
-                uint32_t hi01 = __builtin_amdgcn_perm(v[1], v[0], 0x07030602u);
-                uint32_t lo23 = __builtin_amdgcn_perm(v[3], v[2], 0x05010400u);
-                uint32_t hi23 = __builtin_amdgcn_perm(v[3], v[2], 0x07030602u);
-                uint4 o;
-                o.x = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
-                o.y = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);
-                o.z = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
-                o.w = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
-                reinterpret_cast<uint4*>(table)[x4] = o;
-            }
-            __syncthreads();
-            uint32_t sums[kG];
-            lut_sums<NW, kG>(code, table, sums);
+    };
+    Member m;
+    load_member(0, m);
+    // interleave each group's tables: table[gi][x*4 + g] = lut_{4gi+g}[x] (4x4 byte transpose)
+    for (uint32_t gi = 0; gi < ngroups; ++gi) {
+        for (uint32_t x4 = tid; x4 < TB / 4; x4 += nt) {
+            uint32_t v[kG];
 #pragma unroll
             for (uint32_t g = 0; g < kG; ++g) {
-                const uint32_t qq = s_q[g];
+                const uint32_t qq = s_q[gi * kG + g];
+                v[g] = qq != kNone ? reinterpret_cast<const uint32_t*>(Wk.lut + static_cast<uint64_t>(qq) * TB)[x4] : 0u;
+            }
+            const uint32_t lo01 = __builtin_amdgcn_perm(v[1], v[0], 0x05010400u);
+            const uint32_t hi01 = __builtin_amdgcn_perm(v[1], v[0], 0x07030602u);
+            const uint32_t lo23 = __builtin_amdgcn_perm(v[3], v[2], 0x05010400u);
+            const uint32_t hi23 = __builtin_amdgcn_perm(v[3], v[2], 0x07030602u);
+            uint4 o;
+            o.x = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
+            o.y = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);
+            o.z = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
+            o.w = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
+            reinterpret_cast<uint4*>(table[gi])[x4] = o;
+        }
+    }
+    __syncthreads();
+    for (uint32_t ebase = 0; ebase < len; ebase += nt) {
+        if (ebase) load_member(ebase, m);
+        const uint64_t e = static_cast<uint64_t>(e0) + min(ebase + tid, len - 1);
+        for (uint32_t gi = 0; gi < ngroups; ++gi) {
+            uint32_t sums[kG];
+            lut_sums<NW, kG>(m.code, table[gi], sums);
+#pragma unroll
+            for (uint32_t g = 0; g < kG; ++g) {
+                const uint32_t qq = s_q[gi * kG + g];
                 bool pass = false;
                 uint32_t dv = 0;
-                if (kept && qq != kNone) {
+                if (m.kept && qq != kNone) {
                     dv = A.maxk - sums[g];
-                    if (dv <= s_t[g]) {
+                    if (dv <= s_t[gi * kG + g]) {
                         const uint32_t* probed = Wk.probed + static_cast<uint64_t>(qq) * A.MW;
                         if (A.ma == 2)
-                            pass = !(alt < c && ((probed[alt >> 5] >> (alt & 31)) & 1u));
+                            pass = !(m.alt < c && ((probed[m.alt >> 5] >> (m.alt & 31)) & 1u));
                         else
-                            pass = canonical(A, e, slot, c, probed);
+                            pass = canonical(A, e, m.slot, c, probed);
                     }
                 }
-                uint64_t m = __ballot(pass);
-                if (m) {
+                const uint64_t bm = __ballot(pass);
+                if (bm) {
                     uint32_t wb = 0;
-                    if (lane_id() == 0) wb = atomicAdd(&Wk.cand_cnt[qq], static_cast<uint32_t>(__popcll(m)));
+                    if (lane_id() == 0) wb = atomicAdd(&Wk.cand_cnt[qq], static_cast<uint32_t>(__popcll(bm)));
                     wb = __shfl(wb, 0, kWave);
-                    uint32_t pos = wb + lanes_below(m);
-                    if (pass && pos < K.cand_cap) Wk.cand[static_cast<uint64_t>(qq) * K.cand_cap + pos] = make_uint2(dv, slot);
+                    const uint32_t pos = wb + lanes_below(bm);
+                    if (pass && pos < K.cand_cap)
+                        Wk.cand[static_cast<uint64_t>(qq) * K.cand_cap + pos] = make_uint2(dv, m.slot);
                 }
             }
         }
     }
+    __syncthreads();  // the tables and s_q / s_t are reused by the next item
 }
 
-// The cell-major scan (src/index.rs:2231-2275). Bucket mode: each work item is one cell and one
-// group of kG queries of its bucket, so a popular cell's groups run in parallel workgroups; the
-// grid strides over the items. Counting-sort mode: workgroup c scans cell c for all its queries.
+// The cell-major scan (src/index.rs:2231-2275). Bucket mode: each work item is one cell and up
+// to kItemQ queries of its bucket, so a popular cell's items run in parallel workgroups; the grid
+// strides over the items. Counting-sort mode: workgroup c scans cell c for all its queries,
+// kItemQ at a time.
 template <int NW>
 __global__ void __launch_bounds__(kScanThreads, NW >= 16 ? 4 : 8)
 cell_scan_kernel(DevArena A, Work Wk, KParams K) {
     constexpr uint32_t TB = NW * 256;
-    __shared__ __align__(16) uint8_t table[kG * TB];
-    __shared__ uint32_t s_q[kG], s_t[kG];
+    __shared__ __align__(16) uint8_t table[kItemQ / kG][kG * TB];
+    __shared__ uint32_t s_q[kItemQ], s_t[kItemQ];
+    const uint32_t tid = threadIdx.x;
     if (K.bucket_cap) {
         const uint32_t items = Wk.ctl->n_active;
         for (uint32_t b = blockIdx.x; b < items; b += gridDim.x) {
             const uint32_t it = Wk.active[b];
-            const uint32_t c = it / kItemGroups, g0 = (it % kItemGroups) * kG;
-            const uint32_t nqc = min(Wk.cell_cnt[c], K.bucket_cap);
-            scan_cell_groups<NW>(A, Wk, K, c, Wk.qbuck + static_cast<uint64_t>(c) * K.bucket_cap, g0,
-                                 min(g0 + kG, nqc), table, s_q, s_t);
+            const uint32_t c = it / kItemGroups, g0 = (it % kItemGroups) * kItemQ;
+            // the cell's range, its bucket count and the item's bucket entries, in one round:
+            // g0 + kItemQ <= bucket_cap (both multiples of kItemQ), so the entry reads stay in the bucket
+            const uint32_t e0 = A.mem_off[c], e1 = A.mem_off[c + 1];
+            const uint32_t cnt = min(Wk.cell_cnt[c], K.bucket_cap);
+            const uint32_t qv = tid < kItemQ ? Wk.qbuck[static_cast<uint64_t>(c) * K.bucket_cap + g0 + tid] : kNone;
+            const uint32_t nqi = min(kItemQ, cnt - g0);
+            if (tid < kItemQ) {
+                const bool ok = tid < nqi;
+                s_q[tid] = ok ? qv : kNone;
+                s_t[tid] = ok ? Wk.tau[qv] : 0u;
+            }
+            __syncthreads();
+            scan_item<NW>(A, Wk, K, c, e0, e1 - e0, nqi, table, s_q, s_t);
         }
     } else {
         const uint32_t c = blockIdx.x;
         if (c >= A.M) return;
-        const uint32_t q0 = Wk.cell_off[c];
-        scan_cell_groups<NW>(A, Wk, K, c, Wk.qof + q0, 0, Wk.cell_off[c + 1] - q0, table, s_q, s_t);
+        const uint32_t q0 = Wk.cell_off[c], nqc = Wk.cell_off[c + 1] - q0;
+        const uint32_t e0 = A.mem_off[c], len = A.mem_off[c + 1] - e0;
+        if (len == 0) return;
+        for (uint32_t g0 = 0; g0 < nqc; g0 += kItemQ) {
+            const uint32_t nqi = min(kItemQ, nqc - g0);
+            if (tid < kItemQ) {
+                const bool ok = tid < nqi;
+                const uint32_t qv = ok ? Wk.qof[q0 + g0 + tid] : kNone;
+                s_q[tid] = qv;
+                s_t[tid] = ok ? Wk.tau[qv] : 0u;
+            }
+            __syncthreads();
+            scan_item<NW>(A, Wk, K, c, e0, len, nqi, table, s_q, s_t);
+        }
     }
 }
 

@@ -250,8 +250,8 @@ int ensure_work(maivs_gpu_ctx* ctx, uint32_t nq, uint32_t nprobe, uint32_t k) {
     rc |= dalloc(ctx, o, &W.qof, nql * nprobe);
     const uint32_t bcap_all = std::max(bcap, ctx->cap_bucket);
     rc |= dalloc(ctx, o, &W.qbuck, static_cast<uint64_t>(A.M) * bcap_all);
-    // scan work items: at most one per kG bucket entries plus one per cell
-    rc |= dalloc(ctx, o, &W.active, static_cast<uint64_t>(A.M) + nql * nprobe / kG + 1);
+    // scan work items: at most one per kItemQ bucket entries plus one per cell
+    rc |= dalloc(ctx, o, &W.active, static_cast<uint64_t>(A.M) + nql * nprobe / kItemQ + 1);
     rc |= dalloc(ctx, o, &W.flag_route, nql);
     rc |= dalloc(ctx, o, &W.flag_prune, nql);
     rc |= dalloc(ctx, o, &W.ctl, 1);
@@ -433,7 +433,7 @@ int launch_scan(maivs_gpu_ctx* ctx, const KParams& K, bool recount, bool events 
     }
     if (events) HIP_TRY(ctx, hipEventRecord(ctx->ev[4], ctx->stream));
     // bucket mode: a grid that strides over the work items (their count is on the device)
-    const uint64_t items = static_cast<uint64_t>(A.M) + static_cast<uint64_t>(K.nq) * K.nprobe / kG + 1;
+    const uint64_t items = static_cast<uint64_t>(A.M) + static_cast<uint64_t>(K.nq) * K.nprobe / kItemQ + 1;
     const uint32_t grid = K.bucket_cap ? static_cast<uint32_t>(std::min<uint64_t>(items, kScanGridMax)) : A.M;
     DISPATCH_NW(A.W, hipLaunchKernelGGL(cell_scan_kernel<NW>, dim3(std::max(grid, 1u)), dim3(kScanThreads), 0,
                                         ctx->stream, A, W, K));
