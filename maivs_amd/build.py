@@ -15,7 +15,7 @@ import sysconfig
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
-HOST_SRC = [os.path.join(HERE, "csrc", "host", f) for f in ("bind.cpp", "index.cpp", "tree.cpp")]
+HOST_SRC = [os.path.join(HERE, "csrc", "host", f) for f in ("bind.cpp", "index.cpp", "tree.cpp", "persist.cpp")]
 GPU_SRC = [os.path.join(HERE, "csrc", "gpu", "maivs_gpu.hip")]
 GPU_LIB = os.path.join(HERE, "libmaivs_gpu.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

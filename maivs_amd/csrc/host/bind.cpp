@@ -75,6 +75,8 @@ PYBIND11_MODULE(_maivs, m) {
             PyErr_SetString(PyExc_ValueError, e.what());
         } catch (const maivs::Unsupported& e) {
             PyErr_SetString(PyExc_NotImplementedError, e.what());
+        } catch (const maivs::IoError& e) {
+            PyErr_SetString(PyExc_OSError, e.what());
         }
     });
 
@@ -182,6 +184,24 @@ PYBIND11_MODULE(_maivs, m) {
             },
             py::arg("queries"), py::arg("k"), py::arg("nprobe") = 16, py::arg("target_confidence") = 0.95f,
             py::arg("beta") = 8.0f, py::arg("cell_major") = true)
+        .def(
+            "save",
+            [](PyIndex& s, const std::string& path) {
+                py::gil_scoped_release nogil;
+                translate([&] { s.ix.save(path); });
+            },
+            py::arg("path"))
+        .def_static(
+            "load",
+            [](const std::string& path) {
+                auto p = std::make_unique<PyIndex>(1, "binary", 1, 0, 0);
+                {
+                    py::gil_scoped_release nogil;
+                    translate([&] { p->ix.load_file(path); });
+                }
+                return p;
+            },
+            py::arg("path"))
         .def("stats", [](PyIndex& s) { return s.ix.stats(); })
         .def("__len__", [](PyIndex& s) { return s.ix.len(); })
         .def("recommend", [](PyIndex& s) { return s.ix.recommend(); })

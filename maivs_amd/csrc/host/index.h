@@ -3,8 +3,8 @@
 // search_batch through libmaivs_gpu.so's C ABI on the MI355X.
 //
 // Reference: the pyo3 class FlatCellIndex, src/index.rs:431-566 (state) and :2670-3603
-// (methods). Only the state the batched cell-major search and its build need is kept; the
-// per-query path, HNSW routing, split/merge and persistence are not part of this build.
+// (methods). Only the state the batched cell-major search, its build and persistence need is
+// kept; the per-query path, HNSW routing and split/merge are not part of this build.
 #pragma once
 
 #include <cstdint>
@@ -25,6 +25,9 @@ struct ValueError : std::runtime_error {
     using std::runtime_error::runtime_error;
 };
 struct Unsupported : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+struct IoError : std::runtime_error {
     using std::runtime_error::runtime_error;
 };
 
@@ -78,6 +81,11 @@ public:
                       maivs_gpu_stats* stats = nullptr);
     // Why the batched cell-major path cannot run right now (empty string when it can).
     std::string cellmajor_blocker(bool cell_major) const;
+
+    // ---- persistence (src/persist.rs, format "MAIVS2\0\1" + an extension trailer) ----
+    void save(const std::string& path) const;
+    // Replaces this index's whole state with the file's.
+    void load_file(const std::string& path);
 
     // ---- introspection ----
     std::map<std::string, double> stats() const;
