@@ -15,6 +15,9 @@
  *   maivs_gpu_query_prep     rotate + pack_signs_trunc + FsQuery::new, src/quantize.rs:57-313
  *   maivs_gpu_block_sums     FsQuery::block_sums, src/quantize.rs:323-386
  *   maivs_gpu_route          route_batch, src/index.rs:1873-1980
+ *   maivs_gpu_kmeans         kmeans_spherical, src/tree.rs:179-248, as run by train_centroids'
+ *                            two-level k-means (src/tree.rs:257-348, src/index.rs:2762-2804) and
+ *                            by the centroid tree build (src/tree.rs:354-460)
  */
 #ifndef MAIVS_GPU_H
 #define MAIVS_GPU_H
@@ -184,6 +187,31 @@ int maivs_gpu_last_counters(maivs_gpu_ctx* ctx, maivs_gpu_stats* stats);
 int maivs_gpu_last_candidates(maivs_gpu_ctx* ctx, uint32_t* tau, uint32_t* rest_end,
                               uint32_t* cut, uint32_t* ncand, uint32_t* cand_slots,
                               uint32_t* cand_d, uint64_t cap);
+
+/* ---- index build ---- */
+
+/* One spherical k-means problem of a batch. Its points are rows[first .. first + n) of the
+ * batch's row list; jobs tile the row list in order (first = sum of the earlier jobs' n). */
+typedef struct maivs_kmeans_job {
+    uint32_t first;
+    uint32_t n;       /* points, >= 1 */
+    uint32_t k;       /* clusters, 1 <= k <= n */
+    uint32_t iters;   /* Lloyd iterations (0 leaves the initial centroids and assignment 0) */
+    uint64_t seed;    /* the empty-cluster reseeding state starts at seed | 1 */
+} maivs_kmeans_job;
+
+/*
+ * Batched spherical Lloyd k-means over rows of one host matrix x (n_rows x dim f32, row-major),
+ * bit-identical to the reference's CPU k-means: initial centroid c = point min(c*stride, n-1)
+ * with stride = max(n/k, 1); each iteration assigns every point to the first best centroid by
+ * the 8-lane FMA dot, sums each cluster's points in point order, normalises the sums, and
+ * reseeds empty clusters with xorshift64 picks. rows: the batch's row ids (NULL = 0, 1, 2, ...);
+ * dim <= 2048. Outputs (host): assign[sum n] = cluster within the job at the last iteration,
+ * cents[sum k x dim], the jobs' centroids back to back.
+ */
+int maivs_gpu_kmeans(maivs_gpu_ctx* ctx, const float* x, uint64_t n_rows, uint32_t dim,
+                     const uint32_t* rows, const maivs_kmeans_job* jobs, uint32_t n_jobs,
+                     uint32_t* assign, float* cents);
 
 #ifdef __cplusplus
 }

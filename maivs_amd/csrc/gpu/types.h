@@ -1,0 +1,115 @@
+// Constants and plain structs shared by the search kernels and the host side of the library
+// (the arena in HBM, the per-call work buffers, the control block and the launch parameters).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../../include/maivs_gpu.h"
+
+namespace maivs_dev {
+
+constexpr uint32_t kSeedCells = 8;       // SEED_CELLS, src/index.rs:2018
+constexpr uint32_t kPrepWaves = 4;       // queries per prep workgroup, one wave each
+constexpr uint32_t kPrepReset = 1, kPrepHamming = 2;
+constexpr uint32_t kRouteThreads = 256;
+constexpr uint32_t kSeedThreads = 256;
+constexpr uint32_t kScanThreads = 256;
+constexpr uint32_t kFinishThreads = 256;
+constexpr uint32_t kG = 4;               // queries interleaved per cell_scan table pass
+constexpr uint32_t kItemQ = 2 * kG;      // queries per scan work item (two interleaved tables)
+constexpr uint32_t kItemGroups = 1024;   // work items per cell in a scan work item id (bucket_cap <= 4096)
+constexpr uint32_t kHistBins = 256;
+constexpr uint32_t kFinishLdsCap = 2048; // final candidates kept and sorted in LDS up to this many
+constexpr uint32_t kNoAlt = 0xFFFFFFFEu; // entry_alt: the slot has no other home
+
+// Chain-major row layout for the 8-lane FMA dots: element 8t + l (t < T) of a row is stored at
+// l*Tp + t, the d - 8T tail elements at 8*Tp + i. Lane l of a group of 8 then reads its whole
+// accumulation chain with wide loads, in the reference's order.
+struct Chain {
+    uint32_t T, Tp, tail, stride;
+};
+
+struct DevArena {
+    uint32_t d, P, W, M, N, ma, rerank_mode, npos, maxk, n_live, max_cell_len, MW, Mp;
+    uint64_t E;
+    float fht_scale;
+    Chain cf, cu;               // f32 and u8 chain layouts
+    const uint32_t* codes;      // E x 2W dwords, entry-major 1-bit codes in member order
+    const uint32_t* members;    // E slots
+    const uint32_t* entry_alt;  // E: the entry's other home (max_assign == 2), kNoAlt if none
+    const uint32_t* mem_off;    // M + 1
+    const uint32_t* slot_cells; // N x ma
+    const uint64_t* cent_bits;  // M x W
+    const uint8_t* cent_sq8;    // M x cu.stride (chain-major) or null
+    const float* cents;         // M x cf.stride (chain-major f32 centroids, when cent_sq8 is null)
+    const float* csq_min;
+    const float* csq_step;
+    const float* r_bound;       // M
+    const float* rot_signs;     // 2P
+    const float* vecs;          // N x cf.stride (chain-major f32 rows)
+    const uint8_t* sq8;         // N x cu.stride (chain-major SQ8 rows)
+    const float* sq_min;
+    const float* sq_step;
+    const uint8_t* live;        // M
+    const uint32_t* entry_tag;  // E: the tag of the entry's slot (null without tags)
+};
+
+struct Ctl {
+    uint32_t nflag_route;
+    uint32_t nflag_prune;
+    uint32_t max_cand;        // largest candidate count past the buffer capacity (0 = none)
+    uint32_t err_shortlist;   // a shortlist exceeded the sort capacity
+    uint32_t max_shortlist;
+    uint32_t err_seed;        // a seed set exceeded its on-chip capacity
+    uint32_t bucket_overflow; // a cell's query bucket was full (the pass falls back to the counting sort)
+    uint32_t n_active;        // scan work items: (cell, group of kG bucket entries) (bucket mode)
+    unsigned long long seed_blocks, scan_blocks, scan_pairs, survivors, rerank_rows;
+};
+
+struct Work {
+    float* q;              // nq x d (host-input calls)
+    uint64_t* qbits;       // nq x W
+    uint8_t* lut;          // nq x npos*16
+    float* delta;          // nq
+    float* bias;           // nq
+    float* cqs;            // nq x d: rescore operand q * csq_step (q itself for f32 centroids)
+    float* cqbase;         // nq: sum(q * csq_min), sequential
+    float* rbase;          // nq: SQ8 rerank base sum(q * sq_min), sequential (MAIVS_RERANK_SQ8)
+    uint16_t* hs;          // nq x Mp: Hamming distance to every cell, 0xFFFF for dead cells
+    float* bnd;            // nq x nprobe: adaptive-cut bounds of the probe list (i >= SEED_CELLS)
+    uint32_t* chosen;      // nq x nprobe
+    float* cscore;         // nq x nprobe
+    uint32_t* nchosen;     // nq
+    uint32_t* probed;      // nq x MW
+    uint2* seed;           // nq x seed_cap (d, slot): seed members with d <= tau
+    uint32_t* seed_cnt;    // nq
+    uint32_t* tau;         // nq
+    uint32_t* rest_end;    // nq
+    uint2* cand;           // nq x cand_cap
+    uint32_t* cand_cnt;    // nq
+    uint2* fin;            // nq x fin_cap (d, slot) final candidates
+    uint64_t* keys;        // nq x key_cap (global sort when a final list is large)
+    uint32_t* cut;         // nq
+    uint32_t* ncand;       // nq
+    uint32_t* out_slots;   // nq x k (host-output calls)
+    float* out_scores;     // nq x k
+    uint32_t* cell_cnt;    // M + 1
+    uint32_t* cell_off;    // M + 1
+    uint32_t* cell_cur;    // M
+    uint32_t* qof;         // nq x nprobe
+    uint32_t* qbuck;       // M x bucket_cap: the queries probing each cell (bucket mode)
+    uint32_t* active;      // scan work items, cell * kItemGroups + group, in arrival order (bucket mode)
+    uint32_t* flag_route;  // nq
+    uint32_t* flag_prune;  // nq
+    Ctl* ctl;
+};
+
+struct KParams {
+    uint32_t nq, k, nprobe, want_c, target, adaptive, sort_cap, use_nucleus;
+    uint32_t seed_cap, cand_cap, fin_cap, key_cap, bucket_cap;
+    uint32_t filter, tag_lo, tag_hi;  // keep!: tag in [tag_lo, tag_hi] (filter != 0 only with tags)
+    float tc, beta, at_margin, norm, prune_band, nucleus_band;
+};
+
+}  // namespace maivs_dev

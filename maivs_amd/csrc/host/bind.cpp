@@ -206,6 +206,35 @@ PYBIND11_MODULE(_maivs, m) {
         .def("__len__", [](PyIndex& s) { return s.ix.len(); })
         .def("recommend", [](PyIndex& s) { return s.ix.recommend(); })
         // ---- not in the reference: hooks for the C-ABI tests and the benchmark ----
+        .def("set_gpu_build", [](PyIndex& s, bool on) { s.ix.set_gpu_build(on); },
+             "Run the index build's k-means (train_centroids, the centroid tree) on the GPU; the "
+             "result is bit-identical to the CPU build.")
+        .def("_kmeans",
+             [](PyIndex& s, const py::array& x, std::vector<uint32_t> rows, std::vector<std::vector<uint64_t>> jobs,
+                bool gpu) {
+                 F32Rows r = as_rows(x, "x", "x must be C-contiguous");
+                 std::vector<maivs::KMeansJob> js;
+                 size_t total = 0;
+                 for (auto& j : jobs) {
+                     if (j.size() != 5) throw py::value_error("a job is (first, n, k, iters, seed)");
+                     if (j[0] != total || j[1] == 0) throw py::value_error("jobs must tile the row list in order");
+                     js.push_back(maivs::KMeansJob{j[0], j[1], j[2], j[3], j[4]});
+                     total += j[1];
+                 }
+                 if (rows.empty() ? total > r.rows : rows.size() != total)
+                     throw py::value_error("the row list must hold one row id per point of the jobs");
+                 for (uint32_t v : rows)
+                     if (v >= r.rows) throw py::value_error("row id past the end of x");
+                 std::vector<uint32_t> assign;
+                 std::vector<float> cents;
+                 {
+                     py::gil_scoped_release nogil;
+                     translate([&] { s.ix.run_kmeans(r.ptr, r.rows, r.cols, rows.empty() ? nullptr : rows.data(), js, gpu, assign, cents); });
+                 }
+                 return py::make_tuple(py::cast(assign), py::array_t<float>(static_cast<py::ssize_t>(cents.size()), cents.data()));
+             },
+             py::arg("x"), py::arg("rows"), py::arg("jobs"), py::arg("gpu"),
+             "One batch of k-means jobs (first, n, k, iters, seed) on the CPU or the GPU (test hook).")
         .def("last_search_stats", [](PyIndex& s) { return stats_dict(s.last); },
              "Device timings and work counters of the last search_batch call.")
         .def("cellmajor_blocker", [](PyIndex& s, bool cell_major) { return s.ix.cellmajor_blocker(cell_major); },

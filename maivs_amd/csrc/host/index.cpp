@@ -25,6 +25,8 @@ struct GpuApi {
     int (*upload)(maivs_gpu_ctx*, const maivs_arena_desc*) = nullptr;
     int (*search)(maivs_gpu_ctx*, const float*, uint32_t, const maivs_search_params*, uint32_t*, float*,
                   maivs_gpu_stats*) = nullptr;
+    int (*kmeans)(maivs_gpu_ctx*, const float*, uint64_t, uint32_t, const uint32_t*, const maivs_kmeans_job*,
+                  uint32_t, uint32_t*, float*) = nullptr;
     std::string error;
 };
 
@@ -62,6 +64,7 @@ const GpuApi& gpu_api() {
         api.last_error = reinterpret_cast<decltype(api.last_error)>(sym("maivs_gpu_last_error"));
         api.upload = reinterpret_cast<decltype(api.upload)>(sym("maivs_gpu_upload_arena"));
         api.search = reinterpret_cast<decltype(api.search)>(sym("maivs_gpu_search_batch"));
+        api.kmeans = reinterpret_cast<decltype(api.kmeans)>(sym("maivs_gpu_kmeans"));
     });
     return api;
 }
@@ -92,6 +95,30 @@ public:
     uint64_t uploaded_gen = ~0ull;
     std::mutex mu;
 };
+
+// The k-means runner of the GPU build: every batch of jobs goes to maivs_gpu_kmeans, whose
+// results are bit-identical to run_kmeans_cpu's.
+KMeansRunner FlatCellIndex::gpu_kmeans_runner() {
+    if (!gpu_) gpu_ = std::make_unique<GpuSession>();
+    GpuSession* g = gpu_.get();
+    return [g](const float* x, size_t n_rows, size_t dim, const uint32_t* rows, const std::vector<KMeansJob>& jobs,
+               std::vector<uint32_t>& assign, std::vector<float>& cents) {
+        std::vector<maivs_kmeans_job> js;
+        size_t np = 0, sk = 0;
+        for (const auto& J : jobs) {
+            size_t k = std::min(std::max<size_t>(J.k, 1), J.n);
+            js.push_back(maivs_kmeans_job{static_cast<uint32_t>(J.first), static_cast<uint32_t>(J.n),
+                                          static_cast<uint32_t>(k), static_cast<uint32_t>(J.iters), J.seed});
+            np += J.n;
+            sk += k;
+        }
+        assign.assign(np, 0);
+        cents.assign(sk * dim, 0.0f);
+        g->check(gpu_api().kmeans(g->ctx_, x, n_rows, static_cast<uint32_t>(dim), rows, js.data(),
+                                  static_cast<uint32_t>(js.size()), assign.data(), cents.data()),
+                 "maivs_gpu_kmeans");
+    };
+}
 
 // ---------------------------------------------------------------- construction, config
 
@@ -225,7 +252,9 @@ void FlatCellIndex::train_centroids(const float* data, size_t n_all, size_t n_ce
         n_train = n_all;
     }
     if (n_train == 0) throw ValueError("train_centroids needs at least one vector");
-    std::vector<float> cents = hierarchical_kmeans(train.data(), n_train, dim_, n_cells, seed);
+    KMeansRunner runner;
+    if (gpu_build_) runner = gpu_kmeans_runner();
+    std::vector<float> cents = hierarchical_kmeans(train.data(), n_train, dim_, n_cells, seed, gpu_build_ ? &runner : nullptr);
     size_t k = cents.size() / dim_;
     cells_.clear();
     cells_.resize(k);
@@ -386,7 +415,10 @@ void FlatCellIndex::rebuild_centroid_tree() {  // src/index.rs:684-708
     for (size_t i = 0; i < live.size(); ++i)
         std::memcpy(&flat[i * dim_], cells_[live[i]].centroid.data(), dim_ * sizeof(float));
     auto t = std::make_unique<CentroidTree>();
-    if (t->build(flat.data(), live, dim_, rot_signs_.data(), dim_pad_, n_words_, tree_fanout_, tree_beam_frac_))
+    KMeansRunner runner;
+    if (gpu_build_) runner = gpu_kmeans_runner();
+    if (t->build(flat.data(), live, dim_, rot_signs_.data(), dim_pad_, n_words_, tree_fanout_, tree_beam_frac_,
+                 gpu_build_ ? &runner : nullptr))
         tree_ = std::move(t);
     else
         tree_.reset();

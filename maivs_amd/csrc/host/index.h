@@ -68,6 +68,17 @@ public:
     void set_tags(const std::vector<uint64_t>& ids, const std::vector<uint32_t>& tags);
     void set_filter(std::optional<uint32_t> lo, std::optional<uint32_t> hi);
     void rebuild_tree() { rebuild_centroid_tree(); }
+    // Not in the reference: run the index build's heavy steps on the GPU (bit-identical results).
+    void set_gpu_build(bool on) { gpu_build_ = on; }
+    bool gpu_build() const { return gpu_build_; }
+    // One batch of k-means jobs through the CPU or the GPU runner (test hook).
+    void run_kmeans(const float* x, size_t n_rows, size_t dim, const uint32_t* rows, const std::vector<KMeansJob>& jobs,
+                    bool gpu, std::vector<uint32_t>& assign, std::vector<float>& cents) {
+        if (gpu)
+            gpu_kmeans_runner()(x, n_rows, dim, rows, jobs, assign, cents);
+        else
+            run_kmeans_cpu(x, n_rows, dim, rows, jobs, assign, cents);
+    }
 
     // ---- mutation ----
     void add_batch(const std::vector<uint64_t>& ids, const float* data, size_t n);
@@ -116,6 +127,7 @@ private:
     void compact_arena();
     void recompute_centroid(Cell& c);
     void touch() { ++generation_; compacted_ = false; }
+    KMeansRunner gpu_kmeans_runner();
 
     size_t dim_, rerank_factor_, dim_pad_, n_words_;
     ScanMode scan_mode_;
@@ -170,6 +182,7 @@ private:
     std::vector<float> cents_flat_, r_bound_flat_;
     maivs_arena_desc desc_{};
     uint64_t generation_ = 0;
+    bool gpu_build_ = false;
     std::unique_ptr<GpuSession> gpu_;
 };
 

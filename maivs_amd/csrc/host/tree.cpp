@@ -108,16 +108,59 @@ void kmeans_spherical(const float* x, size_t n, size_t dim, size_t k, size_t ite
     }
 }
 
-std::vector<float> hierarchical_kmeans(const float* x, size_t n, size_t dim, size_t k, uint64_t seed) {
+void run_kmeans_cpu(const float* x, size_t n_rows, size_t dim, const uint32_t* rows, const std::vector<KMeansJob>& jobs,
+                    std::vector<uint32_t>& assign, std::vector<float>& cents) {
+    (void)n_rows;
+    size_t np = 0, sk = 0;
+    std::vector<size_t> coff(jobs.size());
+    for (size_t j = 0; j < jobs.size(); ++j) {
+        coff[j] = sk;
+        np += jobs[j].n;
+        sk += jobs[j].k;
+    }
+    assign.assign(np, 0);
+    cents.assign(sk * dim, 0.0f);
+    // one job: parallel inside it; several (the second level): parallel over jobs
+    const bool single = jobs.size() == 1;
+    auto one = [&](size_t j) {
+        const KMeansJob& J = jobs[j];
+        std::vector<float> buf;
+        const float* xs = x + J.first * dim;
+        if (rows) {
+            buf.resize(J.n * dim);
+            for (size_t r = 0; r < J.n; ++r)
+                std::memcpy(&buf[r * dim], x + static_cast<size_t>(rows[J.first + r]) * dim, dim * sizeof(float));
+            xs = buf.data();
+        }
+        std::vector<uint32_t> a;
+        std::vector<float> cs;
+        kmeans_spherical(xs, J.n, dim, J.k, J.iters, J.seed, a, cs, single);
+        std::copy(a.begin(), a.end(), assign.begin() + J.first);
+        std::copy(cs.begin(), cs.end(), cents.begin() + coff[j] * dim);
+    };
+    if (single)
+        one(0);
+    else
+        parallel_for(jobs.size(), one);
+}
+
+std::vector<float> hierarchical_kmeans(const float* x, size_t n, size_t dim, size_t k, uint64_t seed,
+                                       const KMeansRunner* runner) {
     k = std::min(std::max<size_t>(k, 1), n);
     std::vector<uint32_t> assign;
     std::vector<float> cents;
+    auto run = [&](const uint32_t* rows, const std::vector<KMeansJob>& jobs) {
+        if (runner)
+            (*runner)(x, n, dim, rows, jobs, assign, cents);
+        else
+            run_kmeans_cpu(x, n, dim, rows, jobs, assign, cents);
+    };
     if (k <= 64 || n <= k * 4) {
-        kmeans_spherical(x, n, dim, k, 12, seed, assign, cents, true);
+        run(nullptr, {KMeansJob{0, n, k, 12, seed}});
         return cents;
     }
     size_t k1 = static_cast<size_t>(std::ceil(std::sqrt(static_cast<double>(k))));
-    kmeans_spherical(x, n, dim, k1, 8, seed, assign, cents, true);
+    run(nullptr, {KMeansJob{0, n, k1, 8, seed}});
     std::vector<std::vector<uint32_t>> groups(k1);
     for (size_t i = 0; i < n; ++i) groups[assign[i]].push_back(static_cast<uint32_t>(i));
 
@@ -140,21 +183,26 @@ std::vector<float> hierarchical_kmeans(const float* x, size_t n, size_t dim, siz
         written += subs[g];
     }
     std::vector<float> out(k * dim, 0.0f);
-    std::vector<size_t> order;
-    for (size_t g = 0; g < groups.size(); ++g)
-        if (subs[g] > 0) order.push_back(g);
-    parallel_for(order.size(), [&](size_t oi) {
-        size_t g = order[oi];
-        const auto& idx = groups[g];
-        std::vector<float> buf(idx.size() * dim);
-        for (size_t r = 0; r < idx.size(); ++r)
-            std::memcpy(&buf[r * dim], x + static_cast<size_t>(idx[r]) * dim, dim * sizeof(float));
-        std::vector<uint32_t> a;
-        std::vector<float> cs;
-        kmeans_spherical(buf.data(), idx.size(), dim, subs[g], 12,
-                         seed ^ ((static_cast<uint64_t>(g) + 1) * 0x9E3779B9ull), a, cs, false);
-        std::memcpy(&out[offs[g] * dim], cs.data(), subs[g] * dim * sizeof(float));
-    });
+    // the second level: one job per group with clusters, each over the group's points in order
+    std::vector<uint32_t> rows;
+    std::vector<KMeansJob> jobs;
+    std::vector<size_t> job_group;
+    for (size_t g = 0; g < groups.size(); ++g) {
+        if (subs[g] == 0) continue;
+        jobs.push_back(KMeansJob{rows.size(), groups[g].size(), subs[g], 12,
+                                 seed ^ ((static_cast<uint64_t>(g) + 1) * 0x9E3779B9ull)});
+        job_group.push_back(g);
+        rows.insert(rows.end(), groups[g].begin(), groups[g].end());
+    }
+    if (!jobs.empty()) {
+        run(rows.data(), jobs);
+        size_t coff = 0;
+        for (size_t j = 0; j < jobs.size(); ++j) {
+            size_t g = job_group[j];
+            std::memcpy(&out[offs[g] * dim], &cents[coff * dim], subs[g] * dim * sizeof(float));
+            coff += jobs[j].k;
+        }
+    }
     size_t fill = 0;
     while (written < k) {
         size_t src = (fill * 7919) % n;
@@ -167,7 +215,7 @@ std::vector<float> hierarchical_kmeans(const float* x, size_t n, size_t dim, siz
 
 bool CentroidTree::build(const float* cell_cents, const std::vector<uint32_t>& cell_ids, size_t dim,
                          const float* rot_signs, size_t dim_pad, size_t n_words, size_t fanout,
-                         float beam_frac) {
+                         float beam_frac, const KMeansRunner* runner) {
     size_t m = cell_ids.size();
     if (m < 2 || n_words == 0) return false;
     fanout = std::max<size_t>(fanout, 2);
@@ -191,7 +239,11 @@ bool CentroidTree::build(const float* cell_cents, const std::vector<uint32_t>& c
         if (k >= cur_n) break;
         std::vector<uint32_t> assign;
         std::vector<float> parents;
-        kmeans_spherical(cur.data(), cur_n, dim, k, 10, 0x9E3779B97F4A7C15ull, assign, parents, true);
+        const std::vector<KMeansJob> job{KMeansJob{0, cur_n, k, 10, 0x9E3779B97F4A7C15ull}};
+        if (runner)
+            (*runner)(cur.data(), cur_n, dim, nullptr, job, assign, parents);
+        else
+            run_kmeans_cpu(cur.data(), cur_n, dim, nullptr, job, assign, parents);
         TreeLevel lv;
         lv.n = k;
         lv.child_len.assign(k, 0);

@@ -5,6 +5,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <functional>
 #include <vector>
 
 namespace maivs {
@@ -13,8 +14,25 @@ namespace maivs {
 void kmeans_spherical(const float* x, size_t n, size_t dim, size_t k, size_t iters, uint64_t seed,
                       std::vector<uint32_t>& assign, std::vector<float>& cents, bool parallel);
 
+// A batch of independent spherical k-means problems over rows of one matrix x (n_rows x dim).
+// Job j clusters the points rows[first .. first + n) (row ids into x; no row list = 0, 1, 2, ...)
+// into k clusters with `iters` Lloyd iterations and reseeding state seed | 1. The jobs tile the
+// row list in order. A runner fills assign (sum n, cluster within the job) and cents (sum k x dim,
+// the jobs' centroids back to back). The default runs kmeans_spherical per job on the host; the
+// index's GPU build passes one that calls maivs_gpu_kmeans, which gives bit-identical results.
+struct KMeansJob {
+    size_t first, n, k, iters;
+    uint64_t seed;
+};
+using KMeansRunner = std::function<void(const float* x, size_t n_rows, size_t dim, const uint32_t* rows,
+                                        const std::vector<KMeansJob>& jobs, std::vector<uint32_t>& assign,
+                                        std::vector<float>& cents)>;
+void run_kmeans_cpu(const float* x, size_t n_rows, size_t dim, const uint32_t* rows, const std::vector<KMeansJob>& jobs,
+                    std::vector<uint32_t>& assign, std::vector<float>& cents);
+
 // Two-level balanced k-means, src/tree.rs:257-348. Returns k x dim centroids.
-std::vector<float> hierarchical_kmeans(const float* x, size_t n, size_t dim, size_t k, uint64_t seed);
+std::vector<float> hierarchical_kmeans(const float* x, size_t n, size_t dim, size_t k, uint64_t seed,
+                                       const KMeansRunner* runner = nullptr);
 
 struct TreeLevel {
     size_t n = 0;
@@ -38,7 +56,8 @@ public:
 
     // Build over live cells (cell_cents row i belongs to cell_ids[i]); false if degenerate.
     bool build(const float* cell_cents, const std::vector<uint32_t>& cell_ids, size_t dim,
-               const float* rot_signs, size_t dim_pad, size_t n_words, size_t fanout, float beam_frac);
+               const float* rot_signs, size_t dim_pad, size_t n_words, size_t fanout, float beam_frac,
+               const KMeansRunner* runner = nullptr);
     // Up to `want` leaf cell ids, best first by Hamming (ties in encounter order).
     void search(const uint64_t* q_bits, size_t want, TreeScratch& s, std::vector<uint32_t>& out) const;
     size_t depth() const { return levels_.size(); }
