@@ -18,6 +18,10 @@
  *   maivs_gpu_kmeans         kmeans_spherical, src/tree.rs:179-248, as run by train_centroids'
  *                            two-level k-means (src/tree.rs:257-348, src/index.rs:2762-2804) and
  *                            by the centroid tree build (src/tree.rs:354-460)
+ *   maivs_gpu_place          add_batch's per-vector work, src/index.rs:2442-2610: rotation and
+ *                            sign code, the centroid-tree descent (src/tree.rs:120-159, 559-628),
+ *                            exact centroid scores and the home choice (assign_cells,
+ *                            pick_orthogonal, :2480-2560), the i8 / SQ8 copy (:3083-3123)
  */
 #ifndef MAIVS_GPU_H
 #define MAIVS_GPU_H
@@ -212,6 +216,46 @@ typedef struct maivs_kmeans_job {
 int maivs_gpu_kmeans(maivs_gpu_ctx* ctx, const float* x, uint64_t n_rows, uint32_t dim,
                      const uint32_t* rows, const maivs_kmeans_job* jobs, uint32_t n_jobs,
                      uint32_t* assign, float* cents);
+
+/* The centroid tree (src/tree.rs) in its compacted layout: every node's children are contiguous
+ * in the next level (or the leaves), child_start / child_len give the range. */
+typedef struct maivs_tree_desc {
+    uint32_t n_levels;            /* 0 = no tree: every cell is a candidate */
+    uint32_t n_leaf;
+    uint32_t want;                /* leaves kept at the end, max(64, 8 * max_assign) */
+    uint32_t reserved;
+    const uint32_t* level_n;      /* n_levels: nodes per level, coarsest first */
+    const uint32_t* beams;        /* n_levels: nodes kept per level (CentroidTree::beams(want)) */
+    const uint64_t* level_codes;  /* sum(level_n) x n_words, level by level */
+    const uint32_t* child_start;  /* sum(level_n) */
+    const uint32_t* child_len;    /* sum(level_n) */
+    const uint64_t* leaf_codes;   /* n_leaf x n_words */
+    const uint32_t* leaf_cells;   /* n_leaf: the cell of each leaf */
+} maivs_tree_desc;
+
+/* What placing a vector reads from the index (host pointers). */
+typedef struct maivs_place_desc {
+    uint32_t dim, dim_pad, n_words, n_cells;
+    uint32_t max_assign;          /* homes per vector, 1..64 */
+    float spill_lambda;           /* > 0: orthogonal polysemy strength */
+    float spill_margin;           /* else: homes within this score of the best */
+    uint32_t code_mode;           /* 0: none, 1: per-dimension SQ8, 2: global int8 (quant_scale) */
+    float quant_scale;
+    uint32_t reserved;
+    const float* rot_signs;       /* 2 x dim_pad */
+    const float* centroids;       /* n_cells x dim (f32) */
+    const float* sq_min;          /* dim (code_mode 1) */
+    const float* sq_step;         /* dim (code_mode 1) */
+    maivs_tree_desc tree;
+} maivs_place_desc;
+
+/*
+ * Place n vectors (host, n x dim f32), bit-identical to the reference's CPU placement: homes
+ * n x max_assign (cell ids, primary first, UINT32_MAX padded), bits n x n_words (the 1-bit
+ * code), codes n x dim (the i8 / SQ8 copy; may be NULL when code_mode is 0).
+ */
+int maivs_gpu_place(maivs_gpu_ctx* ctx, const maivs_place_desc* desc, const float* x, uint32_t n,
+                    uint32_t* homes, uint64_t* bits, int8_t* codes);
 
 #ifdef __cplusplus
 }

@@ -14,6 +14,7 @@
 #include <rocprim/device/device_radix_sort.hpp>
 
 #include <algorithm>
+#include <cmath>
 #include <cstring>
 #include <vector>
 
@@ -178,6 +179,122 @@ extern "C" int maivs_gpu_kmeans(maivs_gpu_ctx* ctx, const float* x, uint64_t n_r
     HIP_TRY(ctx, hipGetLastError());
     HIP_TRY(ctx, hipMemcpyAsync(assign, d_best, static_cast<size_t>(np) * 4, hipMemcpyDeviceToHost, ctx->stream));
     HIP_TRY(ctx, hipMemcpyAsync(cents, d_cents, static_cast<size_t>(sk) * dim * 4, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+extern "C" int maivs_gpu_place(maivs_gpu_ctx* ctx, const maivs_place_desc* pd, const float* x, uint32_t n,
+                               uint32_t* homes, uint64_t* bits, int8_t* codes) {
+    if (!ctx) return MAIVS_ERR_ARG;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    if (!pd || !x || !homes || !bits || !pd->rot_signs || !pd->centroids)
+        return fail(ctx, MAIVS_ERR_ARG, "maivs_gpu_place: null buffer");
+    if (n == 0) return 0;
+    const maivs_place_desc& D = *pd;
+    const maivs_tree_desc& T = D.tree;
+    const uint32_t d = D.dim, P = D.dim_pad, W = D.n_words, M = D.n_cells, ma = D.max_assign;
+    if (d == 0 || P < 64 || P > 2048 || (P & (P - 1)) != 0 || d > P || W == 0 || W * 64 > P || M == 0)
+        return fail(ctx, MAIVS_ERR_UNSUPPORTED, "maivs_gpu_place: dim %u / dim_pad %u / words %u / cells %u", d, P, W, M);
+    if (ma == 0 || ma > 64) return fail(ctx, MAIVS_ERR_UNSUPPORTED, "maivs_gpu_place: max_assign %u outside [1, 64]", ma);
+    if (D.code_mode > 2 || (D.code_mode && !codes) || (D.code_mode == 1 && (!D.sq_min || !D.sq_step)))
+        return fail(ctx, MAIVS_ERR_ARG, "maivs_gpu_place: bad code mode");
+    uint32_t total_nodes = 0, cap = 1;
+    std::vector<uint32_t> lv_off(T.n_levels + 1, 0);
+    if (T.n_levels) {
+        if (!T.level_n || !T.beams || !T.level_codes || !T.child_start || !T.child_len || !T.leaf_codes ||
+            !T.leaf_cells || T.n_leaf == 0 || T.want == 0)
+            return fail(ctx, MAIVS_ERR_ARG, "maivs_gpu_place: incomplete tree");
+        for (uint32_t l = 0; l < T.n_levels; ++l) {
+            lv_off[l + 1] = lv_off[l] + T.level_n[l];
+            cap = std::max(cap, T.beams[l]);
+        }
+        total_nodes = lv_off[T.n_levels];
+        // every child range must lie inside the next level (or the leaves); leaves name real cells
+        for (uint32_t l = 0; l < T.n_levels; ++l) {
+            const uint32_t next = l + 1 < T.n_levels ? T.level_n[l + 1] : T.n_leaf;
+            for (uint32_t j = lv_off[l]; j < lv_off[l + 1]; ++j)
+                if (static_cast<uint64_t>(T.child_start[j]) + T.child_len[j] > next)
+                    return fail(ctx, MAIVS_ERR_ARG, "maivs_gpu_place: child range past level %u", l + 1);
+        }
+        for (uint32_t j = 0; j < T.n_leaf; ++j)
+            if (T.leaf_cells[j] >= M) return fail(ctx, MAIVS_ERR_ARG, "maivs_gpu_place: leaf cell out of range");
+    }
+    const uint32_t want = T.n_levels ? T.want : 1;
+    const uint32_t words = place_lds_words(P, d, W, cap, want);
+    const uint32_t lds_per_wave = (words * 4 + 15) & ~15u;
+    if (static_cast<size_t>(lds_per_wave) * kPlaceWaves > 160 * 1024)
+        return fail(ctx, MAIVS_ERR_UNSUPPORTED, "maivs_gpu_place: %u bytes of LDS per wave", lds_per_wave);
+
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    Scratch S(ctx);
+    PlaceArgs a{};
+    float *d_x, *d_signs, *d_cents, *d_sqmin = nullptr, *d_sqstep = nullptr;
+    uint32_t *d_homes, *d_lvoff = nullptr, *d_cs = nullptr, *d_cl = nullptr, *d_beams = nullptr, *d_leaf_ids = nullptr;
+    uint64_t *d_bits, *d_lvcodes = nullptr, *d_leaf_codes = nullptr;
+    int8_t* d_codes = nullptr;
+    int rc = 0;
+    if ((rc = S.upload(&d_x, x, static_cast<size_t>(n) * d)) || (rc = S.upload(&d_signs, D.rot_signs, 2 * static_cast<size_t>(P))) ||
+        (rc = S.upload(&d_cents, D.centroids, static_cast<size_t>(M) * d)) || (rc = S.alloc(&d_homes, static_cast<size_t>(n) * ma)) ||
+        (rc = S.alloc(&d_bits, static_cast<size_t>(n) * W)))
+        return rc;
+    if (D.code_mode) {
+        if ((rc = S.alloc(&d_codes, static_cast<size_t>(n) * d))) return rc;
+        if (D.code_mode == 1 && ((rc = S.upload(&d_sqmin, D.sq_min, d)) || (rc = S.upload(&d_sqstep, D.sq_step, d)))) return rc;
+    }
+    if (T.n_levels) {
+        if ((rc = S.upload(&d_lvoff, lv_off.data(), lv_off.size())) ||
+            (rc = S.upload(&d_lvcodes, T.level_codes, static_cast<size_t>(total_nodes) * W)) ||
+            (rc = S.upload(&d_cs, T.child_start, total_nodes)) || (rc = S.upload(&d_cl, T.child_len, total_nodes)) ||
+            (rc = S.upload(&d_beams, T.beams, T.n_levels)) ||
+            (rc = S.upload(&d_leaf_codes, T.leaf_codes, static_cast<size_t>(T.n_leaf) * W)) ||
+            (rc = S.upload(&d_leaf_ids, T.leaf_cells, T.n_leaf)))
+            return rc;
+    }
+    a.x = d_x;
+    a.signs = d_signs;
+    a.cents = d_cents;
+    a.lv_off = d_lvoff;
+    a.lv_codes = d_lvcodes;
+    a.lv_cs = d_cs;
+    a.lv_cl = d_cl;
+    a.beams = d_beams;
+    a.leaf_codes = d_leaf_codes;
+    a.leaf_ids = d_leaf_ids;
+    a.sq_min = d_sqmin;
+    a.sq_step = d_sqstep;
+    a.homes = d_homes;
+    a.bits = d_bits;
+    a.codes = d_codes;
+    a.fht_scale = 1.0f / std::sqrt(static_cast<float>(P));
+    a.spill_lambda = D.spill_lambda;
+    a.spill_margin = D.spill_margin;
+    a.quant_scale = D.quant_scale;
+    a.n = n;
+    a.d = d;
+    a.P = P;
+    a.W = W;
+    a.M = M;
+    a.n_levels = T.n_levels;
+    a.want = want;
+    a.ma = ma;
+    a.kept_cap = cap;
+    a.code_mode = D.code_mode;
+    a.lds_per_wave = lds_per_wave;
+    const uint32_t blocks = static_cast<uint32_t>(std::min<uint64_t>((n + kPlaceWaves - 1) / kPlaceWaves, 4096));
+    const size_t lds = static_cast<size_t>(lds_per_wave) * kPlaceWaves;
+    switch (P / 64) {
+        case 1: place_kernel<1><<<blocks, kPlaceWaves * kWave, lds, ctx->stream>>>(a); break;
+        case 2: place_kernel<2><<<blocks, kPlaceWaves * kWave, lds, ctx->stream>>>(a); break;
+        case 4: place_kernel<4><<<blocks, kPlaceWaves * kWave, lds, ctx->stream>>>(a); break;
+        case 8: place_kernel<8><<<blocks, kPlaceWaves * kWave, lds, ctx->stream>>>(a); break;
+        case 16: place_kernel<16><<<blocks, kPlaceWaves * kWave, lds, ctx->stream>>>(a); break;
+        default: place_kernel<32><<<blocks, kPlaceWaves * kWave, lds, ctx->stream>>>(a); break;
+    }
+    HIP_TRY(ctx, hipGetLastError());
+    HIP_TRY(ctx, hipMemcpyAsync(homes, d_homes, static_cast<size_t>(n) * ma * 4, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(ctx, hipMemcpyAsync(bits, d_bits, static_cast<size_t>(n) * W * 8, hipMemcpyDeviceToHost, ctx->stream));
+    if (D.code_mode)
+        HIP_TRY(ctx, hipMemcpyAsync(codes, d_codes, static_cast<size_t>(n) * d, hipMemcpyDeviceToHost, ctx->stream));
     HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
     return 0;
 }

@@ -212,3 +212,394 @@ __global__ void km_reseed_kernel(KmArgs a, uint32_t it) {
 }
 
 }  // namespace maivs_dev
+
+// ================================================================ placement (add_batch)
+
+namespace maivs_dev {
+
+// Placement of new vectors (src/index.rs:2442-2560 with the tree descent of src/tree.rs:120-159,
+// 559-628), one wave per vector:
+//   1. the rotation (2 x sign flip + FWHT, as the search's query prep) and the 1-bit code;
+//   2. with a centroid tree: Hamming beam descent, each level keeping its `beam` smallest
+//      distances with ties in encounter order (keep_smallest), children of the kept nodes in
+//      order; the leaves keep `want`; no tree, or an empty result: every cell, in order;
+//   3. exact 8-lane FMA dots against the candidates' f32 centroids;
+//   4. the homes: max_assign 1 = the first best; else the top of (score desc, cell asc), either
+//      cut at best - spill_margin or, with a polysemy strength, chosen greedily from the best 16
+//      by 2 - 2 s_j + sum over chosen homes h of lam * p^2, p = (1 - s_h - s_j + <c_h, c_j>) /
+//      sqrt(max(2 - 2 s_h, 1e-12)), first minimum;
+//   5. the i8 / SQ8 code of the vector when the index keeps one.
+constexpr uint32_t kPlaceWaves = 4;
+constexpr uint32_t kPlacePool = 16;  // candidates the orthogonal choice considers (src/index.rs:2524)
+
+struct PlaceArgs {
+    const float* x;            // n x d
+    const float* signs;        // 2 x P
+    const float* cents;        // M x d
+    const uint32_t* lv_off;    // tree levels: node offsets (n_levels + 1), coarsest first
+    const uint64_t* lv_codes;  // sum of level sizes x W
+    const uint32_t* lv_cs;     // child start of each node (index into the next level / the leaves)
+    const uint32_t* lv_cl;     // child count of each node
+    const uint32_t* beams;     // n_levels
+    const uint64_t* leaf_codes;  // n_leaf x W
+    const uint32_t* leaf_ids;    // n_leaf: cell of each leaf
+    const float* sq_min;
+    const float* sq_step;
+    uint32_t* homes;           // n x ma, UINT32_MAX padded
+    uint64_t* bits;            // n x W
+    int8_t* codes;             // n x d when code_mode != 0
+    float fht_scale, spill_lambda, spill_margin, quant_scale;
+    uint32_t n, d, P, W, M, n_levels, want, ma, kept_cap, code_mode, lds_per_wave;
+};
+
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Per-wave LDS of the placement kernel, in order: qb[W] u64 | xs[P] | vs[d4] | hist[bits + 1, to 4]
+// | rbase[cap + 1] | rpre[cap + 2] | knodes[cap] | outc[want]   (u32 / f32 words after qb)
+struct PlaceLds {
+    uint64_t* qb;
+    float *xs, *vs;
+    uint32_t *hist, *rbase, *rpre, *knodes, *outc;
+};
+
+__host__ __device__ inline uint32_t place_lds_words(uint32_t P, uint32_t d, uint32_t W, uint32_t cap, uint32_t want) {
+    const uint32_t d4 = (d + 3) & ~3u, hb = (W * 64 + 1 + 3) & ~3u;
+    return 2 * W + P + d4 + hb + (cap + 1) + (cap + 2) + cap + want;
+}
+
+__device__ __forceinline__ PlaceLds place_lds(uint8_t* base, const PlaceArgs& a) {
+    PlaceLds L;
+    L.qb = reinterpret_cast<uint64_t*>(base);
+    L.xs = reinterpret_cast<float*>(L.qb + a.W);
+    L.vs = L.xs + a.P;
+    L.hist = reinterpret_cast<uint32_t*>(L.vs + ((a.d + 3) & ~3u));
+    L.rbase = L.hist + ((a.W * 64 + 1 + 3) & ~3u);
+    L.rpre = L.rbase + a.kept_cap + 1;
+    L.knodes = L.rpre + a.kept_cap + 2;
+    L.outc = L.knodes + a.kept_cap;
+    return L;
+}
+
+__device__ __forceinline__ uint32_t hamming_lds(const uint64_t* qb, const uint64_t* code, uint32_t W) {
+    uint32_t h = 0;
+    for (uint32_t w = 0; w < W; ++w) h += __popcll(qb[w] ^ code[w]);
+    return h;
+}
+
+// Total-order key of an f32 (ascending), for a first-minimum search.
+__device__ __forceinline__ uint32_t asc_f32_key(float f) {
+    const uint32_t b = __float_as_uint(f == 0.0f ? 0.0f : f);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// keep_smallest over the frontier positions [0, F) with distance hd(p): emit(k, p) for the kept
+// entries in encounter order (k = 0, 1, ...). Returns the number kept = min(keep, F).
+template <class HD, class EMIT>
+__device__ uint32_t wave_keep_smallest(uint32_t F, uint32_t keep, uint32_t bits, uint32_t* hist, HD hd, EMIT emit) {
+    const uint32_t lane = lane_id();
+    if (keep >= F) {
+        for (uint32_t p = lane; p < F; p += kWave) emit(p, p);
+        return F;
+    }
+    for (uint32_t j = lane; j <= bits; j += kWave) hist[j] = 0;
+    wave_sync();
+    for (uint32_t p = lane; p < F; p += kWave) atomicAdd(&hist[hd(p)], 1u);
+    wave_sync();
+    // t = the smallest distance with count(h <= t) >= keep; below = count(h < t)
+    const uint32_t nb = bits + 1, bpl = (nb + kWave - 1) / kWave;
+    const uint32_t b0 = min(lane * bpl, nb), b1 = min(b0 + bpl, nb);
+    uint32_t mine = 0;
+    for (uint32_t b = b0; b < b1; ++b) mine += hist[b];
+    uint32_t incl = mine;
+    for (int o = 1; o < kWave; o <<= 1) {
+        const uint32_t y = __shfl_up(incl, o, kWave);
+        if (lane >= static_cast<uint32_t>(o)) incl += y;
+    }
+    const uint32_t excl = incl - mine;
+    const bool here = excl < keep && incl >= keep;
+    uint32_t t = 0, below = 0;
+    if (here) {
+        uint32_t cum = excl;
+        for (uint32_t b = b0; b < b1; ++b) {
+            if (cum + hist[b] >= keep) {
+                t = b;
+                below = cum;
+                break;
+            }
+            cum += hist[b];
+        }
+    }
+    const uint64_t hm = __ballot(here);
+    const int src = __ffsll(static_cast<long long>(hm)) - 1;
+    t = __shfl(t, src, kWave);
+    below = __shfl(below, src, kWave);
+    const uint32_t need_eq = keep - below;
+    uint32_t eq_seen = 0, kept = 0;
+    for (uint32_t c0 = 0; c0 < F; c0 += kWave) {
+        const uint32_t p = c0 + lane;
+        const bool valid = p < F;
+        const uint32_t h = valid ? hd(p) : 0xFFFFFFFFu;
+        const uint64_t eqm = __ballot(valid && h == t);
+        const bool take = valid && (h < t || (h == t && eq_seen + lanes_below(eqm) < need_eq));
+        const uint64_t tm = __ballot(take);
+        if (take) emit(kept + lanes_below(tm), p);
+        eq_seen += __popcll(eqm);
+        kept += __popcll(tm);
+    }
+    return kept;
+}
+
+// Frontier position p -> node id, from the ranges of the kept parents (rpre: prefix of lengths).
+__device__ __forceinline__ uint32_t frontier_node(const uint32_t* rbase, const uint32_t* rpre, uint32_t nr, uint32_t p) {
+    uint32_t lo = 0, hi = nr;  // the last r with rpre[r] <= p
+    while (hi - lo > 1) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (rpre[mid] <= p) lo = mid; else hi = mid;
+    }
+    return rbase[lo] + (p - rpre[lo]);
+}
+
+// Exact dot_f32(a, b) by one lane: 8 accumulators, hsum, sequential tail (src/index.rs:136-152).
+template <class LA, class LB>
+__device__ __forceinline__ float dot_lane(uint32_t d, LA la, LB lb) {
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    const uint32_t d8 = d & ~7u;
+    for (uint32_t t = 0; t < d8; t += 8) {
+#pragma unroll
+        for (uint32_t l = 0; l < 8; ++l) acc[l] = __builtin_fmaf(la(t + l), lb(t + l), acc[l]);
+    }
+    float s = ((acc[0] + acc[4]) + (acc[2] + acc[6])) + ((acc[1] + acc[5]) + (acc[3] + acc[7]));
+    for (uint32_t e = d8; e < d; ++e) s += la(e) * lb(e);
+    return s;
+}
+
+template <int EPL>
+__global__ void __launch_bounds__(kPlaceWaves * kWave) place_kernel(PlaceArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const uint32_t lane = lane_id(), wv = threadIdx.x / kWave;
+    const PlaceLds L = place_lds(smem + static_cast<size_t>(wv) * a.lds_per_wave, a);
+    const uint32_t d = a.d, P = a.P, W = a.W, bits = W * 64, ma = a.ma;
+    for (uint32_t i = blockIdx.x * kPlaceWaves + wv; i < a.n; i += gridDim.x * kPlaceWaves) {
+        const float* v = a.x + static_cast<uint64_t>(i) * d;
+        for (uint32_t j = lane; j < d; j += kWave) L.vs[j] = v[j];
+        wave_sync();
+        // ---- the i8 / SQ8 copy (src/index.rs:2582-2610, 3083-3123)
+        if (a.code_mode) {
+            int8_t* out = a.codes + static_cast<uint64_t>(i) * d;
+            for (uint32_t j = lane; j < d; j += kWave) {
+                const float x = L.vs[j];
+                float c;
+                if (a.code_mode == 1) {
+                    c = roundf((x - a.sq_min[j]) / a.sq_step[j]);
+                    c = fminf(fmaxf(c, 0.0f), 255.0f);
+                    out[j] = static_cast<int8_t>(static_cast<uint8_t>(c));
+                } else {
+                    c = roundf(x * a.quant_scale);
+                    c = fminf(fmaxf(c, -127.0f), 127.0f);
+                    out[j] = static_cast<int8_t>(c);
+                }
+            }
+        }
+        // ---- rotation: element lane*EPL + e in x[e]; levels ascending, in-lane then cross-lane
+        float x[EPL];
+        const uint32_t base = lane * EPL;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) x[e] = base + e < d ? L.vs[base + e] : 0.0f;
+        for (int r = 0; r < 2; ++r) {
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) x[e] *= a.signs[r * P + base + e];
+#pragma unroll
+            for (int h = 1; h < EPL; h <<= 1) {
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) {
+                    if ((e & h) == 0) {
+                        const float u = x[e], w = x[e + h];
+                        x[e] = u + w;
+                        x[e + h] = u - w;
+                    }
+                }
+            }
+#pragma unroll
+            for (uint32_t m = 1; m < kWave; m <<= 1) {
+                const bool upper = (lane & m) != 0;
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) {
+                    const float w = __shfl_xor(x[e], static_cast<int>(m), kWave);
+                    x[e] = upper ? w - x[e] : x[e] + w;
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) x[e] *= a.fht_scale;
+        }
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) L.xs[base + e] = x[e];
+        wave_sync();
+        for (uint32_t w = 0; w < W; ++w) {
+            const uint64_t m = __ballot(L.xs[64 * w + lane] < 0.0f);
+            if (lane == 0) {
+                L.qb[w] = m;
+                a.bits[static_cast<uint64_t>(i) * W + w] = m;
+            }
+        }
+        wave_sync();
+        // ---- tree descent (src/tree.rs:574-628)
+        uint32_t nout = 0;
+        bool use_tree = a.n_levels > 0;
+        if (use_tree) {
+            uint32_t nr = 1;
+            if (lane == 0) {
+                L.rbase[0] = 0;
+                L.rpre[0] = 0;
+                L.rpre[1] = a.lv_off[1] - a.lv_off[0];
+            }
+            wave_sync();
+            uint32_t F = a.lv_off[1] - a.lv_off[0];
+            for (uint32_t li = 0; li < a.n_levels && use_tree; ++li) {
+                const uint64_t* codes = a.lv_codes + static_cast<uint64_t>(a.lv_off[li]) * W;
+                const uint32_t keep = min(a.beams[li], F);
+                if (keep == 0) {
+                    use_tree = false;
+                    break;
+                }
+                const uint32_t nk = wave_keep_smallest(
+                    F, keep, bits, L.hist,
+                    [&](uint32_t p) {
+                        const uint32_t node = frontier_node(L.rbase, L.rpre, nr, p);
+                        return hamming_lds(L.qb, codes + static_cast<uint64_t>(node) * W, W);
+                    },
+                    [&](uint32_t k, uint32_t p) { L.knodes[k] = frontier_node(L.rbase, L.rpre, nr, p); });
+                wave_sync();
+                // children of the kept nodes, in order: the next frontier's ranges
+                const uint32_t* cs = a.lv_cs + a.lv_off[li];
+                const uint32_t* cl = a.lv_cl + a.lv_off[li];
+                uint32_t carry = 0;
+                for (uint32_t k0 = 0; k0 < nk; k0 += kWave) {
+                    const uint32_t k = k0 + lane;
+                    const uint32_t node = k < nk ? L.knodes[k] : 0u;
+                    const uint32_t len = k < nk ? cl[node] : 0u;
+                    uint32_t incl = len;
+                    for (int o = 1; o < kWave; o <<= 1) {
+                        const uint32_t y = __shfl_up(incl, o, kWave);
+                        if (lane >= static_cast<uint32_t>(o)) incl += y;
+                    }
+                    if (k < nk) {
+                        L.rbase[k] = cs[node];
+                        L.rpre[k] = carry + incl - len;
+                    }
+                    carry += __shfl(incl, kWave - 1, kWave);
+                }
+                if (lane == 0) L.rpre[nk] = carry;
+                wave_sync();
+                nr = nk;
+                F = carry;
+            }
+            if (use_tree) {
+                const uint32_t keep = min(a.want, F);
+                if (keep == 0) {
+                    use_tree = false;
+                } else {
+                    nout = wave_keep_smallest(
+                        F, keep, bits, L.hist,
+                        [&](uint32_t p) {
+                            const uint32_t leaf = frontier_node(L.rbase, L.rpre, nr, p);
+                            return hamming_lds(L.qb, a.leaf_codes + static_cast<uint64_t>(leaf) * W, W);
+                        },
+                        [&](uint32_t k, uint32_t p) { L.outc[k] = a.leaf_ids[frontier_node(L.rbase, L.rpre, nr, p)]; });
+                    wave_sync();
+                }
+            }
+        }
+        if (!use_tree) nout = a.M;  // every cell, in order (src/index.rs:2480-2509)
+        // ---- exact scores and the running selection
+        uint64_t kmin = kKeyMax;  // ma == 1: (score desc, position asc)
+        uint64_t top = kKeyMax;   // ma > 1: the 64 best (score desc, cell asc), ascending over lanes
+        for (uint32_t c0 = 0; c0 < nout; c0 += kWave) {
+            const uint32_t j = c0 + lane;
+            const bool valid = j < nout;
+            const uint32_t cell = valid ? (use_tree ? L.outc[j] : j) : 0u;
+            float s = 0.0f;
+            if (valid) {
+                const float* cr = a.cents + static_cast<uint64_t>(cell) * d;
+                s = dot_lane(d, [&](uint32_t e) { return L.vs[e]; }, [&](uint32_t e) { return cr[e]; });
+            }
+            if (ma <= 1) {
+                if (valid) kmin = min(kmin, desc_score_key(s, j));
+            } else {
+                uint64_t ck[1] = {valid ? desc_score_key(s, cell) : kKeyMax};
+                wave_sort_u64<1>(ck);
+                const uint64_t other = __shfl(ck[0], kWave - 1 - lane, kWave);
+                uint64_t m[1] = {min(top, other)};
+                wave_sort_u64<1>(m);
+                top = m[0];
+            }
+        }
+        uint32_t* hout = a.homes + static_cast<uint64_t>(i) * ma;
+        if (ma <= 1) {
+            const uint64_t best = [&] {
+                uint64_t b = kmin;
+                for (int o = 32; o > 0; o >>= 1) {
+                    const uint64_t y = __shfl_xor(b, o, kWave);
+                    b = y < b ? y : b;
+                }
+                return b;
+            }();
+            const uint32_t pos = best == kKeyMax ? 0u : static_cast<uint32_t>(best);
+            if (lane == 0) hout[0] = use_tree ? L.outc[pos] : pos;
+            continue;
+        }
+        const uint32_t ncand = min(nout, static_cast<uint32_t>(kWave));
+        const float my_s = key_score(top);
+        const uint32_t my_cell = static_cast<uint32_t>(top);
+        if (a.spill_lambda > 0.0f) {
+            // pick_orthogonal (src/index.rs:2523-2560) over the best min(16, n) candidates
+            const uint32_t pool = min(kPlacePool, nout);
+            const uint32_t r = min(ma, pool);
+            const bool in_pool = lane < pool;
+            float loss = 2.0f - 2.0f * my_s;
+            bool taken = lane == 0;
+            uint32_t nh = 1;
+            uint32_t h_cell = __shfl(my_cell, 0, kWave);
+            float h_s = __shfl(my_s, 0, kWave);
+            if (lane == 0) hout[0] = h_cell;
+            while (nh < r) {
+                // add the newest home's term to every open candidate's loss
+                if (in_pool && !taken) {
+                    const float rn = __builtin_sqrtf(fmaxf(2.0f - 2.0f * h_s, 1e-12f));
+                    const float* ch = a.cents + static_cast<uint64_t>(h_cell) * d;
+                    const float* cj = a.cents + static_cast<uint64_t>(my_cell) * d;
+                    const float g = dot_lane(d, [&](uint32_t e) { return ch[e]; }, [&](uint32_t e) { return cj[e]; });
+                    const float p = (((1.0f - h_s) - my_s) + g) / rn;
+                    loss = loss + (a.spill_lambda * p) * p;
+                }
+                const bool ok = in_pool && !taken && loss < INFINITY;
+                uint64_t k = ok ? ((static_cast<uint64_t>(asc_f32_key(loss)) << 32) | lane) : kKeyMax;
+                for (int o = 32; o > 0; o >>= 1) {
+                    const uint64_t y = __shfl_xor(k, o, kWave);
+                    k = y < k ? y : k;
+                }
+                if (k == kKeyMax) break;
+                const uint32_t pick = static_cast<uint32_t>(k);
+                if (lane == pick) taken = true;
+                h_cell = __shfl(my_cell, static_cast<int>(pick), kWave);
+                h_s = __shfl(my_s, static_cast<int>(pick), kWave);
+                if (lane == 0) hout[nh] = h_cell;
+                ++nh;
+            }
+            for (uint32_t j = nh + lane; j < ma; j += kWave) hout[j] = 0xFFFFFFFFu;
+        } else {
+            // the best r, cut at best - spill_margin (src/index.rs:2496-2508)
+            const uint32_t r = min(ma, ncand);
+            const float cutoff = __shfl(my_s, 0, kWave) - a.spill_margin;
+            const bool take = lane < r && my_s >= cutoff;
+            const uint64_t tm = __ballot(take);
+            if (take) hout[lanes_below(tm)] = my_cell;
+            for (uint32_t j = __popcll(tm) + lane; j < ma; j += kWave) hout[j] = 0xFFFFFFFFu;
+        }
+    }
+}
+
+}  // namespace maivs_dev

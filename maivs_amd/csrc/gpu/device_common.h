@@ -112,6 +112,44 @@ __device__ __forceinline__ void bitonic_sort_u64(uint64_t* keys, uint32_t n) {
     __syncthreads();
 }
 
+// Ascending bitonic sort of 64*KPL keys held in one wave: element i = r*64 + lane sits in k[r].
+template <int KPL>
+__device__ __forceinline__ void wave_sort_u64(uint64_t (&k)[KPL]) {
+    constexpr uint32_t N = 64u * KPL;
+    const uint32_t lane = lane_id();
+#pragma unroll
+    for (uint32_t size = 2; size <= N; size <<= 1) {
+#pragma unroll
+        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+            if (stride >= 64) {
+                const uint32_t rs = stride / 64;
+#pragma unroll
+                for (int r = 0; r < KPL; ++r) {
+                    if ((static_cast<uint32_t>(r) & rs) == 0) {
+                        const int r2 = r | static_cast<int>(rs);
+                        const bool up = ((static_cast<uint32_t>(r) * 64 + lane) & size) == 0;
+                        uint64_t a = k[r], b = k[r2];
+                        uint64_t mn = a < b ? a : b, mx = a < b ? b : a;
+                        k[r] = up ? mn : mx;
+                        k[r2] = up ? mx : mn;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < KPL; ++r) {
+                    const uint32_t i = static_cast<uint32_t>(r) * 64 + lane;
+                    const bool up = (i & size) == 0;
+                    const bool lower = (lane & stride) == 0;
+                    uint64_t a = k[r];
+                    uint64_t b = __shfl_xor(a, static_cast<int>(stride), 64);
+                    uint64_t mn = a < b ? a : b, mx = a < b ? b : a;
+                    k[r] = (lower == up) ? mn : mx;
+                }
+            }
+        }
+    }
+}
+
 // Order-preserving key of an f32 for DESCENDING score, ties broken by the low 32 bits
 // (the id, ascending). -0.0 and +0.0 compare equal in the reference, so they share a key.
 __device__ __forceinline__ uint64_t desc_score_key(float s, uint32_t id) {

@@ -27,6 +27,8 @@ struct GpuApi {
                   maivs_gpu_stats*) = nullptr;
     int (*kmeans)(maivs_gpu_ctx*, const float*, uint64_t, uint32_t, const uint32_t*, const maivs_kmeans_job*,
                   uint32_t, uint32_t*, float*) = nullptr;
+    int (*place)(maivs_gpu_ctx*, const maivs_place_desc*, const float*, uint32_t, uint32_t*, uint64_t*,
+                 int8_t*) = nullptr;
     std::string error;
 };
 
@@ -65,6 +67,7 @@ const GpuApi& gpu_api() {
         api.upload = reinterpret_cast<decltype(api.upload)>(sym("maivs_gpu_upload_arena"));
         api.search = reinterpret_cast<decltype(api.search)>(sym("maivs_gpu_search_batch"));
         api.kmeans = reinterpret_cast<decltype(api.kmeans)>(sym("maivs_gpu_kmeans"));
+        api.place = reinterpret_cast<decltype(api.place)>(sym("maivs_gpu_place"));
     });
     return api;
 }
@@ -554,6 +557,60 @@ void FlatCellIndex::encode_slot(const float* v, uint64_t* bits_out, int8_t* i8_o
     }
 }
 
+// add_batch's per-vector work on the GPU (maivs_gpu_place): the homes of every input vector
+// (assign_cells_routed), its 1-bit code and, when kept, its i8 / SQ8 copy.
+void FlatCellIndex::place_on_gpu(const float* data, size_t n, bool store_i8, std::vector<std::vector<uint32_t>>& asg,
+                                 std::vector<uint64_t>& bits, std::vector<int8_t>& i8) {
+    if (!gpu_) gpu_ = std::make_unique<GpuSession>();
+    const size_t M = cells_.size(), ma = max_assign_;
+    std::vector<float> cents(M * dim_);
+    for (size_t c = 0; c < M; ++c) std::memcpy(&cents[c * dim_], cells_[c].centroid.data(), dim_ * sizeof(float));
+    maivs_place_desc D{};
+    D.dim = static_cast<uint32_t>(dim_);
+    D.dim_pad = static_cast<uint32_t>(dim_pad_);
+    D.n_words = static_cast<uint32_t>(n_words_);
+    D.n_cells = static_cast<uint32_t>(M);
+    D.max_assign = static_cast<uint32_t>(ma);
+    D.spill_lambda = spill_lambda_;
+    D.spill_margin = spill_margin_;
+    D.code_mode = store_i8 ? (per_dim_sq_ ? 1u : 2u) : 0u;
+    D.quant_scale = quant_scale_;
+    D.rot_signs = rot_signs_.data();
+    D.centroids = cents.data();
+    D.sq_min = sq_min_.empty() ? nullptr : sq_min_.data();
+    D.sq_step = sq_step_.empty() ? nullptr : sq_step_.data();
+    TreeFlat tf;
+    if (tree_) {
+        tree_->export_flat(std::max<size_t>(64, ma * 8), tf);  // the want of src/index.rs:2452
+        D.tree.n_levels = static_cast<uint32_t>(tf.level_n.size());
+        D.tree.n_leaf = static_cast<uint32_t>(tf.leaf_cells.size());
+        D.tree.want = static_cast<uint32_t>(std::max<size_t>(64, ma * 8));
+        D.tree.level_n = tf.level_n.data();
+        D.tree.beams = tf.beams.data();
+        D.tree.level_codes = tf.level_codes.data();
+        D.tree.child_start = tf.child_start.data();
+        D.tree.child_len = tf.child_len.data();
+        D.tree.leaf_codes = tf.leaf_codes.data();
+        D.tree.leaf_cells = tf.leaf_cells.data();
+    }
+    std::vector<uint32_t> homes(n * ma);
+    bits.assign(n * n_words_, 0);
+    if (store_i8) i8.assign(n * dim_, 0);
+    // batches of at most 2^20 vectors keep the device copy of the inputs bounded
+    const size_t step = size_t{1} << 20;
+    for (size_t b = 0; b < n; b += step) {
+        const size_t m = std::min(step, n - b);
+        gpu_->check(gpu_api().place(gpu_->ctx_, &D, data + b * dim_, static_cast<uint32_t>(m), &homes[b * ma],
+                                    &bits[b * n_words_], store_i8 ? &i8[b * dim_] : nullptr),
+                    "maivs_gpu_place");
+    }
+    for (size_t i = 0; i < n; ++i) {
+        asg[i].clear();
+        for (size_t j = 0; j < ma; ++j)
+            if (homes[i * ma + j] != UINT32_MAX) asg[i].push_back(homes[i * ma + j]);
+    }
+}
+
 void FlatCellIndex::add_batch(const std::vector<uint64_t>& ids, const float* data, size_t n) {
     // src/index.rs:2987-3212
     if (cells_.empty()) throw ValueError("call set_centroids() before add_batch()");
@@ -576,8 +633,17 @@ void FlatCellIndex::add_batch(const std::vector<uint64_t>& ids, const float* dat
         for (size_t j = 0; j < dim_; ++j) sq_step_[j] = std::max(hi[j] - lo[j], 1e-9f) / 255.0f;
         sq_min_ = lo;
     }
+    const bool store_bits = scan_mode_ == ScanMode::Binary;
+    const bool store_i8 = scan_mode_ == ScanMode::I8 || (scan_mode_ == ScanMode::Binary && i8_rerank_);
+    const size_t nw = n_words_, ma = max_assign_;
     std::vector<std::vector<uint32_t>> asg(n);
-    {
+    // GPU placement: homes, 1-bit codes and i8 / SQ8 copies of the whole batch, bit-identical
+    std::vector<uint64_t> g_bits;
+    std::vector<int8_t> g_i8;
+    const bool on_gpu = gpu_build_ && n > 0;
+    if (on_gpu) {
+        place_on_gpu(data, n, store_i8, asg, g_bits, g_i8);
+    } else {
         // one scratch per chunk of 256 vectors keeps allocation out of the inner loop
         size_t nchunk = (n + 255) / 256;
         parallel_for(nchunk, [&](size_t ch) {
@@ -589,9 +655,15 @@ void FlatCellIndex::add_batch(const std::vector<uint64_t>& ids, const float* dat
             for (size_t i = b; i < e; ++i) asg[i] = assign_cells_routed(data + i * dim_, rot, qb, ts, out);
         });
     }
-    const bool store_bits = scan_mode_ == ScanMode::Binary;
-    const bool store_i8 = scan_mode_ == ScanMode::I8 || (scan_mode_ == ScanMode::Binary && i8_rerank_);
-    const size_t nw = n_words_, ma = max_assign_;
+    // the codes of input vector i into a slot's rows
+    auto encode_input = [&](size_t i, uint64_t* bits_out, int8_t* i8_out) {
+        if (!on_gpu) {
+            encode_slot(data + i * dim_, bits_out, i8_out);
+            return;
+        }
+        if (bits_out) std::memcpy(bits_out, &g_bits[i * nw], nw * 8);
+        if (i8_out) std::memcpy(i8_out, &g_i8[i * dim_], dim_);
+    };
     size_t n_reuse = std::min(free_slots_.size(), n);
     for (size_t i = 0; i < n_reuse; ++i) {
         const float* v = data + i * dim_;
@@ -599,8 +671,7 @@ void FlatCellIndex::add_batch(const std::vector<uint64_t>& ids, const float* dat
         free_slots_.pop_back();
         size_t off = static_cast<size_t>(s) * dim_;
         if (keep_f32_) std::memcpy(&vecs_f32_[off], v, dim_ * sizeof(float));
-        encode_slot(v, store_bits ? &bits_[static_cast<size_t>(s) * nw] : nullptr,
-                    store_i8 ? &scan_i8_[off] : nullptr);
+        encode_input(i, store_bits ? &bits_[static_cast<size_t>(s) * nw] : nullptr, store_i8 ? &scan_i8_[off] : nullptr);
         ext_ids_[s] = ids[i];
         slot_cell_[s] = asg[i][0];
         for (size_t j = 0; j < ma; ++j) slot_cells_[s * ma + j] = j < asg[i].size() ? asg[i][j] : UINT32_MAX;
@@ -622,8 +693,8 @@ void FlatCellIndex::add_batch(const std::vector<uint64_t>& ids, const float* dat
         if (store_bits) bits_.resize((base + m) * nw, 0);
         if (store_i8) scan_i8_.resize((base + m) * dim_, 0);
         parallel_for(m, [&](size_t i) {
-            encode_slot(dat + i * dim_, store_bits ? &bits_[(base + i) * nw] : nullptr,
-                        store_i8 ? &scan_i8_[(base + i) * dim_] : nullptr);
+            encode_input(n_reuse + i, store_bits ? &bits_[(base + i) * nw] : nullptr,
+                         store_i8 ? &scan_i8_[(base + i) * dim_] : nullptr);
         }, 512);
         for (size_t i = 0; i < m; ++i) {
             const auto& a = asg[n_reuse + i];

@@ -128,6 +128,8 @@ private:
     void recompute_centroid(Cell& c);
     void touch() { ++generation_; compacted_ = false; }
     KMeansRunner gpu_kmeans_runner();
+    void place_on_gpu(const float* data, size_t n, bool store_i8, std::vector<std::vector<uint32_t>>& asg,
+                      std::vector<uint64_t>& bits, std::vector<int8_t>& i8);
 
     size_t dim_, rerank_factor_, dim_pad_, n_words_;
     ScanMode scan_mode_;

@@ -4,6 +4,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <stdexcept>
 
 #include "cpu_kernels.h"
 
@@ -334,6 +335,22 @@ size_t CentroidTree::bytes() const {
         b += l.cents.size() * 4 + l.codes.size() * 8 +
              (l.child_start.size() + l.child_len.size() + l.child_idx.size()) * 4;
     return b;
+}
+
+void CentroidTree::export_flat(size_t want, TreeFlat& f) const {
+    f = TreeFlat{};
+    for (const auto& l : levels_) {
+        f.level_n.push_back(static_cast<uint32_t>(l.n));
+        f.level_codes.insert(f.level_codes.end(), l.codes.begin(), l.codes.end());
+        f.child_start.insert(f.child_start.end(), l.child_start.begin(), l.child_start.end());
+        f.child_len.insert(f.child_len.end(), l.child_len.begin(), l.child_len.end());
+        // compact_layout made every child list contiguous: child_idx is the identity
+        for (size_t j = 0; j < l.child_idx.size(); ++j)
+            if (l.child_idx[j] != j) throw std::logic_error("centroid tree is not in its compacted layout");
+    }
+    for (size_t b : beams(want)) f.beams.push_back(static_cast<uint32_t>(b));
+    f.leaf_codes = leaf_codes_;
+    f.leaf_cells = leaf_ids_;
 }
 
 // Beam per level, top-down from the leaves, src/tree.rs:559-570.

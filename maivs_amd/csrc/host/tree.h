@@ -41,6 +41,12 @@ struct TreeLevel {
     std::vector<uint32_t> child_start, child_len, child_idx;
 };
 
+// The tree in its compacted layout as flat arrays (the GPU placement's input).
+struct TreeFlat {
+    std::vector<uint32_t> level_n, beams, child_start, child_len, leaf_cells;
+    std::vector<uint64_t> level_codes, leaf_codes;
+};
+
 struct TreeScratch {
     std::vector<uint32_t> frontier, expand, hist;
     std::vector<std::pair<uint32_t, uint32_t>> scored;  // (hamming, node)
@@ -64,6 +70,8 @@ public:
     size_t n_leaf() const { return n_leaf_; }
     size_t top_width() const { return levels_.empty() ? 0 : levels_.front().n; }
     size_t bytes() const;
+    // Flat arrays of every level (coarsest first) and the leaves, with the beams of search(want).
+    void export_flat(size_t want, TreeFlat& f) const;
 
 private:
     std::vector<size_t> beams(size_t want) const;

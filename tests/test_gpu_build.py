@@ -176,3 +176,69 @@ def test_gpu_build_matches_cpu_build(mix50k):
     assert built[0].stats()["tree_depth"] == built[1].stats()["tree_depth"] >= 1
     q = np.ascontiguousarray(queries[:200])
     assert built[0].search_batch(q, 10, 16, 1.0, 8.0, True) == built[1].search_batch(q, 10, 16, 1.0, 8.0, True)
+
+
+# ---------------------------------------------------------------- GPU placement (add_batch)
+
+
+def _configure(ix, case):
+    if case == "memory":
+        ix.set_per_dim_sq(True)
+    elif case == "replicate3":
+        ix.set_replication(3, 0.02)
+    elif case == "single":
+        ix.set_replication(1, 0.0)
+    elif case == "i8":
+        ix.set_i8_rerank(True)
+
+
+def _pair(x, n_cells, case, tree_min=2048, churn=False):
+    """Two identical indexes (CPU-trained centroids); one places with the GPU. Returns the saved
+    files' bytes of both after add_batch (+ churn) + compact."""
+    import os
+    import tempfile
+    out = []
+    for gpu in (False, True):
+        ix = M.preset(x.shape[1], len(x))
+        _configure(ix, case)
+        ix.set_tree_route(True, tree_min, 16)
+        ix.train_centroids(x, n_cells)
+        ix.set_gpu_build(gpu)
+        n0 = len(x) if not churn else len(x) * 3 // 4
+        ix.add_batch(list(range(n0)), np.ascontiguousarray(x[:n0]))
+        if churn:
+            for v in range(0, n0, 7):
+                assert ix.remove(v)
+            ix.add_batch(list(range(n0, len(x))), np.ascontiguousarray(x[n0:]))  # reuses free slots
+        ix.compact()
+        with tempfile.TemporaryDirectory() as td:
+            p = os.path.join(td, "ix.maivs")
+            ix.save(p)
+            out.append(open(p, "rb").read())
+    return out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", ["quality", "memory", "replicate3", "single", "i8"])
+def test_gpu_placement_matches_cpu_without_tree(mix50k, case):
+    base, _, _ = mix50k
+    x = np.ascontiguousarray(base[:20000])
+    a, b = _pair(x, 156, case)
+    assert a == b
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", ["quality", "replicate3"])
+def test_gpu_placement_matches_cpu_with_tree(mix50k, case):
+    """312 cells with the tree threshold lowered: one 20-node level, beams of 32, 64 leaves."""
+    base, _, _ = mix50k
+    x = np.ascontiguousarray(base[:40000])
+    a, b = _pair(x, 312, case, tree_min=256)
+    assert a == b
+
+
+@pytest.mark.gpu
+def test_gpu_placement_odd_dim_and_churn():
+    x = small_clustered(6000, 37, 40, seed=13)
+    a, b = _pair(x, 46, "quality", churn=True)
+    assert a == b
