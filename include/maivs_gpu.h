@@ -15,6 +15,9 @@
  *   maivs_gpu_query_prep     rotate + pack_signs_trunc + FsQuery::new, src/quantize.rs:57-313
  *   maivs_gpu_block_sums     FsQuery::block_sums, src/quantize.rs:323-386
  *   maivs_gpu_route          route_batch, src/index.rs:1873-1980
+ *   maivs_gpu_search_queries FlatCellIndex::search_one + route_query, src/index.rs:1168-1305,
+ *                            1381-1864, reached from search (:3283-3305) and the per-query
+ *                            branch of search_batch (:3363-3391)
  *   maivs_gpu_kmeans         kmeans_spherical, src/tree.rs:179-248, as run by train_centroids'
  *                            two-level k-means (src/tree.rs:257-348, src/index.rs:2762-2804) and
  *                            by the centroid tree build (src/tree.rs:354-460)
@@ -84,6 +87,8 @@ typedef struct maivs_arena_desc {
     const float* sq_step;       /* d (MAIVS_RERANK_SQ8) */
     /* filtering: one u32 attribute per slot (src/index.rs:551-555), or NULL when unused */
     const uint32_t* tags;       /* N */
+    /* the centroid tree the per-query path routes with (n_levels 0: none); defined below */
+    const struct maivs_tree_desc* tree;
 } maivs_arena_desc;
 
 /* Query-time settings of search_batch (src/index.rs:3316-3326 and the index setters). */
@@ -156,6 +161,23 @@ int maivs_gpu_search_batch_device(maivs_gpu_ctx* ctx, const float* d_queries, ui
                                   const maivs_search_params* params, uint32_t* d_out_slots,
                                   float* d_out_scores, maivs_gpu_stats* stats);
 
+/*
+ * The per-query path: the reference's search_one (src/index.rs:1381-1864) for every query on its
+ * own, as its search() and its search_batch for small batches, filtered searches and
+ * cell_major=False run it (:3283-3392). Each query is routed by route_query (:1168-1305: the
+ * centroid tree when the arena has one, else the two-stage Hamming shortlist of nprobe *
+ * shortlist_mult cells), then its probed cells are scanned in probe order with the FastScan
+ * bucket queue on d >> 6, the rule that a multi-home vector counts at its first-ranked probed home,
+ * the tag filter and the adaptive stop; the k * rerank_factor smallest d (ties by ascending slot)
+ * are reranked exactly. Same buffers and results layout as maivs_gpu_search_batch.
+ */
+int maivs_gpu_search_queries(maivs_gpu_ctx* ctx, const float* queries, uint32_t nq,
+                             const maivs_search_params* params, uint32_t* out_slots,
+                             float* out_scores, maivs_gpu_stats* stats);
+int maivs_gpu_search_queries_device(maivs_gpu_ctx* ctx, const float* d_queries, uint32_t nq,
+                                    const maivs_search_params* params, uint32_t* d_out_slots,
+                                    float* d_out_scores, maivs_gpu_stats* stats);
+
 /* ---- stage entry points for parity tests (host buffers) ---- */
 
 /* Rotation, sign code and FastScan table of nq queries: bits nq x W, lut nq x (W*256),
@@ -218,14 +240,15 @@ int maivs_gpu_kmeans(maivs_gpu_ctx* ctx, const float* x, uint64_t n_rows, uint32
                      uint32_t* assign, float* cents);
 
 /* The centroid tree (src/tree.rs) in its compacted layout: every node's children are contiguous
- * in the next level (or the leaves), child_start / child_len give the range. */
+ * in the next level (or the leaves), child_start / child_len give the range. A descent that
+ * wants `want` leaves keeps, per level from the finest up, clamp(ceil(need * beam_frac),
+ * min_beam, level size) nodes, need starting at want (src/tree.rs:559-570). */
 typedef struct maivs_tree_desc {
-    uint32_t n_levels;            /* 0 = no tree: every cell is a candidate */
+    uint32_t n_levels;            /* 0 = no tree */
     uint32_t n_leaf;
-    uint32_t want;                /* leaves kept at the end, max(64, 8 * max_assign) */
-    uint32_t reserved;
+    float beam_frac;              /* set_tree_route's beam_frac (0.5 by default) */
+    uint32_t min_beam;            /* MIN_BEAM, 32 */
     const uint32_t* level_n;      /* n_levels: nodes per level, coarsest first */
-    const uint32_t* beams;        /* n_levels: nodes kept per level (CentroidTree::beams(want)) */
     const uint64_t* level_codes;  /* sum(level_n) x n_words, level by level */
     const uint32_t* child_start;  /* sum(level_n) */
     const uint32_t* child_len;    /* sum(level_n) */
@@ -241,12 +264,12 @@ typedef struct maivs_place_desc {
     float spill_margin;           /* else: homes within this score of the best */
     uint32_t code_mode;           /* 0: none, 1: per-dimension SQ8, 2: global int8 (quant_scale) */
     float quant_scale;
-    uint32_t reserved;
+    uint32_t tree_want;           /* leaves the descent keeps, max(64, 8 * max_assign) (src/index.rs:2452) */
     const float* rot_signs;       /* 2 x dim_pad */
     const float* centroids;       /* n_cells x dim (f32) */
     const float* sq_min;          /* dim (code_mode 1) */
     const float* sq_step;         /* dim (code_mode 1) */
-    maivs_tree_desc tree;
+    maivs_tree_desc tree;         /* n_levels 0: every cell is a candidate */
 } maivs_place_desc;
 
 /*

@@ -29,7 +29,7 @@ class ArenaDesc(C.Structure):
         ("slot_cells", C.c_void_p), ("cent_bits", C.c_void_p), ("cent_sq8", C.c_void_p),
         ("centroids", C.c_void_p), ("csq_min", C.c_void_p), ("csq_step", C.c_void_p), ("r_bound", C.c_void_p),
         ("rot_signs", C.c_void_p), ("vecs_f32", C.c_void_p), ("sq8_codes", C.c_void_p), ("sq_min", C.c_void_p),
-        ("sq_step", C.c_void_p), ("tags", C.c_void_p),
+        ("sq_step", C.c_void_p), ("tags", C.c_void_p), ("tree", C.c_void_p),
     ]
 
 
@@ -69,6 +69,10 @@ SIGNATURES = {
     "maivs_gpu_route": (I32, [P, P, U32, C.POINTER(SearchParams), P, P, P]),
     "maivs_gpu_last_candidates": (I32, [P, P, P, P, P, P, P, U64]),
     "maivs_gpu_last_counters": (I32, [P, C.POINTER(GpuStats)]),
+    "maivs_gpu_search_queries": (I32, [P, P, U32, C.POINTER(SearchParams), P, P, C.POINTER(GpuStats)]),
+    "maivs_gpu_search_queries_device": (I32, [P, P, U32, C.POINTER(SearchParams), P, P, C.POINTER(GpuStats)]),
+    "maivs_gpu_kmeans": (I32, [P, P, U64, U32, P, P, U32, P, P]),
+    "maivs_gpu_place": (I32, [P, P, P, U32, P, P, P]),
 }
 
 _lib = None
@@ -144,6 +148,24 @@ class Context:
                                                            C.c_void_p(slots_ptr), C.c_void_p(scores_ptr),
                                                            C.byref(stats) if stats is not None else None),
                     "maivs_gpu_search_batch_device")
+
+    def search_queries(self, q: np.ndarray, params: SearchParams, stats: GpuStats | None = None):
+        """The per-query path (maivs_gpu_search_queries)."""
+        q = np.ascontiguousarray(q, np.float32)
+        nq = q.shape[0]
+        slots = np.empty((nq, params.k), np.uint32)
+        scores = np.empty((nq, params.k), np.float32)
+        self._check(self.lib.maivs_gpu_search_queries(self.h, ptr(q), nq, C.byref(params), ptr(slots), ptr(scores),
+                                                      C.byref(stats) if stats is not None else None),
+                    "maivs_gpu_search_queries")
+        return slots, scores
+
+    def search_queries_device(self, q_ptr: int, nq: int, params: SearchParams, slots_ptr: int, scores_ptr: int,
+                              stats: GpuStats | None = None) -> None:
+        self._check(self.lib.maivs_gpu_search_queries_device(self.h, C.c_void_p(q_ptr), nq, C.byref(params),
+                                                             C.c_void_p(slots_ptr), C.c_void_p(scores_ptr),
+                                                             C.byref(stats) if stats is not None else None),
+                    "maivs_gpu_search_queries_device")
 
     def query_prep(self, q: np.ndarray, n_words: int):
         q = np.ascontiguousarray(q, np.float32)

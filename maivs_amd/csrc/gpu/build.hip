@@ -198,28 +198,15 @@ extern "C" int maivs_gpu_place(maivs_gpu_ctx* ctx, const maivs_place_desc* pd, c
     if (ma == 0 || ma > 64) return fail(ctx, MAIVS_ERR_UNSUPPORTED, "maivs_gpu_place: max_assign %u outside [1, 64]", ma);
     if (D.code_mode > 2 || (D.code_mode && !codes) || (D.code_mode == 1 && (!D.sq_min || !D.sq_step)))
         return fail(ctx, MAIVS_ERR_ARG, "maivs_gpu_place: bad code mode");
-    uint32_t total_nodes = 0, cap = 1;
-    std::vector<uint32_t> lv_off(T.n_levels + 1, 0);
-    if (T.n_levels) {
-        if (!T.level_n || !T.beams || !T.level_codes || !T.child_start || !T.child_len || !T.leaf_codes ||
-            !T.leaf_cells || T.n_leaf == 0 || T.want == 0)
-            return fail(ctx, MAIVS_ERR_ARG, "maivs_gpu_place: incomplete tree");
-        for (uint32_t l = 0; l < T.n_levels; ++l) {
-            lv_off[l + 1] = lv_off[l] + T.level_n[l];
-            cap = std::max(cap, T.beams[l]);
-        }
-        total_nodes = lv_off[T.n_levels];
-        // every child range must lie inside the next level (or the leaves); leaves name real cells
-        for (uint32_t l = 0; l < T.n_levels; ++l) {
-            const uint32_t next = l + 1 < T.n_levels ? T.level_n[l + 1] : T.n_leaf;
-            for (uint32_t j = lv_off[l]; j < lv_off[l + 1]; ++j)
-                if (static_cast<uint64_t>(T.child_start[j]) + T.child_len[j] > next)
-                    return fail(ctx, MAIVS_ERR_ARG, "maivs_gpu_place: child range past level %u", l + 1);
-        }
-        for (uint32_t j = 0; j < T.n_leaf; ++j)
-            if (T.leaf_cells[j] >= M) return fail(ctx, MAIVS_ERR_ARG, "maivs_gpu_place: leaf cell out of range");
+    const bool has_tree = T.n_levels > 0;
+    const uint32_t want = has_tree ? std::max(D.tree_want, 1u) : 1u;
+    std::vector<uint32_t> beams(T.n_levels, 0);
+    if (has_tree) {
+        if (!T.level_n) return fail(ctx, MAIVS_ERR_ARG, "maivs_gpu_place: incomplete tree");
+        tree_beams(T.level_n, T.n_levels, T.beam_frac, T.min_beam, want, beams.data());
     }
-    const uint32_t want = T.n_levels ? T.want : 1;
+    uint32_t cap = 1;
+    for (uint32_t b : beams) cap = std::max(cap, b);
     const uint32_t words = place_lds_words(P, d, W, cap, want);
     const uint32_t lds_per_wave = (words * 4 + 15) & ~15u;
     if (static_cast<size_t>(lds_per_wave) * kPlaceWaves > 160 * 1024)
@@ -229,8 +216,8 @@ extern "C" int maivs_gpu_place(maivs_gpu_ctx* ctx, const maivs_place_desc* pd, c
     Scratch S(ctx);
     PlaceArgs a{};
     float *d_x, *d_signs, *d_cents, *d_sqmin = nullptr, *d_sqstep = nullptr;
-    uint32_t *d_homes, *d_lvoff = nullptr, *d_cs = nullptr, *d_cl = nullptr, *d_beams = nullptr, *d_leaf_ids = nullptr;
-    uint64_t *d_bits, *d_lvcodes = nullptr, *d_leaf_codes = nullptr;
+    uint32_t *d_homes, *d_beams = nullptr;
+    uint64_t* d_bits;
     int8_t* d_codes = nullptr;
     int rc = 0;
     if ((rc = S.upload(&d_x, x, static_cast<size_t>(n) * d)) || (rc = S.upload(&d_signs, D.rot_signs, 2 * static_cast<size_t>(P))) ||
@@ -241,25 +228,14 @@ extern "C" int maivs_gpu_place(maivs_gpu_ctx* ctx, const maivs_place_desc* pd, c
         if ((rc = S.alloc(&d_codes, static_cast<size_t>(n) * d))) return rc;
         if (D.code_mode == 1 && ((rc = S.upload(&d_sqmin, D.sq_min, d)) || (rc = S.upload(&d_sqstep, D.sq_step, d)))) return rc;
     }
-    if (T.n_levels) {
-        if ((rc = S.upload(&d_lvoff, lv_off.data(), lv_off.size())) ||
-            (rc = S.upload(&d_lvcodes, T.level_codes, static_cast<size_t>(total_nodes) * W)) ||
-            (rc = S.upload(&d_cs, T.child_start, total_nodes)) || (rc = S.upload(&d_cl, T.child_len, total_nodes)) ||
-            (rc = S.upload(&d_beams, T.beams, T.n_levels)) ||
-            (rc = S.upload(&d_leaf_codes, T.leaf_codes, static_cast<size_t>(T.n_leaf) * W)) ||
-            (rc = S.upload(&d_leaf_ids, T.leaf_cells, T.n_leaf)))
+    if (has_tree) {
+        if ((rc = upload_tree(ctx, S.allocs, &T, W, M, &a.tree, nullptr)) || (rc = S.upload(&d_beams, beams.data(), beams.size())))
             return rc;
     }
     a.x = d_x;
     a.signs = d_signs;
     a.cents = d_cents;
-    a.lv_off = d_lvoff;
-    a.lv_codes = d_lvcodes;
-    a.lv_cs = d_cs;
-    a.lv_cl = d_cl;
     a.beams = d_beams;
-    a.leaf_codes = d_leaf_codes;
-    a.leaf_ids = d_leaf_ids;
     a.sq_min = d_sqmin;
     a.sq_step = d_sqstep;
     a.homes = d_homes;
@@ -274,7 +250,6 @@ extern "C" int maivs_gpu_place(maivs_gpu_ctx* ctx, const maivs_place_desc* pd, c
     a.P = P;
     a.W = W;
     a.M = M;
-    a.n_levels = T.n_levels;
     a.want = want;
     a.ma = ma;
     a.kept_cap = cap;

@@ -18,6 +18,7 @@
 #include <stdint.h>
 
 #include "device_common.h"
+#include "wave_tree.h"
 
 namespace maivs_dev {
 
@@ -236,27 +237,16 @@ struct PlaceArgs {
     const float* x;            // n x d
     const float* signs;        // 2 x P
     const float* cents;        // M x d
-    const uint32_t* lv_off;    // tree levels: node offsets (n_levels + 1), coarsest first
-    const uint64_t* lv_codes;  // sum of level sizes x W
-    const uint32_t* lv_cs;     // child start of each node (index into the next level / the leaves)
-    const uint32_t* lv_cl;     // child count of each node
+    TreeDev tree;              // n_levels == 0: no tree
     const uint32_t* beams;     // n_levels
-    const uint64_t* leaf_codes;  // n_leaf x W
-    const uint32_t* leaf_ids;    // n_leaf: cell of each leaf
     const float* sq_min;
     const float* sq_step;
     uint32_t* homes;           // n x ma, UINT32_MAX padded
     uint64_t* bits;            // n x W
     int8_t* codes;             // n x d when code_mode != 0
     float fht_scale, spill_lambda, spill_margin, quant_scale;
-    uint32_t n, d, P, W, M, n_levels, want, ma, kept_cap, code_mode, lds_per_wave;
+    uint32_t n, d, P, W, M, want, ma, kept_cap, code_mode, lds_per_wave;
 };
-
-__device__ __forceinline__ void wave_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 
 // Per-wave LDS of the placement kernel, in order: qb[W] u64 | xs[P] | vs[d4] | hist[bits + 1, to 4]
 // | rbase[cap + 1] | rpre[cap + 2] | knodes[cap] | outc[want]   (u32 / f32 words after qb)
@@ -282,99 +272,6 @@ __device__ __forceinline__ PlaceLds place_lds(uint8_t* base, const PlaceArgs& a)
     L.knodes = L.rpre + a.kept_cap + 2;
     L.outc = L.knodes + a.kept_cap;
     return L;
-}
-
-__device__ __forceinline__ uint32_t hamming_lds(const uint64_t* qb, const uint64_t* code, uint32_t W) {
-    uint32_t h = 0;
-    for (uint32_t w = 0; w < W; ++w) h += __popcll(qb[w] ^ code[w]);
-    return h;
-}
-
-// Total-order key of an f32 (ascending), for a first-minimum search.
-__device__ __forceinline__ uint32_t asc_f32_key(float f) {
-    const uint32_t b = __float_as_uint(f == 0.0f ? 0.0f : f);
-    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
-
-// keep_smallest over the frontier positions [0, F) with distance hd(p): emit(k, p) for the kept
-// entries in encounter order (k = 0, 1, ...). Returns the number kept = min(keep, F).
-template <class HD, class EMIT>
-__device__ uint32_t wave_keep_smallest(uint32_t F, uint32_t keep, uint32_t bits, uint32_t* hist, HD hd, EMIT emit) {
-    const uint32_t lane = lane_id();
-    if (keep >= F) {
-        for (uint32_t p = lane; p < F; p += kWave) emit(p, p);
-        return F;
-    }
-    for (uint32_t j = lane; j <= bits; j += kWave) hist[j] = 0;
-    wave_sync();
-    for (uint32_t p = lane; p < F; p += kWave) atomicAdd(&hist[hd(p)], 1u);
-    wave_sync();
-    // t = the smallest distance with count(h <= t) >= keep; below = count(h < t)
-    const uint32_t nb = bits + 1, bpl = (nb + kWave - 1) / kWave;
-    const uint32_t b0 = min(lane * bpl, nb), b1 = min(b0 + bpl, nb);
-    uint32_t mine = 0;
-    for (uint32_t b = b0; b < b1; ++b) mine += hist[b];
-    uint32_t incl = mine;
-    for (int o = 1; o < kWave; o <<= 1) {
-        const uint32_t y = __shfl_up(incl, o, kWave);
-        if (lane >= static_cast<uint32_t>(o)) incl += y;
-    }
-    const uint32_t excl = incl - mine;
-    const bool here = excl < keep && incl >= keep;
-    uint32_t t = 0, below = 0;
-    if (here) {
-        uint32_t cum = excl;
-        for (uint32_t b = b0; b < b1; ++b) {
-            if (cum + hist[b] >= keep) {
-                t = b;
-                below = cum;
-                break;
-            }
-            cum += hist[b];
-        }
-    }
-    const uint64_t hm = __ballot(here);
-    const int src = __ffsll(static_cast<long long>(hm)) - 1;
-    t = __shfl(t, src, kWave);
-    below = __shfl(below, src, kWave);
-    const uint32_t need_eq = keep - below;
-    uint32_t eq_seen = 0, kept = 0;
-    for (uint32_t c0 = 0; c0 < F; c0 += kWave) {
-        const uint32_t p = c0 + lane;
-        const bool valid = p < F;
-        const uint32_t h = valid ? hd(p) : 0xFFFFFFFFu;
-        const uint64_t eqm = __ballot(valid && h == t);
-        const bool take = valid && (h < t || (h == t && eq_seen + lanes_below(eqm) < need_eq));
-        const uint64_t tm = __ballot(take);
-        if (take) emit(kept + lanes_below(tm), p);
-        eq_seen += __popcll(eqm);
-        kept += __popcll(tm);
-    }
-    return kept;
-}
-
-// Frontier position p -> node id, from the ranges of the kept parents (rpre: prefix of lengths).
-__device__ __forceinline__ uint32_t frontier_node(const uint32_t* rbase, const uint32_t* rpre, uint32_t nr, uint32_t p) {
-    uint32_t lo = 0, hi = nr;  // the last r with rpre[r] <= p
-    while (hi - lo > 1) {
-        const uint32_t mid = (lo + hi) >> 1;
-        if (rpre[mid] <= p) lo = mid; else hi = mid;
-    }
-    return rbase[lo] + (p - rpre[lo]);
-}
-
-// Exact dot_f32(a, b) by one lane: 8 accumulators, hsum, sequential tail (src/index.rs:136-152).
-template <class LA, class LB>
-__device__ __forceinline__ float dot_lane(uint32_t d, LA la, LB lb) {
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    const uint32_t d8 = d & ~7u;
-    for (uint32_t t = 0; t < d8; t += 8) {
-#pragma unroll
-        for (uint32_t l = 0; l < 8; ++l) acc[l] = __builtin_fmaf(la(t + l), lb(t + l), acc[l]);
-    }
-    float s = ((acc[0] + acc[4]) + (acc[2] + acc[6])) + ((acc[1] + acc[5]) + (acc[3] + acc[7]));
-    for (uint32_t e = d8; e < d; ++e) s += la(e) * lb(e);
-    return s;
 }
 
 template <int EPL>
@@ -446,73 +343,9 @@ __global__ void __launch_bounds__(kPlaceWaves * kWave) place_kernel(PlaceArgs a)
             }
         }
         wave_sync();
-        // ---- tree descent (src/tree.rs:574-628)
-        uint32_t nout = 0;
-        bool use_tree = a.n_levels > 0;
-        if (use_tree) {
-            uint32_t nr = 1;
-            if (lane == 0) {
-                L.rbase[0] = 0;
-                L.rpre[0] = 0;
-                L.rpre[1] = a.lv_off[1] - a.lv_off[0];
-            }
-            wave_sync();
-            uint32_t F = a.lv_off[1] - a.lv_off[0];
-            for (uint32_t li = 0; li < a.n_levels && use_tree; ++li) {
-                const uint64_t* codes = a.lv_codes + static_cast<uint64_t>(a.lv_off[li]) * W;
-                const uint32_t keep = min(a.beams[li], F);
-                if (keep == 0) {
-                    use_tree = false;
-                    break;
-                }
-                const uint32_t nk = wave_keep_smallest(
-                    F, keep, bits, L.hist,
-                    [&](uint32_t p) {
-                        const uint32_t node = frontier_node(L.rbase, L.rpre, nr, p);
-                        return hamming_lds(L.qb, codes + static_cast<uint64_t>(node) * W, W);
-                    },
-                    [&](uint32_t k, uint32_t p) { L.knodes[k] = frontier_node(L.rbase, L.rpre, nr, p); });
-                wave_sync();
-                // children of the kept nodes, in order: the next frontier's ranges
-                const uint32_t* cs = a.lv_cs + a.lv_off[li];
-                const uint32_t* cl = a.lv_cl + a.lv_off[li];
-                uint32_t carry = 0;
-                for (uint32_t k0 = 0; k0 < nk; k0 += kWave) {
-                    const uint32_t k = k0 + lane;
-                    const uint32_t node = k < nk ? L.knodes[k] : 0u;
-                    const uint32_t len = k < nk ? cl[node] : 0u;
-                    uint32_t incl = len;
-                    for (int o = 1; o < kWave; o <<= 1) {
-                        const uint32_t y = __shfl_up(incl, o, kWave);
-                        if (lane >= static_cast<uint32_t>(o)) incl += y;
-                    }
-                    if (k < nk) {
-                        L.rbase[k] = cs[node];
-                        L.rpre[k] = carry + incl - len;
-                    }
-                    carry += __shfl(incl, kWave - 1, kWave);
-                }
-                if (lane == 0) L.rpre[nk] = carry;
-                wave_sync();
-                nr = nk;
-                F = carry;
-            }
-            if (use_tree) {
-                const uint32_t keep = min(a.want, F);
-                if (keep == 0) {
-                    use_tree = false;
-                } else {
-                    nout = wave_keep_smallest(
-                        F, keep, bits, L.hist,
-                        [&](uint32_t p) {
-                            const uint32_t leaf = frontier_node(L.rbase, L.rpre, nr, p);
-                            return hamming_lds(L.qb, a.leaf_codes + static_cast<uint64_t>(leaf) * W, W);
-                        },
-                        [&](uint32_t k, uint32_t p) { L.outc[k] = a.leaf_ids[frontier_node(L.rbase, L.rpre, nr, p)]; });
-                    wave_sync();
-                }
-            }
-        }
+        // ---- tree descent (src/tree.rs:574-628); no tree or no result: every cell
+        uint32_t nout = tree_descent(a.tree, a.beams, a.want, L.qb, W, L.hist, L.rbase, L.rpre, L.knodes, L.outc);
+        const bool use_tree = nout > 0;
         if (!use_tree) nout = a.M;  // every cell, in order (src/index.rs:2480-2509)
         // ---- exact scores and the running selection
         uint64_t kmin = kKeyMax;  // ma == 1: (score desc, position asc)

@@ -12,6 +12,7 @@
 
 #include "../../../include/maivs_gpu.h"
 #include "types.h"
+#include "wave_tree.h"
 
 using namespace maivs_dev;
 
@@ -51,6 +52,15 @@ struct maivs_gpu_ctx {
     uint64_t buf_gen = 0;  // bumped whenever a buffer the graph references is reallocated
     hipGraphExec_t gexec = nullptr;
     GraphKey gkey{};
+    // the per-query path's buffers (tree lists, scan candidates, beams), sized by (nq, tcap, pq_cap)
+    std::vector<void*> pq_allocs;
+    uint32_t cap_pq_nq = 0, cap_tcap = 0, cap_pq = 0, pq_cap_min = 0;
+    uint32_t* d_beams = nullptr;
+    // the centroid tree (per-query path); n_levels 0 when the arena has none
+    TreeDev tree{};
+    std::vector<uint32_t> tree_level_n;
+    float tree_beam_frac = 0.5f;
+    uint32_t tree_min_beam = 32;
 };
 
 namespace maivs_host {
@@ -95,6 +105,56 @@ inline int dupload(maivs_gpu_ctx* ctx, const T* src, size_t count, T** out) {
 inline void free_all(std::vector<void*>& v) {
     for (void* p : v) (void)hipFree(p);
     v.clear();
+}
+
+// Check a centroid tree (every child range inside the next level, leaves naming cells < M) and
+// copy it to HBM; allocations go to `owner`. An absent tree (null or no levels) gives n_levels 0.
+inline int upload_tree(maivs_gpu_ctx* ctx, std::vector<void*>& owner, const maivs_tree_desc* T, uint32_t W, uint32_t M,
+                       TreeDev* out, std::vector<uint32_t>* level_n_host) {
+    *out = TreeDev{};
+    if (level_n_host) level_n_host->clear();
+    if (!T || T->n_levels == 0) return 0;
+    if (!T->level_n || !T->level_codes || !T->child_start || !T->child_len || !T->leaf_codes || !T->leaf_cells ||
+        T->n_leaf == 0 || !(T->beam_frac > 0.0f))
+        return fail(ctx, MAIVS_ERR_ARG, "centroid tree: incomplete description");
+    std::vector<uint32_t> off(T->n_levels + 1, 0);
+    for (uint32_t l = 0; l < T->n_levels; ++l) {
+        if (T->level_n[l] == 0) return fail(ctx, MAIVS_ERR_ARG, "centroid tree: empty level %u", l);
+        off[l + 1] = off[l] + T->level_n[l];
+    }
+    for (uint32_t l = 0; l < T->n_levels; ++l) {
+        const uint32_t next = l + 1 < T->n_levels ? T->level_n[l + 1] : T->n_leaf;
+        for (uint32_t j = off[l]; j < off[l + 1]; ++j)
+            if (static_cast<uint64_t>(T->child_start[j]) + T->child_len[j] > next)
+                return fail(ctx, MAIVS_ERR_ARG, "centroid tree: child range past level %u", l + 1);
+    }
+    for (uint32_t j = 0; j < T->n_leaf; ++j)
+        if (T->leaf_cells[j] >= M) return fail(ctx, MAIVS_ERR_ARG, "centroid tree: leaf cell out of range");
+    const uint32_t nodes = off[T->n_levels];
+    uint32_t *d_off, *d_cs, *d_cl, *d_leaf;
+    uint64_t *d_codes, *d_leaf_codes;
+    int rc;
+    if ((rc = dalloc(ctx, owner, &d_off, off.size())) || (rc = dalloc(ctx, owner, &d_codes, static_cast<size_t>(nodes) * W)) ||
+        (rc = dalloc(ctx, owner, &d_cs, nodes)) || (rc = dalloc(ctx, owner, &d_cl, nodes)) ||
+        (rc = dalloc(ctx, owner, &d_leaf_codes, static_cast<size_t>(T->n_leaf) * W)) ||
+        (rc = dalloc(ctx, owner, &d_leaf, T->n_leaf)))
+        return rc;
+    HIP_TRY(ctx, hipMemcpyAsync(d_off, off.data(), off.size() * 4, hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(ctx, hipMemcpyAsync(d_codes, T->level_codes, static_cast<size_t>(nodes) * W * 8, hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(ctx, hipMemcpyAsync(d_cs, T->child_start, static_cast<size_t>(nodes) * 4, hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(ctx, hipMemcpyAsync(d_cl, T->child_len, static_cast<size_t>(nodes) * 4, hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(ctx, hipMemcpyAsync(d_leaf_codes, T->leaf_codes, static_cast<size_t>(T->n_leaf) * W * 8, hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(ctx, hipMemcpyAsync(d_leaf, T->leaf_cells, static_cast<size_t>(T->n_leaf) * 4, hipMemcpyHostToDevice, ctx->stream));
+    out->lv_off = d_off;
+    out->lv_codes = d_codes;
+    out->lv_cs = d_cs;
+    out->lv_cl = d_cl;
+    out->leaf_codes = d_leaf_codes;
+    out->leaf_ids = d_leaf;
+    out->n_levels = T->n_levels;
+    out->n_leaf = T->n_leaf;
+    if (level_n_host) level_n_host->assign(T->level_n, T->level_n + T->n_levels);
+    return 0;
 }
 
 }  // namespace maivs_host

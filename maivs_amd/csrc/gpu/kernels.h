@@ -14,6 +14,7 @@
 #include "../../../include/maivs_gpu.h"
 #include "device_common.h"
 #include "types.h"
+#include "wave_tree.h"
 
 namespace maivs_dev {
 
@@ -678,6 +679,21 @@ __device__ __forceinline__ void route_phase(const DevArena& A, const Work& Wk, c
     for (uint32_t i = tid; i < nbins; i += nt) hist[i] = 0;
     for (uint32_t i = tid; i < d; i += nt) cqs[i] = Wk.cqs[static_cast<uint64_t>(qi) * d + i];
     __syncthreads();
+    uint32_t nsl = 0;
+    if (K.tree_list) {
+        // the centroid tree's leaves, live cells only (route_query, src/index.rs:1193-1204)
+        const uint32_t* tl = Wk.tlist + static_cast<uint64_t>(qi) * K.tcap;
+        const uint32_t nt_list = Wk.tcount[qi];
+        for (uint32_t r0 = 0; r0 < nt_list; r0 += nt) {
+            const uint32_t i = r0 + tid;
+            const uint32_t c = i < nt_list ? tl[i] : 0u;
+            const bool live = i < nt_list && A.mem_off[c + 1] > A.mem_off[c];
+            uint32_t tot;
+            const uint32_t pos = nsl + block_excl_scan_u32(live ? 1u : 0u, scratch, &tot);
+            if (live && pos < K.sort_cap) keys[pos] = c;
+            nsl += tot;
+        }
+    } else {
     const uint4* hrow = reinterpret_cast<const uint4*>(Wk.hs + static_cast<uint64_t>(qi) * Mp);
     const uint32_t nch8 = Mp / 8;
     auto h_at = [](const uint4& v, int k) -> uint32_t {
@@ -716,7 +732,6 @@ __device__ __forceinline__ void route_phase(const DevArena& A, const Work& Wk, c
     __syncthreads();
     const uint32_t cut = s_cut;
     // ---- shortlist: live cells with h <= cut, ascending id (dead cells and padding hold 0xFFFF)
-    uint32_t nsl = 0;
     for (uint32_t r0 = 0; r0 < nch8; r0 += nt) {
         const uint32_t ch = r0 + tid;
         uint4 v = make_uint4(~0u, ~0u, ~0u, ~0u);
@@ -732,6 +747,7 @@ __device__ __forceinline__ void route_phase(const DevArena& A, const Work& Wk, c
                 if (h_at(v, k) <= cut) keys[pos++] = ch * 8 + k;
         }
         nsl += tot;
+    }
     }
     uint32_t* chosen = Wk.chosen + static_cast<uint64_t>(qi) * K.nprobe;
     float* cscore = Wk.cscore + static_cast<uint64_t>(qi) * K.nprobe;
@@ -782,7 +798,7 @@ __device__ __forceinline__ void route_phase(const DevArena& A, const Work& Wk, c
         const float s = ok ? key_score(keys[i]) : __uint_as_float(0x7fc00000u);
         chosen[i] = c;
         cscore[i] = s;
-        if (K.adaptive && ok && i >= kSeedCells)
+        if (K.adaptive && ok && i >= K.bnd_from)
             Wk.bnd[static_cast<uint64_t>(qi) * K.nprobe + i] =
                 cos_f(fmaxf(acos_f(fminf(fmaxf(s, -1.0f), 1.0f)) - A.r_bound[c], 0.0f));
     }
@@ -1488,6 +1504,293 @@ __global__ void counters_kernel(DevArena A, Work Wk, KParams K) {
         // per-thread partials are < 2^32 for any batch the buffers can hold
         uint32_t s = block_sum_u32(static_cast<uint32_t>(v[k]), scratch);
         if (threadIdx.x == 0) (&Wk.ctl->seed_blocks)[k] = s;
+    }
+}
+
+// ================================================================ the per-query path
+
+// The reference's per-query search (search_one, src/index.rs:1381-1864, routed by route_query,
+// :1168-1305): each query on its own, its probed cells scanned in probe order.
+
+// Routing through the centroid tree (route_query's tree branch, src/index.rs:1185-1206): one wave
+// per query descends the tree on the query's 1-bit code (prep) and lists up to want_c leaf cells,
+// best first by Hamming, for route_phase to rescore. An empty descent lists nothing (the query
+// then probes no cell, as in the reference).
+constexpr uint32_t kPqTreeWaves = 4;
+
+__host__ __device__ inline uint32_t pq_tree_lds_words(uint32_t W, uint32_t cap) {
+    return 2 * W + ((W * 64 + 1 + 3) & ~3u) + (cap + 1) + (cap + 2) + cap;
+}
+
+__global__ void __launch_bounds__(kPqTreeWaves * kWave)
+pq_tree_kernel(DevArena A, Work Wk, KParams K, TreeDev T, const uint32_t* __restrict__ beams, uint32_t cap,
+               uint32_t lds_per_wave) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const uint32_t lane = lane_id(), wv = threadIdx.x / kWave;
+    const uint32_t qi = blockIdx.x * kPqTreeWaves + wv;
+    if (qi >= K.nq) return;  // wave-uniform; the kernel has no workgroup barrier
+    uint64_t* qb = reinterpret_cast<uint64_t*>(smem + static_cast<size_t>(wv) * lds_per_wave);
+    uint32_t* hist = reinterpret_cast<uint32_t*>(qb + A.W);
+    uint32_t* rbase = hist + ((A.W * 64 + 1 + 3) & ~3u);
+    uint32_t* rpre = rbase + cap + 1;
+    uint32_t* knodes = rpre + cap + 2;
+    for (uint32_t w = lane; w < A.W; w += kWave) qb[w] = Wk.qbits[static_cast<uint64_t>(qi) * A.W + w];
+    wave_sync();
+    const uint32_t n =
+        tree_descent(T, beams, K.want_c, qb, A.W, hist, rbase, rpre, knodes, Wk.tlist + static_cast<uint64_t>(qi) * K.tcap);
+    if (lane == 0) Wk.tcount[qi] = n;
+}
+
+// want-th smallest (1-based) of the n u32 values get(i), block-wide, four 8-bit radix passes.
+// Values of 0xFFFFFFFF stand for absent entries; want must not exceed the present ones.
+template <class Get>
+__device__ uint32_t select_kth_u32(uint32_t n, uint32_t want, Get get, uint32_t* hist, uint32_t* scratch) {
+    uint32_t prefix = 0, need = want;
+    for (int pass = 3; pass >= 0; --pass) {
+        const uint32_t shift = 8u * static_cast<uint32_t>(pass);
+        const uint32_t hi_shift = shift + 8;
+        for (uint32_t i = threadIdx.x; i < kHistBins; i += blockDim.x) hist[i] = 0;
+        __syncthreads();
+        for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+            const uint32_t v = get(i);
+            const bool match = hi_shift >= 32 || (v >> hi_shift) == (prefix >> hi_shift);
+            if (match) atomicAdd(&hist[(v >> shift) & 0xFFu], 1u);
+        }
+        __syncthreads();
+        const uint32_t c = threadIdx.x < kHistBins ? hist[threadIdx.x] : 0u;
+        uint32_t total;
+        const uint32_t ex = block_excl_scan_u32(c, scratch, &total);
+        const uint32_t cand = (threadIdx.x < kHistBins && ex < need && ex + c >= need) ? threadIdx.x : kNone;
+        const uint32_t digit = block_min_u32(cand, scratch);
+        const uint32_t below = block_sum_u32(threadIdx.x == digit ? ex : 0u, scratch);
+        prefix |= digit << shift;
+        need -= below;
+    }
+    return prefix;
+}
+
+// An entry of cell c is skipped when its slot has another home already scanned for this query: a
+// multi-home vector counts only at its first-ranked probed home (the seen! rule, src/index.rs:
+// 1433-1447). `scanned` is the LDS bitset of the cells before c in the probe order.
+__device__ __forceinline__ bool pq_seen(const DevArena& A, uint64_t e, uint32_t slot, uint32_t c,
+                                        const uint32_t* scanned) {
+    if (A.ma == 2) {
+        const uint32_t h = A.entry_alt[e];
+        return h != kNoAlt && h != c && ((scanned[h >> 5] >> (h & 31)) & 1u);
+    }
+    for (uint32_t j = 0; j < A.ma; ++j) {
+        const uint32_t h = A.slot_cells[static_cast<uint64_t>(slot) * A.ma + j];
+        if (h != kNone && h != c && ((scanned[h >> 5] >> (h & 31)) & 1u)) return true;
+    }
+    return false;
+}
+
+__host__ __device__ inline uint32_t pq_scan_lds_words(uint32_t MW, uint32_t maxk, uint32_t nprobe) {
+    const uint32_t nbins = (maxk >> 6) + 1;
+    return ((MW + 3) & ~3u) + ((nbins + 3) & ~3u) + ((nprobe + 1 + 3) & ~3u) + kHistBins + 32;
+}
+
+// The FastScan scan of one query (src/index.rs:1689-1757), one workgroup: cells in probe order;
+// after each cell the bucket queue on h = d >> 6 lowers tau while the entries below it already
+// reach the target (tau after a cell depends only on the entries scanned so far, so one
+// workgroup-wide pass per cell gives the reference's value), then the adaptive stop. Survivors
+// h <= tau; the target smallest (d, slot) of them go to the candidate list for finish.
+// LDS: static table[W*256] | scanned[MW4] | hist[bins4] | suffix[np4] | hist2[256] | scratch[32].
+template <int NW>
+__global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work Wk, KParams K) {
+    constexpr uint32_t TB = NW * 256;
+    __shared__ __align__(16) uint8_t table[TB];
+    extern __shared__ __align__(16) uint32_t pq_smem[];
+    __shared__ float s_seg[kScanThreads];
+    __shared__ uint32_t s_cnt, s_start, s_tau, s_kept, s_stop, s_w;
+    const uint32_t qi = blockIdx.x;
+    if (qi >= K.nq) return;
+    const uint32_t tid = threadIdx.x, nt = blockDim.x;
+    const uint32_t nbins = (A.maxk >> 6) + 1;
+    uint32_t* scanned = pq_smem;
+    uint32_t* hist = scanned + ((A.MW + 3) & ~3u);
+    float* suffix = reinterpret_cast<float*>(hist + ((nbins + 3) & ~3u));
+    uint32_t* hist2 = reinterpret_cast<uint32_t*>(suffix + ((K.nprobe + 1 + 3) & ~3u));
+    uint32_t* scratch = hist2 + kHistBins;
+    {
+        const uint4* src = reinterpret_cast<const uint4*>(Wk.lut + static_cast<uint64_t>(qi) * TB);
+        for (uint32_t i = tid; i < TB / 16; i += nt) reinterpret_cast<uint4*>(table)[i] = src[i];
+    }
+    for (uint32_t i = tid; i < A.MW; i += nt) scanned[i] = 0;
+    for (uint32_t i = tid; i < nbins; i += nt) hist[i] = 0;
+    const uint32_t nch = Wk.nchosen[qi];
+    const uint32_t* chosen = Wk.chosen + static_cast<uint64_t>(qi) * K.nprobe;
+    // suffix maxima of the reachability bounds (src/index.rs:1466-1489), suffix[nch] = -inf
+    if (K.adaptive) {
+        const float* bnd = Wk.bnd + static_cast<uint64_t>(qi) * K.nprobe;
+        const uint32_t per = (nch + nt - 1) / nt, b0 = min(tid * per, nch), b1 = min(b0 + per, nch);
+        float run = -INFINITY;
+        for (uint32_t i = b1; i-- > b0;) {
+            run = fmaxf(bnd[i], run);
+            suffix[i] = run;
+        }
+        s_seg[tid] = run;
+        __syncthreads();
+        if (tid == 0) {
+            float right = -INFINITY;
+            for (uint32_t t = nt; t-- > 0;) {
+                const float v = s_seg[t];
+                s_seg[t] = right;
+                right = fmaxf(v, right);
+            }
+            suffix[nch] = -INFINITY;
+        }
+        __syncthreads();
+        for (uint32_t i = b0; i < b1; ++i) suffix[i] = fmaxf(suffix[i], s_seg[tid]);
+    }
+    if (tid == 0) {
+        s_cnt = 0;
+        s_start = 0;
+        s_tau = A.maxk >> 6;
+        s_kept = 0;
+        s_stop = 0;
+    }
+    __syncthreads();
+    uint64_t* cbuf = Wk.pqc + static_cast<uint64_t>(qi) * K.pq_cap;
+    const uint32_t target = K.target;
+    bool flagged = false;
+    for (uint32_t ci_i = 0; ci_i < nch; ++ci_i) {
+        const uint32_t c = chosen[ci_i];
+        const uint32_t e0 = A.mem_off[c], len = A.mem_off[c + 1] - e0;
+        const uint32_t tau = s_tau;
+        for (uint32_t base = 0; base < len; base += nt) {
+            const uint32_t i = base + tid;
+            if (i < len) {
+                const uint64_t e = static_cast<uint64_t>(e0) + i;
+                Code<NW> code;
+                code.load(A.codes + e * (2 * NW));
+                const uint32_t dv = A.maxk - lut_sum1<NW>(code, table);
+                const uint32_t h = dv >> 6;
+                if (h <= tau) {
+                    const uint32_t slot = A.members[e];
+                    bool ok = true;
+                    if (K.filter) {
+                        const uint32_t tg = A.entry_tag[e];
+                        ok = tg >= K.tag_lo && tg <= K.tag_hi;
+                    }
+                    if (ok && A.ma > 1) ok = !pq_seen(A, e, slot, c, scanned);
+                    if (ok) {
+                        const uint32_t pos = atomicAdd(&s_cnt, 1u);
+                        if (pos < K.pq_cap) cbuf[pos] = (static_cast<uint64_t>(dv) << 32) | slot;
+                        atomicAdd(&hist[h], 1u);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        if (tid == 0) {
+            // the bucket queue (src/index.rs:1712-1724): every entry this cell admitted had h <= tau
+            uint32_t kept = s_kept + (s_cnt - s_start), t = tau;
+            while (t > 0 && kept - hist[t] >= target) {
+                kept -= hist[t];
+                --t;
+            }
+            s_tau = t;
+            s_kept = kept;
+            scanned[c >> 5] |= 1u << (c & 31);
+            // the adaptive stop (:1727-1733)
+            if (K.adaptive && kept >= target) {
+                const uint32_t top = ((t + 1) << 6) - 1;
+                const uint32_t worst = A.maxk > top ? A.maxk - top : 0u;
+                const float est = Wk.delta[qi] * static_cast<float>(worst) + Wk.bias[qi];
+                const float thr = fminf(fmaxf(est / K.norm, -1.0f), 1.0f);
+                const float T = thr - K.at_margin;
+                const float sx = suffix[ci_i + 1];
+                if (!K.pq_noflag && fabsf(sx - T) <= K.prune_band) flagged = true;
+                if (sx < T) s_stop = 1;
+            }
+            if (s_cnt > K.pq_cap) s_stop = 2;
+        }
+        __syncthreads();
+        if (s_stop == 2) break;
+        // room for the next cell: drop the entries above tau
+        if (s_stop == 0 && ci_i + 1 < nch && s_cnt + K.pq_room > K.pq_cap) {
+            const uint32_t n = s_cnt, t = s_tau;
+            if (tid == 0) s_w = 0;
+            __syncthreads();
+            for (uint32_t base = 0; base < n; base += nt) {
+                const uint32_t i = base + tid;
+                const uint64_t key = i < n ? cbuf[i] : 0ull;
+                const bool keepit = i < n && (static_cast<uint32_t>(key >> 32) >> 6) <= t;
+                uint32_t tot;
+                const uint32_t off = block_excl_scan_u32(keepit ? 1u : 0u, scratch, &tot);
+                if (keepit) cbuf[s_w + off] = key;
+                __syncthreads();
+                if (tid == 0) s_w += tot;
+                __syncthreads();
+            }
+            if (tid == 0) {
+                s_cnt = s_w;
+                if (s_cnt + K.pq_room > K.pq_cap) s_stop = 2;  // the next cell might not fit
+            }
+            __syncthreads();
+            if (s_stop == 2) break;
+        }
+        if (s_stop) break;
+        if (tid == 0) s_start = s_cnt;  // the next cell's admissions count from here
+        __syncthreads();
+    }
+    __syncthreads();
+    if (tid == 0) {
+        if (flagged) Wk.flag_prune[atomicAdd(&Wk.ctl->nflag_prune, 1u)] = qi;
+        if (s_stop == 2) atomicMax(&Wk.ctl->pq_overflow, s_cnt + K.pq_room);
+    }
+    uint2* cand = Wk.cand + static_cast<uint64_t>(qi) * K.cand_cap;
+    if (s_stop == 2) {
+        if (tid == 0) {
+            Wk.cand_cnt[qi] = 0;
+            Wk.seed_cnt[qi] = 0;
+        }
+        return;
+    }
+    // survivors h <= tau; the target smallest (d, slot) when more (src/index.rs:1743-1757; ties at
+    // the cut by ascending slot)
+    const uint32_t n = s_cnt, t = s_tau;
+    auto surv_d = [&](uint32_t i) -> uint32_t {
+        const uint32_t dv = static_cast<uint32_t>(cbuf[i] >> 32);
+        return (dv >> 6) <= t ? dv : 0xFFFFFFFFu;
+    };
+    uint32_t m = 0;
+    for (uint32_t i = tid; i < n; i += nt) m += surv_d(i) != 0xFFFFFFFFu;
+    m = block_sum_u32(m, scratch);
+    uint32_t dcut = 0xFFFFFFFFu, scut = 0xFFFFFFFFu;
+    if (m > target) {
+        dcut = select_kth(n, target, [&](uint32_t i) { const uint32_t v = surv_d(i); return v == 0xFFFFFFFFu ? 0xFFFFu : v; },
+                          hist2, scratch);
+        uint32_t below = 0;
+        for (uint32_t i = tid; i < n; i += nt) below += surv_d(i) < dcut;
+        below = block_sum_u32(below, scratch);
+        scut = select_kth_u32(n, target - below,
+                              [&](uint32_t i) { return surv_d(i) == dcut ? static_cast<uint32_t>(cbuf[i]) : 0xFFFFFFFFu; },
+                              hist2, scratch);
+    }
+    if (tid == 0) s_w = 0;
+    __syncthreads();
+    for (uint32_t base = 0; base < n; base += nt) {
+        const uint32_t i = base + tid;
+        bool take = false;
+        uint2 e = make_uint2(0, 0);
+        if (i < n) {
+            const uint32_t dv = surv_d(i);
+            const uint32_t slot = static_cast<uint32_t>(cbuf[i]);
+            take = dv != 0xFFFFFFFFu && (dv < dcut || (dv == dcut && slot <= scut));
+            e = make_uint2(dv, slot);
+        }
+        uint32_t tot;
+        const uint32_t off = block_excl_scan_u32(take ? 1u : 0u, scratch, &tot);
+        if (take && s_w + off < K.cand_cap) cand[s_w + off] = e;
+        __syncthreads();
+        if (tid == 0) s_w += tot;
+        __syncthreads();
+    }
+    if (tid == 0) {
+        Wk.cand_cnt[qi] = s_w;
+        Wk.seed_cnt[qi] = 0;
     }
 }
 

@@ -253,6 +253,8 @@ KParams make_params(maivs_gpu_ctx* ctx, uint32_t nq, const maivs_search_params* 
     K.norm = std::sqrt(2.0f * static_cast<float>(A.P) / static_cast<float>(M_PI));
     K.prune_band = kPruneBand;
     K.nucleus_band = kNucleusBand;
+    K.bnd_from = kSeedCells;
+    K.tcap = 1;
     return K;
 }
 
@@ -581,6 +583,208 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
     return 0;
 }
 
+// ---------------------------------------------------------------- the per-query path
+
+constexpr uint32_t kPqMaxProbe = 8192;  // probe-list bound of the per-query scan's on-chip suffix array
+constexpr uint32_t kPqMaxLevels = 64;
+
+// Tree lists (nq x tcap), scan candidate buffers (nq x pq_cap) and the beams; grow only.
+int ensure_pq(maivs_gpu_ctx* ctx, uint32_t nq, uint32_t tcap, uint32_t pq_cap) {
+    if (nq <= ctx->cap_pq_nq && tcap <= ctx->cap_tcap && pq_cap <= ctx->cap_pq && ctx->d_beams) return 0;
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    drop_graph(ctx);
+    free_all(ctx->pq_allocs);
+    const uint32_t n = std::max(nq, ctx->cap_pq_nq), t = std::max(tcap, ctx->cap_tcap), c = std::max(pq_cap, ctx->cap_pq);
+    Work& W = ctx->Wk;
+    int rc = 0;
+    rc |= dalloc(ctx, ctx->pq_allocs, &W.tlist, static_cast<size_t>(n) * t);
+    rc |= dalloc(ctx, ctx->pq_allocs, &W.tcount, n);
+    rc |= dalloc(ctx, ctx->pq_allocs, &W.pqc, static_cast<size_t>(n) * c);
+    rc |= dalloc(ctx, ctx->pq_allocs, &ctx->d_beams, kPqMaxLevels);
+    if (rc) {
+        free_all(ctx->pq_allocs);
+        ctx->cap_pq_nq = ctx->cap_tcap = ctx->cap_pq = 0;
+        ctx->d_beams = nullptr;
+        return rc;
+    }
+    ctx->cap_pq_nq = n;
+    ctx->cap_tcap = t;
+    ctx->cap_pq = c;
+    return 0;
+}
+
+int launch_pq_tree(maivs_gpu_ctx* ctx, const KParams& K, uint32_t cap) {
+    const uint32_t words = pq_tree_lds_words(ctx->A.W, cap);
+    const uint32_t per_wave = (words * 4 + 15) & ~15u;
+    const size_t lds = static_cast<size_t>(per_wave) * kPqTreeWaves;
+    if (lds > kLdsBudget) return fail(ctx, MAIVS_ERR_UNSUPPORTED, "tree descent needs %zu bytes of LDS", lds);
+    if (lds > 64 * 1024)
+        HIP_TRY(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(pq_tree_kernel),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+    hipLaunchKernelGGL(pq_tree_kernel, dim3((K.nq + kPqTreeWaves - 1) / kPqTreeWaves), dim3(kPqTreeWaves * kWave), lds,
+                       ctx->stream, ctx->A, ctx->Wk, K, ctx->tree, ctx->d_beams, cap, per_wave);
+    HIP_TRY(ctx, hipGetLastError());
+    return 0;
+}
+
+int launch_pq_scan(maivs_gpu_ctx* ctx, const KParams& K) {
+    const DevArena& A = ctx->A;
+    const size_t lds = static_cast<size_t>(pq_scan_lds_words(A.MW, A.maxk, K.nprobe)) * 4;
+    if (lds + A.W * 256 + kScanThreads * 4 > kLdsBudget)
+        return fail(ctx, MAIVS_ERR_UNSUPPORTED, "per-query scan needs %zu bytes of LDS", lds);
+    DISPATCH_NW(A.W, {
+        if (lds > 48 * 1024)
+            HIP_TRY(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(pq_scan_kernel<NW>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+        hipLaunchKernelGGL(pq_scan_kernel<NW>, dim3(K.nq), dim3(kScanThreads), lds, ctx->stream, A, ctx->Wk, K);
+    });
+    HIP_TRY(ctx, hipGetLastError());
+    return 0;
+}
+
+// The per-query search of nq queries in device memory (search_one, src/index.rs:1381-1864).
+int run_search_pq(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_search_params* p, uint32_t* d_slots,
+                  float* d_scores, maivs_gpu_stats* st) {
+    if (!ctx->uploaded) return fail(ctx, MAIVS_ERR_NOT_UPLOADED, "no arena uploaded");
+    if (p->k == 0) return fail(ctx, MAIVS_ERR_ARG, "k must be > 0");
+    if (p->nprobe > kPqMaxProbe)
+        return fail(ctx, MAIVS_ERR_UNSUPPORTED, "the per-query path probes at most %u cells", kPqMaxProbe);
+    const DevArena& A = ctx->A;
+    maivs_gpu_stats local{};
+    maivs_gpu_stats& S = st ? *st : local;
+    S = maivs_gpu_stats{};
+    ctx->last_nq = 0;
+    if (nq == 0) return 0;
+    int rc = ensure_all(ctx, nq, p->nprobe, p->k);
+    if (rc) return rc;
+    KParams K = make_params(ctx, nq, p);
+    if (K.target > ctx->cap_cand) {
+        if ((rc = ensure_cand(ctx, K.target))) return rc;
+        K = make_params(ctx, nq, p);
+    }
+    const bool tree = ctx->tree.n_levels > 0;
+    // route_query's shortlist size: the tree keeps nprobe * max(mult, 2) leaves; the two-stage
+    // branch nprobe * mult live cells (src/index.rs:1194, 1245)
+    K.want_c = tree ? std::min<uint32_t>(p->nprobe * std::max<uint32_t>(p->shortlist_mult, 2u), ctx->tree.n_leaf)
+                    : std::min<uint32_t>(p->nprobe * p->shortlist_mult, A.n_live);
+    {
+        uint32_t sc = 1024;
+        while (sc < 4u * K.want_c && sc < ctx->max_sort_cap_route) sc <<= 1;
+        K.sort_cap = std::min(sc, ctx->max_sort_cap_route);
+    }
+    K.tree_list = tree ? 1u : 0u;
+    K.bnd_from = 0;
+    K.tcap = tree ? std::max(K.want_c, 1u) : 1u;
+    K.pq_room = std::max(A.max_cell_len, 1u);
+    const uint32_t pq_need = std::max({4u * K.target + 1024u, 2u * K.pq_room + K.target, ctx->pq_cap_min});
+    if ((rc = ensure_pq(ctx, nq, K.tcap, pq_need))) return rc;
+    K.pq_cap = ctx->cap_pq;
+    K.pq_noflag = 0;
+    if (p->nprobe == 0) {
+        std::vector<uint32_t> s(static_cast<size_t>(nq) * p->k, kNone);
+        std::vector<float> f(static_cast<size_t>(nq) * p->k, -INFINITY);
+        HIP_TRY(ctx, hipMemcpyAsync(d_slots, s.data(), s.size() * 4, hipMemcpyHostToDevice, ctx->stream));
+        HIP_TRY(ctx, hipMemcpyAsync(d_scores, f.data(), f.size() * 4, hipMemcpyHostToDevice, ctx->stream));
+        HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+        return 0;
+    }
+    uint32_t cap = 1;
+    if (tree) {
+        if (ctx->tree_level_n.size() > kPqMaxLevels) return fail(ctx, MAIVS_ERR_UNSUPPORTED, "tree deeper than %u", kPqMaxLevels);
+        std::vector<uint32_t> beams(ctx->tree_level_n.size());
+        tree_beams(ctx->tree_level_n.data(), static_cast<uint32_t>(beams.size()), ctx->tree_beam_frac, ctx->tree_min_beam,
+                   K.want_c, beams.data());
+        for (uint32_t b : beams) cap = std::max(cap, b);
+        HIP_TRY(ctx, hipMemcpyAsync(ctx->d_beams, beams.data(), beams.size() * 4, hipMemcpyHostToDevice, ctx->stream));
+    }
+    Work& W = ctx->Wk;
+    HIP_TRY(ctx, hipEventRecord(ctx->ev[0], ctx->stream));
+    if ((rc = launch_prep(ctx, K, d_q, kPrepReset | (tree ? 0u : kPrepHamming)))) return rc;
+    for (;;) {
+        if (tree && (rc = launch_pq_tree(ctx, K, cap))) return rc;
+        if ((rc = launch_route(ctx, K)) || (rc = launch_pq_scan(ctx, K)) || (rc = launch_finish(ctx, K, d_q, d_slots, d_scores)))
+            return rc;
+        Ctl ctl{};
+        if ((rc = read_ctl(ctx, &ctl))) return rc;
+        if (ctl.err_shortlist && K.sort_cap < ctx->max_sort_cap_route) {
+            K.sort_cap = ctx->max_sort_cap_route;
+            S.reruns++;
+            if ((rc = launch_reset(ctx, nq))) return rc;
+            continue;
+        }
+        if (ctl.err_shortlist)
+            return fail(ctx, MAIVS_ERR_UNSUPPORTED, "a routing shortlist of %u cells exceeds the on-chip sort capacity %u",
+                        ctl.max_shortlist, ctx->max_sort_cap_route);
+        // host checks of libm-sensitive decisions, then candidate-buffer growth; each re-runs the scan
+        for (int pass = 0; pass < 4; ++pass) {
+            bool rerun = false;
+            std::vector<float> cs;
+            std::vector<uint32_t> ch;
+            if (ctl.nflag_route) {
+                std::vector<uint32_t> fl(ctl.nflag_route);
+                HIP_TRY(ctx, hipMemcpy(fl.data(), W.flag_route, fl.size() * 4, hipMemcpyDeviceToHost));
+                for (uint32_t qi : fl) {
+                    uint32_t nch;
+                    HIP_TRY(ctx, hipMemcpy(&nch, W.nchosen + qi, 4, hipMemcpyDeviceToHost));
+                    if ((rc = fetch_probe_list(ctx, qi, p->nprobe, cs, ch))) return rc;
+                    uint32_t capn = 0;
+                    while (capn < p->nprobe && ch[capn] != kNone) ++capn;
+                    const uint32_t exact = host_nucleus(cs.data(), capn, p->target_confidence, p->beta);
+                    S.host_checks++;
+                    if (exact != nch) {
+                        S.host_fixes++;
+                        HIP_TRY(ctx, hipMemcpy(W.nchosen + qi, &exact, 4, hipMemcpyHostToDevice));
+                        rerun = true;
+                    }
+                }
+            }
+            if (ctl.nflag_prune) {
+                // the bounds of a flagged query with the host's libm acos / cos (src/index.rs:1476-1483)
+                std::vector<uint32_t> fl(ctl.nflag_prune);
+                HIP_TRY(ctx, hipMemcpy(fl.data(), W.flag_prune, fl.size() * 4, hipMemcpyDeviceToHost));
+                for (uint32_t qi : fl) {
+                    uint32_t nch;
+                    HIP_TRY(ctx, hipMemcpy(&nch, W.nchosen + qi, 4, hipMemcpyDeviceToHost));
+                    if ((rc = fetch_probe_list(ctx, qi, p->nprobe, cs, ch))) return rc;
+                    std::vector<float> b(nch);
+                    for (uint32_t i = 0; i < nch; ++i) {
+                        const float c = std::fmin(std::fmax(cs[i], -1.0f), 1.0f);
+                        b[i] = std::cos(std::fmax(std::acos(c) - ctx->h_r_bound[ch[i]], 0.0f));
+                    }
+                    if (nch)
+                        HIP_TRY(ctx, hipMemcpy(W.bnd + static_cast<uint64_t>(qi) * p->nprobe, b.data(), nch * 4,
+                                               hipMemcpyHostToDevice));
+                    S.host_checks++;
+                }
+                K.pq_noflag = 1;
+                rerun = true;
+            }
+            if (ctl.pq_overflow) {
+                ctx->pq_cap_min = std::max(ctx->pq_cap_min, 2 * ctl.pq_overflow);
+                if ((rc = ensure_pq(ctx, nq, K.tcap, ctx->pq_cap_min))) return rc;
+                K.pq_cap = ctx->cap_pq;
+                rerun = true;
+            }
+            if (!rerun) break;
+            S.reruns++;
+            if ((rc = launch_reset(ctx, nq)) || (rc = launch_pq_scan(ctx, K)) ||
+                (rc = launch_finish(ctx, K, d_q, d_slots, d_scores)) || (rc = read_ctl(ctx, &ctl)))
+                return rc;
+            ctl.nflag_route = 0;  // decided above; nucleus flags are raised only by the route
+        }
+        if (ctl.pq_overflow) return fail(ctx, MAIVS_ERR_HIP, "per-query candidate buffer still overflows");
+        break;
+    }
+    HIP_TRY(ctx, hipEventRecord(ctx->ev[6], ctx->stream));
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    float ms;
+    if (hipEventElapsedTime(&ms, ctx->ev[0], ctx->ev[6]) == hipSuccess) S.ms_total = ms;
+    (void)hipGetLastError();
+    ctx->last_nq = nq;
+    ctx->last_K = K;
+    return 0;
+}
+
 }  // namespace
 
 // ================================================================ C ABI
@@ -617,6 +821,7 @@ void maivs_gpu_destroy(maivs_gpu_ctx* ctx) {
     if (ctx->gexec) (void)hipGraphExecDestroy(ctx->gexec);
     free_all(ctx->work_allocs);
     free_all(ctx->cand_allocs);
+    free_all(ctx->pq_allocs);
     free_all(ctx->arena_allocs);
     for (auto& e : ctx->ev)
         if (e) (void)hipEventDestroy(e);
@@ -634,6 +839,13 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
         return fail(ctx, MAIVS_ERR_ARG, "arena is missing FastScan blocks, members, centroid codes or radii");
     if (!supported_nw(a->n_words)) return fail(ctx, MAIVS_ERR_UNSUPPORTED, "n_words %u not in {1,2,4,8,16}", a->n_words);
     if (a->max_assign > 1 && !a->slot_cells) return fail(ctx, MAIVS_ERR_ARG, "slot_cells missing");
+    if (a->max_assign > 1) {
+        // homes index per-cell bitsets on the device: every one must name a cell
+        const uint64_t nh = static_cast<uint64_t>(a->n_slots) * a->max_assign;
+        for (uint64_t i = 0; i < nh; ++i)
+            if (a->slot_cells[i] != UINT32_MAX && a->slot_cells[i] >= a->n_cells)
+                return fail(ctx, MAIVS_ERR_ARG, "slot_cells names cell %u of %u", a->slot_cells[i], a->n_cells);
+    }
     if (!a->cent_sq8 && !a->centroids) return fail(ctx, MAIVS_ERR_ARG, "no centroid store for the rescore");
     if (a->cent_sq8 && (!a->csq_min || !a->csq_step)) return fail(ctx, MAIVS_ERR_ARG, "csq_min/csq_step missing");
     if (a->rerank_mode == MAIVS_RERANK_F32 && !a->vecs_f32) return fail(ctx, MAIVS_ERR_ARG, "f32 rows missing");
@@ -647,8 +859,11 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
     drop_graph(ctx);
     free_all(ctx->work_allocs);
     free_all(ctx->cand_allocs);
+    free_all(ctx->pq_allocs);
     free_all(ctx->arena_allocs);
     ctx->cap_nq = ctx->cap_nprobe = ctx->cap_k = ctx->cap_cand = ctx->cap_seed = ctx->cand_nq = 0;
+    ctx->cap_pq_nq = ctx->cap_tcap = ctx->cap_pq = ctx->pq_cap_min = 0;
+    ctx->d_beams = nullptr;
     ctx->uploaded = false;
     ctx->last_nq = 0;
 
@@ -738,6 +953,10 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
                                dim3(256), 0, ctx->stream, members, tags, A.E, etag);
         }
         A.entry_tag = etag;
+        // the centroid tree of the per-query path's routing
+        if ((rc = upload_tree(ctx, ctx->arena_allocs, a->tree, A.W, A.M, &ctx->tree, &ctx->tree_level_n))) return rc;
+        ctx->tree_beam_frac = a->tree ? a->tree->beam_frac : 0.5f;
+        ctx->tree_min_beam = a->tree ? a->tree->min_beam : 32u;
         HIP_TRY(ctx, hipGetLastError());
         // chain-major copies of the rows the 8-lane dots read
         auto chain_f32 = [&](const float* src, uint64_t rows, const float** out) -> int {
@@ -847,6 +1066,34 @@ int maivs_gpu_search_batch(maivs_gpu_ctx* ctx, const float* q, uint32_t nq, cons
     if (rc) return rc;
     HIP_TRY(ctx, hipMemcpyAsync(ctx->Wk.q, q, static_cast<size_t>(nq) * ctx->A.d * 4, hipMemcpyHostToDevice, ctx->stream));
     rc = run_search(ctx, ctx->Wk.q, nq, p, ctx->Wk.out_slots, ctx->Wk.out_scores, st);
+    if (rc) return rc;
+    HIP_TRY(ctx, hipMemcpyAsync(out_slots, ctx->Wk.out_slots, static_cast<size_t>(nq) * p->k * 4, hipMemcpyDeviceToHost,
+                                ctx->stream));
+    HIP_TRY(ctx, hipMemcpyAsync(out_scores, ctx->Wk.out_scores, static_cast<size_t>(nq) * p->k * 4,
+                                hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+int maivs_gpu_search_queries_device(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_search_params* p,
+                                    uint32_t* d_slots, float* d_scores, maivs_gpu_stats* st) {
+    if (!ctx || !p || (nq && (!d_q || !d_slots || !d_scores))) return MAIVS_ERR_ARG;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    return run_search_pq(ctx, d_q, nq, p, d_slots, d_scores, st);
+}
+
+int maivs_gpu_search_queries(maivs_gpu_ctx* ctx, const float* q, uint32_t nq, const maivs_search_params* p,
+                             uint32_t* out_slots, float* out_scores, maivs_gpu_stats* st) {
+    if (!ctx || !p || (nq && (!q || !out_slots || !out_scores))) return MAIVS_ERR_ARG;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    if (!ctx->uploaded) return fail(ctx, MAIVS_ERR_NOT_UPLOADED, "no arena uploaded");
+    if (nq == 0) return 0;
+    int rc = ensure_all(ctx, nq, p->nprobe, p->k);
+    if (rc) return rc;
+    HIP_TRY(ctx, hipMemcpyAsync(ctx->Wk.q, q, static_cast<size_t>(nq) * ctx->A.d * 4, hipMemcpyHostToDevice, ctx->stream));
+    rc = run_search_pq(ctx, ctx->Wk.q, nq, p, ctx->Wk.out_slots, ctx->Wk.out_scores, st);
     if (rc) return rc;
     HIP_TRY(ctx, hipMemcpyAsync(out_slots, ctx->Wk.out_slots, static_cast<size_t>(nq) * p->k * 4, hipMemcpyDeviceToHost,
                                 ctx->stream));

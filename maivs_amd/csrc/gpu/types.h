@@ -64,6 +64,7 @@ struct Ctl {
     uint32_t err_seed;        // a seed set exceeded its on-chip capacity
     uint32_t bucket_overflow; // a cell's query bucket was full (the pass falls back to the counting sort)
     uint32_t n_active;        // scan work items: (cell, group of kG bucket entries) (bucket mode)
+    uint32_t pq_overflow;     // per-query path: largest candidate count past its buffer (0 = none)
     unsigned long long seed_blocks, scan_blocks, scan_pairs, survivors, rerank_rows;
 };
 
@@ -102,6 +103,10 @@ struct Work {
     uint32_t* active;      // scan work items, cell * kItemGroups + group, in arrival order (bucket mode)
     uint32_t* flag_route;  // nq
     uint32_t* flag_prune;  // nq
+    // per-query path
+    uint32_t* tlist;       // nq x tcap: the centroid tree's leaf cells for each query
+    uint32_t* tcount;      // nq
+    uint64_t* pqc;         // nq x pq_cap: scanned candidates (d << 32 | slot)
     Ctl* ctl;
 };
 
@@ -109,6 +114,8 @@ struct KParams {
     uint32_t nq, k, nprobe, want_c, target, adaptive, sort_cap, use_nucleus;
     uint32_t seed_cap, cand_cap, fin_cap, key_cap, bucket_cap;
     uint32_t filter, tag_lo, tag_hi;  // keep!: tag in [tag_lo, tag_hi] (filter != 0 only with tags)
+    // per-query path: routing from the tree's list, bounds from this probe rank on, buffer sizes
+    uint32_t tree_list, bnd_from, tcap, pq_cap, pq_room, pq_noflag;
     float tc, beta, at_margin, norm, prune_band, nucleus_band;
 };
 

@@ -1,0 +1,205 @@
+// Wave-level pieces shared by the index build and the per-query search: LDS ordering inside a
+// wave, Hamming distance, the keep_smallest selection (src/tree.rs:120-159) and the beam descent
+// of the centroid tree (src/tree.rs:574-628), and the exact one-lane f32 dot.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "device_common.h"
+
+namespace maivs_dev {
+
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ uint32_t hamming_lds(const uint64_t* qb, const uint64_t* code, uint32_t W) {
+    uint32_t h = 0;
+    for (uint32_t w = 0; w < W; ++w) h += __popcll(qb[w] ^ code[w]);
+    return h;
+}
+
+// Total-order key of an f32 (ascending), for a first-minimum search.
+__device__ __forceinline__ uint32_t asc_f32_key(float f) {
+    const uint32_t b = __float_as_uint(f == 0.0f ? 0.0f : f);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// keep_smallest over the frontier positions [0, F) with distance hd(p): emit(k, p) for the kept
+// entries in encounter order (k = 0, 1, ...). Returns the number kept = min(keep, F).
+template <class HD, class EMIT>
+__device__ uint32_t wave_keep_smallest(uint32_t F, uint32_t keep, uint32_t bits, uint32_t* hist, HD hd, EMIT emit) {
+    const uint32_t lane = lane_id();
+    if (keep >= F) {
+        for (uint32_t p = lane; p < F; p += kWave) emit(p, p);
+        return F;
+    }
+    for (uint32_t j = lane; j <= bits; j += kWave) hist[j] = 0;
+    wave_sync();
+    for (uint32_t p = lane; p < F; p += kWave) atomicAdd(&hist[hd(p)], 1u);
+    wave_sync();
+    // t = the smallest distance with count(h <= t) >= keep; below = count(h < t)
+    const uint32_t nb = bits + 1, bpl = (nb + kWave - 1) / kWave;
+    const uint32_t b0 = min(lane * bpl, nb), b1 = min(b0 + bpl, nb);
+    uint32_t mine = 0;
+    for (uint32_t b = b0; b < b1; ++b) mine += hist[b];
+    uint32_t incl = mine;
+    for (int o = 1; o < kWave; o <<= 1) {
+        const uint32_t y = __shfl_up(incl, o, kWave);
+        if (lane >= static_cast<uint32_t>(o)) incl += y;
+    }
+    const uint32_t excl = incl - mine;
+    const bool here = excl < keep && incl >= keep;
+    uint32_t t = 0, below = 0;
+    if (here) {
+        uint32_t cum = excl;
+        for (uint32_t b = b0; b < b1; ++b) {
+            if (cum + hist[b] >= keep) {
+                t = b;
+                below = cum;
+                break;
+            }
+            cum += hist[b];
+        }
+    }
+    const uint64_t hm = __ballot(here);
+    const int src = __ffsll(static_cast<long long>(hm)) - 1;
+    t = __shfl(t, src, kWave);
+    below = __shfl(below, src, kWave);
+    const uint32_t need_eq = keep - below;
+    uint32_t eq_seen = 0, kept = 0;
+    for (uint32_t c0 = 0; c0 < F; c0 += kWave) {
+        const uint32_t p = c0 + lane;
+        const bool valid = p < F;
+        const uint32_t h = valid ? hd(p) : 0xFFFFFFFFu;
+        const uint64_t eqm = __ballot(valid && h == t);
+        const bool take = valid && (h < t || (h == t && eq_seen + lanes_below(eqm) < need_eq));
+        const uint64_t tm = __ballot(take);
+        if (take) emit(kept + lanes_below(tm), p);
+        eq_seen += __popcll(eqm);
+        kept += __popcll(tm);
+    }
+    return kept;
+}
+
+// Frontier position p -> node id, from the ranges of the kept parents (rpre: prefix of lengths).
+__device__ __forceinline__ uint32_t frontier_node(const uint32_t* rbase, const uint32_t* rpre, uint32_t nr, uint32_t p) {
+    uint32_t lo = 0, hi = nr;  // the last r with rpre[r] <= p
+    while (hi - lo > 1) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (rpre[mid] <= p) lo = mid; else hi = mid;
+    }
+    return rbase[lo] + (p - rpre[lo]);
+}
+
+// Exact dot_f32(a, b) by one lane: 8 accumulators, hsum, sequential tail (src/index.rs:136-152).
+template <class LA, class LB>
+__device__ __forceinline__ float dot_lane(uint32_t d, LA la, LB lb) {
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    const uint32_t d8 = d & ~7u;
+    for (uint32_t t = 0; t < d8; t += 8) {
+#pragma unroll
+        for (uint32_t l = 0; l < 8; ++l) acc[l] = __builtin_fmaf(la(t + l), lb(t + l), acc[l]);
+    }
+    float s = ((acc[0] + acc[4]) + (acc[2] + acc[6])) + ((acc[1] + acc[5]) + (acc[3] + acc[7]));
+    for (uint32_t e = d8; e < d; ++e) s += la(e) * lb(e);
+    return s;
+}
+
+// The centroid tree in HBM, compacted layout: node j of level l has the children
+// [cs[j], cs[j] + cl[j]) of level l + 1 (the leaves after the last level).
+struct TreeDev {
+    const uint32_t* lv_off;      // n_levels + 1 node offsets, coarsest level first
+    const uint64_t* lv_codes;    // sum of level sizes x W
+    const uint32_t* lv_cs;
+    const uint32_t* lv_cl;
+    const uint64_t* leaf_codes;  // n_leaf x W
+    const uint32_t* leaf_ids;    // n_leaf: the cell of each leaf
+    uint32_t n_levels, n_leaf;
+};
+
+// One wave: the beam descent for the code qb (LDS, W words) keeping beams[l] nodes per level and
+// `want` leaves, ties in encounter order. Writes the leaves' cells, best first by Hamming, to out
+// and returns their number (0: the caller scores every cell, as the reference does on an empty
+// result). Per-wave LDS scratch: hist[W*64 + 1], rbase[cap + 1], rpre[cap + 2], knodes[cap] with
+// cap >= every beam; out[want].
+__device__ inline uint32_t tree_descent(const TreeDev& T, const uint32_t* beams, uint32_t want, const uint64_t* qb, uint32_t W,
+                                 uint32_t* hist, uint32_t* rbase, uint32_t* rpre, uint32_t* knodes, uint32_t* out) {
+    const uint32_t lane = lane_id(), bits = W * 64;
+    if (T.n_levels == 0) return 0;
+    uint32_t nr = 1;
+    if (lane == 0) {
+        rbase[0] = 0;
+        rpre[0] = 0;
+        rpre[1] = T.lv_off[1] - T.lv_off[0];
+    }
+    wave_sync();
+    uint32_t F = T.lv_off[1] - T.lv_off[0];
+    for (uint32_t li = 0; li < T.n_levels; ++li) {
+        const uint64_t* codes = T.lv_codes + static_cast<uint64_t>(T.lv_off[li]) * W;
+        const uint32_t keep = min(beams[li], F);
+        if (keep == 0) return 0;
+        const uint32_t nk = wave_keep_smallest(
+            F, keep, bits, hist,
+            [&](uint32_t p) {
+                const uint32_t node = frontier_node(rbase, rpre, nr, p);
+                return hamming_lds(qb, codes + static_cast<uint64_t>(node) * W, W);
+            },
+            [&](uint32_t k, uint32_t p) { knodes[k] = frontier_node(rbase, rpre, nr, p); });
+        wave_sync();
+        // children of the kept nodes, in order: the next frontier's ranges
+        const uint32_t* cs = T.lv_cs + T.lv_off[li];
+        const uint32_t* cl = T.lv_cl + T.lv_off[li];
+        uint32_t carry = 0;
+        for (uint32_t k0 = 0; k0 < nk; k0 += kWave) {
+            const uint32_t k = k0 + lane;
+            const uint32_t node = k < nk ? knodes[k] : 0u;
+            const uint32_t len = k < nk ? cl[node] : 0u;
+            uint32_t incl = len;
+            for (int o = 1; o < kWave; o <<= 1) {
+                const uint32_t y = __shfl_up(incl, o, kWave);
+                if (lane >= static_cast<uint32_t>(o)) incl += y;
+            }
+            if (k < nk) {
+                rbase[k] = cs[node];
+                rpre[k] = carry + incl - len;
+            }
+            carry += __shfl(incl, kWave - 1, kWave);
+        }
+        if (lane == 0) rpre[nk] = carry;
+        wave_sync();
+        nr = nk;
+        F = carry;
+    }
+    const uint32_t keep = min(want, F);
+    if (keep == 0) return 0;
+    const uint32_t nout = wave_keep_smallest(
+        F, keep, bits, hist,
+        [&](uint32_t p) {
+            const uint32_t leaf = frontier_node(rbase, rpre, nr, p);
+            return hamming_lds(qb, T.leaf_codes + static_cast<uint64_t>(leaf) * W, W);
+        },
+        [&](uint32_t k, uint32_t p) { out[k] = T.leaf_ids[frontier_node(rbase, rpre, nr, p)]; });
+    wave_sync();
+    return nout;
+}
+
+// beams of the descent (src/tree.rs:559-570): from the finest level up, clamp(ceil(need * frac),
+// min_beam, level size), need starting at max(want, 1).
+__host__ inline void tree_beams(const uint32_t* level_n, uint32_t n_levels, float frac, uint32_t min_beam, uint32_t want,
+                                uint32_t* out) {
+    uint32_t need = want > 0 ? want : 1;
+    for (uint32_t i = n_levels; i-- > 0;) {
+        const float raw = static_cast<float>(need) * frac;
+        uint32_t b = static_cast<uint32_t>(__builtin_ceilf(raw));
+        b = b > min_beam ? b : min_beam;
+        b = b < level_n[i] ? b : level_n[i];
+        out[i] = b;
+        need = b;
+    }
+}
+
+}  // namespace maivs_dev

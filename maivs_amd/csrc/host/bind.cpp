@@ -155,10 +155,19 @@ PYBIND11_MODULE(_maivs, m) {
              })
         .def(
             "search",
-            [](PyIndex&, const py::array&, size_t, size_t, float, float) -> py::tuple {
-                PyErr_SetString(PyExc_NotImplementedError,
-                                "the single-query path (search) is not part of this build; use search_batch");
-                throw py::error_already_set();
+            [](PyIndex& s, const py::array& query, size_t k, size_t nprobe, float tc, float beta) -> py::tuple {
+                if (!py::dtype::of<float>().is(query.dtype())) throw py::type_error("query must be a float32 array");
+                if (query.ndim() != 1) throw py::value_error("query must be 1-dimensional");
+                if (static_cast<size_t>(query.shape(0)) != s.ix.dim()) throw py::value_error("query dim mismatch");
+                // the reference copies the query element by element, so any stride is accepted
+                py::array_t<float, py::array::c_style | py::array::forcecast> qc(query);
+                std::vector<uint64_t> ids;
+                std::vector<float> scores;
+                {
+                    py::gil_scoped_release nogil;
+                    translate([&] { s.ix.search(qc.data(), k, nprobe, tc, beta, ids, scores); });
+                }
+                return py::make_tuple(py::cast(ids), py::cast(scores));
             },
             py::arg("query"), py::arg("k"), py::arg("nprobe") = 16, py::arg("target_confidence") = 0.95f,
             py::arg("beta") = 8.0f)
@@ -239,6 +248,12 @@ PYBIND11_MODULE(_maivs, m) {
              "Device timings and work counters of the last search_batch call.")
         .def("cellmajor_blocker", [](PyIndex& s, bool cell_major) { return s.ix.cellmajor_blocker(cell_major); },
              py::arg("cell_major") = true)
+        .def("perquery_blocker", [](PyIndex& s) { return s.ix.perquery_blocker(); })
+        .def("takes_cellmajor", [](PyIndex& s, size_t nq, bool cell_major) { return s.ix.takes_cellmajor(nq, cell_major); },
+             py::arg("nq"), py::arg("cell_major") = true,
+             "Whether search_batch(nq queries) takes the batched cell-major path (the reference's cm_ok).")
+        .def("set_batched_filter", [](PyIndex& s, bool on) { s.ix.set_batched_filter(on); },
+             "Filtered searches take the batched path too (not in the reference; off by default).")
         .def("_arena_desc",
              [](PyIndex& s) -> uintptr_t {
                  const maivs_arena_desc* d = s.ix.arena_desc();
@@ -306,6 +321,28 @@ PYBIND11_MODULE(_maivs, m) {
                  return r;
              },
              "Copies of the compacted arena arrays (for brute-force checks).")
+        .def("_tree_arrays",
+             [](PyIndex& s) -> py::object {
+                 maivs::TreeFlat f;
+                 if (!s.ix.tree_flat(f)) return py::none();
+                 auto arr = [](const auto& v) {
+                     using T = typename std::decay_t<decltype(v)>::value_type;
+                     py::array_t<T> a(static_cast<py::ssize_t>(v.size()));
+                     if (!v.empty()) std::memcpy(a.mutable_data(), v.data(), v.size() * sizeof(T));
+                     return a;
+                 };
+                 py::dict d;
+                 d["level_n"] = arr(f.level_n);
+                 d["level_codes"] = arr(f.level_codes);
+                 d["child_start"] = arr(f.child_start);
+                 d["child_len"] = arr(f.child_len);
+                 d["leaf_codes"] = arr(f.leaf_codes);
+                 d["leaf_cells"] = arr(f.leaf_cells);
+                 d["beam_frac"] = f.beam_frac;
+                 d["min_beam"] = f.min_beam;
+                 return d;
+             },
+             "The centroid tree as flat arrays (None without a tree).")
         .def("_rot_signs", [](PyIndex& s) {
             const auto& r = s.ix.rot_signs();
             py::array_t<float> a(static_cast<py::ssize_t>(r.size()));

@@ -25,6 +25,8 @@ struct GpuApi {
     int (*upload)(maivs_gpu_ctx*, const maivs_arena_desc*) = nullptr;
     int (*search)(maivs_gpu_ctx*, const float*, uint32_t, const maivs_search_params*, uint32_t*, float*,
                   maivs_gpu_stats*) = nullptr;
+    int (*search_pq)(maivs_gpu_ctx*, const float*, uint32_t, const maivs_search_params*, uint32_t*, float*,
+                     maivs_gpu_stats*) = nullptr;
     int (*kmeans)(maivs_gpu_ctx*, const float*, uint64_t, uint32_t, const uint32_t*, const maivs_kmeans_job*,
                   uint32_t, uint32_t*, float*) = nullptr;
     int (*place)(maivs_gpu_ctx*, const maivs_place_desc*, const float*, uint32_t, uint32_t*, uint64_t*,
@@ -66,6 +68,7 @@ const GpuApi& gpu_api() {
         api.last_error = reinterpret_cast<decltype(api.last_error)>(sym("maivs_gpu_last_error"));
         api.upload = reinterpret_cast<decltype(api.upload)>(sym("maivs_gpu_upload_arena"));
         api.search = reinterpret_cast<decltype(api.search)>(sym("maivs_gpu_search_batch"));
+        api.search_pq = reinterpret_cast<decltype(api.search_pq)>(sym("maivs_gpu_search_queries"));
         api.kmeans = reinterpret_cast<decltype(api.kmeans)>(sym("maivs_gpu_kmeans"));
         api.place = reinterpret_cast<decltype(api.place)>(sym("maivs_gpu_place"));
     });
@@ -404,6 +407,7 @@ void FlatCellIndex::maybe_rebuild_centroid_tree() {  // src/index.rs:667-677
 }
 
 void FlatCellIndex::rebuild_centroid_tree() {  // src/index.rs:684-708
+    ++generation_;  // the uploaded arena carries the tree
     tree_cells_ = live_cell_count();
     std::vector<uint32_t> live;
     for (size_t i = 0; i < cells_.size(); ++i)
@@ -557,6 +561,21 @@ void FlatCellIndex::encode_slot(const float* v, uint64_t* bits_out, int8_t* i8_o
     }
 }
 
+// A C view of a flattened tree (valid while tf lives).
+void fill_tree_desc(const TreeFlat& tf, maivs_tree_desc& td) {
+    td = maivs_tree_desc{};
+    td.n_levels = static_cast<uint32_t>(tf.level_n.size());
+    td.n_leaf = static_cast<uint32_t>(tf.leaf_cells.size());
+    td.beam_frac = tf.beam_frac;
+    td.min_beam = tf.min_beam;
+    td.level_n = tf.level_n.data();
+    td.level_codes = tf.level_codes.data();
+    td.child_start = tf.child_start.data();
+    td.child_len = tf.child_len.data();
+    td.leaf_codes = tf.leaf_codes.data();
+    td.leaf_cells = tf.leaf_cells.data();
+}
+
 // add_batch's per-vector work on the GPU (maivs_gpu_place): the homes of every input vector
 // (assign_cells_routed), its 1-bit code and, when kept, its i8 / SQ8 copy.
 void FlatCellIndex::place_on_gpu(const float* data, size_t n, bool store_i8, std::vector<std::vector<uint32_t>>& asg,
@@ -580,18 +599,12 @@ void FlatCellIndex::place_on_gpu(const float* data, size_t n, bool store_i8, std
     D.sq_min = sq_min_.empty() ? nullptr : sq_min_.data();
     D.sq_step = sq_step_.empty() ? nullptr : sq_step_.data();
     TreeFlat tf;
+    maivs_tree_desc td{};
     if (tree_) {
-        tree_->export_flat(std::max<size_t>(64, ma * 8), tf);  // the want of src/index.rs:2452
-        D.tree.n_levels = static_cast<uint32_t>(tf.level_n.size());
-        D.tree.n_leaf = static_cast<uint32_t>(tf.leaf_cells.size());
-        D.tree.want = static_cast<uint32_t>(std::max<size_t>(64, ma * 8));
-        D.tree.level_n = tf.level_n.data();
-        D.tree.beams = tf.beams.data();
-        D.tree.level_codes = tf.level_codes.data();
-        D.tree.child_start = tf.child_start.data();
-        D.tree.child_len = tf.child_len.data();
-        D.tree.leaf_codes = tf.leaf_codes.data();
-        D.tree.leaf_cells = tf.leaf_cells.data();
+        tree_->export_flat(std::max<size_t>(64, ma * 8), tf);
+        fill_tree_desc(tf, td);
+        D.tree = td;
+        D.tree_want = static_cast<uint32_t>(std::max<size_t>(64, ma * 8));  // the want of src/index.rs:2452
     }
     std::vector<uint32_t> homes(n * ma);
     bits.assign(n * n_words_, 0);
@@ -939,6 +952,12 @@ const maivs_arena_desc* FlatCellIndex::arena_desc() {
         if (tags_.size() < ext_ids_.size()) tags_.resize(ext_ids_.size(), 0);
         a.tags = tags_.data();
     }
+    // the centroid tree, for the per-query path's routing (route_query, src/index.rs:1185-1206)
+    if (tree_) {
+        tree_->export_flat(64, tree_flat_);
+        fill_tree_desc(tree_flat_, tree_desc_);
+        a.tree = &tree_desc_;
+    }
     return &desc_;
 }
 
@@ -961,30 +980,81 @@ maivs_search_params FlatCellIndex::search_params(size_t k, size_t nprobe, float 
     return p;
 }
 
-void FlatCellIndex::search_batch(const float* q, size_t nq, size_t k, size_t nprobe, float tc, float beta,
-                                 bool cell_major, std::vector<uint64_t>& ids, std::vector<float>& scores,
-                                 maivs_gpu_stats* stats) {
-    // src/index.rs:3317-3362
-    ids.assign(nq * k, UINT64_MAX);
-    scores.assign(nq * k, -INFINITY);
-    if (cells_.empty() || n_live_ == 0 || nq == 0 || k == 0) return;
-    std::string why = cellmajor_blocker(cell_major);
-    if (!why.empty()) throw Unsupported(why);
+std::string FlatCellIndex::perquery_blocker() const {
+    // what the GPU per-query path runs: search_one's FastScan branch (src/index.rs:1689-1757) with
+    // route_query's tree or two-stage router (:1185-1257)
+    if (scan_mode_ != ScanMode::Binary) return "the per-query path needs scan_mode='binary'";
+    if (!fastscan_ || !compacted_ || fs_off_.empty())
+        return "the per-query path runs the FastScan scan: set_fastscan(True) and compact() first";
+    if (!tree_ && graph_route_ && cells_.size() >= graph_min_cells_)
+        return "the centroid-graph router is not part of this build (set_graph_route(False, ...))";
+    if (!tree_ && (!two_stage_ || cent_bits_.empty()))
+        return "the per-query path routes with the centroid tree or set_two_stage(True, mult)";
+    if (par_scan_ && !adaptive_ && max_assign_ <= 1)
+        return "set_parallel_scan's within-query parallel scan is not part of this build";
+    if (f16_rerank_) return "the f16 rerank store is not part of this build";
+    if (!per_dim_sq_ && (!keep_f32_ || vecs_f32_.empty()))
+        return "the rerank needs the f32 rows or the per-dimension SQ8 store";
+    if (n_words_ * 64 > 65536) return "codes longer than 65536 bits";
+    return "";
+}
+
+void FlatCellIndex::ensure_uploaded() {
     if (!gpu_) gpu_ = std::make_unique<GpuSession>();
-    std::lock_guard<std::mutex> lk(gpu_->mu);
     if (gpu_->uploaded_gen != generation_) {
         gpu_->check(gpu_api().upload(gpu_->ctx_, arena_desc()), "maivs_gpu_upload_arena");
         gpu_->uploaded_gen = generation_;
     }
+}
+
+bool FlatCellIndex::takes_cellmajor(size_t nq, bool cell_major) const {
+    // cm_ok, src/index.rs:3343-3348
+    return cell_major && scan_mode_ == ScanMode::Binary && compacted_ && (max_assign_ == 1 || !rep_off_.empty()) &&
+           (!tag_filter_ || batched_filter_) && nq >= 2 * static_cast<size_t>(std::max(num_threads(), 1u));
+}
+
+void FlatCellIndex::search_batch(const float* q, size_t nq, size_t k, size_t nprobe, float tc, float beta,
+                                 bool cell_major, std::vector<uint64_t>& ids, std::vector<float>& scores,
+                                 maivs_gpu_stats* stats) {
+    // src/index.rs:3317-3392
+    ids.assign(nq * k, UINT64_MAX);
+    scores.assign(nq * k, -INFINITY);
+    if (cells_.empty() || n_live_ == 0 || nq == 0 || k == 0) return;
+    const bool cm = takes_cellmajor(nq, cell_major);
+    std::string why = cm ? cellmajor_blocker(true) : perquery_blocker();
+    if (!why.empty()) throw Unsupported(why);
+    if (!gpu_) gpu_ = std::make_unique<GpuSession>();
+    std::lock_guard<std::mutex> lk(gpu_->mu);
+    ensure_uploaded();
     maivs_search_params p = search_params(k, nprobe, tc, beta);
     std::vector<uint32_t> slots(nq * k);
     std::vector<float> sc(nq * k);
-    gpu_->check(gpu_api().search(gpu_->ctx_, q, static_cast<uint32_t>(nq), &p, slots.data(), sc.data(), stats),
-                "maivs_gpu_search_batch");
+    if (cm)
+        gpu_->check(gpu_api().search(gpu_->ctx_, q, static_cast<uint32_t>(nq), &p, slots.data(), sc.data(), stats),
+                    "maivs_gpu_search_batch");
+    else
+        gpu_->check(gpu_api().search_pq(gpu_->ctx_, q, static_cast<uint32_t>(nq), &p, slots.data(), sc.data(), stats),
+                    "maivs_gpu_search_queries");
     for (size_t i = 0; i < nq * k; ++i) {
         if (slots[i] == UINT32_MAX) continue;
         ids[i] = ext_ids_[slots[i]];
         scores[i] = sc[i];
+    }
+}
+
+void FlatCellIndex::search(const float* q, size_t k, size_t nprobe, float tc, float beta, std::vector<uint64_t>& ids,
+                           std::vector<float>& scores) {
+    // src/index.rs:3283-3305: one query through search_one; only the results found, best first
+    ids.clear();
+    scores.clear();
+    if (cells_.empty() || n_live_ == 0 || k == 0) return;
+    std::vector<uint64_t> i2;
+    std::vector<float> s2;
+    search_batch(q, 1, k, nprobe, tc, beta, false, i2, s2);
+    for (size_t i = 0; i < k; ++i) {
+        if (i2[i] == UINT64_MAX) break;
+        ids.push_back(i2[i]);
+        scores.push_back(s2[i]);
     }
 }
 

@@ -41,6 +41,8 @@ struct Cell {
 
 class GpuSession;  // owns a maivs_gpu_ctx (index.cpp)
 
+void fill_tree_desc(const TreeFlat& tf, maivs_tree_desc& td);
+
 class FlatCellIndex {
 public:
     FlatCellIndex(size_t dim, const std::string& scan_mode, size_t rerank_factor, uint64_t seed,
@@ -90,8 +92,18 @@ public:
     void search_batch(const float* q, size_t nq, size_t k, size_t nprobe, float tc, float beta,
                       bool cell_major, std::vector<uint64_t>& ids, std::vector<float>& scores,
                       maivs_gpu_stats* stats = nullptr);
+    // One query through the per-query path (src/index.rs:3283-3305): up to k results, best first.
+    void search(const float* q, size_t k, size_t nprobe, float tc, float beta, std::vector<uint64_t>& ids,
+                std::vector<float>& scores);
     // Why the batched cell-major path cannot run right now (empty string when it can).
     std::string cellmajor_blocker(bool cell_major) const;
+    // Why the per-query path cannot run right now (empty string when it can).
+    std::string perquery_blocker() const;
+    // Whether search_batch takes the batched cell-major path for nq queries (the reference's cm_ok).
+    bool takes_cellmajor(size_t nq, bool cell_major) const;
+    // Not in the reference: filtered searches take the batched path too (the filter is applied in
+    // its scans); by default they take the per-query path, as the reference's do.
+    void set_batched_filter(bool on) { batched_filter_ = on; }
 
     // ---- persistence (src/persist.rs, format "MAIVS2\0\1" + an extension trailer) ----
     void save(const std::string& path) const;
@@ -110,6 +122,12 @@ public:
     const std::vector<uint64_t>& bits() const { return bits_; }
     const std::vector<float>& rot_signs() const { return rot_signs_; }
     uint64_t generation() const { return generation_; }
+    // The centroid tree's flat arrays (false when there is no tree).
+    bool tree_flat(TreeFlat& f) const {
+        if (!tree_) return false;
+        tree_->export_flat(64, f);
+        return true;
+    }
 
 private:
     void refresh_derived();
@@ -128,6 +146,7 @@ private:
     void recompute_centroid(Cell& c);
     void touch() { ++generation_; compacted_ = false; }
     KMeansRunner gpu_kmeans_runner();
+    void ensure_uploaded();
     void place_on_gpu(const float* data, size_t n, bool store_i8, std::vector<std::vector<uint32_t>>& asg,
                       std::vector<uint64_t>& bits, std::vector<int8_t>& i8);
 
@@ -183,8 +202,11 @@ private:
     std::vector<uint32_t> mem_off_, members_flat_;
     std::vector<float> cents_flat_, r_bound_flat_;
     maivs_arena_desc desc_{};
+    TreeFlat tree_flat_;
+    maivs_tree_desc tree_desc_{};
     uint64_t generation_ = 0;
     bool gpu_build_ = false;
+    bool batched_filter_ = false;
     std::unique_ptr<GpuSession> gpu_;
 };
 

@@ -349,6 +349,8 @@ void CentroidTree::export_flat(size_t want, TreeFlat& f) const {
             if (l.child_idx[j] != j) throw std::logic_error("centroid tree is not in its compacted layout");
     }
     for (size_t b : beams(want)) f.beams.push_back(static_cast<uint32_t>(b));
+    f.beam_frac = beam_frac_;
+    f.min_beam = static_cast<uint32_t>(kMinBeam);
     f.leaf_codes = leaf_codes_;
     f.leaf_cells = leaf_ids_;
 }

@@ -45,6 +45,8 @@ struct TreeLevel {
 struct TreeFlat {
     std::vector<uint32_t> level_n, beams, child_start, child_len, leaf_cells;
     std::vector<uint64_t> level_codes, leaf_codes;
+    float beam_frac = 0.5f;
+    uint32_t min_beam = 32;
 };
 
 struct TreeScratch {

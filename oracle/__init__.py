@@ -35,6 +35,8 @@ _SIGS = {
     "orc_search_batch": (C.c_int, [P, P, U32, C.POINTER(SearchParams), U32, P, P]),
     "orc_last_candidates": (C.c_int, [P, P, P, P, P, P, U64]),
     "orc_last_total_candidates": (U64, []),
+    "orc_search_one": (C.c_int, [P, P, U32, C.POINTER(SearchParams), U32, P, P]),
+    "orc_route_query": (C.c_int, [P, P, U32, C.POINTER(SearchParams), U32, P, P, P]),
 }
 
 
@@ -160,6 +162,31 @@ def search_batch(desc_addr: int, q: np.ndarray, params: SearchParams, nthreads: 
     if rc != 0:
         raise RuntimeError(f"orc_search_batch failed ({rc})")
     return slots, scores
+
+
+def search_one(desc_addr: int, q: np.ndarray, params: SearchParams, nthreads: int = 8):
+    """The per-query path (route_query + search_one + rerank_exact) for every query."""
+    q = np.ascontiguousarray(q, np.float32)
+    nq = q.shape[0]
+    slots = np.empty((nq, params.k), np.uint32)
+    scores = np.empty((nq, params.k), np.float32)
+    rc = lib().orc_search_one(C.c_void_p(desc_addr), _p(q), nq, C.byref(params), nthreads, _p(slots), _p(scores))
+    if rc != 0:
+        raise RuntimeError(f"orc_search_one failed ({rc})")
+    return slots, scores
+
+
+def route_query(desc_addr: int, q: np.ndarray, params: SearchParams, nthreads: int = 8):
+    q = np.ascontiguousarray(q, np.float32)
+    nq = q.shape[0]
+    chosen = np.empty((nq, params.nprobe), np.uint32)
+    cscore = np.empty((nq, params.nprobe), np.float32)
+    nchosen = np.empty(nq, np.uint32)
+    rc = lib().orc_route_query(C.c_void_p(desc_addr), _p(q), nq, C.byref(params), nthreads, _p(chosen), _p(cscore),
+                               _p(nchosen))
+    if rc != 0:
+        raise RuntimeError(f"orc_route_query failed ({rc})")
+    return chosen, cscore, nchosen
 
 
 def last_candidates(nq: int):

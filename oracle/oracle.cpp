@@ -673,3 +673,299 @@ int orc_last_candidates(uint32_t* tau, uint32_t* rest_end, uint32_t* cut, uint32
 }
 
 }  // extern "C"
+
+// ================================================================ the per-query path
+
+namespace {
+
+// keep_smallest, src/tree.rs:120-159: the `keep` smallest distances, ties at the cut-off in
+// encounter order, order preserved.
+void keep_smallest(std::vector<std::pair<uint32_t, uint32_t>>& v, size_t keep, uint32_t bits) {
+    if (keep >= v.size()) return;
+    std::vector<uint32_t> hist(bits + 1, 0);
+    for (auto& e : v) hist[e.first] += 1;
+    size_t cum = 0, t = 0;
+    while (t < bits) {
+        cum += hist[t];
+        if (cum >= keep) break;
+        ++t;
+    }
+    if (t == bits) cum += hist[t];
+    size_t need_eq = keep - (cum - hist[t]);
+    size_t w = 0;
+    for (size_t r = 0; r < v.size(); ++r) {
+        auto e = v[r];
+        if (e.first < t || (e.first == t && need_eq > 0)) {
+            if (e.first == t) --need_eq;
+            v[w++] = e;
+        }
+    }
+    v.resize(w);
+}
+
+// CentroidTree::search, src/tree.rs:559-628 (beams :559-570), over the arena's tree description.
+std::vector<uint32_t> tree_search(const maivs_tree_desc& T, uint32_t nw, const uint64_t* qb, size_t want) {
+    std::vector<uint32_t> out;
+    const uint32_t L = T.n_levels, bits = nw * 64;
+    if (L == 0) return out;
+    std::vector<size_t> off(L + 1, 0);
+    for (uint32_t l = 0; l < L; ++l) off[l + 1] = off[l] + T.level_n[l];
+    std::vector<size_t> beams(L);
+    size_t need = std::max<size_t>(want, 1);
+    for (uint32_t i = L; i-- > 0;) {
+        size_t raw = static_cast<size_t>(std::ceil(static_cast<float>(need) * T.beam_frac));
+        size_t b = std::min<size_t>(std::max<size_t>(raw, T.min_beam), T.level_n[i]);
+        beams[i] = b;
+        need = b;
+    }
+    std::vector<uint32_t> frontier(T.level_n[0]);
+    for (uint32_t i = 0; i < T.level_n[0]; ++i) frontier[i] = i;
+    std::vector<std::pair<uint32_t, uint32_t>> scored;
+    for (uint32_t li = 0; li < L; ++li) {
+        scored.clear();
+        for (uint32_t node : frontier)
+            scored.emplace_back(orc_hamming(qb, T.level_codes + (off[li] + node) * nw, nw), node);
+        size_t keep = std::min(beams[li], scored.size());
+        if (keep == 0) return out;
+        keep_smallest(scored, keep, bits);
+        std::vector<uint32_t> expand;
+        for (auto& e : scored) {
+            uint32_t st = T.child_start[off[li] + e.second], ln = T.child_len[off[li] + e.second];
+            for (uint32_t c = 0; c < ln; ++c) expand.push_back(st + c);  // compacted layout: contiguous
+        }
+        frontier.swap(expand);
+    }
+    scored.clear();
+    for (uint32_t leaf : frontier) scored.emplace_back(orc_hamming(qb, T.leaf_codes + static_cast<size_t>(leaf) * nw, nw), leaf);
+    size_t keep = std::min(want, scored.size());
+    if (keep == 0) return out;
+    keep_smallest(scored, keep, bits);
+    for (auto& e : scored) out.push_back(T.leaf_cells[e.second]);
+    return out;
+}
+
+struct QRoute {
+    std::vector<uint64_t> bits;
+    std::vector<float> rot;
+    std::vector<uint32_t> chosen;
+    std::vector<float> cscore;
+};
+
+// route_query, src/index.rs:1168-1305 (the tree, two-stage and flat branches; no graph router)
+QRoute route_query(const Arena& A, const float* q, const maivs_search_params* p) {
+    const maivs_arena_desc* a = A.a;
+    const uint32_t d = A.d, nw = A.nw, M = A.M, cl = nw * 64;
+    QRoute r;
+    std::vector<float> cqs(d, 0.0f);
+    float cqbase = 0.0f;
+    if (a->cent_sq8) {
+        for (uint32_t j = 0; j < d; ++j) {
+            cqs[j] = q[j] * a->csq_step[j];
+            cqbase += q[j] * a->csq_min[j];
+        }
+    }
+    r.rot.assign(A.P, 0.0f);
+    r.bits.assign(nw, 0);
+    orc_rotate(q, d, a->rot_signs, A.P, r.rot.data());
+    orc_pack_signs(r.rot.data(), A.P, r.bits.data(), nw);
+    std::vector<std::pair<uint32_t, float>> cs;
+    const maivs_tree_desc* T = a->tree;
+    if (T && T->n_levels > 0) {
+        size_t want_c = std::min<size_t>(static_cast<size_t>(p->nprobe) * std::max<uint32_t>(p->shortlist_mult, 2), T->n_leaf);
+        for (uint32_t ci : tree_search(*T, nw, r.bits.data(), want_c))
+            if (A.live[ci]) cs.emplace_back(ci, cent_score(A, ci, q, cqs.data(), cqbase));
+    } else if (a->cent_bits) {
+        std::vector<uint16_t> hs(M);
+        for (uint32_t c = 0; c < M; ++c)
+            hs[c] = static_cast<uint16_t>(orc_hamming(r.bits.data(), a->cent_bits + static_cast<size_t>(c) * nw, nw));
+        uint32_t want_c = std::min<uint32_t>(p->nprobe * p->shortlist_mult, A.n_live);
+        uint32_t cut = orc_hamming_cutoff(hs.data(), A.live.data(), M, want_c, cl);
+        for (uint32_t c = 0; c < M; ++c)
+            if (hs[c] <= cut && A.live[c]) cs.emplace_back(c, cent_score(A, c, q, cqs.data(), cqbase));
+    } else {
+        for (uint32_t c = 0; c < M; ++c)
+            if (A.live[c]) cs.emplace_back(c, cent_score(A, c, q, cqs.data(), cqbase));
+    }
+    uint32_t cap = std::min<uint32_t>(p->nprobe, static_cast<uint32_t>(cs.size()));
+    if (cap == 0) return r;
+    if (cap < cs.size()) {
+        std::nth_element(cs.begin(), cs.begin() + (cap - 1), cs.end(), score_before);
+        cs.resize(cap);
+    }
+    std::sort(cs.begin(), cs.end(), score_before);
+    if (p->target_confidence >= 1.0f) {
+        for (auto& e : cs) r.chosen.push_back(e.first);
+    } else {
+        float max_s = cs[0].second;
+        float z = 0.0f;
+        for (auto& e : cs) z += std::exp((e.second - max_s) * p->beta);
+        float cum = 0.0f;
+        for (auto& e : cs) {
+            r.chosen.push_back(e.first);
+            cum += std::exp((e.second - max_s) * p->beta) / (z + 1e-9f);
+            if (cum >= p->target_confidence) break;
+        }
+    }
+    for (size_t i = 0; i < r.chosen.size(); ++i) r.cscore.push_back(cs[i].second);
+    return r;
+}
+
+// rerank_exact, src/index.rs:1309-1378: exact scores of the candidates, top k (score desc, slot asc).
+void rerank_top(const Arena& A, const float* q, const std::vector<uint32_t>& slots, uint32_t k, uint32_t* out_slots,
+                float* out_scores) {
+    const maivs_arena_desc* a = A.a;
+    const uint32_t d = A.d;
+    std::vector<std::pair<uint32_t, float>> scored;
+    scored.reserve(slots.size());
+    if (a->rerank_mode == MAIVS_RERANK_SQ8) {
+        std::vector<float> qs(d);
+        float base = 0.0f;
+        for (uint32_t j = 0; j < d; ++j) {
+            qs[j] = q[j] * a->sq_step[j];
+            base += q[j] * a->sq_min[j];
+        }
+        for (uint32_t s : slots)
+            scored.emplace_back(s, base + orc_dot_f32_u8(qs.data(), a->sq8_codes + static_cast<size_t>(s) * d, d));
+    } else {
+        for (uint32_t s : slots) scored.emplace_back(s, orc_dot_f32(q, a->vecs_f32 + static_cast<size_t>(s) * d, d));
+    }
+    uint32_t kk = std::min<uint32_t>(k, static_cast<uint32_t>(scored.size()));
+    if (kk > 0) std::partial_sort(scored.begin(), scored.begin() + kk, scored.end(), score_before);
+    for (uint32_t i = 0; i < k; ++i) {
+        out_slots[i] = i < kk ? scored[i].first : UINT32_MAX;
+        out_scores[i] = i < kk ? scored[i].second : -INFINITY;
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+int orc_route_query(const maivs_arena_desc* a, const float* q, uint32_t nq, const maivs_search_params* p,
+                    uint32_t nthreads, uint32_t* chosen, float* cscore, uint32_t* nchosen) {
+    if (!a || !p || (!q && nq)) return MAIVS_ERR_ARG;
+    Arena A(a);
+    par_for(nthreads, nq, [&](size_t qi) {
+        QRoute r = route_query(A, q + qi * A.d, p);
+        if (nchosen) nchosen[qi] = static_cast<uint32_t>(r.chosen.size());
+        for (uint32_t j = 0; j < p->nprobe; ++j) {
+            bool ok = j < r.chosen.size();
+            if (chosen) chosen[qi * p->nprobe + j] = ok ? r.chosen[j] : UINT32_MAX;
+            if (cscore) cscore[qi * p->nprobe + j] = ok ? r.cscore[j] : NAN;
+        }
+    }, 4);
+    return 0;
+}
+
+// search_one, src/index.rs:1381-1864, binary mode with FastScan on a compacted index (:1689-1742).
+int orc_search_one(const maivs_arena_desc* a, const float* data, uint32_t nq, const maivs_search_params* p,
+                   uint32_t nthreads, uint32_t* out_slots, float* out_scores) {
+    if (!a || !p || (!data && nq) || !a->fs_codes || !a->fs_off || p->k == 0) return MAIVS_ERR_ARG;
+    Arena A(a);
+    const uint32_t d = A.d, nw = A.nw, M = A.M, maxk = A.maxk, k = p->k;
+    const uint32_t ma = a->max_assign;
+    const bool dedup = ma > 1;
+    const uint32_t want0 = k * std::max<uint32_t>(p->rerank_factor, 1);
+    const uint32_t target = std::max<uint32_t>(want0, 1);
+    const uint32_t npairs = A.npos / 2;
+    const bool filtering = p->filter && a->tags;
+    const float norm = std::sqrt(2.0f * static_cast<float>(A.P) / static_cast<float>(M_PI));
+    par_for(nthreads, nq, [&](size_t qi) {
+        const float* q = data + qi * d;
+        uint32_t* os = out_slots + qi * k;
+        float* osc = out_scores + qi * k;
+        for (uint32_t i = 0; i < k; ++i) {
+            os[i] = UINT32_MAX;
+            osc[i] = -INFINITY;
+        }
+        QRoute r = route_query(A, q, p);
+        const size_t n = r.chosen.size();
+        if (n == 0) return;
+        // rank of every probed cell: a slot counts only at its first-ranked probed home (:1405-1447)
+        std::vector<uint32_t> crank(M, UINT32_MAX);
+        for (size_t i = 0; i < n; ++i) crank[r.chosen[i]] = static_cast<uint32_t>(i);
+        auto seen = [&](uint32_t slot, uint32_t ci) {
+            if (!dedup) return false;
+            const uint32_t rc = crank[ci];
+            for (uint32_t j = 0; j < ma; ++j) {
+                uint32_t h = a->slot_cells[static_cast<size_t>(slot) * ma + j];
+                if (h != UINT32_MAX && h != ci && crank[h] != UINT32_MAX && crank[h] < rc) return true;
+            }
+            return false;
+        };
+        auto keep = [&](uint32_t slot) {
+            if (!filtering) return true;
+            const uint32_t t = a->tags[slot];
+            return t >= p->tag_lo && t <= p->tag_hi;
+        };
+        // reachability bounds and their suffix maxima (:1466-1489)
+        std::vector<float> suffix;
+        if (p->adaptive) {
+            suffix.assign(n + 1, -INFINITY);
+            std::vector<float> bounds(n);
+            for (size_t i = 0; i < n; ++i) {
+                float cs = std::fmin(std::fmax(r.cscore[i], -1.0f), 1.0f);
+                float ang = std::acos(cs);
+                bounds[i] = std::cos(std::fmax(ang - a->r_bound[r.chosen[i]], 0.0f));
+            }
+            for (size_t i = n; i-- > 0;) suffix[i] = std::fmax(bounds[i], suffix[i + 1]);
+        }
+        // FastScan scan with the bucket queue on d >> 6 (:1689-1742)
+        std::vector<uint8_t> lut(A.npos * 16);
+        float delta, bias;
+        orc_fs_query(r.rot.data(), A.P, nw, lut.data(), &delta, &bias);
+        std::vector<uint32_t> hist(nw * 64 + 1, 0);
+        struct H {
+            uint32_t hc, slot, d;
+        };
+        std::vector<H> hc;
+        uint32_t tau = maxk >> 6;
+        size_t kept = 0;
+        uint16_t sums[32];
+        for (size_t ci_i = 0; ci_i < n; ++ci_i) {
+            const uint32_t ci = r.chosen[ci_i];
+            const uint32_t len = A.mem_len(ci);
+            const uint32_t* mem = a->members + a->mem_off[ci];
+            for (uint32_t b = a->fs_off[ci]; b < a->fs_off[ci + 1]; ++b) {
+                orc_fs_block_sums(a->fs_codes + static_cast<size_t>(b) * A.bb, lut.data(), npairs, sums);
+                uint32_t base = (b - a->fs_off[ci]) * 32, nv = std::min<uint32_t>(32, len - base);
+                for (uint32_t i = 0; i < nv; ++i) {
+                    uint32_t dd = maxk - sums[i];
+                    uint32_t h = dd >> 6;
+                    if (h <= tau) {
+                        uint32_t slot = mem[base + i];
+                        if (!keep(slot) || seen(slot, ci)) continue;
+                        hc.push_back({h, slot, dd});
+                        hist[h] += 1;
+                        kept += 1;
+                        while (tau > 0 && kept - hist[tau] >= target) {
+                            kept -= hist[tau];
+                            tau -= 1;
+                        }
+                    }
+                }
+            }
+            if (p->adaptive && kept >= target) {
+                uint32_t top = ((tau + 1) << 6) - 1;
+                uint32_t worst = maxk > top ? maxk - top : 0;
+                float thr = std::fmin(std::fmax(orc_fs_estimate(delta, bias, worst) / norm, -1.0f), 1.0f);
+                if (suffix[ci_i + 1] < thr - p->at_margin) break;
+            }
+        }
+        // survivors h <= tau; the want0 smallest d (ties: ascending slot, the fixed order), :1743-1757
+        std::vector<H> cands;
+        for (auto& e : hc)
+            if (e.hc <= tau) cands.push_back(e);
+        if (want0 > 0 && cands.size() > want0) {
+            std::nth_element(cands.begin(), cands.begin() + (want0 - 1), cands.end(),
+                             [](const H& x, const H& y) { return x.d != y.d ? x.d < y.d : x.slot < y.slot; });
+            cands.resize(want0);
+        }
+        std::vector<uint32_t> slots;
+        for (auto& e : cands) slots.push_back(e.slot);
+        rerank_top(A, q, slots, k, os, osc);
+    }, 4);
+    return 0;
+}
+
+}  // extern "C"

@@ -43,6 +43,17 @@ int orc_route_batch(const maivs_arena_desc* a, const float* q, uint32_t nq, cons
 int orc_search_batch(const maivs_arena_desc* a, const float* q, uint32_t nq, const maivs_search_params* p,
                      uint32_t nthreads, uint32_t* out_slots, float* out_scores);
 
+/* The per-query path: route_query + search_one + rerank_exact (src/index.rs:1168-1305,
+ * 1381-1864, 1309-1378) for the binary FastScan configuration, every query on its own. Routing
+ * uses a->tree when it has levels (src/tree.rs:559-628), else the two-stage shortlist with
+ * want = nprobe * shortlist_mult. out nq x k as orc_search_batch. */
+int orc_search_one(const maivs_arena_desc* a, const float* q, uint32_t nq, const maivs_search_params* p,
+                   uint32_t nthreads, uint32_t* out_slots, float* out_scores);
+
+/* route_query alone: chosen / cscore nq x nprobe (tail UINT32_MAX / NaN), nchosen nq. */
+int orc_route_query(const maivs_arena_desc* a, const float* q, uint32_t nq, const maivs_search_params* p,
+                    uint32_t nthreads, uint32_t* chosen, float* cscore, uint32_t* nchosen);
+
 /* Intermediates of the last orc_search_batch (same layout as maivs_gpu_last_candidates). */
 int orc_last_candidates(uint32_t* tau, uint32_t* rest_end, uint32_t* cut, uint32_t* ncand, uint32_t* cand_slots,
                         uint32_t* cand_d, uint64_t cap);
