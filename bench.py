@@ -76,6 +76,7 @@ def main() -> int:
     ap.add_argument("--target", type=float, default=0.99)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0 = all host cores")
+    ap.add_argument("--no-pq", action="store_true", help="skip the per-query path's measurements")
     ap.add_argument("--only", default="", help="time only this point, e.g. 12:8 (nprobe:rf)")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="after the run, copy this many MiB device-to-device 5 times (the plain copy whose "
@@ -192,6 +193,54 @@ def main() -> int:
     log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step, {value:.0f} QPS, R@10 {r_final:.4f} "
         f"(stage-by-stage launches: {staged_ms:.3f} ms/step)")
 
+    # ---- the per-query path (search / small batches / cell_major=False) at the same point
+    pq = None
+    if not args.no_pq:
+        pq = {"nprobe": npb, "rerank_factor": rf}
+
+        def pq_call(nqq):
+            ctx.search_queries_device(dq.data_ptr(), nqq, p, d_slots.data_ptr(), d_scores.data_ptr())
+
+        pq_call(nq)
+        torch.cuda.synchronize()
+        pq["recall_at_10"] = round(recall_of(d_slots.cpu().numpy()), 4)
+        for nqq in (32, nq):
+            best = float("inf")
+            for _ in range(5):
+                torch.cuda.synchronize()
+                t = time.perf_counter()
+                pq_call(nqq)
+                torch.cuda.synchronize()
+                best = min(best, time.perf_counter() - t)
+            pq[f"qps_nq{nqq}"] = round(nqq / best, 1)
+        lat = []
+        for i in range(200):
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            pq_call(1)
+            torch.cuda.synchronize()
+            lat.append(time.perf_counter() - t)
+        pq["latency_ms_nq1_median"] = round(1e3 * float(np.median(lat)), 4)
+        pq["latency_ms_nq1_p99"] = round(1e3 * float(np.percentile(lat, 99)), 4)
+        if not args.no_cpu:
+            import oracle
+            desc = ix._arena_desc()
+            threads = args.cpu_threads or (os.cpu_count() or 1)
+            dt = float("inf")
+            for _ in range(3):
+                t = time.perf_counter()
+                oracle.search_one(desc, queries, p, threads)
+                dt = min(dt, time.perf_counter() - t)
+            pq["cpu_qps_nq1000"] = round(nq / dt, 1)
+            lat = []
+            for i in range(50):
+                t = time.perf_counter()
+                oracle.search_one(desc, queries[i:i + 1], p, 1)
+                lat.append(time.perf_counter() - t)
+            pq["cpu_latency_ms_nq1_median"] = round(1e3 * float(np.median(lat)), 4)
+            pq["cpu_threads"] = threads
+        log("per-query path: " + ", ".join(f"{kk}={v}" for kk, v in pq.items()))
+
     if args.copy_mb:
         n = args.copy_mb << 20
         src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
@@ -292,7 +341,8 @@ def main() -> int:
                    "scan_gbs": round(scan_gbs, 1), "scan_frac_of_hbm": round(scan_gbs / HBM_PEAK_GBS, 4),
                    "stage_ms": {s_: round(stages[s_][0], 4) for s_ in stages},
                    "staged_ms_per_step": round(staged_ms, 4),
-                   "matched_recall_qps": matched},
+                   "matched_recall_qps": matched,
+                   "per_query_path": pq},
         "roofline": roofline,
         "cpu_baseline": cpu,
     }

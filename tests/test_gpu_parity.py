@@ -143,7 +143,8 @@ def test_binding_search_batch(quality50k, mix50k):
     ix = quality50k
     ids, scores = ix.search_batch(queries, 10, 16, 1.0, 8.0, True)
     p = _params(ix, 10, 16)
-    oslots, oscores = oracle.search_batch(ix._arena_desc(), queries, p, 8)
+    check = oracle.search_batch if ix.takes_cellmajor(len(queries), True) else oracle.search_one
+    oslots, oscores = check(ix._arena_desc(), queries, p, 8)
     ext = ix._ext_ids()
     oids = np.where(oslots == 0xFFFFFFFF, np.iinfo(np.uint64).max, ext[np.minimum(oslots, len(ext) - 1)])
     assert np.array_equal(np.array(ids, dtype=np.uint64).reshape(oids.shape), oids)
