@@ -77,6 +77,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0 = all host cores")
     ap.add_argument("--no-pq", action="store_true", help="skip the per-query path's measurements")
+    ap.add_argument("--gpu-build", action="store_true",
+                    help="build the index with the GPU k-means and placement (bit-identical index)")
     ap.add_argument("--only", default="", help="time only this point, e.g. 12:8 (nprobe:rf)")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="after the run, copy this many MiB device-to-device 5 times (the plain copy whose "
@@ -104,7 +106,7 @@ def main() -> int:
     gt = mixture.exact_topk(base, queries, k, device="cuda:0")
     log(f"exact ground truth ({time.time() - t0:.1f}s)")
     t0 = time.time()
-    ix = M.build_preset(base, args.profile)
+    ix = M.build_preset(base, args.profile, gpu_build=args.gpu_build)
     st = ix.stats()
     log(f"index built: {int(st['n_cells'])} cells, {st['member_entries']:.0f} entries ({time.time() - t0:.1f}s)")
     ext = ix._ext_ids()
@@ -134,14 +136,21 @@ def main() -> int:
         return mixture.recall_at(ids, gt, k)
 
     # ---- sweep (GPU), recall per point
-    grid = [(npb, rf) for rf in RF_GRID for npb in NPROBE_GRID if npb <= st["n_cells"]]
+    # the reference's grids reach nprobe 2048 on its large configurations; here the grid grows
+    # with the index, up to n_cells / 32
+    nprobe_grid = list(NPROBE_GRID) + [n for n in (192, 256, 384, 512, 768, 1024) if n <= st["n_cells"] / 32]
+    grid = [(npb, rf) for rf in RF_GRID for npb in nprobe_grid if npb <= st["n_cells"]]
     if args.only:
         a, b = args.only.split(":")
         grid = [(int(a), int(b))]
     pts = []
     for npb, rf in grid:
         p = params(npb, rf)
-        gpu_call(p)
+        try:
+            gpu_call(p)
+        except capi.GpuError as e:  # a configuration the device refuses (e.g. a shortlist past its sort)
+            log(f"np{npb}/rf{rf} skipped: {e}")
+            continue
         torch.cuda.synchronize()
         r = recall_of(d_slots.cpu().numpy())
         best = float("inf")

@@ -37,12 +37,14 @@ def preset(dim: int, n: int, profile: str = "quality") -> FlatCellIndex:
     return ix
 
 
-def build_preset(base, profile: str = "quality", ids=None) -> FlatCellIndex:
-    """train_centroids(base, max(16, n // 128)) -> add_batch -> compact, as the reference's bench."""
+def build_preset(base, profile: str = "quality", ids=None, gpu_build: bool = False) -> FlatCellIndex:
+    """train_centroids(base, max(16, n // 128)) -> add_batch -> compact, as the reference's bench.
+    gpu_build runs the build's k-means and placement on the GPU (bit-identical index)."""
     import numpy as np
 
     n = len(base)
     ix = preset(base.shape[1], n, profile)
+    ix.set_gpu_build(gpu_build)
     ix.train_centroids(base, max(16, n // 128))
     ix.add_batch(list(range(n)) if ids is None else list(ids), np.ascontiguousarray(base, np.float32))
     ix.compact()

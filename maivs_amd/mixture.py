@@ -124,6 +124,8 @@ def exact_topk(base: np.ndarray, queries: np.ndarray, k: int = 10, chunk: int = 
     Uses torch on ``device`` when given (the GPU on the bench box), numpy otherwise.
     """
     nq = len(queries)
+    if device is not None and nq * len(base) > 2_000_000_000:
+        return _exact_topk_on_device(base, queries, k, device)
     best_s = np.full((nq, k), -np.inf, np.float32)
     best_i = np.full((nq, k), np.iinfo(np.int64).max, np.int64)
     if device is not None:
@@ -148,6 +150,32 @@ def exact_topk(base: np.ndarray, queries: np.ndarray, k: int = 10, chunk: int = 
             best_s[qi] = cs[o]
             best_i[qi] = ci[o]
     return best_i
+
+
+def _exact_topk_on_device(base, queries, k, device, chunk=262144, qblk=2048):
+    """exact_topk for large products, entirely on the device: per base chunk the k best of every
+    query (torch.topk), merged with the running best by (score desc, id asc). An exact score tie
+    that straddles a chunk's k-th place may keep either id (ties elsewhere go to the lower id)."""
+    import torch
+    nq = len(queries)
+    qt = torch.from_numpy(np.ascontiguousarray(queries, np.float32)).to(device)
+    bs = torch.full((nq, k), float("-inf"), device=device)
+    bi = torch.full((nq, k), np.iinfo(np.int64).max, dtype=torch.int64, device=device)
+    for s in range(0, len(base), chunk):
+        bt = torch.from_numpy(np.ascontiguousarray(base[s:s + chunk], np.float32)).to(device)
+        kk = min(k, bt.shape[0])
+        for q0 in range(0, nq, qblk):
+            q1 = min(nq, q0 + qblk)
+            v, i = torch.topk(qt[q0:q1] @ bt.T, kk, dim=1)
+            cs = torch.cat([bs[q0:q1], v], 1)
+            ci = torch.cat([bi[q0:q1], i.to(torch.int64) + s], 1)
+            o = torch.argsort(ci, dim=1, stable=True)
+            cs, ci = torch.gather(cs, 1, o), torch.gather(ci, 1, o)
+            o = torch.argsort(-cs, dim=1, stable=True)[:, :k]
+            bs[q0:q1] = torch.gather(cs, 1, o)
+            bi[q0:q1] = torch.gather(ci, 1, o)
+        del bt
+    return bi.cpu().numpy()
 
 
 def recall_at(ids: np.ndarray, gt: np.ndarray, k: int = 10) -> float:
