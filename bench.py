@@ -90,6 +90,9 @@ def main() -> int:
               f"(the multi-GPU sharding is a design, see the design notes)", file=sys.stderr)
         return 2
 
+    if args.workload == "churn400k":
+        return run_churn_filter(args)
+
     import torch
 
     import maivs_amd as M
@@ -358,6 +361,109 @@ def main() -> int:
     print(json.dumps(out), flush=True)
     ctx.close()
     ctx_st.close()
+    return 0
+
+
+def run_churn_filter(args) -> int:
+    """The update-and-filter configuration: a 400k index from the 500k mixture under 25% turnover
+    (10 rounds of 10k deletes + 10k inserts, churn seed 501, then compact(); bench/fair/churn.py:
+    29,47-61), a tag in [0, 1000) per vector (seed 502), then the 1,000 queries with the filter
+    tag < t for t in 1, 10, 100, 500 (selectivity 0.1% .. 50%; bench/fair/filtered.py:28,83-85),
+    over the reference's grid nprobe {64, 256, 1024, 2048, cells} x rerank_factor {16, 32}.
+    A filtered search_batch takes the reference's per-query path; the batched path with the filter
+    inside its scans (set_batched_filter) is timed beside it. Ground truth: the exact top-10 among
+    the live vectors that pass. One JSON line with the per-selectivity results."""
+    import torch
+
+    import maivs_amd as M
+    from maivs_amd import capi, mixture
+
+    dev = torch.device("cuda:0")
+    torch.cuda.init()
+    k = 10
+    t0 = time.time()
+    base, queries = mixture.workload("mix500k")
+    nq = len(queries)
+    n0, nnew, rounds = 400_000, 100_000, 10
+    ix = M.build_preset(base[:n0], "quality", gpu_build=args.gpu_build)
+    log(f"initial 400k index ({time.time() - t0:.1f}s)")
+    dele = np.random.RandomState(501).choice(n0, nnew, replace=False)
+    per = nnew // rounds
+    t0 = time.time()
+    for r in range(rounds):
+        for i in dele[r * per:(r + 1) * per]:
+            ix.remove(int(i))
+        lo = n0 + r * per
+        ix.add_batch(list(range(lo, lo + per)), np.ascontiguousarray(base[lo:lo + per]))
+    ix.compact()
+    gone = np.zeros(n0 + nnew, bool)
+    gone[dele] = True
+    live = np.nonzero(~gone)[0]
+    tags = np.random.RandomState(502).randint(0, 1000, n0 + nnew).astype(np.uint32)
+    ix.set_tags([int(i) for i in live], [int(tags[i]) for i in live])
+    st = ix.stats()
+    cells = int(st["n_cells"])
+    log(f"churned: {int(st['n_live'])} live, {cells} cells ({time.time() - t0:.1f}s)")
+    ctx = capi.Context(0)
+    dq = torch.from_numpy(queries).to(dev)
+    d_slots = torch.empty((nq, k), dtype=torch.int32, device=dev)
+    d_scores = torch.empty((nq, k), dtype=torch.float32, device=dev)
+    grid = [(npb, rf) for rf in (16, 32) for npb in (64, 256, 1024, 2048, cells) if npb <= cells]
+    out_sel = {}
+    for t in (500, 100, 10, 1):
+        ix.set_filter(0, t - 1)
+        sub = live[tags[live] < t]
+        gt = sub[mixture.exact_topk(base[sub], queries, k, device="cuda:0")]
+        ctx.upload(ix._arena_desc())
+        ext = ix._ext_ids()
+        res = {"selectivity": t / 1000.0, "passing": int(len(sub)), "per_query_path": [], "batched_filter": []}
+        for npb, rf in grid:
+            ix.set_rerank_factor(rf)
+            p = capi.params_from_bytes(ix._search_params(k, npb, 1.0, 8.0))
+            for name, call in (("per_query_path", ctx.search_queries_device), ("batched_filter", ctx.search_device)):
+                try:
+                    call(dq.data_ptr(), nq, p, d_slots.data_ptr(), d_scores.data_ptr())
+                except capi.GpuError as e:  # a configuration the device refuses
+                    log(f"{name} np{npb}/rf{rf} skipped: {e}")
+                    continue
+                torch.cuda.synchronize()
+                sl = d_slots.cpu().numpy().astype(np.uint32)
+                ids = np.where(sl == 0xFFFFFFFF, -1, ext[np.minimum(sl, len(ext) - 1)].astype(np.int64))
+                rec = mixture.recall_at(ids, gt, k)
+                best = float("inf")
+                for _ in range(3):  # best of 3, as bench/fair/fairbench.py:52-58
+                    torch.cuda.synchronize()
+                    t1 = time.perf_counter()
+                    call(dq.data_ptr(), nq, p, d_slots.data_ptr(), d_scores.data_ptr())
+                    torch.cuda.synchronize()
+                    best = min(best, time.perf_counter() - t1)
+                res[name].append({"nprobe": npb, "rf": rf, "recall": round(rec, 4), "qps": round(nq / best, 1)})
+        if not args.no_cpu:
+            import oracle
+            threads = args.cpu_threads or (os.cpu_count() or 1)
+            # the reference's filtered path (search_one) restated, at the GPU per-query path's
+            # cheapest point with the best recall
+            bestp = max(res["per_query_path"], key=lambda e: (e["recall"], e["qps"]))
+            ix.set_rerank_factor(bestp["rf"])
+            p = capi.params_from_bytes(ix._search_params(k, bestp["nprobe"], 1.0, 8.0))
+            t1 = time.perf_counter()
+            oracle.search_one(ix._arena_desc(), queries, p, threads)
+            res["cpu_per_query_path"] = {"nprobe": bestp["nprobe"], "rf": bestp["rf"],
+                                         "qps": round(nq / (time.perf_counter() - t1), 1), "threads": threads}
+        out_sel[str(t / 1000.0)] = res
+        pq = max(res["per_query_path"], key=lambda e: (e["recall"], e["qps"]))
+        bf = max(res["batched_filter"], key=lambda e: (e["recall"], e["qps"]))
+        log(f"sel {t / 1000.0}: {len(sub)} pass; per-query best R@10 {pq['recall']} @ {pq['qps']:.0f} QPS "
+            f"(np{pq['nprobe']}/rf{pq['rf']}); batched filter best R@10 {bf['recall']} @ {bf['qps']:.0f} QPS"
+            + (f"; CPU {res['cpu_per_query_path']['qps']:.0f} QPS" if "cpu_per_query_path" in res else ""))
+    ix.set_filter()
+    print(json.dumps({"metric": "filtered batch QPS and R@10 after 25% turnover, 400k x 384, 1 MI355X",
+                      "unit": "queries/s", "n_gpus": 1, "data": "synthetic (seeded Gaussian mixture)",
+                      "config": {"workload": "churn400k: 400k from the 500k mixture, 10 x (10k deletes + 10k "
+                                             "inserts), compact(), tags in [0, 1000)", "batch": nq, "k": k,
+                                 "cells": cells},
+                      "selectivity": out_sel}), flush=True)
+    ctx.close()
     return 0
 
 
