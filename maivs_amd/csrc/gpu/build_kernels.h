@@ -249,16 +249,17 @@ struct PlaceArgs {
 };
 
 // Per-wave LDS of the placement kernel, in order: qb[W] u64 | xs[P] | vs[d4] | hist[bits + 1, to 4]
-// | rbase[cap + 1] | rpre[cap + 2] | knodes[cap] | outc[want]   (u32 / f32 words after qb)
+// | rbase[cap + 1] | rpre[cap + 2] | knodes[cap] | outc[want] | hcache[kTreeHCache] u16
 struct PlaceLds {
     uint64_t* qb;
     float *xs, *vs;
     uint32_t *hist, *rbase, *rpre, *knodes, *outc;
+    uint16_t* hcache;
 };
 
 __host__ __device__ inline uint32_t place_lds_words(uint32_t P, uint32_t d, uint32_t W, uint32_t cap, uint32_t want) {
     const uint32_t d4 = (d + 3) & ~3u, hb = (W * 64 + 1 + 3) & ~3u;
-    return 2 * W + P + d4 + hb + (cap + 1) + (cap + 2) + cap + want;
+    return 2 * W + P + d4 + hb + (cap + 1) + (cap + 2) + cap + want + kTreeHCache / 2;
 }
 
 __device__ __forceinline__ PlaceLds place_lds(uint8_t* base, const PlaceArgs& a) {
@@ -271,6 +272,7 @@ __device__ __forceinline__ PlaceLds place_lds(uint8_t* base, const PlaceArgs& a)
     L.rpre = L.rbase + a.kept_cap + 1;
     L.knodes = L.rpre + a.kept_cap + 2;
     L.outc = L.knodes + a.kept_cap;
+    L.hcache = reinterpret_cast<uint16_t*>(L.outc + a.want);
     return L;
 }
 
@@ -344,7 +346,8 @@ __global__ void __launch_bounds__(kPlaceWaves * kWave) place_kernel(PlaceArgs a)
         }
         wave_sync();
         // ---- tree descent (src/tree.rs:574-628); no tree or no result: every cell
-        uint32_t nout = tree_descent(a.tree, a.beams, a.want, L.qb, W, L.hist, L.rbase, L.rpre, L.knodes, L.outc);
+        uint32_t nout = tree_descent(a.tree, a.beams, a.want, L.qb, W, L.hist, L.rbase, L.rpre, L.knodes, L.outc,
+                                     L.hcache, kTreeHCache);
         const bool use_tree = nout > 0;
         if (!use_tree) nout = a.M;  // every cell, in order (src/index.rs:2480-2509)
         // ---- exact scores and the running selection

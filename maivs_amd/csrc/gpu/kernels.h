@@ -1519,7 +1519,7 @@ __global__ void counters_kernel(DevArena A, Work Wk, KParams K) {
 constexpr uint32_t kPqTreeWaves = 4;
 
 __host__ __device__ inline uint32_t pq_tree_lds_words(uint32_t W, uint32_t cap) {
-    return 2 * W + ((W * 64 + 1 + 3) & ~3u) + (cap + 1) + (cap + 2) + cap;
+    return 2 * W + ((W * 64 + 1 + 3) & ~3u) + (cap + 1) + (cap + 2) + cap + kTreeHCache / 2;
 }
 
 __global__ void __launch_bounds__(kPqTreeWaves * kWave)
@@ -1534,10 +1534,11 @@ pq_tree_kernel(DevArena A, Work Wk, KParams K, TreeDev T, const uint32_t* __rest
     uint32_t* rbase = hist + ((A.W * 64 + 1 + 3) & ~3u);
     uint32_t* rpre = rbase + cap + 1;
     uint32_t* knodes = rpre + cap + 2;
+    uint16_t* hcache = reinterpret_cast<uint16_t*>(knodes + cap);
     for (uint32_t w = lane; w < A.W; w += kWave) qb[w] = Wk.qbits[static_cast<uint64_t>(qi) * A.W + w];
     wave_sync();
-    const uint32_t n =
-        tree_descent(T, beams, K.want_c, qb, A.W, hist, rbase, rpre, knodes, Wk.tlist + static_cast<uint64_t>(qi) * K.tcap);
+    const uint32_t n = tree_descent(T, beams, K.want_c, qb, A.W, hist, rbase, rpre, knodes,
+                                    Wk.tlist + static_cast<uint64_t>(qi) * K.tcap, hcache, kTreeHCache);
     if (lane == 0) Wk.tcount[qi] = n;
 }
 
@@ -1592,20 +1593,21 @@ __host__ __device__ inline uint32_t pq_scan_lds_words(uint32_t MW, uint32_t maxk
 
 // The FastScan scan of one query (src/index.rs:1689-1757), one workgroup: cells in probe order;
 // after each cell the bucket queue on h = d >> 6 lowers tau while the entries below it already
-// reach the target (tau after a cell depends only on the entries scanned so far, so one
-// workgroup-wide pass per cell gives the reference's value), then the adaptive stop. Survivors
-// h <= tau; the target smallest (d, slot) of them go to the candidate list for finish.
+// reach the target. The reference lowers it entry by entry; its value after a cell depends only on
+// the entries scanned so far (tau = min(tau, the first u with #(h <= u) >= target)), so wave 0
+// recomputes it from the LDS histogram with a prefix scan after each cell, then the adaptive stop.
+// The next cell's first round of member data is loaded before that barrier. Survivors h <= tau;
+// the target smallest (d, slot) of them go to the candidate list for finish.
 // LDS: static table[W*256] | scanned[MW4] | hist[bins4] | suffix[np4] | hist2[256] | scratch[32].
 template <int NW>
 __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work Wk, KParams K) {
     constexpr uint32_t TB = NW * 256;
     __shared__ __align__(16) uint8_t table[TB];
     extern __shared__ __align__(16) uint32_t pq_smem[];
-    __shared__ float s_seg[kScanThreads];
-    __shared__ uint32_t s_cnt, s_start, s_tau, s_kept, s_stop, s_w;
+    __shared__ uint32_t s_cnt, s_tau, s_kept, s_stop, s_w;
     const uint32_t qi = blockIdx.x;
     if (qi >= K.nq) return;
-    const uint32_t tid = threadIdx.x, nt = blockDim.x;
+    const uint32_t tid = threadIdx.x, nt = blockDim.x, lane = lane_id();
     const uint32_t nbins = (A.maxk >> 6) + 1;
     uint32_t* scanned = pq_smem;
     uint32_t* hist = scanned + ((A.MW + 3) & ~3u);
@@ -1620,91 +1622,155 @@ __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work 
     for (uint32_t i = tid; i < nbins; i += nt) hist[i] = 0;
     const uint32_t nch = Wk.nchosen[qi];
     const uint32_t* chosen = Wk.chosen + static_cast<uint64_t>(qi) * K.nprobe;
-    // suffix maxima of the reachability bounds (src/index.rs:1466-1489), suffix[nch] = -inf
-    if (K.adaptive) {
+    const float delta = Wk.delta[qi], bias = Wk.bias[qi];
+    // suffix maxima of the reachability bounds (src/index.rs:1466-1489), suffix[nch] = -inf: wave 0,
+    // 64 probe ranks at a time from the end
+    if (K.adaptive && tid < kWave) {
         const float* bnd = Wk.bnd + static_cast<uint64_t>(qi) * K.nprobe;
-        const uint32_t per = (nch + nt - 1) / nt, b0 = min(tid * per, nch), b1 = min(b0 + per, nch);
-        float run = -INFINITY;
-        for (uint32_t i = b1; i-- > b0;) {
-            run = fmaxf(bnd[i], run);
-            suffix[i] = run;
-        }
-        s_seg[tid] = run;
-        __syncthreads();
-        if (tid == 0) {
-            float right = -INFINITY;
-            for (uint32_t t = nt; t-- > 0;) {
-                const float v = s_seg[t];
-                s_seg[t] = right;
-                right = fmaxf(v, right);
+        float carry = -INFINITY;
+        for (int32_t base = static_cast<int32_t>((nch + kWave - 1) / kWave) * kWave - kWave; base >= 0; base -= kWave) {
+            const uint32_t i = static_cast<uint32_t>(base) + lane;
+            float v = i < nch ? bnd[i] : -INFINITY;
+            for (int o = 1; o < kWave; o <<= 1) {
+                const float y = __shfl_down(v, o, kWave);
+                if (lane + o < kWave) v = fmaxf(v, y);
             }
-            suffix[nch] = -INFINITY;
+            v = fmaxf(v, carry);
+            if (i < nch) suffix[i] = v;
+            carry = __shfl(v, 0, kWave);
         }
-        __syncthreads();
-        for (uint32_t i = b0; i < b1; ++i) suffix[i] = fmaxf(suffix[i], s_seg[tid]);
+        if (lane == 0) suffix[nch] = -INFINITY;
     }
     if (tid == 0) {
         s_cnt = 0;
-        s_start = 0;
         s_tau = A.maxk >> 6;
         s_kept = 0;
         s_stop = 0;
     }
-    __syncthreads();
     uint64_t* cbuf = Wk.pqc + static_cast<uint64_t>(qi) * K.pq_cap;
     const uint32_t target = K.target;
     bool flagged = false;
+    // one member's data; the first round of the next cell is loaded ahead
+    struct Mem {
+        Code<NW> code;
+        uint32_t slot, alt, tag;
+        bool have;
+    };
+    auto load_mem = [&](uint32_t e0, uint32_t len, uint32_t base, Mem& m) {
+        const uint32_t i = base + tid;
+        m.have = i < len;
+        if (m.have) {
+            const uint64_t e = static_cast<uint64_t>(e0) + i;
+            m.code.load(A.codes + e * (2 * NW));
+            m.slot = A.members[e];
+            m.alt = A.ma == 2 ? A.entry_alt[e] : 0u;
+            m.tag = K.filter ? A.entry_tag[e] : 0u;
+        }
+    };
+    Mem nxt;
+    nxt.have = false;
+    if (nch > 0) {
+        const uint32_t c0 = chosen[0];
+        load_mem(A.mem_off[c0], A.mem_off[c0 + 1] - A.mem_off[c0], 0, nxt);
+    }
+    __syncthreads();
     for (uint32_t ci_i = 0; ci_i < nch; ++ci_i) {
         const uint32_t c = chosen[ci_i];
         const uint32_t e0 = A.mem_off[c], len = A.mem_off[c + 1] - e0;
         const uint32_t tau = s_tau;
         for (uint32_t base = 0; base < len; base += nt) {
-            const uint32_t i = base + tid;
-            if (i < len) {
-                const uint64_t e = static_cast<uint64_t>(e0) + i;
-                Code<NW> code;
-                code.load(A.codes + e * (2 * NW));
-                const uint32_t dv = A.maxk - lut_sum1<NW>(code, table);
-                const uint32_t h = dv >> 6;
-                if (h <= tau) {
-                    const uint32_t slot = A.members[e];
-                    bool ok = true;
-                    if (K.filter) {
-                        const uint32_t tg = A.entry_tag[e];
-                        ok = tg >= K.tag_lo && tg <= K.tag_hi;
-                    }
-                    if (ok && A.ma > 1) ok = !pq_seen(A, e, slot, c, scanned);
-                    if (ok) {
-                        const uint32_t pos = atomicAdd(&s_cnt, 1u);
-                        if (pos < K.pq_cap) cbuf[pos] = (static_cast<uint64_t>(dv) << 32) | slot;
-                        atomicAdd(&hist[h], 1u);
+            Mem m;
+            if (base == 0)
+                m = nxt;
+            else
+                load_mem(e0, len, base, m);
+            bool ok = false;
+            uint32_t dv = 0;
+            if (m.have) {
+                const uint64_t e = static_cast<uint64_t>(e0) + base + tid;
+                dv = A.maxk - lut_sum1<NW>(m.code, table);
+                if ((dv >> 6) <= tau) {
+                    ok = !K.filter || (m.tag >= K.tag_lo && m.tag <= K.tag_hi);
+                    if (ok && A.ma > 1) {
+                        if (A.ma == 2)
+                            ok = !(m.alt != kNoAlt && m.alt != c && ((scanned[m.alt >> 5] >> (m.alt & 31)) & 1u));
+                        else
+                            ok = !pq_seen(A, e, m.slot, c, scanned);
                     }
                 }
             }
+            // one counter update per wave
+            const uint64_t bm = __ballot(ok);
+            if (bm) {
+                uint32_t wb = 0;
+                if (lane == 0) wb = atomicAdd(&s_cnt, static_cast<uint32_t>(__popcll(bm)));
+                wb = __shfl(wb, 0, kWave);
+                if (ok) {
+                    const uint32_t pos = wb + lanes_below(bm);
+                    if (pos < K.pq_cap) cbuf[pos] = (static_cast<uint64_t>(dv) << 32) | m.slot;
+                    atomicAdd(&hist[dv >> 6], 1u);
+                }
+            }
+        }
+        // the next cell's first round, in flight across the barrier and the bucket-queue update
+        nxt.have = false;
+        if (ci_i + 1 < nch) {
+            const uint32_t cn = chosen[ci_i + 1];
+            load_mem(A.mem_off[cn], A.mem_off[cn + 1] - A.mem_off[cn], 0, nxt);
         }
         __syncthreads();
-        if (tid == 0) {
-            // the bucket queue (src/index.rs:1712-1724): every entry this cell admitted had h <= tau
-            uint32_t kept = s_kept + (s_cnt - s_start), t = tau;
-            while (t > 0 && kept - hist[t] >= target) {
-                kept -= hist[t];
-                --t;
+        if (tid < kWave) {
+            // the bucket queue (src/index.rs:1712-1724): tau = min(tau, first u with #(h <= u) >= target)
+            const uint32_t nb = tau + 1, per = (nb + kWave - 1) / kWave;
+            const uint32_t b0 = min(lane * per, nb), b1 = min(b0 + per, nb);
+            uint32_t loc = 0;
+            for (uint32_t bb = b0; bb < b1; ++bb) loc += hist[bb];
+            uint32_t incl = loc;
+            for (int o = 1; o < kWave; o <<= 1) {
+                const uint32_t y = __shfl_up(incl, o, kWave);
+                if (lane >= static_cast<uint32_t>(o)) incl += y;
             }
-            s_tau = t;
-            s_kept = kept;
-            scanned[c >> 5] |= 1u << (c & 31);
+            const uint32_t total = __shfl(incl, kWave - 1, kWave);  // #(h <= tau)
+            const uint32_t excl = incl - loc;
+            const bool here = excl < target && incl >= target;
+            uint32_t u = 0, cu = 0;
+            if (here) {
+                uint32_t cum = excl;
+                for (uint32_t bb = b0; bb < b1; ++bb) {
+                    cum += hist[bb];
+                    if (cum >= target) {
+                        u = bb;
+                        cu = cum;
+                        break;
+                    }
+                }
+            }
+            const uint64_t hm = __ballot(here);
+            uint32_t t = tau, kept = total;
+            if (hm) {
+                const int src = __ffsll(static_cast<long long>(hm)) - 1;
+                t = __shfl(u, src, kWave);
+                kept = __shfl(cu, src, kWave);
+            }
+            uint32_t stop = 0;
             // the adaptive stop (:1727-1733)
             if (K.adaptive && kept >= target) {
                 const uint32_t top = ((t + 1) << 6) - 1;
                 const uint32_t worst = A.maxk > top ? A.maxk - top : 0u;
-                const float est = Wk.delta[qi] * static_cast<float>(worst) + Wk.bias[qi];
+                const float est = delta * static_cast<float>(worst) + bias;
                 const float thr = fminf(fmaxf(est / K.norm, -1.0f), 1.0f);
                 const float T = thr - K.at_margin;
                 const float sx = suffix[ci_i + 1];
                 if (!K.pq_noflag && fabsf(sx - T) <= K.prune_band) flagged = true;
-                if (sx < T) s_stop = 1;
+                if (sx < T) stop = 1;
             }
-            if (s_cnt > K.pq_cap) s_stop = 2;
+            if (s_cnt > K.pq_cap) stop = 2;
+            if (lane == 0) {
+                s_tau = t;
+                s_kept = kept;
+                s_stop = stop;
+                scanned[c >> 5] |= 1u << (c & 31);
+            }
         }
         __syncthreads();
         if (s_stop == 2) break;
@@ -1732,14 +1798,12 @@ __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work 
             if (s_stop == 2) break;
         }
         if (s_stop) break;
-        if (tid == 0) s_start = s_cnt;  // the next cell's admissions count from here
-        __syncthreads();
     }
     __syncthreads();
     if (tid == 0) {
-        if (flagged) Wk.flag_prune[atomicAdd(&Wk.ctl->nflag_prune, 1u)] = qi;
         if (s_stop == 2) atomicMax(&Wk.ctl->pq_overflow, s_cnt + K.pq_room);
     }
+    if (tid == 0 && flagged) Wk.flag_prune[atomicAdd(&Wk.ctl->nflag_prune, 1u)] = qi;
     uint2* cand = Wk.cand + static_cast<uint64_t>(qi) * K.cand_cap;
     if (s_stop == 2) {
         if (tid == 0) {

@@ -10,6 +10,8 @@
 
 namespace maivs_dev {
 
+constexpr uint32_t kTreeHCache = 2048;  // frontier positions whose distance is kept in LDS per wave
+
 __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -30,8 +32,10 @@ __device__ __forceinline__ uint32_t asc_f32_key(float f) {
 
 // keep_smallest over the frontier positions [0, F) with distance hd(p): emit(k, p) for the kept
 // entries in encounter order (k = 0, 1, ...). Returns the number kept = min(keep, F).
+// hcache (LDS, hcap entries): the distances of the first hcap positions, computed once.
 template <class HD, class EMIT>
-__device__ uint32_t wave_keep_smallest(uint32_t F, uint32_t keep, uint32_t bits, uint32_t* hist, HD hd, EMIT emit) {
+__device__ uint32_t wave_keep_smallest(uint32_t F, uint32_t keep, uint32_t bits, uint32_t* hist, HD hd, EMIT emit,
+                                       uint16_t* hcache = nullptr, uint32_t hcap = 0) {
     const uint32_t lane = lane_id();
     if (keep >= F) {
         for (uint32_t p = lane; p < F; p += kWave) emit(p, p);
@@ -39,7 +43,23 @@ __device__ uint32_t wave_keep_smallest(uint32_t F, uint32_t keep, uint32_t bits,
     }
     for (uint32_t j = lane; j <= bits; j += kWave) hist[j] = 0;
     wave_sync();
-    for (uint32_t p = lane; p < F; p += kWave) atomicAdd(&hist[hd(p)], 1u);
+    // four positions per lane at a time, so their code loads are in flight together
+    for (uint32_t p0 = lane; p0 < F; p0 += 4 * kWave) {
+        uint32_t hv[4];
+#pragma unroll
+        for (uint32_t u = 0; u < 4; ++u) {
+            const uint32_t p = p0 + u * kWave;
+            hv[u] = p < F ? hd(p) : 0u;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < 4; ++u) {
+            const uint32_t p = p0 + u * kWave;
+            if (p < F) {
+                atomicAdd(&hist[hv[u]], 1u);
+                if (p < hcap) hcache[p] = static_cast<uint16_t>(hv[u]);
+            }
+        }
+    }
     wave_sync();
     // t = the smallest distance with count(h <= t) >= keep; below = count(h < t)
     const uint32_t nb = bits + 1, bpl = (nb + kWave - 1) / kWave;
@@ -74,7 +94,7 @@ __device__ uint32_t wave_keep_smallest(uint32_t F, uint32_t keep, uint32_t bits,
     for (uint32_t c0 = 0; c0 < F; c0 += kWave) {
         const uint32_t p = c0 + lane;
         const bool valid = p < F;
-        const uint32_t h = valid ? hd(p) : 0xFFFFFFFFu;
+        const uint32_t h = valid ? (p < hcap ? static_cast<uint32_t>(hcache[p]) : hd(p)) : 0xFFFFFFFFu;
         const uint64_t eqm = __ballot(valid && h == t);
         const bool take = valid && (h < t || (h == t && eq_seen + lanes_below(eqm) < need_eq));
         const uint64_t tm = __ballot(take);
@@ -125,9 +145,10 @@ struct TreeDev {
 // `want` leaves, ties in encounter order. Writes the leaves' cells, best first by Hamming, to out
 // and returns their number (0: the caller scores every cell, as the reference does on an empty
 // result). Per-wave LDS scratch: hist[W*64 + 1], rbase[cap + 1], rpre[cap + 2], knodes[cap] with
-// cap >= every beam; out[want].
+// cap >= every beam; out[want]; hcache[hcap] u16 (distances kept between the two passes).
 __device__ inline uint32_t tree_descent(const TreeDev& T, const uint32_t* beams, uint32_t want, const uint64_t* qb, uint32_t W,
-                                 uint32_t* hist, uint32_t* rbase, uint32_t* rpre, uint32_t* knodes, uint32_t* out) {
+                                        uint32_t* hist, uint32_t* rbase, uint32_t* rpre, uint32_t* knodes, uint32_t* out,
+                                        uint16_t* hcache, uint32_t hcap) {
     const uint32_t lane = lane_id(), bits = W * 64;
     if (T.n_levels == 0) return 0;
     uint32_t nr = 1;
@@ -148,7 +169,7 @@ __device__ inline uint32_t tree_descent(const TreeDev& T, const uint32_t* beams,
                 const uint32_t node = frontier_node(rbase, rpre, nr, p);
                 return hamming_lds(qb, codes + static_cast<uint64_t>(node) * W, W);
             },
-            [&](uint32_t k, uint32_t p) { knodes[k] = frontier_node(rbase, rpre, nr, p); });
+            [&](uint32_t k, uint32_t p) { knodes[k] = frontier_node(rbase, rpre, nr, p); }, hcache, hcap);
         wave_sync();
         // children of the kept nodes, in order: the next frontier's ranges
         const uint32_t* cs = T.lv_cs + T.lv_off[li];
@@ -182,7 +203,7 @@ __device__ inline uint32_t tree_descent(const TreeDev& T, const uint32_t* beams,
             const uint32_t leaf = frontier_node(rbase, rpre, nr, p);
             return hamming_lds(qb, T.leaf_codes + static_cast<uint64_t>(leaf) * W, W);
         },
-        [&](uint32_t k, uint32_t p) { out[k] = T.leaf_ids[frontier_node(rbase, rpre, nr, p)]; });
+        [&](uint32_t k, uint32_t p) { out[k] = T.leaf_ids[frontier_node(rbase, rpre, nr, p)]; }, hcache, hcap);
     wave_sync();
     return nout;
 }
