@@ -269,13 +269,12 @@ def main() -> int:
     row_bytes = d * 4 if args.profile == "quality" else d
     blk = 2048  # one 32-vector FastScan block of 64-byte codes
     ncell = int(st["n_cells"])
-    mp = (ncell + 7) // 8 * 8
     stages = {
         # name: (avg ms, algorithmic bytes per launch, what the bytes are)
-        "prep_kernel (+Hamming)": (avg["ms_prep"], nq * (d * 4 + 2048 + mp * 2) + (nq // 4) * ncell * 64,
-                                   "query f32 + FastScan table + Hamming row written, cell codes once per 4 queries"),
-        "route_seed_kernel": (avg["ms_route"], avg["seed_blocks"] * blk + nq * (2048 + mp * 2),
-                              "seed cells' FastScan blocks + the query table + its Hamming row"),
+        "reset_kernel": (avg["ms_prep"], (ncell + 1 + nq) * 4, "per-call counters cleared"),
+        "front_kernel (prep + route + seed)": (avg["ms_route"], avg["seed_blocks"] * blk + nq * (d * 4 + 2048) + ncell * 64,
+                                               "seed cells' FastScan blocks + query f32 read + FastScan table written "
+                                               "+ the cell codes once"),
         "cell_scan_kernel": (avg["ms_scan"], avg["scan_blocks"] * blk + nq * 2048,
                              "probed cells' FastScan blocks per (query, cell) + the query table"),
         "finish_kernel": (avg["ms_rerank"], avg["rerank_rows"] * row_bytes,
@@ -284,7 +283,7 @@ def main() -> int:
     dom = max(stages, key=lambda s_: stages[s_][0])
     ms_dom, bytes_dom, what = stages[dom]
     achieved = bytes_dom / (ms_dom * 1e-3) / 1e9 if ms_dom > 0 else 0.0
-    scan_ms = avg["ms_route"] + avg["ms_seed"] + avg["ms_scan"]  # the seed scan runs inside route_seed
+    scan_ms = avg["ms_route"] + avg["ms_seed"] + avg["ms_scan"]  # the seed scan runs inside the front kernel
     scan_bytes = (avg["seed_blocks"] + avg["scan_blocks"]) * blk + nq * 2048
     scan_gbs = scan_bytes / (scan_ms * 1e-3) / 1e9 if scan_ms > 0 else 0.0
     traffic = _traffic(dom, args.workload, args.profile)

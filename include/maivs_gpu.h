@@ -119,9 +119,12 @@ typedef struct maivs_search_params {
  * filled on demand by maivs_gpu_last_counters. */
 typedef struct maivs_gpu_stats {
     float ms_total;       /* device time of the whole pipeline (hipEvents) */
-    float ms_prep;        /* rotation, sign codes, FastScan tables */
-    float ms_route;       /* Hamming shortlist + SQ8 rescore + probe-list sort */
-    float ms_seed;        /* seed-cell scan + seed cut-off + adaptive cut */
+    float ms_prep;        /* per-call counter reset; with the query prep (rotation, sign codes,
+                             FastScan tables) when that runs as its own kernel */
+    float ms_route;       /* Hamming shortlist + SQ8 rescore + probe-list sort and the seed scan,
+                             cut-off and adaptive cut; with the query prep when the codes cover the
+                             whole padded dimension (one fused kernel) */
+    float ms_seed;        /* the seed stage when it runs as its own kernel (0: fused with the route) */
     float ms_invert;      /* query -> cell inversion */
     float ms_scan;        /* the cell-major scan kernel */
     float ms_select;      /* tie-inclusive cut at k * rerank_factor */

@@ -370,16 +370,16 @@ __global__ void reset_kernel(Work Wk, uint32_t M, uint32_t nq) {
 
 // ---------------------------------------------------------------- prep + Hamming (one wave per query)
 
-// Rotation, sign code, FastScan table and the two sequential sums of one query, by one wave
-// (src/quantize.rs:57-67,152-163,279-313; src/index.rs:1934-1942). Lane l holds rotated
+// Rotation and sign code of one query, by one wave (src/quantize.rs:57-67,152-163;
+// src/index.rs:1934-1942), with the rescore operands. Lane l holds rotated
 // coordinates [l*EPL, (l+1)*EPL) in registers: FWHT levels below EPL run inside the lane, the
 // others across lanes (partner l ^ (h / EPL)), in the reference's ascending level order, so every
 // butterfly sees the reference's operands. `xs` is the wave's LDS region (x[P] | mins[npos4] |
-// cqp[d4] | rqp[d4]); `qw` receives the code words. For an SQ8 rerank store it also computes the
-// rerank base sum(q * sq_min) (src/index.rs:1326-1330).
+// cqp[d4] | rqp[d4]): it receives the rotated query and the summands q * csq_min (and, for an SQ8
+// rerank store, q * sq_min) that prep_wave_tables adds up; `qw` receives the code words.
 template <int EPL>
-__device__ __forceinline__ void prep_wave(const DevArena& A, const Work& Wk, const float* __restrict__ queries,
-                                          uint32_t qi, uint32_t lane, float* xs, uint64_t* qw) {
+__device__ __forceinline__ void prep_wave_codes(const DevArena& A, const Work& Wk, const float* __restrict__ queries,
+                                                uint32_t qi, uint32_t lane, float* xs, uint64_t* qw) {
     const uint32_t P = A.P, d = A.d, npos = A.npos;
     const uint32_t np4 = (npos + 3) & ~3u;
     float* mins = xs + P;
@@ -507,6 +507,20 @@ __device__ __forceinline__ void prep_wave(const DevArena& A, const Work& Wk, con
             qw[lane] = mine;
         }
     }
+    (void)mins;
+}
+
+// The FastScan table and the sequential sums of one query, by one wave, from prep_wave_codes'
+// LDS region (src/quantize.rs:279-313; src/index.rs:1326-1330,1934-1942).
+__device__ __forceinline__ void prep_wave_tables(const DevArena& A, const Work& Wk, uint32_t qi, uint32_t lane,
+                                                 float* xs) {
+    const uint32_t P = A.P, d = A.d, npos = A.npos;
+    const uint32_t np4 = (npos + 3) & ~3u;
+    float* mins = xs + P;
+    float* cqp = mins + np4;
+    float* rqp = cqp + ((d + 3) & ~3u);
+    const bool sq8 = A.cent_sq8 != nullptr;
+    const bool rsq8 = A.rerank_mode == MAIVS_RERANK_SQ8;
     // ---- FastScan table: position j from x[4j .. 4j+3], 16 sums accumulated from 0 in order t = 0..3
     auto raw_of = [&](const float4& v, int e) {
         float s = 0.0f;
@@ -588,40 +602,20 @@ __device__ __forceinline__ void prep_wave(const DevArena& A, const Work& Wk, con
     }
 }
 
-// The block's nqb query codes (LDS) against every cell code: h = popcount(q ^ c) per word
-// (src/index.rs:1896-1915), 0xFFFF for dead cells and the padding up to Mp. Each thread takes
-// cells tid, tid + nt, ... four at a time so that four codes are in flight together.
-template <int NW>
-__device__ __forceinline__ void hamming_tile(const DevArena& A, const Work& Wk, const uint64_t* qb, uint32_t q0,
-                                             uint32_t nqb) {
-    const uint32_t Mp = A.Mp, nt = blockDim.x;
-    uint16_t* out = Wk.hs + static_cast<uint64_t>(q0) * Mp;
-    for (uint32_t c0 = threadIdx.x; c0 < Mp; c0 += 4 * nt) {
-        uint64_t cw[4][NW];
-        bool live[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const uint32_t c = c0 + u * nt;
-            live[u] = c < A.M && A.live[c] != 0;
-#pragma unroll
-            for (int w = 0; w < NW; ++w) cw[u][w] = c < A.M ? A.cent_bits[static_cast<uint64_t>(c) * NW + w] : 0ull;
-        }
-        for (uint32_t j = 0; j < nqb; ++j) {
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const uint32_t c = c0 + u * nt;
-                uint32_t h = 0;
-#pragma unroll
-                for (int w = 0; w < NW; ++w) h += __popcll(qb[j * 16 + w] ^ cw[u][w]);
-                if (c < Mp) out[static_cast<uint64_t>(j) * Mp + c] = live[u] ? static_cast<uint16_t>(h) : static_cast<uint16_t>(0xFFFFu);
-            }
-        }
-    }
+// Rotation, sign code, FastScan table and sums of one query by one wave (prep_wave_codes, then
+// prep_wave_tables once the wave's LDS writes are visible to it).
+template <int EPL>
+__device__ __forceinline__ void prep_wave(const DevArena& A, const Work& Wk, const float* __restrict__ queries,
+                                          uint32_t qi, uint32_t lane, float* xs, uint64_t* qw) {
+    prep_wave_codes<EPL>(A, Wk, queries, qi, lane, xs, qw);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    prep_wave_tables(A, Wk, qi, lane, xs);
 }
 
-// kPrepWaves queries per workgroup, one wave each (prep_wave). Flags: kPrepReset also clears the
-// per-call counters (control block, probe counts, candidate counts); kPrepHamming then runs the
-// block's queries against every cell code (hamming_tile).
+// kPrepWaves queries per workgroup, one wave each (prep_wave). Flag kPrepReset also clears the
+// per-call counters (control block, probe counts, candidate counts).
 // LDS: codes[kPrepWaves * 16] u64 | per wave x[P] | mins[npos4] | cqp[d4] | rqp[d4].
 template <int EPL>
 __global__ void __launch_bounds__(kPrepWaves * kWave)
@@ -638,30 +632,90 @@ prep_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries, u
     uint64_t* qbl = reinterpret_cast<uint64_t*>(smem);
     if (qi < K.nq) prep_wave<EPL>(A, Wk, queries, qi, lane, reinterpret_cast<float*>(qbl + kPrepWaves * 16) +
                                   wv * (A.P + ((A.npos + 3) & ~3u) + 2 * ((A.d + 3) & ~3u)), qbl + wv * 16);
-    if (flags & kPrepHamming) {
-        __syncthreads();
-        const uint32_t q0 = blockIdx.x * kPrepWaves;
-        const uint32_t nqb = min(kPrepWaves, K.nq - q0);
-        switch (A.W) {
-            case 1: hamming_tile<1>(A, Wk, qbl, q0, nqb); break;
-            case 2: hamming_tile<2>(A, Wk, qbl, q0, nqb); break;
-            case 4: hamming_tile<4>(A, Wk, qbl, q0, nqb); break;
-            case 8: hamming_tile<8>(A, Wk, qbl, q0, nqb); break;
-            default: hamming_tile<16>(A, Wk, qbl, q0, nqb); break;
-        }
-    }
 }
 
 
 // ---------------------------------------------------------------- route (one WG per query)
 
-// route_batch (src/index.rs:1873-1980) from the query's Hamming row: cut-off (hamming_cutoff,
-// :86-104), shortlist of live cells with h <= cut in ascending id, exact rescore, probe list
-// sorted by (score desc, cell asc), nucleus. Also the adaptive-cut bounds of the probe list
-// b_i = cos(max(acos(clamp(s_i)) - r_bound_c, 0)) for i >= SEED_CELLS (:2171-2176), which
-// depend on routing alone.
-// LDS: cqs[d4] | ex[np4] | keys[sort_cap] u64 | hist[nbins4] | scratch[16].
+// The query's Hamming row (src/index.rs:1896-1915): h = popcount(q ^ c) over the code words for
+// every cell, into hd (LDS, up to kHdLdsCells cells; else the query's row of Wk.hs) with the
+// padding up to Mp holding 0xFFFF, and the histogram of the cells' h. Dead cells are counted too:
+// dead_fixup takes them out afterwards (there are few or none). Run by threads t = 0 .. nt-1
+// (nt a multiple of 64) of the workgroup. L lanes share a cell code, a 16-byte chunk each
+// (NW = 1: one lane, the whole 8-byte code), so that one load instruction reads a contiguous run
+// of codes; the partial counts meet by lane exchange. Rounds of U codes per lane are double
+// buffered: the next round's loads are in flight while this round is counted. The loop bounds are
+// uniform: every lane takes part in the exchanges.
 template <int NW>
+__device__ __forceinline__ void hamming_row(const DevArena& A, const Work& Wk, uint32_t qi, uint32_t* hist,
+                                            uint16_t* hd_lds, uint32_t t, uint32_t nt) {
+    const uint32_t M = A.M, Mp = A.Mp;
+    auto run = [&](auto* out) {
+        constexpr uint32_t L = NW >= 2 ? NW / 2 : 1;
+        constexpr uint32_t U = 8;
+        const uint32_t sub = t % L, cpr = nt / L, cl = t / L, step = U * cpr;
+        const uint64_t* qg = Wk.qbits + static_cast<uint64_t>(qi) * NW;
+        const uint64_t q0 = qg[NW >= 2 ? 2 * sub : 0];
+        const uint64_t q1 = NW >= 2 ? qg[2 * sub + 1] : 0ull;
+        auto load = [&](uint32_t base, uint64_t (&w0)[U], uint64_t (&w1)[U]) {
+#pragma unroll
+            for (uint32_t u = 0; u < U; ++u) {
+                const uint32_t c = base + u * cpr + cl;
+                const uint64_t* src = A.cent_bits + static_cast<uint64_t>(c < M ? c : 0u) * NW;
+                if constexpr (NW == 1) {
+                    w0[u] = src[0];
+                    w1[u] = 0ull;
+                } else {
+                    const uint4 v = reinterpret_cast<const uint4*>(src)[sub];
+                    w0[u] = (static_cast<uint64_t>(v.y) << 32) | v.x;
+                    w1[u] = (static_cast<uint64_t>(v.w) << 32) | v.z;
+                }
+            }
+        };
+        auto count = [&](uint32_t base, const uint64_t (&w0)[U], const uint64_t (&w1)[U]) {
+#pragma unroll
+            for (uint32_t u = 0; u < U; ++u) {
+                uint32_t h = __popcll(q0 ^ w0[u]) + (NW >= 2 ? __popcll(q1 ^ w1[u]) : 0u);
+                if constexpr (L >= 2) h += static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(h), 0xB1, 0xF, 0xF, true));
+                if constexpr (L >= 4) h += static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(h), 0x4E, 0xF, 0xF, true));
+                if constexpr (L >= 8) h += __shfl_xor(h, 4, kWave);
+                const uint32_t c = base + u * cpr + cl;
+                if (sub == 0 && c < Mp) {
+                    out[c] = c < M ? static_cast<uint16_t>(h) : static_cast<uint16_t>(0xFFFFu);
+                    if (c < M) atomicAdd(&hist[h], 1u);
+                }
+            }
+        };
+        uint64_t a0[U], a1[U], b0[U], b1[U];
+        load(0, a0, a1);
+        for (uint32_t base = 0; base < Mp; base += 2 * step) {
+            if (base + step < Mp) load(base + step, b0, b1);
+            count(base, a0, a1);
+            if (base + step >= Mp) break;
+            if (base + 2 * step < Mp) load(base + 2 * step, a0, a1);
+            count(base + step, b0, b1);
+        }
+    };
+    if (Mp <= kHdLdsCells)
+        run(hd_lds);
+    else
+        run(Wk.hs + static_cast<uint64_t>(qi) * Mp);
+}
+
+// Takes the dead cells (no members) out of hamming_row's histogram and row: h = 0xFFFF.
+__device__ __forceinline__ void dead_fixup(const DevArena& A, const Work& Wk, uint32_t qi, uint32_t* hist,
+                                           uint16_t* hd_lds, uint32_t t, uint32_t nt) {
+    uint16_t* hd = A.Mp <= kHdLdsCells ? hd_lds : Wk.hs + static_cast<uint64_t>(qi) * A.Mp;
+    for (uint32_t i = t; i < A.n_dead; i += nt) {
+        const uint32_t c = A.dead[i];
+        atomicSub(&hist[hd[c]], 1u);
+        hd[c] = static_cast<uint16_t>(0xFFFFu);
+    }
+}
+
+// kFront: the caller (front_kernel) already cleared the histogram, staged cqs and ran hamming_row,
+// and K.tree_list is 0.
+template <int NW, bool kFront = false>
 __device__ __forceinline__ void route_phase(const DevArena& A, const Work& Wk, const KParams& K, uint32_t qi) {
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t tid = threadIdx.x, nt = blockDim.x;
@@ -676,11 +730,13 @@ __device__ __forceinline__ void route_phase(const DevArena& A, const Work& Wk, c
     __shared__ uint32_t s_cut;
     (void)M;
 
-    for (uint32_t i = tid; i < nbins; i += nt) hist[i] = 0;
-    for (uint32_t i = tid; i < d; i += nt) cqs[i] = Wk.cqs[static_cast<uint64_t>(qi) * d + i];
-    __syncthreads();
+    if constexpr (!kFront) {
+        for (uint32_t i = tid; i < nbins; i += nt) hist[i] = 0;
+        for (uint32_t i = tid; i < d; i += nt) cqs[i] = Wk.cqs[static_cast<uint64_t>(qi) * d + i];
+        __syncthreads();
+    }
     uint32_t nsl = 0;
-    if (K.tree_list) {
+    if (!kFront && K.tree_list) {
         // the centroid tree's leaves, live cells only (route_query, src/index.rs:1193-1204)
         const uint32_t* tl = Wk.tlist + static_cast<uint64_t>(qi) * K.tcap;
         const uint32_t nt_list = Wk.tcount[qi];
@@ -694,23 +750,14 @@ __device__ __forceinline__ void route_phase(const DevArena& A, const Work& Wk, c
             nsl += tot;
         }
     } else {
-    const uint4* hrow = reinterpret_cast<const uint4*>(Wk.hs + static_cast<uint64_t>(qi) * Mp);
-    const uint32_t nch8 = Mp / 8;
-    auto h_at = [](const uint4& v, int k) -> uint32_t {
-        const uint32_t w = k < 2 ? v.x : k < 4 ? v.y : k < 6 ? v.z : v.w;
-        return (k & 1) ? (w >> 16) : (w & 0xFFFFu);
-    };
-    uint4 first = make_uint4(~0u, ~0u, ~0u, ~0u);
-    for (uint32_t ch = tid; ch < nch8; ch += nt) {
-        const uint4 v = hrow[ch];
-        if (ch == tid) first = v;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const uint32_t h = h_at(v, k);
-            if (h != 0xFFFFu) atomicAdd(&hist[h], 1u);
-        }
+    if constexpr (!kFront) {
+        hamming_row<NW>(A, Wk, qi, hist, reinterpret_cast<uint16_t*>(scratch + 16), tid, nt);
+        __syncthreads();
     }
-    __syncthreads();
+    if (A.n_dead) {
+        dead_fixup(A, Wk, qi, hist, reinterpret_cast<uint16_t*>(scratch + 16), tid, nt);
+        __syncthreads();
+    }
     // cut = smallest t whose cumulative live count reaches want_c
     {
         const uint32_t per = (nbins + nt - 1) / nt, b0 = tid * per, b1 = min(b0 + per, nbins);
@@ -732,22 +779,34 @@ __device__ __forceinline__ void route_phase(const DevArena& A, const Work& Wk, c
     __syncthreads();
     const uint32_t cut = s_cut;
     // ---- shortlist: live cells with h <= cut, ascending id (dead cells and padding hold 0xFFFF)
-    for (uint32_t r0 = 0; r0 < nch8; r0 += nt) {
-        const uint32_t ch = r0 + tid;
-        uint4 v = make_uint4(~0u, ~0u, ~0u, ~0u);
-        if (ch < nch8) v = r0 == 0 ? first : hrow[ch];
-        uint32_t cnt = 0;
+    auto shortlist = [&](const auto* hd) {
+        const uint4* hrow = reinterpret_cast<const uint4*>(hd);
+        const uint32_t nch8 = Mp / 8;
+        auto h_at = [](const uint4& v, int k) -> uint32_t {
+            const uint32_t w = k < 2 ? v.x : k < 4 ? v.y : k < 6 ? v.z : v.w;
+            return (k & 1) ? (w >> 16) : (w & 0xFFFFu);
+        };
+        for (uint32_t r0 = 0; r0 < nch8; r0 += nt) {
+            const uint32_t ch = r0 + tid;
+            uint4 v = make_uint4(~0u, ~0u, ~0u, ~0u);
+            if (ch < nch8) v = hrow[ch];
+            uint32_t cnt = 0;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) cnt += h_at(v, k) <= cut;
-        uint32_t tot;
-        uint32_t pos = nsl + block_excl_scan_u32(cnt, scratch, &tot);
-        if (nsl + tot <= K.sort_cap) {
+            for (int k = 0; k < 8; ++k) cnt += h_at(v, k) <= cut;
+            uint32_t tot;
+            uint32_t pos = nsl + block_excl_scan_u32(cnt, scratch, &tot);
+            if (nsl + tot <= K.sort_cap) {
 #pragma unroll
-            for (int k = 0; k < 8; ++k)
-                if (h_at(v, k) <= cut) keys[pos++] = ch * 8 + k;
+                for (int k = 0; k < 8; ++k)
+                    if (h_at(v, k) <= cut) keys[pos++] = ch * 8 + k;
+            }
+            nsl += tot;
         }
-        nsl += tot;
-    }
+    };
+    if (Mp <= kHdLdsCells)
+        shortlist(reinterpret_cast<const uint16_t*>(scratch + 16));
+    else
+        shortlist(Wk.hs + static_cast<uint64_t>(qi) * Mp);
     }
     uint32_t* chosen = Wk.chosen + static_cast<uint64_t>(qi) * K.nprobe;
     float* cscore = Wk.cscore + static_cast<uint64_t>(qi) * K.nprobe;
@@ -862,7 +921,7 @@ __device__ __forceinline__ uint32_t lut_sum1(const Code<NW>& c, const uint8_t* _
 // d <= tau is kept; then the adaptive cut (:2166-2188) from the route's bounds, and the per-cell
 // probe counts for the inversion.
 // LDS: static table[TB] at offset 0; dynamic probed[MW4] | coarse[256] | fine[256] | misc[32] |
-// sbuf[seed_cap4] (d << 16 | item, item < 65536).
+// sbuf[seed_cap4] u16 (d by item index).
 template <int NW>
 __device__ __forceinline__ void seed_phase(const DevArena& A, const Work& Wk, const KParams& K, uint32_t qi) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -875,7 +934,7 @@ __device__ __forceinline__ void seed_phase(const DevArena& A, const Work& Wk, co
     uint32_t* coarse = probed + ((A.MW + 3) & ~3u);
     uint32_t* fine = coarse + 256;
     uint32_t* misc = fine + 256;
-    uint32_t* sbuf = misc + 32;
+    uint16_t* sbuf = reinterpret_cast<uint16_t*>(misc + 32);
 
     const uint32_t nch = Wk.nchosen[qi];
     const uint32_t* chosen = Wk.chosen + static_cast<uint64_t>(qi) * K.nprobe;
@@ -922,66 +981,73 @@ __device__ __forceinline__ void seed_phase(const DevArena& A, const Work& Wk, co
         if (tid == 0) atomicAdd(&Wk.ctl->err_seed, 1u);
         return;
     }
+    // seed-cell boundaries in scalar registers: a member's cell is the number of boundaries at or
+    // below its item index
+    uint32_t offv[kSeedCells];
+#pragma unroll
+    for (uint32_t k = 1; k < kSeedCells; ++k)
+        offv[k] = k < ns ? __builtin_amdgcn_readfirstlane(misc[kOff + k]) : 0xFFFFFFFFu;
     auto seed_cell = [&](uint32_t it) {
         uint32_t s = 0;
 #pragma unroll
-        for (uint32_t k = 1; k < kSeedCells; ++k) s += (k < ns && it >= misc[kOff + k]);
+        for (uint32_t k = 1; k < kSeedCells; ++k) s += it >= offv[k];
         return s;
     };
     // ---- score every seed member, all cells at once; coarse histogram of d >> 8 on the fly.
-    // Software pipeline: the next round's code (and other home) is in flight during this round's
-    // lookups.
+    // sbuf[item] = d, or kNoD for a member another probed home scores (or the filter drops).
+    // Each thread scores two members per round while the next round's two codes are in flight.
+    uint32_t npass = 0;
     if (total > 0) {
-        auto locate = [&](uint32_t it, uint32_t& c) -> uint64_t {
+        const bool filt = K.filter != 0;
+        struct Mem {
+            Code<NW> code;
+            uint64_t e;
+            uint32_t c, alt, tag;
+        };
+        auto fetch = [&](uint32_t it, Mem& m) {
             const uint32_t j = min(it, total - 1);
             const uint32_t s = seed_cell(j);
-            c = misc[kCell + s];
-            return static_cast<uint64_t>(misc[kE0 + s]) + (j - misc[kOff + s]);
+            m.c = misc[kCell + s];
+            m.e = static_cast<uint64_t>(misc[kE0 + s]) + (j - misc[kOff + s]);
+            m.code.load(A.codes + m.e * (2 * NW));
+            m.alt = A.ma == 2 ? A.entry_alt[m.e] : kNoAlt;
+            m.tag = filt ? A.entry_tag[m.e] : 0u;
         };
-        const bool filt = K.filter != 0;
-        uint32_t c_cur;
-        uint64_t e_cur = locate(tid, c_cur);
-        Code<NW> cur;
-        cur.load(A.codes + e_cur * (2 * NW));
-        uint32_t alt_cur = A.ma == 2 ? A.entry_alt[e_cur] : kNoAlt;
-        uint32_t tag_cur = filt ? A.entry_tag[e_cur] : 0u;
-        for (uint32_t b = 0; b < total; b += nt) {
-            const uint32_t it = b + tid;
-            const bool have = it < total;
-            const bool more = b + nt < total;
-            uint32_t c_nxt = 0, alt_nxt = kNoAlt, tag_nxt = 0;
-            uint64_t e_nxt = 0;
-            Code<NW> nxt;
-            if (more) {
-                e_nxt = locate(it + nt, c_nxt);
-                nxt.load(A.codes + e_nxt * (2 * NW));
-                if (A.ma == 2) alt_nxt = A.entry_alt[e_nxt];
-                if (filt) tag_nxt = A.entry_tag[e_nxt];
+        auto score = [&](const Mem& m, uint32_t it) {
+            bool pass;
+            if (A.ma == 2)
+                pass = !(m.alt < m.c && ((probed[m.alt >> 5] >> (m.alt & 31)) & 1u));
+            else
+                pass = canonical(A, m.e, A.ma > 2 ? A.members[m.e] : 0u, m.c, probed);
+            if (filt) pass = pass && m.tag >= K.tag_lo && m.tag <= K.tag_hi;
+            const uint32_t dv = A.maxk - lut_sum1<NW>(m.code, table);
+            if (pass) {
+                atomicAdd(&coarse[dv >> 8], 1u);
+                ++npass;
             }
-            bool pass = false;
-            uint32_t dv = 0;
-            if (have) {
-                if (A.ma == 2)
-                    pass = !(alt_cur < c_cur && ((probed[alt_cur >> 5] >> (alt_cur & 31)) & 1u));
-                else
-                    pass = canonical(A, e_cur, A.ma > 2 ? A.members[e_cur] : 0u, c_cur, probed);
-                if (filt) pass = pass && tag_cur >= K.tag_lo && tag_cur <= K.tag_hi;
-                dv = A.maxk - lut_sum1<NW>(cur, table);
-                if (pass) atomicAdd(&coarse[dv >> 8], 1u);
-            }
-            const uint64_t m = __ballot(pass);
-            uint32_t wb = 0;
-            if (lane == 0 && m) wb = atomicAdd(&misc[kCnt], static_cast<uint32_t>(__popcll(m)));
-            wb = __shfl(wb, 0, kWave);
-            if (pass) sbuf[wb + lanes_below(m)] = (dv << 16) | it;
+            sbuf[it] = static_cast<uint16_t>(pass ? dv : kNoD);
+        };
+        Mem a, b;
+        fetch(tid, a);
+        fetch(tid + nt, b);
+        for (uint32_t r = 0; r < total; r += 2 * nt) {
+            const bool more = r + 2 * nt < total;
+            Mem na, nb;
             if (more) {
-                cur = nxt;
-                e_cur = e_nxt;
-                c_cur = c_nxt;
-                alt_cur = alt_nxt;
-                tag_cur = tag_nxt;
+                fetch(r + 2 * nt + tid, na);
+                fetch(r + 3 * nt + tid, nb);
+            }
+            if (r + tid < total) score(a, r + tid);
+            if (r + nt + tid < total) score(b, r + nt + tid);
+            if (more) {
+                a = na;
+                b = nb;
             }
         }
+    }
+    {
+        const uint32_t ws = wave_sum_u32(npass);
+        if (lane == 0 && ws) atomicAdd(&misc[kCnt], ws);
     }
     __syncthreads();
     const uint32_t cnt = misc[kCnt];
@@ -1017,30 +1083,29 @@ __device__ __forceinline__ void seed_phase(const DevArena& A, const Work& Wk, co
         if (tid < kWave) find_bin(coarse, K.target, &misc[kHb], &misc[kBelow]);
         __syncthreads();
         const uint32_t hb = misc[kHb], need = K.target - misc[kBelow];
-        for (uint32_t i = tid; i < cnt; i += nt) {
-            const uint32_t dd = sbuf[i] >> 16;
-            if ((dd >> 8) == hb) atomicAdd(&fine[dd & 0xFFu], 1u);
+        for (uint32_t i = tid; i < total; i += nt) {
+            const uint32_t dd = sbuf[i];
+            if (dd != kNoD && (dd >> 8) == hb) atomicAdd(&fine[dd & 0xFFu], 1u);
         }
         __syncthreads();
         if (tid < kWave) find_bin(fine, need, &misc[kTau], &misc[kBelow]);
         __syncthreads();
         tau = (hb << 8) | misc[kTau];
     }
-    // ---- keep d <= tau, with the member's slot
+    // ---- keep d <= tau, with the member's slot (kNoD exceeds every tau: tau <= maxk < kNoD)
     uint2* seed = Wk.seed + static_cast<uint64_t>(qi) * K.seed_cap;
-    for (uint32_t b = 0; b < cnt; b += nt) {
+    for (uint32_t b = 0; b < total; b += nt) {
         const uint32_t i = b + tid;
-        const uint32_t v = i < cnt ? sbuf[i] : 0u;
-        const bool keep = i < cnt && (v >> 16) <= tau;
+        const uint32_t v = i < total ? sbuf[i] : kNoD;
+        const bool keep = v <= tau;
         const uint64_t m = __ballot(keep);
         uint32_t wb = 0;
         if (lane == 0 && m) wb = atomicAdd(&misc[kKeep], static_cast<uint32_t>(__popcll(m)));
         wb = __shfl(wb, 0, kWave);
         if (keep) {
-            const uint32_t it = v & 0xFFFFu;
-            const uint32_t s = seed_cell(it);
-            const uint32_t slot = A.members[misc[kE0 + s] + (it - misc[kOff + s])];
-            seed[wb + lanes_below(m)] = make_uint2(v >> 16, slot);
+            const uint32_t s = seed_cell(i);
+            const uint32_t slot = A.members[misc[kE0 + s] + (i - misc[kOff + s])];
+            seed[wb + lanes_below(m)] = make_uint2(v, slot);
         }
     }
     __syncthreads();  // every wave's kept count is in misc[kKeep]
@@ -1116,6 +1181,46 @@ route_seed_kernel(DevArena A, Work Wk, KParams K) {
     route_phase<NW>(A, Wk, K, blockIdx.x);
     __syncthreads();
     seed_phase<NW>(A, Wk, K, blockIdx.x);
+}
+
+// Prep, route and seed of one query in one workgroup, for codes over the whole padded dimension
+// (n_words * 64 == dim_pad, so prep's coordinates per lane equal NW). Wave 0 computes the query's
+// rotation and code (prep_wave_codes) while the other waves clear the route's histogram; then wave
+// 0 builds the FastScan table and sums (prep_wave_tables) while the others compute the Hamming row
+// and stage the rescore operand; then every wave routes and seeds the query. Each phase reads what
+// the previous ones wrote to global memory after the barrier between them. LDS: the route's
+// regions (route_phase's layout) | the prep region (codes[16] u64 | x[P] | mins | cqp | rqp); the
+// seed phase reuses all of it.
+template <int NW>
+__global__ void __launch_bounds__(kSeedThreads, NW >= 16 ? 3 : 4)
+front_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const uint32_t qi = blockIdx.x;
+    if (qi >= K.nq) return;
+    const uint32_t tid = threadIdx.x, nt = blockDim.x;
+    const uint32_t d = A.d, d4 = (d + 3) & ~3u, np4 = min((K.nprobe + 3) & ~3u, K.sort_cap);
+    const uint32_t nbins = NW * 64 + 1;
+    float* cqs = reinterpret_cast<float*>(smem);
+    uint32_t* hist = reinterpret_cast<uint32_t*>(reinterpret_cast<uint64_t*>(cqs + d4 + np4) + K.sort_cap);
+    uint32_t* scratch = hist + ((nbins + 3) & ~3u);
+    uint8_t* prep = smem + route_lds_bytes(d, NW, A.Mp, K.sort_cap, K.nprobe);
+    float* xs = reinterpret_cast<float*>(prep + 16 * 8);
+    if (tid < kWave) {
+        prep_wave_codes<NW>(A, Wk, queries, qi, lane_id(), xs, reinterpret_cast<uint64_t*>(prep));
+    } else {
+        for (uint32_t i = tid - kWave; i < nbins; i += nt - kWave) hist[i] = 0;
+    }
+    __syncthreads();
+    if (tid < kWave) {
+        prep_wave_tables(A, Wk, qi, lane_id(), xs);
+    } else {
+        for (uint32_t i = tid - kWave; i < d; i += nt - kWave) cqs[i] = Wk.cqs[static_cast<uint64_t>(qi) * d + i];
+        hamming_row<NW>(A, Wk, qi, hist, reinterpret_cast<uint16_t*>(scratch + 16), tid - kWave, nt - kWave);
+    }
+    __syncthreads();
+    route_phase<NW, true>(A, Wk, K, qi);
+    __syncthreads();
+    seed_phase<NW>(A, Wk, K, qi);
 }
 
 // ---------------------------------------------------------------- inversion: cell -> queries

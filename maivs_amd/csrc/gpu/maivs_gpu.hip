@@ -82,18 +82,24 @@ size_t prep_lds(const DevArena& A) {
            static_cast<size_t>(kPrepWaves) * (A.P + ((A.npos + 3) & ~3u) + 2 * ((A.d + 3) & ~3u)) * 4;
 }
 
-// LDS of route: cqs[d4] | ex[np4] | keys[sort_cap] u64 | hist[nbins4] | scratch[16]
-// (ex holds the nucleus weights of the capped list, at most min(nprobe, sort_cap) of them)
+// LDS of route (route_lds_bytes; ex holds the nucleus weights of the capped list, at most
+// min(nprobe, sort_cap) of them)
 size_t route_lds(const DevArena& A, uint32_t sort_cap, uint32_t nprobe) {
-    const size_t np4 = std::min<size_t>((nprobe + 3) & ~3u, sort_cap);
-    return ((A.d + 3) & ~3u) * 4 + np4 * 4 + static_cast<size_t>(sort_cap) * 8 +
-           (((A.W * 64 + 1) + 3) & ~3u) * 4 + 16 * 4;
+    return route_lds_bytes(A.d, A.W, A.Mp, sort_cap, nprobe);
 }
 
-// Dynamic LDS of seed: probed[MW4] | coarse[256] | fine[256] | misc[32] | sbuf[seed_cap4]
+// LDS of one query's prep in the fused front kernel: codes[16] u64 | x[P] | mins[npos4] | cqp[d4] | rqp[d4]
+size_t prep1_lds(const DevArena& A) {
+    return 16 * 8 + static_cast<size_t>(A.P + ((A.npos + 3) & ~3u) + 2 * ((A.d + 3) & ~3u)) * 4;
+}
+
+// The fused front kernel runs when the code covers the whole padded dimension.
+bool fused_front(const DevArena& A) { return static_cast<uint64_t>(A.W) * 64 == A.P; }
+
+// Dynamic LDS of seed: probed[MW4] | coarse[256] | fine[256] | misc[32] | sbuf[seed_cap8] u16
 // (plus its static table of W*256 bytes)
 size_t seed_lds(const DevArena& A, uint32_t seed_cap) {
-    return ((A.MW + 3) & ~3u) * 4 + 512 * 4 + 32 * 4 + static_cast<size_t>((seed_cap + 3) & ~3u) * 4;
+    return ((A.MW + 3) & ~3u) * 4 + 512 * 4 + 32 * 4 + static_cast<size_t>((seed_cap + 7) & ~7u) * 2;
 }
 
 // LDS of finish: hist[256] | scratch[32] | qs[d4] | ent[kFinishLdsCap] (d, slot) | keys[kFinishLdsCap] u64
@@ -149,7 +155,8 @@ int ensure_work(maivs_gpu_ctx* ctx, uint32_t nq, uint32_t nprobe, uint32_t k) {
     rc |= dalloc(ctx, o, &W.cqs, nql * A.d);
     rc |= dalloc(ctx, o, &W.cqbase, nql);
     rc |= dalloc(ctx, o, &W.rbase, nql);
-    rc |= dalloc(ctx, o, &W.hs, nql * A.Mp);
+    W.hs = nullptr;
+    if (A.Mp > kHdLdsCells) rc |= dalloc(ctx, o, &W.hs, nql * A.Mp);
     rc |= dalloc(ctx, o, &W.bnd, nql * nprobe);
     rc |= dalloc(ctx, o, &W.chosen, nql * nprobe);
     rc |= dalloc(ctx, o, &W.cscore, nql * nprobe);
@@ -318,6 +325,16 @@ int launch_route(maivs_gpu_ctx* ctx, const KParams& K) {
     return 0;
 }
 
+// Prep, route and seed fused, one workgroup per query (the counters are reset beforehand).
+int launch_front(maivs_gpu_ctx* ctx, const KParams& K, const float* d_q) {
+    const DevArena& A = ctx->A;
+    const size_t lds = std::max(route_lds(A, K.sort_cap, K.nprobe) + prep1_lds(A), ctx->lds_seed);
+    DISPATCH_NW(A.W, hipLaunchKernelGGL(front_kernel<NW>, dim3(K.nq), dim3(kSeedThreads), lds, ctx->stream, A,
+                                        ctx->Wk, K, d_q));
+    HIP_TRY(ctx, hipGetLastError());
+    return 0;
+}
+
 // Route and seed fused, one workgroup per query.
 int launch_route_seed(maivs_gpu_ctx* ctx, const KParams& K) {
     const DevArena& A = ctx->A;
@@ -429,8 +446,13 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
             if (events) HIP_TRY(ctx, hipEventRecord(ctx->ev[i], ctx->stream));
             return 0;
         };
-        if ((r = mark(0)) || (r = launch_prep(ctx, K, d_q, kPrepReset | kPrepHamming)) || (r = mark(3))) return r;
-        if ((r = launch_route_seed(ctx, K)) || (r = mark(2))) return r;
+        if (fused_front(ctx->A)) {
+            if ((r = mark(0)) || (r = launch_reset(ctx, K.nq)) || (r = mark(3))) return r;
+            if ((r = launch_front(ctx, K, d_q)) || (r = mark(2))) return r;
+        } else {
+            if ((r = mark(0)) || (r = launch_prep(ctx, K, d_q, kPrepReset)) || (r = mark(3))) return r;
+            if ((r = launch_route_seed(ctx, K)) || (r = mark(2))) return r;
+        }
         if ((r = launch_scan(ctx, K, false, events)) || (r = mark(5))) return r;
         if ((r = launch_finish(ctx, K, d_q, d_slots, d_scores)) || (r = mark(6))) return r;
         return 0;
@@ -699,7 +721,7 @@ int run_search_pq(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs
     }
     Work& W = ctx->Wk;
     HIP_TRY(ctx, hipEventRecord(ctx->ev[0], ctx->stream));
-    if ((rc = launch_prep(ctx, K, d_q, kPrepReset | (tree ? 0u : kPrepHamming)))) return rc;
+    if ((rc = launch_prep(ctx, K, d_q, kPrepReset))) return rc;
     for (;;) {
         if (tree && (rc = launch_pq_tree(ctx, K, cap))) return rc;
         if ((rc = launch_route(ctx, K)) || (rc = launch_pq_scan(ctx, K)) || (rc = launch_finish(ctx, K, d_q, d_slots, d_scores)))
@@ -884,17 +906,18 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
     A.fht_scale = 1.0f / std::sqrt(static_cast<float>(A.P));
     A.cf = make_chain(A.d, 4);
     A.cu = make_chain(A.d, 16);
-    std::vector<uint8_t> live(A.M);
+    std::vector<uint32_t> dead;
     uint32_t max_len = 0, n_live = 0;
     for (uint32_t c = 0; c < A.M; ++c) {
         uint32_t len = a->mem_off[c + 1] - a->mem_off[c];
-        live[c] = len > 0;
+        if (len == 0) dead.push_back(c);
         n_live += len > 0;
         max_len = std::max(max_len, len);
         if (a->fs_off[c + 1] - a->fs_off[c] != (len + 31) / 32)
             return fail(ctx, MAIVS_ERR_ARG, "fs_off does not match the member lists at cell %u", c);
     }
     A.n_live = n_live;
+    A.n_dead = static_cast<uint32_t>(dead.size());
     A.max_cell_len = max_len;
     // a seed set holds the members of at most SEED_CELLS cells: bound it by the largest ones
     uint32_t seed_cap = 0;
@@ -921,7 +944,8 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
     };
     auto run = [&]() -> int {
         int rc = 0;
-        uint8_t *fs = nullptr, *dlive = nullptr;
+        uint8_t* fs = nullptr;
+        uint32_t* ddead = nullptr;
         uint32_t *fs_off = nullptr, *codes = nullptr, *members = nullptr, *mem_off = nullptr, *slot_cells = nullptr,
                  *alt = nullptr;
         uint64_t* cent_bits = nullptr;
@@ -938,7 +962,7 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
         if ((rc = dupload(ctx, a->cent_bits, static_cast<uint64_t>(A.M) * A.W, &cent_bits))) return rc;
         if ((rc = dupload(ctx, a->r_bound, A.M, &r_bound))) return rc;
         if ((rc = dupload(ctx, a->rot_signs, 2ull * A.P, &signs))) return rc;
-        if ((rc = dupload(ctx, live.data(), A.M, &dlive))) return rc;
+        if (!dead.empty() && (rc = dupload(ctx, dead.data(), dead.size(), &ddead))) return rc;
         hipLaunchKernelGGL(fs_to_codes_kernel, dim3(std::max<uint32_t>(A.M, 1)), dim3(256), 0, ctx->stream, fs, fs_off,
                            mem_off, A.M, A.W, codes);
         if (A.ma == 2)
@@ -1007,7 +1031,7 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
         A.rot_signs = signs;
         A.sq_min = sq_min;
         A.sq_step = sq_step;
-        A.live = dlive;
+        A.dead = ddead;
         return 0;
     };
     int rc = run();
@@ -1019,7 +1043,8 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
     }
     ctx->h_r_bound.assign(a->r_bound, a->r_bound + A.M);
     // LDS plan: the route's shortlist sort size is per call (12 bytes per entry: key + weight)
-    const size_t route_fixed = route_lds(A, 0, 0);
+    // (the fused front kernel also holds one query's prep region beside the route's)
+    const size_t route_fixed = route_lds(A, 0, 0) + (fused_front(A) ? prep1_lds(A) : 0);
     size_t room = kLdsBudget - 8192 > route_fixed ? (kLdsBudget - 8192 - route_fixed) / 12 : 0;
     if (room < 1024) return fail(ctx, MAIVS_ERR_UNSUPPORTED, "routing tables do not fit in LDS");
     uint32_t sc = 1024;
@@ -1042,6 +1067,8 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
         hipFuncSetAttribute(reinterpret_cast<const void*>(route_seed_kernel<NW>),
                             hipFuncAttributeMaxDynamicSharedMemorySize,
                             static_cast<int>(std::max(route_lds(A, sc, sc), ctx->lds_seed)));
+        hipFuncSetAttribute(reinterpret_cast<const void*>(front_kernel<NW>), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(std::max(route_lds(A, sc, sc) + prep1_lds(A), ctx->lds_seed)));
     });
     ctx->uploaded = true;
     return 0;
@@ -1192,7 +1219,7 @@ int maivs_gpu_route(maivs_gpu_ctx* ctx, const float* q, uint32_t nq, const maivs
         return 0;
     }
     HIP_TRY(ctx, hipMemcpyAsync(W.q, q, static_cast<size_t>(nq) * ctx->A.d * 4, hipMemcpyHostToDevice, ctx->stream));
-    if ((rc = launch_prep(ctx, K, W.q, kPrepReset | kPrepHamming))) return rc;
+    if ((rc = launch_prep(ctx, K, W.q, kPrepReset))) return rc;
     if ((rc = launch_route(ctx, K))) return rc;
     Ctl ctl{};
     HIP_TRY(ctx, hipMemcpyAsync(&ctl, W.ctl, sizeof(Ctl), hipMemcpyDeviceToHost, ctx->stream));

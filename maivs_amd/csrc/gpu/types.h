@@ -11,7 +11,8 @@ namespace maivs_dev {
 
 constexpr uint32_t kSeedCells = 8;       // SEED_CELLS, src/index.rs:2018
 constexpr uint32_t kPrepWaves = 4;       // queries per prep workgroup, one wave each
-constexpr uint32_t kPrepReset = 1, kPrepHamming = 2;
+constexpr uint32_t kPrepReset = 1;
+constexpr uint32_t kHdLdsCells = 8192;  // the route keeps its Hamming row in LDS up to this many cells
 constexpr uint32_t kRouteThreads = 256;
 constexpr uint32_t kSeedThreads = 256;
 constexpr uint32_t kScanThreads = 256;
@@ -22,6 +23,7 @@ constexpr uint32_t kItemGroups = 1024;   // work items per cell in a scan work i
 constexpr uint32_t kHistBins = 256;
 constexpr uint32_t kFinishLdsCap = 2048; // final candidates kept and sorted in LDS up to this many
 constexpr uint32_t kNoAlt = 0xFFFFFFFEu; // entry_alt: the slot has no other home
+constexpr uint32_t kNoD = 0xFFFFu;        // seed score buffer: member not scored here (d <= 255 * 256 < kNoD)
 
 // Chain-major row layout for the 8-lane FMA dots: element 8t + l (t < T) of a row is stored at
 // l*Tp + t, the d - 8T tail elements at 8*Tp + i. Lane l of a group of 8 then reads its whole
@@ -31,7 +33,7 @@ struct Chain {
 };
 
 struct DevArena {
-    uint32_t d, P, W, M, N, ma, rerank_mode, npos, maxk, n_live, max_cell_len, MW, Mp;
+    uint32_t d, P, W, M, N, ma, rerank_mode, npos, maxk, n_live, n_dead, max_cell_len, MW, Mp;
     uint64_t E;
     float fht_scale;
     Chain cf, cu;               // f32 and u8 chain layouts
@@ -51,7 +53,7 @@ struct DevArena {
     const uint8_t* sq8;         // N x cu.stride (chain-major SQ8 rows)
     const float* sq_min;
     const float* sq_step;
-    const uint8_t* live;        // M
+    const uint32_t* dead;       // n_dead: the cells with no members, ascending
     const uint32_t* entry_tag;  // E: the tag of the entry's slot (null without tags)
 };
 
@@ -68,16 +70,27 @@ struct Ctl {
     unsigned long long seed_blocks, scan_blocks, scan_pairs, survivors, rerank_rows;
 };
 
+// Bytes of the route's LDS layout: cqs[d4] | ex[np4] | keys[sort_cap] u64 | hist[nbins4] |
+// scratch[16] | hd[Mp] u16 (hd only up to kHdLdsCells cells). A multiple of 16.
+__host__ __device__ inline size_t route_lds_bytes(uint32_t d, uint32_t W, uint32_t Mp, uint32_t sort_cap,
+                                                  uint32_t nprobe) {
+    const size_t d4 = (d + 3) & ~3u;
+    const size_t np4 = ((nprobe + 3) & ~3u) < sort_cap ? ((nprobe + 3) & ~3u) : sort_cap;
+    const size_t nbins4 = ((W * 64 + 1) + 3) & ~3u;
+    return d4 * 4 + np4 * 4 + static_cast<size_t>(sort_cap) * 8 + nbins4 * 4 + 16 * 4 +
+           (Mp <= kHdLdsCells ? static_cast<size_t>(Mp) * 2 : 0);
+}
+
 struct Work {
     float* q;              // nq x d (host-input calls)
     uint64_t* qbits;       // nq x W
+    uint16_t* hs;          // nq x Mp Hamming rows, only when Mp > kHdLdsCells (else in LDS)
     uint8_t* lut;          // nq x npos*16
     float* delta;          // nq
     float* bias;           // nq
     float* cqs;            // nq x d: rescore operand q * csq_step (q itself for f32 centroids)
     float* cqbase;         // nq: sum(q * csq_min), sequential
     float* rbase;          // nq: SQ8 rerank base sum(q * sq_min), sequential (MAIVS_RERANK_SQ8)
-    uint16_t* hs;          // nq x Mp: Hamming distance to every cell, 0xFFFF for dead cells
     float* bnd;            // nq x nprobe: adaptive-cut bounds of the probe list (i >= SEED_CELLS)
     uint32_t* chosen;      // nq x nprobe
     float* cscore;         // nq x nprobe

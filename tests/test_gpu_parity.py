@@ -213,3 +213,49 @@ def test_search_churned_unfiltered_matches_oracle(ctx, churn50k, mix50k):
     _, queries, _ = mix50k
     ix, _, _ = churn50k
     _compare_search(ctx, ix, queries, _params(ix, 10, 16))
+
+
+@pytest.fixture(scope="module")
+def dead20k(mix50k):
+    """20k vectors in 156 cells with every member of four cells removed, then compact(): the
+    emptied (dead) cells must leave the Hamming histogram and never be routed."""
+    import maivs_amd as M
+    base, _, _ = mix50k
+    x = np.ascontiguousarray(base[:20000])
+    ix = M.preset(384, len(x))
+    ix.train_centroids(x, 156)
+    ix.add_batch(list(range(len(x))), x)
+    ix.compact()
+    arr = ix._arena_arrays()
+    ext = ix._ext_ids()
+    gone = set()
+    for c in (5, 17, 42, 99):
+        for slot in arr["members"][arr["mem_off"][c]: arr["mem_off"][c + 1]].tolist():
+            gone.add(int(ext[slot]))
+    for v in sorted(gone):
+        assert ix.remove(v)
+    ix.compact()
+    mo = ix._arena_arrays()["mem_off"]
+    assert int((np.diff(mo) == 0).sum()) >= 4
+    return ix
+
+
+@pytest.mark.parametrize("nprobe", [8, 40, 152])
+def test_dead_cells_match_oracle(ctx, dead20k, mix50k, nprobe):
+    _, queries, _ = mix50k
+    ix = dead20k
+    _upload(ctx, ix)
+    p = _params(ix, 10, nprobe)
+    ch, cs, nch = ctx.route(queries, p)
+    _, och, ocs, onch = oracle.route_batch(ix._arena_desc(), queries, p, 8)
+    assert np.array_equal(nch, onch)
+    dead = set(np.nonzero(np.diff(ix._arena_arrays()["mem_off"]) == 0)[0].tolist())
+    for i in range(len(queries)):
+        n = onch[i]
+        assert np.array_equal(ch[i, :n], och[i, :n]), i
+        assert not dead & set(ch[i, :n].tolist()), i
+    _compare_search(ctx, ix, queries, p)
+    s, v = ctx.search_queries(queries[:200], p)
+    os_, ov = oracle.search_one(ix._arena_desc(), queries[:200], p, 8)
+    assert np.array_equal(s, os_)
+    assert v.tobytes() == ov.tobytes()
