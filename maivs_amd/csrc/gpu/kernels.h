@@ -1144,9 +1144,106 @@ __device__ __forceinline__ void seed_phase(const DevArena& A, const Work& Wk, co
         __syncthreads();
         rest_end = misc[kRe];
     }
-    // ---- the query into each rest cell's bucket (bucket mode), else probe counts for the
+    // ---- the first rest cells, ranks [ns, r_in), scanned here and query-major (the cell-major
+    // scan takes the others): their canonical members with d <= tau become the query's first
+    // candidates, as the cell-major scan would emit them (src/index.rs:2231-2275)
+    const uint32_t r_in = min(rest_end, ns + K.front_rest);
+    if (r_in > ns) {
+        const uint32_t nr = r_in - ns;
+        if (tid < kWave) {
+            uint32_t c = 0, e0 = 0, len = 0;
+            if (tid < nr) {
+                c = chosen[ns + tid];
+                e0 = A.mem_off[c];
+                len = A.mem_off[c + 1] - e0;
+            }
+            uint32_t x = len;
+#pragma unroll
+            for (int o = 1; o < static_cast<int>(kFrontRestMax); o <<= 1) {
+                const uint32_t y = __shfl_up(x, o, kWave);
+                if (tid >= static_cast<uint32_t>(o)) x += y;
+            }
+            if (tid < nr) {
+                misc[kOff + tid + 1] = x;
+                misc[kCell + tid] = c;
+                misc[kE0 + tid] = e0;
+            }
+            if (tid == 0) {
+                misc[kOff] = 0;
+                misc[kCnt] = 0;
+            }
+        }
+        __syncthreads();
+        const uint32_t rtotal = misc[kOff + nr];
+        uint32_t roff[kFrontRestMax];
+#pragma unroll
+        for (uint32_t k = 1; k < kFrontRestMax; ++k)
+            roff[k] = k < nr ? __builtin_amdgcn_readfirstlane(misc[kOff + k]) : 0xFFFFFFFFu;
+        if (rtotal > 0) {
+            const bool filt = K.filter != 0;
+            struct RMem {
+                Code<NW> code;
+                uint64_t e;
+                uint32_t c, alt, tag, slot;
+            };
+            auto fetch = [&](uint32_t it, RMem& m) {
+                const uint32_t j = min(it, rtotal - 1);
+                uint32_t s = 0;
+#pragma unroll
+                for (uint32_t k = 1; k < kFrontRestMax; ++k) s += j >= roff[k];
+                m.c = misc[kCell + s];
+                m.e = static_cast<uint64_t>(misc[kE0 + s]) + (j - misc[kOff + s]);
+                m.code.load(A.codes + m.e * (2 * NW));
+                m.alt = A.ma == 2 ? A.entry_alt[m.e] : kNoAlt;
+                m.tag = filt ? A.entry_tag[m.e] : 0u;
+                m.slot = A.members[m.e];
+            };
+            auto keep = [&](const RMem& m, bool have, uint32_t& dv) {
+                dv = A.maxk - lut_sum1<NW>(m.code, table);
+                if (!have || dv > tau) return false;
+                bool pass;
+                if (A.ma == 2)
+                    pass = !(m.alt < m.c && ((probed[m.alt >> 5] >> (m.alt & 31)) & 1u));
+                else
+                    pass = canonical(A, m.e, m.slot, m.c, probed);
+                return pass && (!filt || (m.tag >= K.tag_lo && m.tag <= K.tag_hi));
+            };
+            uint2* cand = Wk.cand + static_cast<uint64_t>(qi) * K.cand_cap;
+            RMem a, b;
+            fetch(tid, a);
+            fetch(tid + nt, b);
+            for (uint32_t r = 0; r < rtotal; r += 2 * nt) {
+                const bool more = r + 2 * nt < rtotal;
+                RMem na, nb;
+                if (more) {
+                    fetch(r + 2 * nt + tid, na);
+                    fetch(r + 3 * nt + tid, nb);
+                }
+                uint32_t da, db;
+                const bool pa = keep(a, r + tid < rtotal, da);
+                const bool pb = keep(b, r + nt + tid < rtotal, db);
+                const uint64_t ma = __ballot(pa), mb = __ballot(pb);
+                if (ma | mb) {
+                    uint32_t wb = 0;
+                    if (lane == 0) wb = atomicAdd(&misc[kCnt], static_cast<uint32_t>(__popcll(ma) + __popcll(mb)));
+                    wb = __shfl(wb, 0, kWave);
+                    const uint32_t posa = wb + lanes_below(ma), posb = wb + static_cast<uint32_t>(__popcll(ma)) + lanes_below(mb);
+                    if (pa && posa < K.cand_cap) cand[posa] = make_uint2(da, a.slot);
+                    if (pb && posb < K.cand_cap) cand[posb] = make_uint2(db, b.slot);
+                }
+                if (more) {
+                    a = na;
+                    b = nb;
+                }
+            }
+        }
+        __syncthreads();
+        // the query's count so far (the counters were cleared; the cell-major scan adds to it later)
+        if (tid == 0) Wk.cand_cnt[qi] = misc[kCnt];
+    }
+    // ---- the query into each other rest cell's bucket (bucket mode), else probe counts for the
     // counting-sort inversion
-    for (uint32_t i = ns + tid; i < rest_end; i += nt) {
+    for (uint32_t i = r_in + tid; i < rest_end; i += nt) {
         const uint32_t c = chosen[i];
         const uint32_t slot = atomicAdd(&Wk.cell_cnt[c], 1u);
         if (K.bucket_cap) {
@@ -1230,8 +1327,9 @@ __global__ void invert_count_kernel(Work Wk, KParams K) {
     uint32_t qi = blockIdx.x;
     if (qi >= K.nq) return;
     uint32_t ns = min(kSeedCells, Wk.nchosen[qi]), re = Wk.rest_end[qi];
+    const uint32_t r0 = min(re, ns + K.front_rest);  // the seed stage scanned ranks [ns, r0)
     const uint32_t* chosen = Wk.chosen + static_cast<uint64_t>(qi) * K.nprobe;
-    for (uint32_t i = ns + threadIdx.x; i < re; i += blockDim.x) atomicAdd(&Wk.cell_cnt[chosen[i]], 1u);
+    for (uint32_t i = r0 + threadIdx.x; i < re; i += blockDim.x) atomicAdd(&Wk.cell_cnt[chosen[i]], 1u);
 }
 
 // Single workgroup: exclusive scan of cell_cnt[0..M) -> cell_off[0..M], cell_cur = cell_off.
@@ -1261,8 +1359,9 @@ __global__ void invert_fill_kernel(Work Wk, KParams K) {
     uint32_t qi = blockIdx.x;
     if (qi >= K.nq) return;
     uint32_t ns = min(kSeedCells, Wk.nchosen[qi]), re = Wk.rest_end[qi];
+    const uint32_t r0 = min(re, ns + K.front_rest);  // the seed stage scanned ranks [ns, r0)
     const uint32_t* chosen = Wk.chosen + static_cast<uint64_t>(qi) * K.nprobe;
-    for (uint32_t i = ns + threadIdx.x; i < re; i += blockDim.x) {
+    for (uint32_t i = r0 + threadIdx.x; i < re; i += blockDim.x) {
         uint32_t c = chosen[i];
         uint32_t pos = atomicAdd(&Wk.cell_cur[c], 1u);
         Wk.qof[pos] = qi;
@@ -1288,6 +1387,8 @@ __device__ __forceinline__ void scan_item(const DevArena& A, const Work& Wk, con
         Code<NW> code;
         uint32_t slot, alt;
         bool kept;
+        uint32_t pw[kItemQ];  // with two homes: each query's probed-bitset word of the other home
+        uint32_t pmask;       // bit j: query j probed the other home (from pw, by resolve)
     };
     auto load_member = [&](uint32_t ebase, Member& m) {
         const uint32_t i = ebase + tid;
@@ -1301,22 +1402,51 @@ __device__ __forceinline__ void scan_item(const DevArena& A, const Work& Wk, con
             const uint32_t tg = A.entry_tag[e];
             m.kept = m.kept && tg >= K.tag_lo && tg <= K.tag_hi;
         }
+        if (A.ma == 2) {
+            // loaded with the code, so that their latency overlaps the lookups (unconditional
+            // loads from valid addresses; only a home h < c is ever tested)
+            const uint32_t w = m.alt < c ? m.alt >> 5 : 0u;
+#pragma unroll
+            for (uint32_t j = 0; j < kItemQ; ++j) {
+                const uint32_t qq = s_q[j];
+                m.pw[j] = Wk.probed[static_cast<uint64_t>(qq != kNone ? qq : 0u) * A.MW + w];
+            }
+        }
+    };
+    // the probed bits out of the loaded words (waits for them: called once they are needed)
+    auto resolve = [&](Member& m) {
+        uint32_t mk = 0;
+        if (A.ma == 2) {
+#pragma unroll
+            for (uint32_t j = 0; j < kItemQ; ++j) mk |= ((m.pw[j] >> (m.alt & 31)) & 1u) << j;
+        }
+        m.pmask = mk;
     };
     Member m;
     load_member(0, m);
-    // interleave each group's tables: table[gi][x*4 + g] = lut_{4gi+g}[x] (4x4 byte transpose)
+    // interleave each group's tables: table[gi][x*4 + g] = lut_{4gi+g}[x] (4x4 byte transpose).
+    // A group's table words are all loaded before its first transpose: one round trip per group.
     for (uint32_t gi = 0; gi < ngroups; ++gi) {
-        for (uint32_t x4 = tid; x4 < TB / 4; x4 += nt) {
-            uint32_t v[kG];
+        constexpr uint32_t X4 = (TB / 4 + kScanThreads - 1) / kScanThreads;
+        uint32_t v[X4][kG];
+#pragma unroll
+        for (uint32_t xi = 0; xi < X4; ++xi)
 #pragma unroll
             for (uint32_t g = 0; g < kG; ++g) {
-                const uint32_t qq = s_q[gi * kG + g];
-                v[g] = qq != kNone ? reinterpret_cast<const uint32_t*>(Wk.lut + static_cast<uint64_t>(qq) * TB)[x4] : 0u;
+                const uint32_t x4 = tid + xi * nt, qq = s_q[gi * kG + g];
+                v[xi][g] = x4 < TB / 4 && qq != kNone
+                               ? reinterpret_cast<const uint32_t*>(Wk.lut + static_cast<uint64_t>(qq) * TB)[x4]
+                               : 0u;
             }
-            const uint32_t lo01 = __builtin_amdgcn_perm(v[1], v[0], 0x05010400u);
-            const uint32_t hi01 = __builtin_amdgcn_perm(v[1], v[0], 0x07030602u);
-            const uint32_t lo23 = __builtin_amdgcn_perm(v[3], v[2], 0x05010400u);
-            const uint32_t hi23 = __builtin_amdgcn_perm(v[3], v[2], 0x07030602u);
+#pragma unroll
+        for (uint32_t xi = 0; xi < X4; ++xi) {
+            const uint32_t x4 = tid + xi * nt;
+            if (x4 >= TB / 4) continue;
+            const uint32_t* w = v[xi];
+            const uint32_t lo01 = __builtin_amdgcn_perm(w[1], w[0], 0x05010400u);
+            const uint32_t hi01 = __builtin_amdgcn_perm(w[1], w[0], 0x07030602u);
+            const uint32_t lo23 = __builtin_amdgcn_perm(w[3], w[2], 0x05010400u);
+            const uint32_t hi23 = __builtin_amdgcn_perm(w[3], w[2], 0x07030602u);
             uint4 o;
             o.x = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
             o.y = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);
@@ -1326,36 +1456,47 @@ __device__ __forceinline__ void scan_item(const DevArena& A, const Work& Wk, con
         }
     }
     __syncthreads();
+    const uint32_t lane = lane_id();
     for (uint32_t ebase = 0; ebase < len; ebase += nt) {
         if (ebase) load_member(ebase, m);
+        resolve(m);
         const uint64_t e = static_cast<uint64_t>(e0) + min(ebase + tid, len - 1);
         for (uint32_t gi = 0; gi < ngroups; ++gi) {
             uint32_t sums[kG];
             lut_sums<NW, kG>(m.code, table[gi], sums);
+            bool pass[kG];
+            uint32_t dv[kG];
+            uint64_t bm[kG];
 #pragma unroll
             for (uint32_t g = 0; g < kG; ++g) {
                 const uint32_t qq = s_q[gi * kG + g];
-                bool pass = false;
-                uint32_t dv = 0;
+                pass[g] = false;
+                dv[g] = 0;
                 if (m.kept && qq != kNone) {
-                    dv = A.maxk - sums[g];
-                    if (dv <= s_t[gi * kG + g]) {
-                        const uint32_t* probed = Wk.probed + static_cast<uint64_t>(qq) * A.MW;
+                    dv[g] = A.maxk - sums[g];
+                    if (dv[g] <= s_t[gi * kG + g]) {
                         if (A.ma == 2)
-                            pass = !(m.alt < c && ((probed[m.alt >> 5] >> (m.alt & 31)) & 1u));
+                            pass[g] = !(m.alt < c && ((m.pmask >> (gi * kG + g)) & 1u));
                         else
-                            pass = canonical(A, e, m.slot, c, probed);
+                            pass[g] = canonical(A, e, m.slot, c, Wk.probed + static_cast<uint64_t>(qq) * A.MW);
                     }
                 }
-                const uint64_t bm = __ballot(pass);
-                if (bm) {
-                    uint32_t wb = 0;
-                    if (lane_id() == 0) wb = atomicAdd(&Wk.cand_cnt[qq], static_cast<uint32_t>(__popcll(bm)));
-                    wb = __shfl(wb, 0, kWave);
-                    const uint32_t pos = wb + lanes_below(bm);
-                    if (pass && pos < K.cand_cap)
-                        Wk.cand[static_cast<uint64_t>(qq) * K.cand_cap + pos] = make_uint2(dv, m.slot);
-                }
+                bm[g] = __ballot(pass[g]);
+            }
+            // one atomic round for the group's queries: lane g reserves query g's slots
+            if ((bm[0] | bm[1] | bm[2] | bm[3]) == 0) continue;
+            uint32_t mine = 0;
+#pragma unroll
+            for (uint32_t g = 0; g < kG; ++g)
+                if (lane == g) mine = static_cast<uint32_t>(__popcll(bm[g]));
+            uint32_t wb = 0;
+            if (lane < kG && mine) wb = atomicAdd(&Wk.cand_cnt[s_q[gi * kG + lane]], mine);
+#pragma unroll
+            for (uint32_t g = 0; g < kG; ++g) {
+                const uint32_t base = __shfl(wb, static_cast<int>(g), kWave);
+                const uint32_t pos = base + lanes_below(bm[g]);
+                if (pass[g] && pos < K.cand_cap)
+                    Wk.cand[static_cast<uint64_t>(s_q[gi * kG + g]) * K.cand_cap + pos] = make_uint2(dv[g], m.slot);
             }
         }
     }
@@ -1367,7 +1508,7 @@ __device__ __forceinline__ void scan_item(const DevArena& A, const Work& Wk, con
 // strides over the items. Counting-sort mode: workgroup c scans cell c for all its queries,
 // kItemQ at a time.
 template <int NW>
-__global__ void __launch_bounds__(kScanThreads, NW >= 16 ? 4 : 8)
+__global__ void __launch_bounds__(kScanThreads, NW >= 16 ? 4 : 6)
 cell_scan_kernel(DevArena A, Work Wk, KParams K) {
     constexpr uint32_t TB = NW * 256;
     __shared__ __align__(16) uint8_t table[kItemQ / kG][kG * TB];

@@ -247,6 +247,7 @@ KParams make_params(maivs_gpu_ctx* ctx, uint32_t nq, const maivs_search_params* 
     K.use_nucleus = p->target_confidence < 1.0f;
     K.seed_cap = ctx->cap_seed;
     K.bucket_cap = ctx->cap_bucket;
+    K.front_rest = kFrontRestMax;
     K.cand_cap = ctx->cap_cand;
     K.fin_cap = ctx->cap_fin;
     K.key_cap = ctx->cap_key;
@@ -380,9 +381,11 @@ int launch_scan(maivs_gpu_ctx* ctx, const KParams& K, bool recount, bool events 
     return 0;
 }
 
-// The same parameters with the counting-sort inversion instead of the buckets (every re-run).
+// The same parameters with the counting-sort inversion instead of the buckets, and every rest
+// cell left to the cell-major scan (every re-run).
 KParams csr(KParams K) {
     K.bucket_cap = 0;
+    K.front_rest = 0;
     return K;
 }
 
@@ -453,7 +456,12 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
             if ((r = mark(0)) || (r = launch_prep(ctx, K, d_q, kPrepReset)) || (r = mark(3))) return r;
             if ((r = launch_route_seed(ctx, K)) || (r = mark(2))) return r;
         }
-        if ((r = launch_scan(ctx, K, false, events)) || (r = mark(5))) return r;
+        // with at most SEED_CELLS + front_rest probes the seed stage scanned every rest cell itself
+        if (K.nprobe > kSeedCells + K.front_rest) {
+            if ((r = launch_scan(ctx, K, false, events)) || (r = mark(5))) return r;
+        } else if ((r = mark(4)) || (r = mark(5))) {
+            return r;
+        }
         if ((r = launch_finish(ctx, K, d_q, d_slots, d_scores)) || (r = mark(6))) return r;
         return 0;
     };

@@ -10,6 +10,7 @@
 namespace maivs_dev {
 
 constexpr uint32_t kSeedCells = 8;       // SEED_CELLS, src/index.rs:2018
+constexpr uint32_t kFrontRestMax = 8;    // rest cells the seed stage may scan itself (<= kSeedCells)
 constexpr uint32_t kPrepWaves = 4;       // queries per prep workgroup, one wave each
 constexpr uint32_t kPrepReset = 1;
 constexpr uint32_t kHdLdsCells = 8192;  // the route keeps its Hamming row in LDS up to this many cells
@@ -129,6 +130,8 @@ struct KParams {
     uint32_t filter, tag_lo, tag_hi;  // keep!: tag in [tag_lo, tag_hi] (filter != 0 only with tags)
     // per-query path: routing from the tree's list, bounds from this probe rank on, buffer sizes
     uint32_t tree_list, bnd_from, tcap, pq_cap, pq_room, pq_noflag;
+    // batched path: rest cells (probe ranks SEED_CELLS on) the seed stage scans itself, query-major
+    uint32_t front_rest;
     float tc, beta, at_margin, norm, prune_band, nucleus_band;
 };
 
