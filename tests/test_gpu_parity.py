@@ -259,3 +259,34 @@ def test_dead_cells_match_oracle(ctx, dead20k, mix50k, nprobe):
     os_, ov = oracle.search_one(ix._arena_desc(), queries[:200], p, 8)
     assert np.array_equal(s, os_)
     assert v.tobytes() == ov.tobytes()
+
+
+@pytest.fixture(scope="module")
+def cells9k(mix50k):
+    """50k vectors in 9,000 cells: more cells than the route keeps in LDS (8,192), so every query's
+    Hamming row goes through its global-memory row instead."""
+    import maivs_amd as M
+    base, _, _ = mix50k
+    x = np.ascontiguousarray(base)
+    ix = M.preset(384, len(x))
+    ix.train_centroids(x, 9000)
+    ix.add_batch(list(range(len(x))), x)
+    ix.compact()
+    assert ix.stats()["n_cells"] == 9000
+    return ix
+
+
+@pytest.mark.parametrize("nprobe", [10, 40])
+def test_global_hamming_rows_match_oracle(ctx, cells9k, mix50k, nprobe):
+    _, queries, gt = mix50k
+    ix = cells9k
+    _upload(ctx, ix)
+    p = _params(ix, 10, nprobe)
+    ch, cs, nch = ctx.route(queries, p)
+    _, och, ocs, onch = oracle.route_batch(ix._arena_desc(), queries, p, 8)
+    assert np.array_equal(nch, onch)
+    for i in range(len(queries)):
+        n = onch[i]
+        assert np.array_equal(ch[i, :n], och[i, :n]), i
+        assert cs[i, :n].tobytes() == ocs[i, :n].tobytes(), i
+    _compare_search(ctx, ix, queries, p, gt)
