@@ -120,34 +120,6 @@ __device__ __forceinline__ float dot_cm_u8(const uint8_t* __restrict__ row, cons
     return r;
 }
 
-// Sort n <= 256 keys from `src` (padded with max keys) in wave 0 and write the first `out_n`
-// ascending keys to `dst` (both may alias). Other waves only wait at the caller's barrier.
-__device__ __forceinline__ void wave0_sort_prefix(const uint64_t* src, uint32_t n, uint64_t* dst, uint32_t out_n) {
-    if (threadIdx.x >= 64) return;
-    const uint32_t lane = lane_id();
-    auto run = [&](auto kpl_tag) {
-        constexpr int KPL = decltype(kpl_tag)::value;
-        uint64_t k[KPL];
-#pragma unroll
-        for (int r = 0; r < KPL; ++r) {
-            uint32_t i = static_cast<uint32_t>(r) * 64 + lane;
-            k[r] = i < n ? src[i] : kKeyMax;
-        }
-        wave_sort_u64<KPL>(k);
-#pragma unroll
-        for (int r = 0; r < KPL; ++r) {
-            uint32_t i = static_cast<uint32_t>(r) * 64 + lane;
-            if (i < out_n) dst[i] = k[r];
-        }
-    };
-    if (n <= 64)
-        run(std::integral_constant<int, 1>{});
-    else if (n <= 128)
-        run(std::integral_constant<int, 2>{});
-    else
-        run(std::integral_constant<int, 4>{});
-}
-
 // One member's nibble sums against a FastScan table of G interleaved queries in LDS (table byte
 // [(j*16 + e)*G + g] = query g's entry e of position j). The member's code (2*NW dwords, nibble j
 // at dword j/8, bits 4*(j%8)) is loaded whole before the lookups so its latency is paid once.
@@ -513,7 +485,7 @@ __device__ __forceinline__ void prep_wave_codes(const DevArena& A, const Work& W
 // The FastScan table and the sequential sums of one query, by one wave, from prep_wave_codes'
 // LDS region (src/quantize.rs:279-313; src/index.rs:1326-1330,1934-1942).
 __device__ __forceinline__ void prep_wave_tables(const DevArena& A, const Work& Wk, uint32_t qi, uint32_t lane,
-                                                 float* xs) {
+                                                 float* xs, uint8_t* lds_table = nullptr) {
     const uint32_t P = A.P, d = A.d, npos = A.npos;
     const uint32_t np4 = (npos + 3) & ~3u;
     float* mins = xs + P;
@@ -556,6 +528,7 @@ __device__ __forceinline__ void prep_wave_tables(const DevArena& A, const Work& 
             pk[e >> 2] |= static_cast<uint32_t>(qv) << (8 * (e & 3));
         }
         lut[j] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        if (lds_table) reinterpret_cast<uint4*>(lds_table)[j] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -758,23 +731,31 @@ __device__ __forceinline__ void route_phase(const DevArena& A, const Work& Wk, c
         dead_fixup(A, Wk, qi, hist, reinterpret_cast<uint16_t*>(scratch + 16), tid, nt);
         __syncthreads();
     }
-    // cut = smallest t whose cumulative live count reaches want_c
-    {
-        const uint32_t per = (nbins + nt - 1) / nt, b0 = tid * per, b1 = min(b0 + per, nbins);
+    // cut = smallest t whose cumulative live count reaches want_c (wave 0: a run of bins per lane,
+    // a wave scan, and the one lane whose run crosses want_c)
+    if (tid < kWave) {
+        const uint32_t lane = tid, per = (nbins + kWave - 1) / kWave, b0 = lane * per, b1 = min(b0 + per, nbins);
         uint32_t loc = 0;
         for (uint32_t i = b0; i < b1; ++i) loc += hist[i];
-        uint32_t total;
-        const uint32_t ex0 = block_excl_scan_u32(loc, scratch, &total);
-        uint32_t cand = kNone, cum = ex0;
-        for (uint32_t i = b0; i < b1; ++i) {
-            cum += hist[i];
-            if (cum >= K.want_c) {
-                cand = i;
-                break;
+        uint32_t x = loc;
+#pragma unroll
+        for (int o = 1; o < kWave; o <<= 1) {
+            const uint32_t y = __shfl_up(x, o, kWave);
+            if (lane >= static_cast<uint32_t>(o)) x += y;
+        }
+        uint32_t cand = kNone, cum = x - loc;
+        if (cum < K.want_c && x >= K.want_c) {
+            for (uint32_t i = b0; i < b1; ++i) {
+                cum += hist[i];
+                if (cum >= K.want_c) {
+                    cand = i;
+                    break;
+                }
             }
         }
-        const uint32_t cut = block_min_u32(cand, scratch);
-        if (tid == 0) s_cut = cut == kNone ? NW * 64 : cut;
+        const uint64_t m = __ballot(cand != kNone);
+        const uint32_t cut = m ? __shfl(cand, __ffsll(static_cast<long long>(m)) - 1, kWave) : NW * 64;
+        if (lane == 0) s_cut = cut;
     }
     __syncthreads();
     const uint32_t cut = s_cut;
@@ -786,22 +767,25 @@ __device__ __forceinline__ void route_phase(const DevArena& A, const Work& Wk, c
             const uint32_t w = k < 2 ? v.x : k < 4 ? v.y : k < 6 ? v.z : v.w;
             return (k & 1) ? (w >> 16) : (w & 0xFFFFu);
         };
-        for (uint32_t r0 = 0; r0 < nch8; r0 += nt) {
-            const uint32_t ch = r0 + tid;
-            uint4 v = make_uint4(~0u, ~0u, ~0u, ~0u);
-            if (ch < nch8) v = hrow[ch];
-            uint32_t cnt = 0;
+        // each thread a run of consecutive chunks of 8 cells, so one block scan orders them all
+        const uint32_t per = (nch8 + nt - 1) / nt, c0 = min(tid * per, nch8), c1 = min(c0 + per, nch8);
+        uint32_t cnt = 0;
+        for (uint32_t ch = c0; ch < c1; ++ch) {
+            const uint4 v = hrow[ch];
 #pragma unroll
             for (int k = 0; k < 8; ++k) cnt += h_at(v, k) <= cut;
-            uint32_t tot;
-            uint32_t pos = nsl + block_excl_scan_u32(cnt, scratch, &tot);
-            if (nsl + tot <= K.sort_cap) {
+        }
+        uint32_t tot;
+        uint32_t pos = block_excl_scan_u32(cnt, scratch, &tot);
+        if (tot <= K.sort_cap) {
+            for (uint32_t ch = c0; ch < c1; ++ch) {
+                const uint4 v = hrow[ch];
 #pragma unroll
                 for (int k = 0; k < 8; ++k)
                     if (h_at(v, k) <= cut) keys[pos++] = ch * 8 + k;
             }
-            nsl += tot;
         }
+        nsl = tot;
     };
     if (Mp <= kHdLdsCells)
         shortlist(reinterpret_cast<const uint16_t*>(scratch + 16));
@@ -842,8 +826,16 @@ __device__ __forceinline__ void route_phase(const DevArena& A, const Work& Wk, c
     __syncthreads();
     // ---- probe list: ascending keys = (score desc, cell asc)
     const uint32_t cap = min(K.nprobe, nsl);
-    if (nsl <= 256) {
-        wave0_sort_prefix(keys, nsl, keys, nsl);
+    if (nsl <= nt) {
+        // keys are unique: each one's rank among the nsl places it (read all, then write)
+        uint64_t mine = 0;
+        uint32_t r = 0;
+        if (tid < nsl) {
+            mine = keys[tid];
+            for (uint32_t j = 0; j < nsl; ++j) r += keys[j] < mine;
+        }
+        __syncthreads();
+        if (tid < nsl) keys[r] = mine;
     } else {
         uint32_t n2 = 1;
         while (n2 < nsl) n2 <<= 1;
@@ -922,14 +914,22 @@ __device__ __forceinline__ uint32_t lut_sum1(const Code<NW>& c, const uint8_t* _
 // probe counts for the inversion.
 // LDS: static table[TB] at offset 0; dynamic probed[MW4] | coarse[256] | fine[256] | misc[32] |
 // sbuf[seed_cap4] u16 (d by item index).
+// The seed stage's FastScan table in static LDS: the kernel's largest static LDS variable, at
+// address 0, so the table lookups need no base add.
 template <int NW>
+__device__ __forceinline__ uint8_t* seed_table() {
+    __shared__ __align__(16) uint8_t table[NW * 256];
+    return table;
+}
+
+// kTableReady: the caller already wrote the query's table into seed_table<NW>().
+template <int NW, bool kTableReady = false>
 __device__ __forceinline__ void seed_phase(const DevArena& A, const Work& Wk, const KParams& K, uint32_t qi) {
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t tid = threadIdx.x, nt = blockDim.x, lane = lane_id();
     constexpr uint32_t TB = NW * 256;
     constexpr uint32_t kOff = 0, kCell = 9, kE0 = 17, kCnt = 25, kKeep = 26, kTau = 27, kRe = 28, kHb = 29, kBelow = 30;
-    // the kernel's only static LDS: its address is the constant 0, so the table lookups need no base add
-    __shared__ __align__(16) uint8_t table[TB];
+    uint8_t* const table = seed_table<NW>();
     uint32_t* probed = reinterpret_cast<uint32_t*>(smem);
     uint32_t* coarse = probed + ((A.MW + 3) & ~3u);
     uint32_t* fine = coarse + 256;
@@ -939,7 +939,7 @@ __device__ __forceinline__ void seed_phase(const DevArena& A, const Work& Wk, co
     const uint32_t nch = Wk.nchosen[qi];
     const uint32_t* chosen = Wk.chosen + static_cast<uint64_t>(qi) * K.nprobe;
     const uint32_t ns = min(kSeedCells, nch);
-    {
+    if constexpr (!kTableReady) {
         const uint4* src = reinterpret_cast<const uint4*>(Wk.lut + static_cast<uint64_t>(qi) * TB);
         for (uint32_t i = tid; i < TB / 16; i += nt) reinterpret_cast<uint4*>(table)[i] = src[i];
     }
@@ -1309,7 +1309,7 @@ front_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries) 
     }
     __syncthreads();
     if (tid < kWave) {
-        prep_wave_tables(A, Wk, qi, lane_id(), xs);
+        prep_wave_tables(A, Wk, qi, lane_id(), xs, seed_table<NW>());
     } else {
         for (uint32_t i = tid - kWave; i < d; i += nt - kWave) cqs[i] = Wk.cqs[static_cast<uint64_t>(qi) * d + i];
         hamming_row<NW>(A, Wk, qi, hist, reinterpret_cast<uint16_t*>(scratch + 16), tid - kWave, nt - kWave);
@@ -1317,7 +1317,7 @@ front_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries) 
     __syncthreads();
     route_phase<NW, true>(A, Wk, K, qi);
     __syncthreads();
-    seed_phase<NW>(A, Wk, K, qi);
+    seed_phase<NW, true>(A, Wk, K, qi);
 }
 
 // ---------------------------------------------------------------- inversion: cell -> queries
