@@ -35,6 +35,7 @@ struct maivs_gpu_ctx {
     uint32_t max_sort_cap_route = 0;  // largest shortlist sort the route kernel's LDS can hold
     uint32_t seed_cap = 0;            // sum of the SEED_CELLS largest cells: bound of one seed set
     size_t lds_prep = 0, lds_seed = 0, lds_finish = 0;
+    Ctl* h_ctl = nullptr;  // pinned host copy of the control block (read after each pass)
     hipEvent_t ev[8] = {};
     // last call, for maivs_gpu_last_candidates / maivs_gpu_last_counters
     uint32_t last_nq = 0, last_fin_cap = 0;

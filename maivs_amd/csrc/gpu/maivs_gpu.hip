@@ -409,8 +409,9 @@ int fetch_probe_list(maivs_gpu_ctx* ctx, uint32_t qi, uint32_t nprobe, std::vect
 }
 
 int read_ctl(maivs_gpu_ctx* ctx, Ctl* ctl) {
-    HIP_TRY(ctx, hipMemcpyAsync(ctl, ctx->Wk.ctl, sizeof(Ctl), hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(ctx, hipMemcpyAsync(ctx->h_ctl, ctx->Wk.ctl, sizeof(Ctl), hipMemcpyDeviceToHost, ctx->stream));
     HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    *ctl = *ctx->h_ctl;
     return 0;
 }
 
@@ -497,11 +498,12 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
                 }
                 ctx->gkey = key;
             }
-            // whole-pass time only: events recorded inside a graph do not time stages
+            // whole-pass time only (events recorded inside a graph do not time stages), and only
+            // when the caller asks for measurements
             staged = false;
-            HIP_TRY(ctx, hipEventRecord(ctx->ev[0], ctx->stream));
+            if (st) HIP_TRY(ctx, hipEventRecord(ctx->ev[0], ctx->stream));
             HIP_TRY(ctx, hipGraphLaunch(ctx->gexec, ctx->stream));
-            HIP_TRY(ctx, hipEventRecord(ctx->ev[6], ctx->stream));
+            if (st) HIP_TRY(ctx, hipEventRecord(ctx->ev[6], ctx->stream));
             return 0;
         }
         staged = true;
@@ -523,7 +525,7 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
                     ctl.max_shortlist, ctx->max_sort_cap_route);
     if (ctl.err_seed) return fail(ctx, MAIVS_ERR_UNSUPPORTED, "a seed set exceeds its on-chip capacity");
     float ms;
-    if (hipEventElapsedTime(&ms, ctx->ev[0], ctx->ev[6]) == hipSuccess) S.ms_total = ms;
+    if ((st || staged) && hipEventElapsedTime(&ms, ctx->ev[0], ctx->ev[6]) == hipSuccess) S.ms_total = ms;
     if (staged) {
         if (hipEventElapsedTime(&ms, ctx->ev[0], ctx->ev[3]) == hipSuccess) S.ms_prep = ms;
         if (hipEventElapsedTime(&ms, ctx->ev[3], ctx->ev[2]) == hipSuccess) S.ms_route = ms;
@@ -836,9 +838,15 @@ int maivs_gpu_create(int device, maivs_gpu_ctx** out) {
     }
     for (auto& e : ctx->ev) {
         if (hipEventCreate(&e) != hipSuccess) {
-            delete ctx;
+            maivs_gpu_destroy(ctx);
             return MAIVS_ERR_HIP;
         }
+    }
+    // the control block's host copy in pinned memory: one DMA per pass, no staging copy
+    if (hipHostMalloc(reinterpret_cast<void**>(&ctx->h_ctl), sizeof(Ctl), hipHostMallocDefault) != hipSuccess) {
+        ctx->h_ctl = nullptr;
+        maivs_gpu_destroy(ctx);
+        return MAIVS_ERR_OOM;
     }
     *out = ctx;
     return 0;
@@ -855,6 +863,7 @@ void maivs_gpu_destroy(maivs_gpu_ctx* ctx) {
     free_all(ctx->arena_allocs);
     for (auto& e : ctx->ev)
         if (e) (void)hipEventDestroy(e);
+    if (ctx->h_ctl) (void)hipHostFree(ctx->h_ctl);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
 }
