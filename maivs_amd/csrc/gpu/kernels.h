@@ -332,10 +332,11 @@ __global__ void entry_sums_kernel(const uint32_t* __restrict__ codes, const uint
     }
 }
 
-// Zero the per-call counters: control block, cell counts, candidate counts.
+// Zero the per-call counters: control block, cell counts, candidate counts, the epilogue's count.
 __global__ void reset_kernel(Work Wk, uint32_t M, uint32_t nq) {
     uint32_t i = blockIdx.x * blockDim.x + threadIdx.x, stride = gridDim.x * blockDim.x;
     if (i < sizeof(Ctl) / 4) reinterpret_cast<uint32_t*>(Wk.ctl)[i] = 0;
+    if (i == 0) *Wk.done = 0;
     for (uint32_t j = i; j <= M; j += stride) Wk.cell_cnt[j] = 0;
     for (uint32_t j = i; j < nq; j += stride) Wk.cand_cnt[j] = 0;
 }
@@ -597,6 +598,7 @@ prep_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries, u
     if (flags & kPrepReset) {
         const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x, stride = gridDim.x * blockDim.x;
         if (i < sizeof(Ctl) / 4) reinterpret_cast<uint32_t*>(Wk.ctl)[i] = 0;
+        if (i == 0) *Wk.done = 0;
         for (uint32_t j = i; j <= A.M; j += stride) Wk.cell_cnt[j] = 0;
         for (uint32_t j = i; j < K.nq; j += stride) Wk.cand_cnt[j] = 0;
     }
@@ -1580,12 +1582,10 @@ __device__ __forceinline__ uint32_t wave_select_kth(const uint32_t (&v)[KPL], ui
 // Up to kFinishLdsCap candidates are staged in LDS once; the cut G is then a one-wave radix
 // select, and the top k of up to 256 reranked keys come from their ranks (keys are unique).
 // LDS: hist[256] | scratch[32] | qs[d4] | ent[kFinishLdsCap] (d, slot) | keys[kFinishLdsCap] u64.
-__global__ void __launch_bounds__(kFinishThreads, 4)
-finish_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries, uint32_t* __restrict__ out_slots,
-              float* __restrict__ out_scores) {
+__device__ __forceinline__ uint32_t finish_phase(const DevArena& A, const Work& Wk, const KParams& K,
+                                                 const float* __restrict__ queries, uint32_t* __restrict__ out_slots,
+                                                 float* __restrict__ out_scores, uint32_t qi) {
     extern __shared__ __align__(16) uint8_t smem[];
-    const uint32_t qi = blockIdx.x;
-    if (qi >= K.nq) return;
     const uint32_t tid = threadIdx.x, nt = blockDim.x, d = A.d, lane = lane_id();
     uint32_t* hist = reinterpret_cast<uint32_t*>(smem);
     uint32_t* scratch = hist + kHistBins;
@@ -1597,6 +1597,7 @@ finish_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries,
     const uint32_t ns_cnt = Wk.seed_cnt[qi];
     const uint32_t cc = Wk.cand_cnt[qi];
     const uint32_t nc = min(cc, K.cand_cap);
+    if (tid == 0) Wk.cand_n[qi] = cc;
     const uint2* seed = Wk.seed + static_cast<uint64_t>(qi) * K.seed_cap;
     const uint2* cand = Wk.cand + static_cast<uint64_t>(qi) * K.cand_cap;
     const uint32_t total = ns_cnt + nc;
@@ -1724,8 +1725,48 @@ finish_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries,
     if (tid == 0) {
         Wk.cut[qi] = cutv;
         Wk.ncand[qi] = n;
-        if (cc > K.cand_cap) atomicMax(&Wk.ctl->max_cand, cc);
     }
+    return cc;  // the candidate count, past the buffer when it overflowed
+}
+
+// The end of a pass, in its last kernel: the workgroup that finishes last copies the control block
+// to its pinned host mirror and clears the per-call counters (control block, probe counts,
+// candidate counts, its own count) for the next pass, so a pass needs no clearing kernel and no
+// copy of its own. The control block is only ever changed by device-scope atomics; this kernel's
+// one update (max_cand, when `over` is non-zero) returns before the workgroup counts itself in,
+// by a data dependency rather than a device-wide fence (a fence would write back the L2 of every
+// workgroup's XCD). The last workgroup reads the block with device-scope atomic loads. Other
+// workgroups' candidate-count reads are done before they count themselves in, so clearing those
+// counts is safe; the clears reach the next kernel at the kernel boundary.
+__device__ __forceinline__ void pass_epilogue(const Work& Wk, uint32_t M, uint32_t nq, uint32_t over) {
+    __shared__ uint32_t s_last;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t prev = over ? atomicMax(&Wk.ctl->max_cand, over) : 0u, zero;
+        asm volatile("v_mov_b32 %0, 0" : "=v"(zero) : "v"(prev));
+        s_last = atomicAdd(Wk.done + zero, 1u) == gridDim.x - 1 ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    const uint32_t t = threadIdx.x, nt = blockDim.x;
+    constexpr uint32_t kWords = sizeof(Ctl) / 4;
+    static_assert(kWords <= kFinishThreads, "one control word per thread");
+    uint32_t* c = reinterpret_cast<uint32_t*>(Wk.ctl);
+    if (t < kWords) {
+        reinterpret_cast<uint32_t*>(Wk.h_ctl)[t] = __hip_atomic_load(c + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        c[t] = 0;
+    }
+    for (uint32_t j = t; j <= M; j += nt) Wk.cell_cnt[j] = 0;
+    for (uint32_t j = t; j < nq; j += nt) Wk.cand_cnt[j] = 0;
+    if (t == 0) *Wk.done = 0;
+}
+
+__global__ void __launch_bounds__(kFinishThreads, 4)
+finish_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries, uint32_t* __restrict__ out_slots,
+              float* __restrict__ out_scores) {
+    uint32_t cc = 0;
+    if (blockIdx.x < K.nq) cc = finish_phase(A, Wk, K, queries, out_slots, out_scores, blockIdx.x);
+    pass_epilogue(Wk, A.M, K.nq, cc > K.cand_cap ? cc : 0u);
 }
 
 // Work counters of the last batch (on demand, one workgroup), from the routed lists: seed and
@@ -1743,7 +1784,7 @@ __global__ void counters_kernel(DevArena A, Work Wk, KParams K) {
             v[i < ns ? 0 : 1] += nb;
         }
         v[2] += re > ns ? re - ns : 0u;
-        v[3] += Wk.cand_cnt[q];
+        v[3] += Wk.cand_n[q];
         v[4] += Wk.ncand[q];
     }
     for (int k = 0; k < 5; ++k) {

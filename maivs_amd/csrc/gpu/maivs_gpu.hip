@@ -182,6 +182,9 @@ int ensure_work(maivs_gpu_ctx* ctx, uint32_t nq, uint32_t nprobe, uint32_t k) {
     rc |= dalloc(ctx, o, &W.flag_route, nql);
     rc |= dalloc(ctx, o, &W.flag_prune, nql);
     rc |= dalloc(ctx, o, &W.ctl, 1);
+    rc |= dalloc(ctx, o, &W.cand_n, nql);
+    rc |= dalloc(ctx, o, &W.done, 1);
+    ctx->counters_clean = false;  // fresh buffers: the next pass clears them first
     if (rc) {
         free_all(ctx->work_allocs);
         ctx->cap_nq = ctx->cap_nprobe = ctx->cap_k = ctx->cap_seed = ctx->cap_bucket = 0;
@@ -408,7 +411,18 @@ int fetch_probe_list(maivs_gpu_ctx* ctx, uint32_t qi, uint32_t nprobe, std::vect
     return 0;
 }
 
+// The control block of a pass that ended with finish_kernel: its epilogue mirrored the block to
+// pinned host memory and cleared the counters, so this only waits for the stream.
 int read_ctl(maivs_gpu_ctx* ctx, Ctl* ctl) {
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    *ctl = *ctx->h_ctl;
+    ctx->counters_clean = true;
+    return 0;
+}
+
+// The live control block (after kernels other than finish_kernel; the counters stay set).
+int read_ctl_live(maivs_gpu_ctx* ctx, Ctl* ctl) {
+    ctx->counters_clean = false;
     HIP_TRY(ctx, hipMemcpyAsync(ctx->h_ctl, ctx->Wk.ctl, sizeof(Ctl), hipMemcpyDeviceToHost, ctx->stream));
     HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
     *ctl = *ctx->h_ctl;
@@ -451,7 +465,8 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
             return 0;
         };
         if (fused_front(ctx->A)) {
-            if ((r = mark(0)) || (r = launch_reset(ctx, K.nq)) || (r = mark(3))) return r;
+            // the counters are clear: the previous pass's epilogue (or a clearing launch) did it
+            if ((r = mark(0)) || (r = mark(3))) return r;
             if ((r = launch_front(ctx, K, d_q)) || (r = mark(2))) return r;
         } else {
             if ((r = mark(0)) || (r = launch_prep(ctx, K, d_q, kPrepReset)) || (r = mark(3))) return r;
@@ -510,6 +525,8 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
         return enqueue_main(true);
     };
     for (;;) {
+        if (!ctx->counters_clean && (rc = launch_reset(ctx, nq))) return rc;
+        ctx->counters_clean = false;
         if ((rc = run_main())) return rc;
         if ((rc = read_ctl(ctx, &ctl))) return rc;
         if (ctl.err_shortlist && K.sort_cap < ctx->max_sort_cap_route) {
@@ -731,6 +748,7 @@ int run_search_pq(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs
     }
     Work& W = ctx->Wk;
     HIP_TRY(ctx, hipEventRecord(ctx->ev[0], ctx->stream));
+    ctx->counters_clean = false;  // cleared here by the prep, and again by the finish's epilogue
     if ((rc = launch_prep(ctx, K, d_q, kPrepReset))) return rc;
     for (;;) {
         if (tree && (rc = launch_pq_tree(ctx, K, cap))) return rc;
@@ -832,6 +850,8 @@ int maivs_gpu_create(int device, maivs_gpu_ctx** out) {
     if (!ctx) return MAIVS_ERR_OOM;
     ctx->device = device;
     if (const char* g = std::getenv("MAIVS_GPU_GRAPH")) ctx->use_graph = std::strcmp(g, "0") != 0;
+    // the first candidate buffer's room per query (it grows to the exact need on overflow)
+    if (const char* c = std::getenv("MAIVS_GPU_CAND_CAP")) ctx->initial_cand_cap = std::max(16, std::atoi(c));
     if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
         delete ctx;
         return MAIVS_ERR_HIP;
@@ -842,12 +862,19 @@ int maivs_gpu_create(int device, maivs_gpu_ctx** out) {
             return MAIVS_ERR_HIP;
         }
     }
-    // the control block's host copy in pinned memory: one DMA per pass, no staging copy
+    // the control block's host mirror in pinned memory, written by the last kernel of each pass
+    void* dev_ctl = nullptr;
     if (hipHostMalloc(reinterpret_cast<void**>(&ctx->h_ctl), sizeof(Ctl), hipHostMallocDefault) != hipSuccess) {
         ctx->h_ctl = nullptr;
         maivs_gpu_destroy(ctx);
         return MAIVS_ERR_OOM;
     }
+    if (hipHostGetDevicePointer(&dev_ctl, ctx->h_ctl, 0) != hipSuccess || !dev_ctl) {
+        maivs_gpu_destroy(ctx);
+        return MAIVS_ERR_HIP;
+    }
+    std::memset(ctx->h_ctl, 0, sizeof(Ctl));
+    ctx->Wk.h_ctl = static_cast<Ctl*>(dev_ctl);
     *out = ctx;
     return 0;
 }
@@ -1236,6 +1263,7 @@ int maivs_gpu_route(maivs_gpu_ctx* ctx, const float* q, uint32_t nq, const maivs
         return 0;
     }
     HIP_TRY(ctx, hipMemcpyAsync(W.q, q, static_cast<size_t>(nq) * ctx->A.d * 4, hipMemcpyHostToDevice, ctx->stream));
+    ctx->counters_clean = false;  // the route sets control counters that no epilogue clears
     if ((rc = launch_prep(ctx, K, W.q, kPrepReset))) return rc;
     if ((rc = launch_route(ctx, K))) return rc;
     Ctl ctl{};
@@ -1270,7 +1298,7 @@ int maivs_gpu_last_counters(maivs_gpu_ctx* ctx, maivs_gpu_stats* stats) {
     hipLaunchKernelGGL(counters_kernel, dim3(1), dim3(1024), 0, ctx->stream, ctx->A, ctx->Wk, ctx->last_K);
     HIP_TRY(ctx, hipGetLastError());
     Ctl ctl{};
-    int rc = read_ctl(ctx, &ctl);
+    int rc = read_ctl_live(ctx, &ctl);
     if (rc) return rc;
     stats->seed_blocks = ctl.seed_blocks;
     stats->scan_blocks = ctl.scan_blocks;

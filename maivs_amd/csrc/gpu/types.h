@@ -103,6 +103,8 @@ struct Work {
     uint32_t* rest_end;    // nq
     uint2* cand;           // nq x cand_cap
     uint32_t* cand_cnt;    // nq
+    uint32_t* cand_n;      // nq: each query's candidate count as the finish read it (kept after the clear)
+    uint32_t* done;        // 1: finished workgroups of the pass's last kernel (pass_epilogue)
     uint2* fin;            // nq x fin_cap (d, slot) final candidates
     uint64_t* keys;        // nq x key_cap (global sort when a final list is large)
     uint32_t* cut;         // nq
@@ -122,6 +124,7 @@ struct Work {
     uint32_t* tcount;      // nq
     uint64_t* pqc;         // nq x pq_cap: scanned candidates (d << 32 | slot)
     Ctl* ctl;
+    Ctl* h_ctl;            // pinned host mirror of ctl, written by pass_epilogue (device address)
 };
 
 struct KParams {

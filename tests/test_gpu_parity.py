@@ -290,3 +290,28 @@ def test_global_hamming_rows_match_oracle(ctx, cells9k, mix50k, nprobe):
         assert np.array_equal(ch[i, :n], och[i, :n]), i
         assert cs[i, :n].tobytes() == ocs[i, :n].tobytes(), i
     _compare_search(ctx, ix, queries, p, gt)
+
+
+def test_candidate_overflow_regrows(quality50k, mix50k, monkeypatch):
+    """A candidate buffer of 16 per query overflows: the pass's end reports the largest count
+    through the control block's host mirror, the buffer grows to it and the scan re-runs; the
+    answer is the oracle's, and a second pass on the grown buffer needs no re-run."""
+    _, queries, _ = mix50k
+    ix = quality50k
+    monkeypatch.setenv("MAIVS_GPU_CAND_CAP", "16")
+    c = capi.Context(0)
+    try:
+        c.upload(ix._arena_desc())
+        for nprobe in (12, 40):
+            p = _params(ix, 10, nprobe)
+            st = capi.GpuStats()
+            s, v = c.search(queries, p, st)
+            assert st.reruns >= 1, nprobe  # the 16-candidate buffer overflowed
+            o_s, o_v = oracle.search_batch(ix._arena_desc(), queries, p, 8)
+            assert np.array_equal(s, o_s) and v.tobytes() == o_v.tobytes()
+            st2 = capi.GpuStats()
+            s2, _ = c.search(queries, p, st2)
+            assert np.array_equal(s2, s)
+            assert st2.reruns == 0
+    finally:
+        c.close()
