@@ -271,7 +271,11 @@ def main() -> int:
     ncell = int(st["n_cells"])
     stages = {
         # name: (avg ms, algorithmic bytes per launch, what the bytes are)
-        "reset_kernel": (avg["ms_prep"], (ncell + 1 + nq) * 4, "per-call counters cleared"),
+        # past 8,192 cells the prep and the query-tiled Hamming rows run before the route; otherwise
+        # this stage is empty (the counters are cleared by the previous pass's last kernel)
+        "prep_kernel + hamming_kernel": (avg["ms_prep"], nq * (d * 4 + 2048) + ncell * 64 * ((nq + 15) // 16)
+                                         + nq * ((ncell + 7) // 8 * 8) * 2 if ncell > 8192 else 0,
+                                         "queries read, tables written, cell codes once per 16 queries, Hamming rows written"),
         "front_kernel (prep + route + seed)": (avg["ms_route"], avg["seed_blocks"] * blk + nq * (d * 4 + 2048) + ncell * 64,
                                                "seed cells' FastScan blocks + query f32 read + FastScan table written "
                                                "+ the cell codes once"),

@@ -41,6 +41,7 @@ struct maivs_gpu_ctx {
     uint32_t last_nq = 0, last_fin_cap = 0;
     KParams last_K{};
     uint32_t initial_cand_cap = 4096;
+    int front_rest_mode = -1;  // rest ranks the seed stage scans itself: -1 by cell sharing, else 0 or 8
     // the main pass captured as one HIP graph, replayed while its key matches
     struct GraphKey {
         KParams K;

@@ -689,8 +689,9 @@ __device__ __forceinline__ void dead_fixup(const DevArena& A, const Work& Wk, ui
 }
 
 // kFront: the caller (front_kernel) already cleared the histogram, staged cqs and ran hamming_row,
-// and K.tree_list is 0.
-template <int NW, bool kFront = false>
+// and K.tree_list is 0. kRowsReady: hamming_kernel already wrote the query's row of Wk.hs (more
+// cells than the LDS row holds); the histogram is built from it.
+template <int NW, bool kFront = false, bool kRowsReady = false>
 __device__ __forceinline__ void route_phase(const DevArena& A, const Work& Wk, const KParams& K, uint32_t qi) {
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t tid = threadIdx.x, nt = blockDim.x;
@@ -725,7 +726,14 @@ __device__ __forceinline__ void route_phase(const DevArena& A, const Work& Wk, c
             nsl += tot;
         }
     } else {
-    if constexpr (!kFront) {
+    if constexpr (kRowsReady) {
+        const uint16_t* row = Wk.hs + static_cast<uint64_t>(qi) * Mp;
+        for (uint32_t c = tid; c < Mp; c += nt) {
+            const uint32_t h = row[c];
+            if (h != 0xFFFFu) atomicAdd(&hist[h], 1u);
+        }
+        __syncthreads();
+    } else if constexpr (!kFront) {
         hamming_row<NW>(A, Wk, qi, hist, reinterpret_cast<uint16_t*>(scratch + 16), tid, nt);
         __syncthreads();
     }
@@ -1273,13 +1281,39 @@ seed_kernel(DevArena A, Work Wk, KParams K) {
 
 // Route and seed of one query in one workgroup (the seed reads the probe list the route just
 // wrote; LDS is reused: the route's regions are dead once the list is written).
-template <int NW>
+template <int NW, bool kRowsReady = false>
 __global__ void __launch_bounds__(kSeedThreads)
 route_seed_kernel(DevArena A, Work Wk, KParams K) {
     if (blockIdx.x >= K.nq) return;
-    route_phase<NW>(A, Wk, K, blockIdx.x);
+    route_phase<NW, false, kRowsReady>(A, Wk, K, blockIdx.x);
     __syncthreads();
     seed_phase<NW>(A, Wk, K, blockIdx.x);
+}
+
+// Hamming rows of a tile of kHamQ queries against kHamC cells (src/index.rs:1896-1915), for
+// indexes with more cells than a route keeps in LDS: one cell per thread, its code in registers,
+// the tile's query codes in LDS, so each code is loaded once per kHamQ queries. Dead cells get
+// their distance too (the route's dead_fixup takes them out); the padding up to Mp gets 0xFFFF.
+template <int NW>
+__global__ void __launch_bounds__(kHamC)
+hamming_kernel(DevArena A, Work Wk, uint32_t nq) {
+    __shared__ uint64_t qb[kHamQ][NW];
+    const uint32_t q0 = blockIdx.x * kHamQ, c = blockIdx.y * kHamC + threadIdx.x;
+    const uint32_t nqt = min(kHamQ, nq - q0);
+    for (uint32_t i = threadIdx.x; i < kHamQ * NW; i += kHamC)
+        qb[i / NW][i % NW] = i / NW < nqt ? Wk.qbits[static_cast<uint64_t>(q0 + i / NW) * NW + i % NW] : 0ull;
+    uint64_t cw[NW];
+    const uint64_t* src = A.cent_bits + static_cast<uint64_t>(c < A.M ? c : 0u) * NW;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) cw[w] = src[w];
+    __syncthreads();
+    if (c >= A.Mp) return;
+    for (uint32_t j = 0; j < nqt; ++j) {
+        uint32_t h = 0;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) h += __popcll(qb[j][w] ^ cw[w]);
+        Wk.hs[static_cast<uint64_t>(q0 + j) * A.Mp + c] = c < A.M ? static_cast<uint16_t>(h) : static_cast<uint16_t>(0xFFFFu);
+    }
 }
 
 // Prep, route and seed of one query in one workgroup, for codes over the whole padded dimension
@@ -1389,8 +1423,6 @@ __device__ __forceinline__ void scan_item(const DevArena& A, const Work& Wk, con
         Code<NW> code;
         uint32_t slot, alt;
         bool kept;
-        uint32_t pw[kItemQ];  // with two homes: each query's probed-bitset word of the other home
-        uint32_t pmask;       // bit j: query j probed the other home (from pw, by resolve)
     };
     auto load_member = [&](uint32_t ebase, Member& m) {
         const uint32_t i = ebase + tid;
@@ -1404,25 +1436,6 @@ __device__ __forceinline__ void scan_item(const DevArena& A, const Work& Wk, con
             const uint32_t tg = A.entry_tag[e];
             m.kept = m.kept && tg >= K.tag_lo && tg <= K.tag_hi;
         }
-        if (A.ma == 2) {
-            // loaded with the code, so that their latency overlaps the lookups (unconditional
-            // loads from valid addresses; only a home h < c is ever tested)
-            const uint32_t w = m.alt < c ? m.alt >> 5 : 0u;
-#pragma unroll
-            for (uint32_t j = 0; j < kItemQ; ++j) {
-                const uint32_t qq = s_q[j];
-                m.pw[j] = Wk.probed[static_cast<uint64_t>(qq != kNone ? qq : 0u) * A.MW + w];
-            }
-        }
-    };
-    // the probed bits out of the loaded words (waits for them: called once they are needed)
-    auto resolve = [&](Member& m) {
-        uint32_t mk = 0;
-        if (A.ma == 2) {
-#pragma unroll
-            for (uint32_t j = 0; j < kItemQ; ++j) mk |= ((m.pw[j] >> (m.alt & 31)) & 1u) << j;
-        }
-        m.pmask = mk;
     };
     Member m;
     load_member(0, m);
@@ -1461,7 +1474,6 @@ __device__ __forceinline__ void scan_item(const DevArena& A, const Work& Wk, con
     const uint32_t lane = lane_id();
     for (uint32_t ebase = 0; ebase < len; ebase += nt) {
         if (ebase) load_member(ebase, m);
-        resolve(m);
         const uint64_t e = static_cast<uint64_t>(e0) + min(ebase + tid, len - 1);
         for (uint32_t gi = 0; gi < ngroups; ++gi) {
             uint32_t sums[kG];
@@ -1469,19 +1481,27 @@ __device__ __forceinline__ void scan_item(const DevArena& A, const Work& Wk, con
             bool pass[kG];
             uint32_t dv[kG];
             uint64_t bm[kG];
+            // the members under a query's cut-off (few), then their exactly-once tests: with two
+            // homes every query's probed-bitset word is loaded before any is used
+            bool under[kG];
+            uint32_t pw[kG];
 #pragma unroll
             for (uint32_t g = 0; g < kG; ++g) {
                 const uint32_t qq = s_q[gi * kG + g];
+                dv[g] = A.maxk - sums[g];
+                under[g] = m.kept && qq != kNone && dv[g] <= s_t[gi * kG + g];
+                pw[g] = 0;
+                if (A.ma == 2 && under[g] && m.alt < c)
+                    pw[g] = Wk.probed[static_cast<uint64_t>(qq) * A.MW + (m.alt >> 5)];
+            }
+#pragma unroll
+            for (uint32_t g = 0; g < kG; ++g) {
                 pass[g] = false;
-                dv[g] = 0;
-                if (m.kept && qq != kNone) {
-                    dv[g] = A.maxk - sums[g];
-                    if (dv[g] <= s_t[gi * kG + g]) {
-                        if (A.ma == 2)
-                            pass[g] = !(m.alt < c && ((m.pmask >> (gi * kG + g)) & 1u));
-                        else
-                            pass[g] = canonical(A, e, m.slot, c, Wk.probed + static_cast<uint64_t>(qq) * A.MW);
-                    }
+                if (under[g]) {
+                    if (A.ma == 2)
+                        pass[g] = !(m.alt < c && ((pw[g] >> (m.alt & 31)) & 1u));
+                    else
+                        pass[g] = canonical(A, e, m.slot, c, Wk.probed + static_cast<uint64_t>(s_q[gi * kG + g]) * A.MW);
                 }
                 bm[g] = __ballot(pass[g]);
             }
@@ -1510,7 +1530,7 @@ __device__ __forceinline__ void scan_item(const DevArena& A, const Work& Wk, con
 // strides over the items. Counting-sort mode: workgroup c scans cell c for all its queries,
 // kItemQ at a time.
 template <int NW>
-__global__ void __launch_bounds__(kScanThreads, NW >= 16 ? 4 : 6)
+__global__ void __launch_bounds__(kScanThreads, NW >= 16 ? 4 : 7)
 cell_scan_kernel(DevArena A, Work Wk, KParams K) {
     constexpr uint32_t TB = NW * 256;
     __shared__ __align__(16) uint8_t table[kItemQ / kG][kG * TB];

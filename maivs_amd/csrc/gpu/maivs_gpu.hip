@@ -250,7 +250,16 @@ KParams make_params(maivs_gpu_ctx* ctx, uint32_t nq, const maivs_search_params* 
     K.use_nucleus = p->target_confidence < 1.0f;
     K.seed_cap = ctx->cap_seed;
     K.bucket_cap = ctx->cap_bucket;
-    K.front_rest = kFrontRestMax;
+    // The seed stage scans every rest cell itself, query-major, when there are at most 8 per query
+    // (nprobe <= 16) and the batch shares them little (under kFrontRestShare probes per live cell):
+    // the cell-major scan is then not launched at all. Past that its 4-query tables pay off.
+    {
+        const double rest = p->nprobe > kSeedCells ? static_cast<double>(p->nprobe - kSeedCells) : 0.0;
+        const double per_cell = static_cast<double>(nq) * rest / std::max<uint32_t>(A.n_live, 1u);
+        const bool front = p->nprobe <= kSeedCells + kFrontRestMax && per_cell < kFrontRestShare;
+        K.front_rest = ctx->front_rest_mode >= 0 ? static_cast<uint32_t>(std::min<int>(ctx->front_rest_mode, kFrontRestMax))
+                                                 : (front ? kFrontRestMax : 0u);
+    }
     K.cand_cap = ctx->cap_cand;
     K.fin_cap = ctx->cap_fin;
     K.key_cap = ctx->cap_key;
@@ -339,12 +348,26 @@ int launch_front(maivs_gpu_ctx* ctx, const KParams& K, const float* d_q) {
     return 0;
 }
 
-// Route and seed fused, one workgroup per query.
-int launch_route_seed(maivs_gpu_ctx* ctx, const KParams& K) {
+// Route and seed fused, one workgroup per query. rows_ready: hamming_kernel wrote the Hamming rows.
+int launch_route_seed(maivs_gpu_ctx* ctx, const KParams& K, bool rows_ready = false) {
     const DevArena& A = ctx->A;
     const size_t lds = std::max(route_lds(A, K.sort_cap, K.nprobe), ctx->lds_seed);
-    DISPATCH_NW(A.W, hipLaunchKernelGGL(route_seed_kernel<NW>, dim3(K.nq), dim3(kSeedThreads), lds, ctx->stream, A,
-                                        ctx->Wk, K));
+    if (rows_ready) {
+        DISPATCH_NW(A.W, hipLaunchKernelGGL((route_seed_kernel<NW, true>), dim3(K.nq), dim3(kSeedThreads), lds,
+                                            ctx->stream, A, ctx->Wk, K));
+    } else {
+        DISPATCH_NW(A.W, hipLaunchKernelGGL((route_seed_kernel<NW, false>), dim3(K.nq), dim3(kSeedThreads), lds,
+                                            ctx->stream, A, ctx->Wk, K));
+    }
+    HIP_TRY(ctx, hipGetLastError());
+    return 0;
+}
+
+// The Hamming rows of every query (indexes with more cells than a route keeps in LDS).
+int launch_hamming(maivs_gpu_ctx* ctx, uint32_t nq) {
+    const DevArena& A = ctx->A;
+    const dim3 grid((nq + kHamQ - 1) / kHamQ, (A.Mp + kHamC - 1) / kHamC);
+    DISPATCH_NW(A.W, hipLaunchKernelGGL(hamming_kernel<NW>, grid, dim3(kHamC), 0, ctx->stream, A, ctx->Wk, nq));
     HIP_TRY(ctx, hipGetLastError());
     return 0;
 }
@@ -464,7 +487,12 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
             if (events) HIP_TRY(ctx, hipEventRecord(ctx->ev[i], ctx->stream));
             return 0;
         };
-        if (fused_front(ctx->A)) {
+        if (ctx->A.Mp > kHdLdsCells) {
+            // many cells: Hamming rows by query tiles, then route and seed from them
+            if ((r = mark(0)) || (r = launch_prep(ctx, K, d_q, 0)) || (r = launch_hamming(ctx, K.nq)) || (r = mark(3)))
+                return r;
+            if ((r = launch_route_seed(ctx, K, true)) || (r = mark(2))) return r;
+        } else if (fused_front(ctx->A)) {
             // the counters are clear: the previous pass's epilogue (or a clearing launch) did it
             if ((r = mark(0)) || (r = mark(3))) return r;
             if ((r = launch_front(ctx, K, d_q)) || (r = mark(2))) return r;
@@ -852,6 +880,8 @@ int maivs_gpu_create(int device, maivs_gpu_ctx** out) {
     if (const char* g = std::getenv("MAIVS_GPU_GRAPH")) ctx->use_graph = std::strcmp(g, "0") != 0;
     // the first candidate buffer's room per query (it grows to the exact need on overflow)
     if (const char* c = std::getenv("MAIVS_GPU_CAND_CAP")) ctx->initial_cand_cap = std::max(16, std::atoi(c));
+    // the seed stage's own rest scan: unset = by cell sharing, else a fixed count of ranks (0 or 8)
+    if (const char* f = std::getenv("MAIVS_GPU_FRONT_REST")) ctx->front_rest_mode = std::max(0, std::atoi(f));
     if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
         delete ctx;
         return MAIVS_ERR_HIP;
@@ -1108,7 +1138,10 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
                             static_cast<int>(route_lds(A, sc, sc)));
         hipFuncSetAttribute(reinterpret_cast<const void*>(seed_kernel<NW>), hipFuncAttributeMaxDynamicSharedMemorySize,
                             static_cast<int>(ctx->lds_seed));
-        hipFuncSetAttribute(reinterpret_cast<const void*>(route_seed_kernel<NW>),
+        hipFuncSetAttribute(reinterpret_cast<const void*>(route_seed_kernel<NW, false>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(std::max(route_lds(A, sc, sc), ctx->lds_seed)));
+        hipFuncSetAttribute(reinterpret_cast<const void*>(route_seed_kernel<NW, true>),
                             hipFuncAttributeMaxDynamicSharedMemorySize,
                             static_cast<int>(std::max(route_lds(A, sc, sc), ctx->lds_seed)));
         hipFuncSetAttribute(reinterpret_cast<const void*>(front_kernel<NW>), hipFuncAttributeMaxDynamicSharedMemorySize,

@@ -11,9 +11,11 @@ namespace maivs_dev {
 
 constexpr uint32_t kSeedCells = 8;       // SEED_CELLS, src/index.rs:2018
 constexpr uint32_t kFrontRestMax = 8;    // rest cells the seed stage may scan itself (<= kSeedCells)
+constexpr double kFrontRestShare = 8.0;  // ... when the batch's rest probes per live cell are fewer
 constexpr uint32_t kPrepWaves = 4;       // queries per prep workgroup, one wave each
 constexpr uint32_t kPrepReset = 1;
 constexpr uint32_t kHdLdsCells = 8192;  // the route keeps its Hamming row in LDS up to this many cells
+constexpr uint32_t kHamQ = 16, kHamC = 256;  // hamming_kernel's tile: queries x cells
 constexpr uint32_t kRouteThreads = 256;
 constexpr uint32_t kSeedThreads = 256;
 constexpr uint32_t kScanThreads = 256;
