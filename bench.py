@@ -265,6 +265,10 @@ def main() -> int:
         del src, dst
 
     # ---- roofline of the dominant kernel (algorithmic bytes / its average duration)
+    # The library's rule (make_params): with nprobe <= 16 and fewer than 8 rest probes per live cell
+    # over the batch, the seed stage scans every rest cell itself and the cell scan is not launched.
+    n_live = int((np.diff(ix._arena_arrays()["mem_off"]) > 0).sum())  # live cells
+    front_rest = npb <= 16 and nq * max(npb - 8, 0) / max(n_live, 1) < 8
     d = base.shape[1]
     row_bytes = d * 4 if args.profile == "quality" else d
     blk = 2048  # one 32-vector FastScan block of 64-byte codes
@@ -276,10 +280,11 @@ def main() -> int:
         "prep_kernel + hamming_kernel": (avg["ms_prep"], nq * (d * 4 + 2048) + ncell * 64 * ((nq + 15) // 16)
                                          + nq * ((ncell + 7) // 8 * 8) * 2 if ncell > 8192 else 0,
                                          "queries read, tables written, cell codes once per 16 queries, Hamming rows written"),
-        "front_kernel (prep + route + seed)": (avg["ms_route"], avg["seed_blocks"] * blk + nq * (d * 4 + 2048) + ncell * 64,
-                                               "seed cells' FastScan blocks + query f32 read + FastScan table written "
-                                               "+ the cell codes once"),
-        "cell_scan_kernel": (avg["ms_scan"], avg["scan_blocks"] * blk + nq * 2048,
+        "front_kernel (prep + route + seed)": (avg["ms_route"], (avg["seed_blocks"] + (avg["scan_blocks"] if front_rest else 0)) * blk
+                                               + nq * (d * 4 + 2048) + ncell * 64,
+                                               "seed cells' FastScan blocks (and the rest cells' when the seed stage scans "
+                                               "them) + query f32 read + FastScan table written + the cell codes once"),
+        "cell_scan_kernel": (avg["ms_scan"], 0 if front_rest else avg["scan_blocks"] * blk + nq * 2048,
                              "probed cells' FastScan blocks per (query, cell) + the query table"),
         "finish_kernel": (avg["ms_rerank"], avg["rerank_rows"] * row_bytes,
                           "rerank rows gathered"),
