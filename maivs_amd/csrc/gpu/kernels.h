@@ -192,6 +192,68 @@ __device__ __forceinline__ void lut_sums(const Code<NW>& c, const uint8_t* table
     }
 }
 
+// One member's nibble sums against an 8-query interleaved FastScan table in LDS (table byte
+// x*8 + g = query g's entry x, x = position*16 + value). kWide: one 8-byte lookup serves queries
+// 0-7; otherwise a 4-byte lookup serves queries 0-3 (items of at most 4 queries). Each half
+// accumulates as in lut_sums: whole words S and the odd bytes T as u16 lanes, un-mixed at the end.
+template <int NW, bool kWide>
+__device__ __forceinline__ void lut_chunk8(uint32_t dw0, uint32_t dw1, uint32_t dw2, uint32_t dw3, int npos,
+                                           const uint8_t* tk, uint32_t& S0, uint32_t& T0, uint32_t& S1,
+                                           uint32_t& T1) {
+#pragma unroll
+    for (int t = 0; t < 32; ++t) {
+        if (t < npos) {
+            const uint32_t dw = t < 8 ? dw0 : t < 16 ? dw1 : t < 24 ? dw2 : dw3;
+            const uint32_t nib = (dw >> (4 * (t & 7))) & 0xFu;
+            if constexpr (kWide) {
+                const uint2 e = reinterpret_cast<const uint2*>(tk)[t * 16 + nib];
+                S0 += e.x;
+                T0 += __builtin_amdgcn_perm(0u, e.x, 0x0c030c01u);
+                S1 += e.y;
+                T1 += __builtin_amdgcn_perm(0u, e.y, 0x0c030c01u);
+                if ((t & 3) == 3) asm volatile("" : "+v"(S0), "+v"(T0), "+v"(S1), "+v"(T1));
+            } else {
+                const uint32_t e = reinterpret_cast<const uint32_t*>(tk)[2 * (t * 16 + nib)];
+                S0 += e;
+                T0 += __builtin_amdgcn_perm(0u, e, 0x0c030c01u);
+                if ((t & 7) == 7) asm volatile("" : "+v"(S0), "+v"(T0));
+            }
+        }
+    }
+}
+
+template <int NW, bool kWide>
+__device__ __forceinline__ void lut_sums8(const Code<NW>& c, const uint8_t* table, uint32_t (&sum)[8]) {
+    uint32_t S0 = 0, T0 = 0, S1 = 0, T1 = 0;
+    if constexpr (NW == 1) {
+        lut_chunk8<NW, kWide>(c.v[0].x, c.v[0].y, 0u, 0u, 16, table, S0, T0, S1, T1);
+    } else {
+        uint4 v[Code<NW>::NCH];
+#pragma unroll
+        for (int k = 0; k < Code<NW>::NCH; ++k) v[k] = c.v[k];
+#pragma unroll 1
+        for (int k = 0; k < Code<NW>::NCH; ++k) {
+            lut_chunk8<NW, kWide>(v[0].x, v[0].y, v[0].z, v[0].w, 32, table + static_cast<uint32_t>(k) * 32 * 16 * 8,
+                                  S0, T0, S1, T1);
+#pragma unroll
+            for (int r = 0; r + 1 < Code<NW>::NCH; ++r) v[r] = v[r + 1];  // rotate: chunk k+1 to the front
+        }
+    }
+    auto unmix = [](uint32_t S, uint32_t T, uint32_t* out) {
+        const uint32_t b1 = T & 0xFFFFu, b3 = T >> 16;
+        const uint32_t r = S - (b1 << 8) - (b3 << 24);
+        out[0] = r & 0xFFFFu;
+        out[1] = b1;
+        out[2] = r >> 16;
+        out[3] = b3;
+    };
+    unmix(S0, T0, sum);
+    if constexpr (kWide)
+        unmix(S1, T1, sum + 4);
+    else
+        sum[4] = sum[5] = sum[6] = sum[7] = 0;
+}
+
 // canonical(slot, c, probed) of src/index.rs:2036-2045: false when another home h < c of the
 // slot was probed by the query. With two homes the other home is precomputed per entry.
 __device__ __forceinline__ bool canonical(const DevArena& A, uint64_t e, uint32_t slot, uint32_t c,
@@ -1414,11 +1476,11 @@ __global__ void invert_fill_kernel(Work Wk, KParams K) {
 // chunk is loaded before the tables are built so both latencies overlap.
 template <int NW>
 __device__ __forceinline__ void scan_item(const DevArena& A, const Work& Wk, const KParams& K, uint32_t c, uint32_t e0,
-                                          uint32_t len, uint32_t nqi, uint8_t (*table)[kG * NW * 256],
-                                          const uint32_t* s_q, const uint32_t* s_t) {
+                                          uint32_t len, uint32_t nqi, uint8_t* table, const uint32_t* s_q,
+                                          const uint32_t* s_t) {
     constexpr uint32_t TB = NW * 256;
     const uint32_t tid = threadIdx.x, nt = blockDim.x;
-    const uint32_t ngroups = (nqi + kG - 1) / kG;
+    const bool wide = nqi > 4;
     struct Member {
         Code<NW> code;
         uint32_t slot, alt;
@@ -1439,17 +1501,29 @@ __device__ __forceinline__ void scan_item(const DevArena& A, const Work& Wk, con
     };
     Member m;
     load_member(0, m);
-    // interleave each group's tables: table[gi][x*4 + g] = lut_{4gi+g}[x] (4x4 byte transpose).
-    // A group's table words are all loaded before its first transpose: one round trip per group.
-    for (uint32_t gi = 0; gi < ngroups; ++gi) {
+    // interleave the item's tables: table[x*8 + g] = lut_g[x]. Per table dword x4 of the queries,
+    // two 4x4 byte transposes (queries 0-3 and 4-7) give the 8-byte entries of x = 4*x4 .. 4*x4+3;
+    // every word the thread needs is loaded before the first transpose (one round trip). Items of
+    // at most 4 queries fill only the low half of each entry, the part their lookups read.
+    {
         constexpr uint32_t X4 = (TB / 4 + kScanThreads - 1) / kScanThreads;
-        uint32_t v[X4][kG];
+        auto transpose = [](const uint32_t* w, uint32_t (&o)[4]) {
+            const uint32_t lo01 = __builtin_amdgcn_perm(w[1], w[0], 0x05010400u);
+            const uint32_t hi01 = __builtin_amdgcn_perm(w[1], w[0], 0x07030602u);
+            const uint32_t lo23 = __builtin_amdgcn_perm(w[3], w[2], 0x05010400u);
+            const uint32_t hi23 = __builtin_amdgcn_perm(w[3], w[2], 0x07030602u);
+            o[0] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
+            o[1] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);
+            o[2] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
+            o[3] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
+        };
+        uint32_t v[X4][kItemQ];
 #pragma unroll
         for (uint32_t xi = 0; xi < X4; ++xi)
 #pragma unroll
-            for (uint32_t g = 0; g < kG; ++g) {
-                const uint32_t x4 = tid + xi * nt, qq = s_q[gi * kG + g];
-                v[xi][g] = x4 < TB / 4 && qq != kNone
+            for (uint32_t g = 0; g < kItemQ; ++g) {
+                const uint32_t x4 = tid + xi * nt, qq = s_q[g];
+                v[xi][g] = x4 < TB / 4 && qq != kNone && (g < 4 || wide)
                                ? reinterpret_cast<const uint32_t*>(Wk.lut + static_cast<uint64_t>(qq) * TB)[x4]
                                : 0u;
             }
@@ -1457,17 +1531,12 @@ __device__ __forceinline__ void scan_item(const DevArena& A, const Work& Wk, con
         for (uint32_t xi = 0; xi < X4; ++xi) {
             const uint32_t x4 = tid + xi * nt;
             if (x4 >= TB / 4) continue;
-            const uint32_t* w = v[xi];
-            const uint32_t lo01 = __builtin_amdgcn_perm(w[1], w[0], 0x05010400u);
-            const uint32_t hi01 = __builtin_amdgcn_perm(w[1], w[0], 0x07030602u);
-            const uint32_t lo23 = __builtin_amdgcn_perm(w[3], w[2], 0x05010400u);
-            const uint32_t hi23 = __builtin_amdgcn_perm(w[3], w[2], 0x07030602u);
-            uint4 o;
-            o.x = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
-            o.y = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);
-            o.z = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
-            o.w = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
-            reinterpret_cast<uint4*>(table[gi])[x4] = o;
+            uint32_t lo[4], hi[4];
+            transpose(v[xi], lo);
+            transpose(v[xi] + 4, hi);
+            uint4* dst = reinterpret_cast<uint4*>(table + static_cast<size_t>(x4) * 32);
+            dst[0] = make_uint4(lo[0], hi[0], lo[1], hi[1]);
+            dst[1] = make_uint4(lo[2], hi[2], lo[3], hi[3]);
         }
     }
     __syncthreads();
@@ -1475,9 +1544,13 @@ __device__ __forceinline__ void scan_item(const DevArena& A, const Work& Wk, con
     for (uint32_t ebase = 0; ebase < len; ebase += nt) {
         if (ebase) load_member(ebase, m);
         const uint64_t e = static_cast<uint64_t>(e0) + min(ebase + tid, len - 1);
-        for (uint32_t gi = 0; gi < ngroups; ++gi) {
-            uint32_t sums[kG];
-            lut_sums<NW, kG>(m.code, table[gi], sums);
+        uint32_t sums[8];
+        if (wide)
+            lut_sums8<NW, true>(m.code, table, sums);
+        else
+            lut_sums8<NW, false>(m.code, table, sums);
+        // survivors, four queries at a time
+        for (uint32_t h = 0; h < (wide ? 2u : 1u); ++h) {
             bool pass[kG];
             uint32_t dv[kG];
             uint64_t bm[kG];
@@ -1487,9 +1560,9 @@ __device__ __forceinline__ void scan_item(const DevArena& A, const Work& Wk, con
             uint32_t pw[kG];
 #pragma unroll
             for (uint32_t g = 0; g < kG; ++g) {
-                const uint32_t qq = s_q[gi * kG + g];
-                dv[g] = A.maxk - sums[g];
-                under[g] = m.kept && qq != kNone && dv[g] <= s_t[gi * kG + g];
+                const uint32_t qq = s_q[h * kG + g];
+                dv[g] = A.maxk - (h ? sums[4 + g] : sums[g]);
+                under[g] = m.kept && qq != kNone && dv[g] <= s_t[h * kG + g];
                 pw[g] = 0;
                 if (A.ma == 2 && under[g] && m.alt < c)
                     pw[g] = Wk.probed[static_cast<uint64_t>(qq) * A.MW + (m.alt >> 5)];
@@ -1501,28 +1574,28 @@ __device__ __forceinline__ void scan_item(const DevArena& A, const Work& Wk, con
                     if (A.ma == 2)
                         pass[g] = !(m.alt < c && ((pw[g] >> (m.alt & 31)) & 1u));
                     else
-                        pass[g] = canonical(A, e, m.slot, c, Wk.probed + static_cast<uint64_t>(s_q[gi * kG + g]) * A.MW);
+                        pass[g] = canonical(A, e, m.slot, c, Wk.probed + static_cast<uint64_t>(s_q[h * kG + g]) * A.MW);
                 }
                 bm[g] = __ballot(pass[g]);
             }
-            // one atomic round for the group's queries: lane g reserves query g's slots
+            // one atomic round for the four queries: lane g reserves query g's slots
             if ((bm[0] | bm[1] | bm[2] | bm[3]) == 0) continue;
             uint32_t mine = 0;
 #pragma unroll
             for (uint32_t g = 0; g < kG; ++g)
                 if (lane == g) mine = static_cast<uint32_t>(__popcll(bm[g]));
             uint32_t wb = 0;
-            if (lane < kG && mine) wb = atomicAdd(&Wk.cand_cnt[s_q[gi * kG + lane]], mine);
+            if (lane < kG && mine) wb = atomicAdd(&Wk.cand_cnt[s_q[h * kG + lane]], mine);
 #pragma unroll
             for (uint32_t g = 0; g < kG; ++g) {
                 const uint32_t base = __shfl(wb, static_cast<int>(g), kWave);
                 const uint32_t pos = base + lanes_below(bm[g]);
                 if (pass[g] && pos < K.cand_cap)
-                    Wk.cand[static_cast<uint64_t>(s_q[gi * kG + g]) * K.cand_cap + pos] = make_uint2(dv[g], m.slot);
+                    Wk.cand[static_cast<uint64_t>(s_q[h * kG + g]) * K.cand_cap + pos] = make_uint2(dv[g], m.slot);
             }
         }
     }
-    __syncthreads();  // the tables and s_q / s_t are reused by the next item
+    __syncthreads();  // the table and s_q / s_t are reused by the next item
 }
 
 // The cell-major scan (src/index.rs:2231-2275). Bucket mode: each work item is one cell and up
@@ -1533,7 +1606,7 @@ template <int NW>
 __global__ void __launch_bounds__(kScanThreads, NW >= 16 ? 4 : 7)
 cell_scan_kernel(DevArena A, Work Wk, KParams K) {
     constexpr uint32_t TB = NW * 256;
-    __shared__ __align__(16) uint8_t table[kItemQ / kG][kG * TB];
+    __shared__ __align__(16) uint8_t table[kItemQ * TB];
     __shared__ uint32_t s_q[kItemQ], s_t[kItemQ];
     const uint32_t tid = threadIdx.x;
     if (K.bucket_cap) {
