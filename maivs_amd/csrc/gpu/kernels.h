@@ -1314,18 +1314,35 @@ __device__ __forceinline__ void seed_phase(const DevArena& A, const Work& Wk, co
         if (tid == 0) Wk.cand_cnt[qi] = misc[kCnt];
     }
     // ---- the query into each other rest cell's bucket (bucket mode), else probe counts for the
-    // counting-sort inversion
-    for (uint32_t i = r_in + tid; i < rest_end; i += nt) {
-        const uint32_t c = chosen[i];
-        const uint32_t slot = atomicAdd(&Wk.cell_cnt[c], 1u);
+    // counting-sort inversion. Every kItemQ-th query of a cell opens a lookup work item for those
+    // bucket entries, or, when the pass uses the matrix-core scan, every kBucketQ-th one a work
+    // item of kBucketQ entries; the openings take one list-counter atomic per wave.
+    const uint32_t per_item = K.mma_min ? kBucketQ : kItemQ;
+    uint32_t* const list = K.mma_min ? Wk.active : Wk.active8;
+    uint32_t* const list_n = K.mma_min ? &Wk.ctl->n_active : &Wk.ctl->n_active8;
+    for (uint32_t i0 = r_in; i0 < rest_end; i0 += nt) {
+        const uint32_t i = i0 + tid;
+        bool opens = false;
+        uint32_t c = 0, slot = 0;
+        if (i < rest_end) {
+            c = chosen[i];
+            slot = atomicAdd(&Wk.cell_cnt[c], 1u);
+            if (K.bucket_cap) {
+                opens = slot % per_item == 0 && slot < K.bucket_cap;
+                if (slot < K.bucket_cap)
+                    Wk.qbuck[static_cast<uint64_t>(c) * K.bucket_cap + slot] = qi;
+                else
+                    atomicOr(&Wk.ctl->bucket_overflow, 1u);
+            }
+        }
         if (K.bucket_cap) {
-            // every kItemQ-th query of a cell opens a scan work item for those bucket entries
-            if (slot % kItemQ == 0 && slot < K.bucket_cap)
-                Wk.active[atomicAdd(&Wk.ctl->n_active, 1u)] = c * kItemGroups + slot / kItemQ;
-            if (slot < K.bucket_cap)
-                Wk.qbuck[static_cast<uint64_t>(c) * K.bucket_cap + slot] = qi;
-            else
-                atomicOr(&Wk.ctl->bucket_overflow, 1u);
+            const uint64_t bm = __ballot(opens);
+            if (bm) {
+                uint32_t wb = 0;
+                if (lane_id() == 0) wb = atomicAdd(list_n, static_cast<uint32_t>(__popcll(bm)));
+                wb = __shfl(wb, 0, kWave);
+                if (opens) list[wb + lanes_below(bm)] = c * kItemGroups + slot / per_item;
+            }
         }
     }
     if (tid == 0) {
@@ -1599,9 +1616,10 @@ __device__ __forceinline__ void scan_item(const DevArena& A, const Work& Wk, con
 }
 
 // The cell-major scan (src/index.rs:2231-2275). Bucket mode: each work item is one cell and up
-// to kItemQ queries of its bucket, so a popular cell's items run in parallel workgroups; the grid
-// strides over the items. Counting-sort mode: workgroup c scans cell c for all its queries,
-// kItemQ at a time.
+// to kBucketQ queries of its bucket, so a popular cell's items run in parallel workgroups; the grid
+// strides over the items, and items of at least K.mma_min queries are left to cell_mma_kernel.
+// Counting-sort mode: workgroup c scans cell c for all its queries. Either way the lookups run
+// kItemQ queries at a time.
 template <int NW>
 __global__ void __launch_bounds__(kScanThreads, NW >= 16 ? 4 : 7)
 cell_scan_kernel(DevArena A, Work Wk, KParams K) {
@@ -1610,23 +1628,73 @@ cell_scan_kernel(DevArena A, Work Wk, KParams K) {
     __shared__ uint32_t s_q[kItemQ], s_t[kItemQ];
     const uint32_t tid = threadIdx.x;
     if (K.bucket_cap) {
-        const uint32_t items = Wk.ctl->n_active;
-        for (uint32_t b = blockIdx.x; b < items; b += gridDim.x) {
-            const uint32_t it = Wk.active[b];
-            const uint32_t c = it / kItemGroups, g0 = (it % kItemGroups) * kItemQ;
-            // the cell's range, its bucket count and the item's bucket entries, in one round:
-            // g0 + kItemQ <= bucket_cap (both multiples of kItemQ), so the entry reads stay in the bucket
-            const uint32_t e0 = A.mem_off[c], e1 = A.mem_off[c + 1];
-            const uint32_t cnt = min(Wk.cell_cnt[c], K.bucket_cap);
-            const uint32_t qv = tid < kItemQ ? Wk.qbuck[static_cast<uint64_t>(c) * K.bucket_cap + g0 + tid] : kNone;
-            const uint32_t nqi = min(kItemQ, cnt - g0);
-            if (tid < kItemQ) {
-                const bool ok = tid < nqi;
-                s_q[tid] = ok ? qv : kNone;
-                s_t[tid] = ok ? Wk.tau[qv] : 0u;
+        if (!K.mma_min) {
+            // every work item of kItemQ queries, grid-stride
+            const uint32_t items = Wk.ctl->n_active8;
+            for (uint32_t b = blockIdx.x; b < items; b += gridDim.x) {
+                const uint32_t it = Wk.active8[b];
+                const uint32_t c = it / kItemGroups, g0 = (it % kItemGroups) * kItemQ;
+                // the cell's range, its bucket count and the item's bucket entries, in one round:
+                // g0 + kItemQ <= bucket_cap (both multiples of kItemQ), so the entry reads stay in the bucket
+                const uint32_t e0 = A.mem_off[c], e1 = A.mem_off[c + 1];
+                const uint32_t cnt = min(Wk.cell_cnt[c], K.bucket_cap);
+                const uint32_t qv = tid < kItemQ ? Wk.qbuck[static_cast<uint64_t>(c) * K.bucket_cap + g0 + tid] : kNone;
+                const uint32_t nqi = min(kItemQ, cnt - g0);
+                if (tid < kItemQ) {
+                    const bool ok = tid < nqi;
+                    s_q[tid] = ok ? qv : kNone;
+                    s_t[tid] = ok ? Wk.tau[qv] : 0u;
+                }
+                __syncthreads();
+                scan_item<NW>(A, Wk, K, c, e0, e1 - e0, nqi, table, s_q, s_t);
             }
+            return;
+        }
+        // with the matrix-core scan: the kItemQ groups of the work items it leaves (fewer than
+        // K.mma_min queries), grid-stride over (item, group); the groups of one item run in
+        // parallel workgroups. A workgroup screens its next kScanThreads of them in one round of
+        // loads and keeps those it scans (groups past the item's count and items left to the
+        // matrix-core scan drop out), so a skipped group costs no round trip of its own.
+        constexpr uint32_t kSub = kBucketQ / kItemQ;
+        __shared__ uint32_t s_list[kScanThreads], s_nl;
+        const uint32_t n = Wk.ctl->n_active * kSub, lane = lane_id();
+        for (uint32_t base = blockIdx.x; base < n; base += gridDim.x * kScanThreads) {
+            const uint32_t v = base + tid * gridDim.x;
+            bool keep = false;
+            if (v < n) {
+                const uint32_t it = Wk.active[v / kSub], s0 = (v % kSub) * kItemQ;
+                const uint32_t c = it / kItemGroups, g0 = (it % kItemGroups) * kBucketQ;
+                const uint32_t nb = min(kBucketQ, min(Wk.cell_cnt[c], K.bucket_cap) - g0);
+                keep = s0 < nb && !(K.mma_min && nb >= K.mma_min);
+            }
+            if (tid == 0) s_nl = 0;
             __syncthreads();
-            scan_item<NW>(A, Wk, K, c, e0, e1 - e0, nqi, table, s_q, s_t);
+            const uint64_t bm = __ballot(keep);
+            uint32_t wb = 0;
+            if (lane == 0 && bm) wb = atomicAdd(&s_nl, static_cast<uint32_t>(__popcll(bm)));
+            wb = __shfl(wb, 0, kWave);
+            if (keep) s_list[wb + lanes_below(bm)] = v;
+            __syncthreads();
+            const uint32_t nl = s_nl;
+            for (uint32_t k = 0; k < nl; ++k) {
+                const uint32_t vk = s_list[k];
+                const uint32_t it = Wk.active[vk / kSub], s0 = (vk % kSub) * kItemQ;
+                const uint32_t c = it / kItemGroups, g0 = (it % kItemGroups) * kBucketQ;
+                // the cell's range, its bucket count and the group's bucket entries, in one round:
+                // g0 + kBucketQ <= bucket_cap (both multiples of kBucketQ), so the entry reads stay in the bucket
+                const uint32_t e0 = A.mem_off[c], e1 = A.mem_off[c + 1];
+                const uint32_t cnt = min(Wk.cell_cnt[c], K.bucket_cap);
+                const uint32_t qv = tid < kItemQ ? Wk.qbuck[static_cast<uint64_t>(c) * K.bucket_cap + g0 + s0 + tid] : kNone;
+                const uint32_t nqi = min(kItemQ, min(kBucketQ, cnt - g0) - s0);
+                if (tid < kItemQ) {
+                    const bool ok = tid < nqi;
+                    s_q[tid] = ok ? qv : kNone;
+                    s_t[tid] = ok ? Wk.tau[qv] : 0u;
+                }
+                __syncthreads();
+                scan_item<NW>(A, Wk, K, c, e0, e1 - e0, nqi, table, s_q, s_t);
+            }
+            __syncthreads();  // s_list / s_nl are rewritten by the next batch
         }
     } else {
         const uint32_t c = blockIdx.x;
@@ -1645,6 +1713,205 @@ cell_scan_kernel(DevArena A, Work Wk, KParams K) {
             __syncthreads();
             scan_item<NW>(A, Wk, K, c, e0, len, nqi, table, s_q, s_t);
         }
+    }
+}
+
+// ---------------------------------------------------------------- cell-major scan, matrix cores
+
+typedef int mma_v4 __attribute__((ext_vector_type(4)));
+typedef int mma_v16 __attribute__((ext_vector_type(16)));
+
+// The cell-major scan of bucket work items with many queries (at least K.mma_min of kBucketQ) on
+// the matrix cores. A member's FastScan sum is an integer dot product,
+//   sum_p lut_p[n_p] = sum_p onehot(n_p) . (lut_p - 128) + 128 * npos,
+// with onehot(n) the 16 bytes whose byte n is 1, so v_mfma_i32_32x32x32_i8 over K = 16 * npos
+// gives exactly the integers of the table lookups (|partial sums| <= 128 * npos). Operands of
+// one 32x32x32 step (two positions): A row i = member i of a 32-member tile, B column j = query j
+// of the item; lanes i + 32g and j + 32g hold the 16 values of position 2s + g. Result register r
+// of lane l is member 8(r/4) + 4(l/32) + r%4, query l%32.
+// The four waves split K: wave w takes positions [w, w+1) * npos/4 and holds that quarter of the
+// item's 32 tables in registers for the whole item; per tile the partial sums meet in LDS and wave
+// w finishes members 8w .. 8w+7 for every query. Members with d <= tau go to an LDS queue that is
+// settled (keep!, exactly-once, one append per query) at the item's end, or earlier when it could
+// not take another tile, so these global round trips are paid per item, not per tile.
+constexpr uint32_t kMmaQueue = kBucketQ * 32;  // one tile's worst case of (member, d | query << 16)
+
+template <int NW>
+__global__ void __launch_bounds__(kScanThreads, NW >= 16 ? 2 : 4)
+cell_mma_kernel(DevArena A, Work Wk, KParams K) {
+    constexpr uint32_t TB = NW * 256;               // table bytes per query, 16 per position
+    constexpr uint32_t NPOS = NW * 16;
+    constexpr uint32_t SPW = NPOS / 8;              // 32x32x32 steps per wave, two positions each
+    constexpr uint32_t CDW = NW >= 2 ? NW / 2 : 1;  // code dwords one wave reads per member
+    constexpr uint32_t PER = kMmaQueue / kScanThreads;
+    __shared__ uint32_t red[4][16][kWave];          // partial sums of one tile, by wave
+    __shared__ uint2 queue[kMmaQueue];
+    __shared__ uint32_t s_q[kBucketQ], s_t[kBucketQ], s_cnt[kBucketQ], s_base[kBucketQ], s_tot[4];
+    const uint32_t tid = threadIdx.x, lane = lane_id(), w = tid / kWave;
+    const uint32_t g = lane >> 5, j = lane & 31;
+    const uint32_t dw_lo = (w * SPW) >> 2;          // first code dword of this wave's positions
+    if (tid < kBucketQ) s_cnt[tid] = 0;
+    // keep!, exactly-once and the appends of the n queued survivors of cell c; every thread calls
+    // it after a barrier that follows the last queue write, and it ends with a barrier
+    auto settle = [&](uint32_t n, uint32_t c, uint32_t e0) {
+        uint32_t slot[PER], dq[PER], off[PER];
+#pragma unroll
+        for (uint32_t k = 0; k < PER; ++k) {
+            const uint32_t i = tid + k * kScanThreads;
+            bool ok = i < n;
+            const uint2 qe = ok ? queue[i] : make_uint2(0u, 0u);
+            const uint64_t e = static_cast<uint64_t>(e0) + qe.x;
+            dq[k] = qe.y;
+            slot[k] = ok ? A.members[e] : 0u;
+            if (K.filter && ok) {
+                const uint32_t tg = A.entry_tag[e];
+                ok = tg >= K.tag_lo && tg <= K.tag_hi;
+            }
+            off[k] = !ok ? kNone : A.ma == 2 ? A.entry_alt[e] : qe.x;  // the other home, or the member
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < PER; ++k) {
+            if (off[k] == kNone) continue;
+            const uint32_t qv = s_q[dq[k] >> 16];
+            bool ok;
+            if (A.ma == 2) {
+                const uint32_t alt = off[k];
+                ok = !(alt < c && ((Wk.probed[static_cast<uint64_t>(qv) * A.MW + (alt >> 5)] >> (alt & 31)) & 1u));
+            } else {
+                ok = canonical(A, static_cast<uint64_t>(e0) + off[k], slot[k], c, Wk.probed + static_cast<uint64_t>(qv) * A.MW);
+            }
+            off[k] = ok ? atomicAdd(&s_cnt[dq[k] >> 16], 1u) : kNone;  // rank within the query's appends
+        }
+        __syncthreads();
+        if (tid < kBucketQ) {
+            const uint32_t m = s_cnt[tid];
+            s_base[tid] = m ? atomicAdd(&Wk.cand_cnt[s_q[tid]], m) : 0u;
+            s_cnt[tid] = 0;
+        }
+        __syncthreads();
+#pragma unroll
+        for (uint32_t k = 0; k < PER; ++k) {
+            if (off[k] == kNone) continue;
+            const uint32_t jj = dq[k] >> 16, pos = s_base[jj] + off[k];
+            if (pos < K.cand_cap) Wk.cand[static_cast<uint64_t>(s_q[jj]) * K.cand_cap + pos] = make_uint2(dq[k] & 0xFFFFu, slot[k]);
+        }
+        __syncthreads();
+    };
+    const uint32_t items = Wk.ctl->n_active;
+    for (uint32_t b = blockIdx.x; b < items; b += gridDim.x) {
+        const uint32_t it = Wk.active[b];
+        const uint32_t c = it / kItemGroups, g0 = (it % kItemGroups) * kBucketQ;
+        const uint32_t cnt = min(Wk.cell_cnt[c], K.bucket_cap);
+        const uint32_t nqi = min(kBucketQ, cnt - g0);
+        if (nqi < K.mma_min) continue;
+        const uint32_t e0 = A.mem_off[c], len = A.mem_off[c + 1] - e0;
+        if (tid < kBucketQ) {
+            const bool ok = tid < nqi;
+            const uint32_t qv = ok ? Wk.qbuck[static_cast<uint64_t>(c) * K.bucket_cap + g0 + tid] : kNone;
+            s_q[tid] = qv;
+            s_t[tid] = ok ? Wk.tau[qv] : 0u;
+        }
+        __syncthreads();
+        const uint32_t qj = s_q[j], tj = s_t[j];
+        // this wave's code dwords of member t*32 + j (zero past the cell's end)
+        auto load_codes = [&](uint32_t t, uint32_t (&dw)[CDW]) {
+            const uint32_t mi = t * 32 + j;
+            const uint32_t* src = A.codes + static_cast<uint64_t>(e0 + (mi < len ? mi : 0u)) * (2 * NW) + dw_lo;
+            if constexpr (CDW % 4 == 0) {
+#pragma unroll
+                for (uint32_t k = 0; k < CDW; k += 4) {
+                    const uint4 v = reinterpret_cast<const uint4*>(src)[k / 4];
+                    dw[k] = v.x;
+                    dw[k + 1] = v.y;
+                    dw[k + 2] = v.z;
+                    dw[k + 3] = v.w;
+                }
+            } else {
+#pragma unroll
+                for (uint32_t k = 0; k < CDW; ++k) dw[k] = src[k];
+            }
+            if (mi >= len) {
+#pragma unroll
+                for (uint32_t k = 0; k < CDW; ++k) dw[k] = 0u;
+            }
+        };
+        const uint32_t ntile = (len + 31) / 32;
+        uint32_t cur[CDW], nx1[CDW], nx2[CDW];
+        load_codes(0, cur);
+        if (ntile > 1) load_codes(1, nx1);
+        // B operands: this wave's quarter of query j's table, 128 subtracted from every byte
+        mma_v4 bq[SPW];
+        {
+            const uint4* lut = reinterpret_cast<const uint4*>(Wk.lut + static_cast<uint64_t>(qj != kNone ? qj : 0u) * TB);
+#pragma unroll
+            for (uint32_t s = 0; s < SPW; ++s) {
+                const uint4 v = qj != kNone ? lut[2 * (w * SPW + s) + g] : make_uint4(0u, 0u, 0u, 0u);
+                bq[s] = mma_v4{static_cast<int>(v.x ^ 0x80808080u), static_cast<int>(v.y ^ 0x80808080u),
+                               static_cast<int>(v.z ^ 0x80808080u), static_cast<int>(v.w ^ 0x80808080u)};
+            }
+        }
+        uint32_t n = 0;  // queued survivors (the same in every thread)
+        for (uint32_t t = 0; t < ntile; ++t) {
+            if (t + 2 < ntile) load_codes(t + 2, nx2);
+            // nibble * 8 of each of this lane's positions, one per byte
+            uint32_t cw8[CDW];
+#pragma unroll
+            for (uint32_t k = 0; k < CDW; ++k) cw8[k] = ((cur[k] >> (4 * g)) & 0x0F0F0F0Fu) << 3;
+            mma_v16 acc = {};
+#pragma unroll
+            for (uint32_t s = 0; s < SPW; ++s) {
+                const uint32_t sub = NW >= 2 ? (s & 3) : ((w * SPW + s) & 3);
+                const uint32_t ld = NW >= 2 ? (s >> 2) : 0u;
+                const uint32_t n8 = (cw8[ld] >> (8 * sub)) & 0xFFu;  // 8 * nibble
+                const uint32_t hb = n8 >> 6;                          // nibble >= 8
+                const uint64_t lo = static_cast<uint64_t>(hb ^ 1u) << (n8 & 63u);
+                const uint64_t hi = static_cast<uint64_t>(hb) << (n8 & 63u);
+                const mma_v4 a = {static_cast<int>(static_cast<uint32_t>(lo)), static_cast<int>(static_cast<uint32_t>(lo >> 32)),
+                                  static_cast<int>(static_cast<uint32_t>(hi)), static_cast<int>(static_cast<uint32_t>(hi >> 32))};
+                acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bq[s], acc, 0, 0, 0);
+            }
+            __syncthreads();  // the previous tile's partial sums and survivor counts are read
+#pragma unroll
+            for (uint32_t r = 0; r < 16; ++r) red[w][r][lane] = static_cast<uint32_t>(acc[r]);
+            __syncthreads();
+            // registers 4w .. 4w+3 of every wave: members 8w + 4g + rr of the tile, query j
+            uint64_t bm[4];
+            uint32_t dv[4], total = 0;
+#pragma unroll
+            for (uint32_t rr = 0; rr < 4; ++rr) {
+                const uint32_t r = 4 * w + rr;
+                const uint32_t tot = red[0][r][lane] + red[1][r][lane] + red[2][r][lane] + red[3][r][lane] + 128u * NPOS;
+                const uint32_t mi = t * 32 + 8 * w + 4 * g + rr;
+                dv[rr] = A.maxk - tot;
+                bm[rr] = __ballot(mi < len && qj != kNone && dv[rr] <= tj);
+                total += static_cast<uint32_t>(__popcll(bm[rr]));
+            }
+            if (lane == 0) s_tot[w] = total;
+            __syncthreads();
+            const uint32_t t0 = s_tot[0], t1 = s_tot[1], t2 = s_tot[2], t3 = s_tot[3];
+            if (n + t0 + t1 + t2 + t3 > kMmaQueue) {
+                settle(n, c, e0);
+                n = 0;
+            }
+            if (total) {
+                uint32_t base = n + (w > 0 ? t0 : 0u) + (w > 1 ? t1 : 0u) + (w > 2 ? t2 : 0u);
+#pragma unroll
+                for (uint32_t rr = 0; rr < 4; ++rr) {
+                    if ((bm[rr] >> lane) & 1u)
+                        queue[base + lanes_below(bm[rr])] = make_uint2(t * 32 + 8 * w + 4 * g + rr, dv[rr] | (j << 16));
+                    base += static_cast<uint32_t>(__popcll(bm[rr]));
+                }
+            }
+            n += t0 + t1 + t2 + t3;
+#pragma unroll
+            for (uint32_t k = 0; k < CDW; ++k) {
+                cur[k] = nx1[k];
+                nx1[k] = nx2[k];
+            }
+        }
+        __syncthreads();  // the last tile's queue entries are written
+        if (n) settle(n, c, e0);
+        else __syncthreads();  // s_q / s_t are rewritten by the next item
     }
 }
 

@@ -39,6 +39,8 @@ namespace {
 constexpr float kPruneBand = 4e-6f;
 constexpr float kNucleusBand = 2e-3f;
 constexpr size_t kLdsBudget = 160 * 1024;
+constexpr uint32_t kMmaMinQ = 12;      // least queries of a matrix-core scan work item (of kBucketQ)
+constexpr double kMmaShare = 32.0;     // ... used when the cell-major scan averages this many queries per cell
 constexpr uint32_t kScanGridMax = 16384;  // workgroups of the bucket-mode scan (they stride over the items)
 }  // namespace
 
@@ -177,8 +179,9 @@ int ensure_work(maivs_gpu_ctx* ctx, uint32_t nq, uint32_t nprobe, uint32_t k) {
     rc |= dalloc(ctx, o, &W.qof, nql * nprobe);
     const uint32_t bcap_all = std::max(bcap, ctx->cap_bucket);
     rc |= dalloc(ctx, o, &W.qbuck, static_cast<uint64_t>(A.M) * bcap_all);
-    // scan work items: at most one per kItemQ bucket entries plus one per cell
-    rc |= dalloc(ctx, o, &W.active, static_cast<uint64_t>(A.M) + nql * nprobe / kItemQ + 1);
+    // scan work items: at most one per kBucketQ (kItemQ) bucket entries plus one per cell
+    rc |= dalloc(ctx, o, &W.active, static_cast<uint64_t>(A.M) + nql * nprobe / kBucketQ + 1);
+    rc |= dalloc(ctx, o, &W.active8, static_cast<uint64_t>(A.M) + nql * nprobe / kItemQ + 1);
     rc |= dalloc(ctx, o, &W.flag_route, nql);
     rc |= dalloc(ctx, o, &W.flag_prune, nql);
     rc |= dalloc(ctx, o, &W.ctl, 1);
@@ -259,6 +262,12 @@ KParams make_params(maivs_gpu_ctx* ctx, uint32_t nq, const maivs_search_params* 
         const bool front = p->nprobe <= kSeedCells + kFrontRestMax && per_cell < kFrontRestShare;
         K.front_rest = ctx->front_rest_mode >= 0 ? static_cast<uint32_t>(std::min<int>(ctx->front_rest_mode, kFrontRestMax))
                                                  : (front ? kFrontRestMax : 0u);
+        // work items of at least mma_min queries run on the matrix cores, when cells gather
+        // enough queries of the batch for such items to be common
+        const double scan_rest = p->nprobe > kSeedCells + K.front_rest ? static_cast<double>(p->nprobe - kSeedCells - K.front_rest) : 0.0;
+        const double scan_per_cell = static_cast<double>(nq) * scan_rest / std::max<uint32_t>(A.n_live, 1u);
+        K.mma_min = ctx->mma_min_mode >= 0 ? static_cast<uint32_t>(std::min<int>(ctx->mma_min_mode, kBucketQ))
+                                           : (scan_per_cell >= kMmaShare ? kMmaMinQ : 0u);
     }
     K.cand_cap = ctx->cap_cand;
     K.fin_cap = ctx->cap_fin;
@@ -399,11 +408,19 @@ int launch_scan(maivs_gpu_ctx* ctx, const KParams& K, bool recount, bool events 
     }
     if (events) HIP_TRY(ctx, hipEventRecord(ctx->ev[4], ctx->stream));
     // bucket mode: a grid that strides over the work items (their count is on the device)
-    const uint64_t items = static_cast<uint64_t>(A.M) + static_cast<uint64_t>(K.nq) * K.nprobe / kItemQ + 1;
+    const uint64_t items = static_cast<uint64_t>(A.M) + static_cast<uint64_t>(K.nq) * K.nprobe / kBucketQ + 1;
     const uint32_t grid = K.bucket_cap ? static_cast<uint32_t>(std::min<uint64_t>(items, kScanGridMax)) : A.M;
-    DISPATCH_NW(A.W, hipLaunchKernelGGL(cell_scan_kernel<NW>, dim3(std::max(grid, 1u)), dim3(kScanThreads), 0,
+    const uint64_t items8 = static_cast<uint64_t>(A.M) + static_cast<uint64_t>(K.nq) * K.nprobe / kItemQ + 1;
+    const uint32_t sgrid = K.bucket_cap ? static_cast<uint32_t>(std::min<uint64_t>(items8, kScanGridMax)) : A.M;
+    DISPATCH_NW(A.W, hipLaunchKernelGGL(cell_scan_kernel<NW>, dim3(std::max(sgrid, 1u)), dim3(kScanThreads), 0,
                                         ctx->stream, A, W, K));
     HIP_TRY(ctx, hipGetLastError());
+    // the items with many queries, on the matrix cores
+    if (K.bucket_cap && K.mma_min) {
+        DISPATCH_NW(A.W, hipLaunchKernelGGL(cell_mma_kernel<NW>, dim3(std::max(grid, 1u)), dim3(kScanThreads), 0,
+                                            ctx->stream, A, W, K));
+        HIP_TRY(ctx, hipGetLastError());
+    }
     return 0;
 }
 
@@ -412,6 +429,7 @@ int launch_scan(maivs_gpu_ctx* ctx, const KParams& K, bool recount, bool events 
 KParams csr(KParams K) {
     K.bucket_cap = 0;
     K.front_rest = 0;
+    K.mma_min = 0;
     return K;
 }
 
@@ -882,6 +900,8 @@ int maivs_gpu_create(int device, maivs_gpu_ctx** out) {
     if (const char* c = std::getenv("MAIVS_GPU_CAND_CAP")) ctx->initial_cand_cap = std::max(16, std::atoi(c));
     // the seed stage's own rest scan: unset = by cell sharing, else a fixed count of ranks (0 or 8)
     if (const char* f = std::getenv("MAIVS_GPU_FRONT_REST")) ctx->front_rest_mode = std::max(0, std::atoi(f));
+    // the matrix-core scan: unset = by cell sharing, 0 = off, else the least queries of its work items
+    if (const char* m = std::getenv("MAIVS_GPU_MMA_MIN")) ctx->mma_min_mode = std::max(0, std::atoi(m));
     if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
         delete ctx;
         return MAIVS_ERR_HIP;

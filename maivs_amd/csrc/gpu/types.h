@@ -22,6 +22,7 @@ constexpr uint32_t kScanThreads = 256;
 constexpr uint32_t kFinishThreads = 256;
 constexpr uint32_t kG = 4;               // queries interleaved per cell_scan table pass
 constexpr uint32_t kItemQ = 2 * kG;      // queries per scan work item (two interleaved tables)
+constexpr uint32_t kBucketQ = 32;       // bucket entries per scan work item (one matrix-core query tile)
 constexpr uint32_t kItemGroups = 1024;   // work items per cell in a scan work item id (bucket_cap <= 4096)
 constexpr uint32_t kHistBins = 256;
 constexpr uint32_t kFinishLdsCap = 2048; // final candidates kept and sorted in LDS up to this many
@@ -68,7 +69,8 @@ struct Ctl {
     uint32_t max_shortlist;
     uint32_t err_seed;        // a seed set exceeded its on-chip capacity
     uint32_t bucket_overflow; // a cell's query bucket was full (the pass falls back to the counting sort)
-    uint32_t n_active;        // scan work items: (cell, group of kG bucket entries) (bucket mode)
+    uint32_t n_active;        // scan work items: (cell, block of kBucketQ bucket entries) (bucket mode)
+    uint32_t n_active8;       // the same by groups of kItemQ bucket entries (the lookup scan's items)
     uint32_t pq_overflow;     // per-query path: largest candidate count past its buffer (0 = none)
     unsigned long long seed_blocks, scan_blocks, scan_pairs, survivors, rerank_rows;
 };
@@ -118,7 +120,8 @@ struct Work {
     uint32_t* cell_cur;    // M
     uint32_t* qof;         // nq x nprobe
     uint32_t* qbuck;       // M x bucket_cap: the queries probing each cell (bucket mode)
-    uint32_t* active;      // scan work items, cell * kItemGroups + group, in arrival order (bucket mode)
+    uint32_t* active;      // scan work items, cell * kItemGroups + group of kBucketQ, in arrival order (bucket mode)
+    uint32_t* active8;     // the same by groups of kItemQ (cell * kItemGroups + group)
     uint32_t* flag_route;  // nq
     uint32_t* flag_prune;  // nq
     // per-query path
@@ -137,6 +140,8 @@ struct KParams {
     uint32_t tree_list, bnd_from, tcap, pq_cap, pq_room, pq_noflag;
     // batched path: rest cells (probe ranks SEED_CELLS on) the seed stage scans itself, query-major
     uint32_t front_rest;
+    // bucket work items with at least this many queries go to the matrix-core scan (0: none)
+    uint32_t mma_min;
     float tc, beta, at_margin, norm, prune_band, nucleus_band;
 };
 

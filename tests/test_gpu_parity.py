@@ -292,6 +292,28 @@ def test_global_hamming_rows_match_oracle(ctx, cells9k, mix50k, nprobe):
     _compare_search(ctx, ix, queries, p, gt)
 
 
+@pytest.mark.parametrize("mode", ["1", "0"])
+def test_scan_paths_match_oracle(quality50k, memory50k, churn50k, mix50k, monkeypatch, mode):
+    """The cell-major scan with every bucket work item on the matrix cores (MAIVS_GPU_MMA_MIN=1:
+    one-hot int8 products, even for items of one query) or every item on the table lookups (0):
+    both bit-exact with the oracle, for both presets and with the tag filter."""
+    monkeypatch.setenv("MAIVS_GPU_MMA_MIN", mode)
+    _, queries, gt = mix50k
+    c = capi.Context(0)
+    try:
+        for nprobe in (24, 64):
+            _compare_search(c, quality50k, queries, _params(quality50k, 10, nprobe), gt)
+        _compare_search(c, memory50k, queries, _params(memory50k, 10, 40), gt)
+        ix, _, _ = churn50k
+        ix.set_filter(0, 99)
+        try:
+            _compare_search(c, ix, queries, _params(ix, 10, 64))
+        finally:
+            ix.set_filter()
+    finally:
+        c.close()
+
+
 def test_candidate_overflow_regrows(quality50k, mix50k, monkeypatch):
     """A candidate buffer of 16 per query overflows: the pass's end reports the largest count
     through the control block's host mirror, the buffer grows to it and the scan re-runs; the
