@@ -269,6 +269,10 @@ def main() -> int:
     # over the batch, the seed stage scans every rest cell itself and the cell scan is not launched.
     n_live = int((np.diff(ix._arena_arrays()["mem_off"]) > 0).sum())  # live cells
     front_rest = npb <= 16 and nq * max(npb - 8, 0) / max(n_live, 1) < 8
+    # ... and with at least 32 cell-major scan queries per live cell on average, work items of 32
+    # queries of a cell run on the matrix cores (cell_mma_kernel) beside the lookup scan
+    mma = nq * max(npb - 8 - (8 if front_rest else 0), 0) / max(n_live, 1) >= 32
+    scan_name = "cell_scan_kernel + cell_mma_kernel" if mma else "cell_scan_kernel"
     d = base.shape[1]
     row_bytes = d * 4 if args.profile == "quality" else d
     blk = 2048  # one 32-vector FastScan block of 64-byte codes
@@ -284,7 +288,7 @@ def main() -> int:
                                                + nq * (d * 4 + 2048) + ncell * 64,
                                                "seed cells' FastScan blocks (and the rest cells' when the seed stage scans "
                                                "them) + query f32 read + FastScan table written + the cell codes once"),
-        "cell_scan_kernel": (avg["ms_scan"], 0 if front_rest else avg["scan_blocks"] * blk + nq * 2048,
+        scan_name: (avg["ms_scan"], 0 if front_rest else avg["scan_blocks"] * blk + nq * 2048,
                              "probed cells' FastScan blocks per (query, cell) + the query table"),
         "finish_kernel": (avg["ms_rerank"], avg["rerank_rows"] * row_bytes,
                           "rerank rows gathered"),
