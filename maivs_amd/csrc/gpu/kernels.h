@@ -1746,7 +1746,7 @@ cell_mma_kernel(DevArena A, Work Wk, KParams K) {
     constexpr uint32_t PER = kMmaQueue / kScanThreads;
     __shared__ uint32_t red[4][16][kWave];          // partial sums of one tile, by wave
     __shared__ uint2 queue[kMmaQueue];
-    __shared__ uint32_t s_q[kBucketQ], s_t[kBucketQ], s_cnt[kBucketQ], s_base[kBucketQ], s_tot[4];
+    __shared__ uint32_t s_q[kBucketQ], s_cnt[kBucketQ], s_base[kBucketQ], s_tot[4];
     const uint32_t tid = threadIdx.x, lane = lane_id(), w = tid / kWave;
     const uint32_t g = lane >> 5, j = lane & 31;
     const uint32_t dw_lo = (w * SPW) >> 2;          // first code dword of this wave's positions
@@ -1798,21 +1798,31 @@ cell_mma_kernel(DevArena A, Work Wk, KParams K) {
         __syncthreads();
     };
     const uint32_t items = Wk.ctl->n_active;
+    uint32_t itn = blockIdx.x < items ? Wk.active[blockIdx.x] : 0u;  // the next item's id, one item ahead
     for (uint32_t b = blockIdx.x; b < items; b += gridDim.x) {
-        const uint32_t it = Wk.active[b];
+        const uint32_t it = itn;
+        if (b + gridDim.x < items) itn = Wk.active[b + gridDim.x];
         const uint32_t c = it / kItemGroups, g0 = (it % kItemGroups) * kBucketQ;
         const uint32_t cnt = min(Wk.cell_cnt[c], K.bucket_cap);
         const uint32_t nqi = min(kBucketQ, cnt - g0);
         if (nqi < K.mma_min) continue;
         const uint32_t e0 = A.mem_off[c], len = A.mem_off[c + 1] - e0;
-        if (tid < kBucketQ) {
-            const bool ok = tid < nqi;
-            const uint32_t qv = ok ? Wk.qbuck[static_cast<uint64_t>(c) * K.bucket_cap + g0 + tid] : kNone;
-            s_q[tid] = qv;
-            s_t[tid] = ok ? Wk.tau[qv] : 0u;
+        // every wave reads the item's bucket entries itself (lane j: query j), so its table loads
+        // follow the bucket read directly; wave 0 also publishes them for the settle
+        const uint32_t qj = j < nqi ? Wk.qbuck[static_cast<uint64_t>(c) * K.bucket_cap + g0 + j] : kNone;
+        // B operands: this wave's quarter of query j's table, 128 subtracted from every byte
+        mma_v4 bq[SPW];
+        {
+            const uint4* lut = reinterpret_cast<const uint4*>(Wk.lut + static_cast<uint64_t>(qj != kNone ? qj : 0u) * TB);
+#pragma unroll
+            for (uint32_t s = 0; s < SPW; ++s) {
+                const uint4 v = qj != kNone ? lut[2 * (w * SPW + s) + g] : make_uint4(0u, 0u, 0u, 0u);
+                bq[s] = mma_v4{static_cast<int>(v.x ^ 0x80808080u), static_cast<int>(v.y ^ 0x80808080u),
+                               static_cast<int>(v.z ^ 0x80808080u), static_cast<int>(v.w ^ 0x80808080u)};
+            }
         }
-        __syncthreads();
-        const uint32_t qj = s_q[j], tj = s_t[j];
+        const uint32_t tj = qj != kNone ? Wk.tau[qj] : 0u;
+        if (tid < kBucketQ) s_q[tid] = qj;
         // this wave's code dwords of member t*32 + j (zero past the cell's end)
         auto load_codes = [&](uint32_t t, uint32_t (&dw)[CDW]) {
             const uint32_t mi = t * 32 + j;
@@ -1839,17 +1849,6 @@ cell_mma_kernel(DevArena A, Work Wk, KParams K) {
         uint32_t cur[CDW], nx1[CDW], nx2[CDW];
         load_codes(0, cur);
         if (ntile > 1) load_codes(1, nx1);
-        // B operands: this wave's quarter of query j's table, 128 subtracted from every byte
-        mma_v4 bq[SPW];
-        {
-            const uint4* lut = reinterpret_cast<const uint4*>(Wk.lut + static_cast<uint64_t>(qj != kNone ? qj : 0u) * TB);
-#pragma unroll
-            for (uint32_t s = 0; s < SPW; ++s) {
-                const uint4 v = qj != kNone ? lut[2 * (w * SPW + s) + g] : make_uint4(0u, 0u, 0u, 0u);
-                bq[s] = mma_v4{static_cast<int>(v.x ^ 0x80808080u), static_cast<int>(v.y ^ 0x80808080u),
-                               static_cast<int>(v.z ^ 0x80808080u), static_cast<int>(v.w ^ 0x80808080u)};
-            }
-        }
         uint32_t n = 0;  // queued survivors (the same in every thread)
         for (uint32_t t = 0; t < ntile; ++t) {
             if (t + 2 < ntile) load_codes(t + 2, nx2);
@@ -1911,7 +1910,7 @@ cell_mma_kernel(DevArena A, Work Wk, KParams K) {
         }
         __syncthreads();  // the last tile's queue entries are written
         if (n) settle(n, c, e0);
-        else __syncthreads();  // s_q / s_t are rewritten by the next item
+        else __syncthreads();  // s_q is rewritten by the next item
     }
 }
 
