@@ -269,10 +269,10 @@ def main() -> int:
     # over the batch, the seed stage scans every rest cell itself and the cell scan is not launched.
     n_live = int((np.diff(ix._arena_arrays()["mem_off"]) > 0).sum())  # live cells
     front_rest = npb <= 16 and nq * max(npb - 8, 0) / max(n_live, 1) < 8
-    # ... and with at least 32 cell-major scan queries per live cell on average, work items of 32
-    # queries of a cell run on the matrix cores (cell_mma_kernel) beside the lookup scan
-    mma = nq * max(npb - 8 - (8 if front_rest else 0), 0) / max(n_live, 1) >= 32
-    scan_name = "cell_scan_kernel + cell_mma_kernel" if mma else "cell_scan_kernel"
+    # ... and with at least 16 cell-major scan queries per live cell on average, the work items (a
+    # cell and up to 32 of its queries) run on the matrix cores (cell_mma_kernel) instead
+    mma = nq * max(npb - 8 - (8 if front_rest else 0), 0) / max(n_live, 1) >= 16
+    scan_name = "cell_mma_kernel" if mma else "cell_scan_kernel"
     d = base.shape[1]
     row_bytes = d * 4 if args.profile == "quality" else d
     blk = 2048  # one 32-vector FastScan block of 64-byte codes

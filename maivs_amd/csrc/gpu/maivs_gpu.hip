@@ -39,8 +39,11 @@ namespace {
 constexpr float kPruneBand = 4e-6f;
 constexpr float kNucleusBand = 2e-3f;
 constexpr size_t kLdsBudget = 160 * 1024;
-constexpr uint32_t kMmaMinQ = 12;      // least queries of a matrix-core scan work item (of kBucketQ)
-constexpr double kMmaShare = 32.0;     // ... used when the cell-major scan averages this many queries per cell
+// The matrix-core scan takes every bucket work item (of up to kBucketQ queries) when the
+// cell-major scan averages at least kMmaShare queries per live cell; below that the lookups win
+// (measured on the 500k mixture: lookups ahead at 12 queries per cell, matrix cores at 20 and up).
+constexpr uint32_t kMmaMinQ = 1;
+constexpr double kMmaShare = 16.0;
 constexpr uint32_t kScanGridMax = 16384;  // workgroups of the bucket-mode scan (they stride over the items)
 }  // namespace
 
@@ -412,9 +415,12 @@ int launch_scan(maivs_gpu_ctx* ctx, const KParams& K, bool recount, bool events 
     const uint32_t grid = K.bucket_cap ? static_cast<uint32_t>(std::min<uint64_t>(items, kScanGridMax)) : A.M;
     const uint64_t items8 = static_cast<uint64_t>(A.M) + static_cast<uint64_t>(K.nq) * K.nprobe / kItemQ + 1;
     const uint32_t sgrid = K.bucket_cap ? static_cast<uint32_t>(std::min<uint64_t>(items8, kScanGridMax)) : A.M;
-    DISPATCH_NW(A.W, hipLaunchKernelGGL(cell_scan_kernel<NW>, dim3(std::max(sgrid, 1u)), dim3(kScanThreads), 0,
-                                        ctx->stream, A, W, K));
-    HIP_TRY(ctx, hipGetLastError());
+    // the lookup scan, unless the matrix-core scan takes every bucket work item
+    if (!(K.bucket_cap && K.mma_min == 1)) {
+        DISPATCH_NW(A.W, hipLaunchKernelGGL(cell_scan_kernel<NW>, dim3(std::max(sgrid, 1u)), dim3(kScanThreads), 0,
+                                            ctx->stream, A, W, K));
+        HIP_TRY(ctx, hipGetLastError());
+    }
     // the items with many queries, on the matrix cores
     if (K.bucket_cap && K.mma_min) {
         DISPATCH_NW(A.W, hipLaunchKernelGGL(cell_mma_kernel<NW>, dim3(std::max(grid, 1u)), dim3(kScanThreads), 0,

@@ -292,11 +292,12 @@ def test_global_hamming_rows_match_oracle(ctx, cells9k, mix50k, nprobe):
     _compare_search(ctx, ix, queries, p, gt)
 
 
-@pytest.mark.parametrize("mode", ["1", "0"])
+@pytest.mark.parametrize("mode", ["1", "0", "12"])
 def test_scan_paths_match_oracle(quality50k, memory50k, churn50k, mix50k, monkeypatch, mode):
     """The cell-major scan with every bucket work item on the matrix cores (MAIVS_GPU_MMA_MIN=1:
-    one-hot int8 products, even for items of one query) or every item on the table lookups (0):
-    both bit-exact with the oracle, for both presets and with the tag filter."""
+    one-hot int8 products, even for items of one query), every item on the table lookups (0), or
+    split by size (12: items of fewer queries go to the lookups, screened per workgroup): all
+    bit-exact with the oracle, for both presets and with the tag filter."""
     monkeypatch.setenv("MAIVS_GPU_MMA_MIN", mode)
     _, queries, gt = mix50k
     c = capi.Context(0)
