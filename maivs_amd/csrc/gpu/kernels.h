@@ -1164,20 +1164,29 @@ __device__ __forceinline__ void seed_phase(const DevArena& A, const Work& Wk, co
         __syncthreads();
         tau = (hb << 8) | misc[kTau];
     }
-    // ---- keep d <= tau, with the member's slot (kNoD exceeds every tau: tau <= maxk < kNoD)
+    // ---- keep d <= tau, with the member's slot (kNoD exceeds every tau: tau <= maxk < kNoD);
+    // four rounds at a time, so that their slot loads are in flight together
     uint2* seed = Wk.seed + static_cast<uint64_t>(qi) * K.seed_cap;
-    for (uint32_t b = 0; b < total; b += nt) {
-        const uint32_t i = b + tid;
-        const uint32_t v = i < total ? sbuf[i] : kNoD;
-        const bool keep = v <= tau;
-        const uint64_t m = __ballot(keep);
-        uint32_t wb = 0;
-        if (lane == 0 && m) wb = atomicAdd(&misc[kKeep], static_cast<uint32_t>(__popcll(m)));
-        wb = __shfl(wb, 0, kWave);
-        if (keep) {
-            const uint32_t s = seed_cell(i);
-            const uint32_t slot = A.members[misc[kE0 + s] + (i - misc[kOff + s])];
-            seed[wb + lanes_below(m)] = make_uint2(v, slot);
+    for (uint32_t b = 0; b < total; b += 4 * nt) {
+        uint32_t v[4], slot[4];
+#pragma unroll
+        for (uint32_t u = 0; u < 4; ++u) {
+            const uint32_t i = b + u * nt + tid;
+            v[u] = i < total ? sbuf[i] : kNoD;
+            slot[u] = 0;
+            if (v[u] <= tau) {
+                const uint32_t sc = seed_cell(i);
+                slot[u] = A.members[misc[kE0 + sc] + (i - misc[kOff + sc])];
+            }
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < 4; ++u) {
+            const bool keep = v[u] <= tau;
+            const uint64_t m = __ballot(keep);
+            uint32_t wb = 0;
+            if (lane == 0 && m) wb = atomicAdd(&misc[kKeep], static_cast<uint32_t>(__popcll(m)));
+            wb = __shfl(wb, 0, kWave);
+            if (keep) seed[wb + lanes_below(m)] = make_uint2(v[u], slot[u]);
         }
     }
     __syncthreads();  // every wave's kept count is in misc[kKeep]
