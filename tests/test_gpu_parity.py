@@ -315,6 +315,26 @@ def test_scan_paths_match_oracle(quality50k, memory50k, churn50k, mix50k, monkey
         c.close()
 
 
+@pytest.mark.parametrize("d", [64, 128, 200, 768])
+def test_other_code_widths_match_oracle(monkeypatch, d):
+    """The batched pass at other dimensions, so that every code width the kernels are built for
+    runs (padded dims 64, 128, 256, 1024: 1, 2, 4 and 16 words): seed, rest and cell-major scans on
+    the lookups and on the matrix cores, bit-exact with the oracle."""
+    import maivs_amd as M
+    from .conftest import small_clustered
+    x = small_clustered(12400, d, 60, seed=31 + d)
+    base, queries = np.ascontiguousarray(x[:12000]), np.ascontiguousarray(x[12000:])
+    ix = M.build_preset(base, "quality")
+    for mode in ("0", "1"):
+        monkeypatch.setenv("MAIVS_GPU_MMA_MIN", mode)
+        c = capi.Context(0)
+        try:
+            for nprobe in (10, 40):
+                _compare_search(c, ix, queries, _params(ix, 10, nprobe))
+        finally:
+            c.close()
+
+
 def test_candidate_overflow_regrows(quality50k, mix50k, monkeypatch):
     """A candidate buffer of 16 per query overflows: the pass's end reports the largest count
     through the control block's host mirror, the buffer grows to it and the scan re-runs; the
