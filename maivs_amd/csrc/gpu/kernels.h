@@ -1925,14 +1925,16 @@ cell_mma_kernel(DevArena A, Work Wk, KParams K) {
 
 // ---------------------------------------------------------------- finish (one WG per query)
 
-// Exact `want`-th smallest (1-based) of the n <= 64 * KPL values v (d < 65536) held by one wave,
-// lane-major (value r*64 + lane in v[r]; invalid ones are 0xFFFFFFFF): a most-significant-bit-first
-// radix select with ballots, no LDS and no barriers. Every lane returns the value.
-template <int KPL>
+// Exact `want`-th smallest (1-based) of the n <= 64 * KPL values v (below 2^BITS, or below
+// 0xFFFFFFFF for BITS = 32) held by one wave, lane-major (value r*64 + lane in v[r]; invalid ones
+// are 0xFFFFFFFF, never counted: they never match a prefix whose current bit is 0), with want at
+// most the number of valid values: a most-significant-bit-first radix select with ballots, no LDS
+// and no barriers. Every lane returns the value.
+template <int KPL, int BITS = 16>
 __device__ __forceinline__ uint32_t wave_select_kth(const uint32_t (&v)[KPL], uint32_t want) {
     uint32_t prefix = 0;
 #pragma unroll 1
-    for (int b = 15; b >= 0; --b) {
+    for (int b = BITS - 1; b >= 0; --b) {
         const uint32_t hi = prefix >> b;  // the candidate prefix with bit b = 0
         uint32_t cnt0 = 0;
 #pragma unroll
@@ -2241,9 +2243,11 @@ __device__ __forceinline__ bool pq_seen(const DevArena& A, uint64_t e, uint32_t 
     return false;
 }
 
+constexpr uint32_t kPqStage = 2048;  // survivor keys staged in LDS for the final selection
+
 __host__ __device__ inline uint32_t pq_scan_lds_words(uint32_t MW, uint32_t maxk, uint32_t nprobe) {
     const uint32_t nbins = (maxk >> 6) + 1;
-    return ((MW + 3) & ~3u) + ((nbins + 3) & ~3u) + ((nprobe + 1 + 3) & ~3u) + kHistBins + 32;
+    return ((MW + 3) & ~3u) + ((nbins + 3) & ~3u) + ((nprobe + 1 + 3) & ~3u) + kHistBins + 32 + 2 * kPqStage;
 }
 
 // The FastScan scan of one query (src/index.rs:1689-1757), one workgroup: cells in probe order;
@@ -2253,7 +2257,8 @@ __host__ __device__ inline uint32_t pq_scan_lds_words(uint32_t MW, uint32_t maxk
 // recomputes it from the LDS histogram with a prefix scan after each cell, then the adaptive stop.
 // The next cell's first round of member data is loaded before that barrier. Survivors h <= tau;
 // the target smallest (d, slot) of them go to the candidate list for finish.
-// LDS: static table[W*256] | scanned[MW4] | hist[bins4] | suffix[np4] | hist2[256] | scratch[32].
+// LDS: static table[W*256] | scanned[MW4] | hist[bins4] | suffix[np4] | hist2[256] | scratch[32] |
+// stage[kPqStage] u64.
 template <int NW>
 __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work Wk, KParams K) {
     constexpr uint32_t TB = NW * 256;
@@ -2269,6 +2274,7 @@ __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work 
     float* suffix = reinterpret_cast<float*>(hist + ((nbins + 3) & ~3u));
     uint32_t* hist2 = reinterpret_cast<uint32_t*>(suffix + ((K.nprobe + 1 + 3) & ~3u));
     uint32_t* scratch = hist2 + kHistBins;
+    uint64_t* stage = reinterpret_cast<uint64_t*>(scratch + 32);  // 8-byte aligned: every region is a multiple of 16 bytes
     {
         const uint4* src = reinterpret_cast<const uint4*>(Wk.lut + static_cast<uint64_t>(qi) * TB);
         for (uint32_t i = tid; i < TB / 16; i += nt) reinterpret_cast<uint4*>(table)[i] = src[i];
@@ -2324,14 +2330,27 @@ __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work 
     };
     Mem nxt;
     nxt.have = false;
+    // The probe list in a three-stage pipeline, so that no cell waits on its own id or range: a
+    // cell's id is read two cells ahead, its member range one cell ahead, and its first round of
+    // member data before the previous cell's barrier.
+    uint32_t c_cur = 0, e0_cur = 0, len_cur = 0;  // this cell
+    uint32_t c_n1 = 0, e0_n1 = 0, len_n1 = 0;     // the next one
+    uint32_t c_n2 = 0;                            // the one after
     if (nch > 0) {
-        const uint32_t c0 = chosen[0];
-        load_mem(A.mem_off[c0], A.mem_off[c0 + 1] - A.mem_off[c0], 0, nxt);
+        c_cur = chosen[0];
+        e0_cur = A.mem_off[c_cur];
+        len_cur = A.mem_off[c_cur + 1] - e0_cur;
+        load_mem(e0_cur, len_cur, 0, nxt);
     }
+    if (nch > 1) {
+        c_n1 = chosen[1];
+        e0_n1 = A.mem_off[c_n1];
+        len_n1 = A.mem_off[c_n1 + 1] - e0_n1;
+    }
+    if (nch > 2) c_n2 = chosen[2];
     __syncthreads();
     for (uint32_t ci_i = 0; ci_i < nch; ++ci_i) {
-        const uint32_t c = chosen[ci_i];
-        const uint32_t e0 = A.mem_off[c], len = A.mem_off[c + 1] - e0;
+        const uint32_t c = c_cur, e0 = e0_cur, len = len_cur;
         const uint32_t tau = s_tau;
         for (uint32_t base = 0; base < len; base += nt) {
             Mem m;
@@ -2367,12 +2386,19 @@ __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work 
                 }
             }
         }
-        // the next cell's first round, in flight across the barrier and the bucket-queue update
+        // the next cell's first round, in flight across the barrier and the bucket-queue update;
+        // the range of the cell after it and the id of the third
         nxt.have = false;
-        if (ci_i + 1 < nch) {
-            const uint32_t cn = chosen[ci_i + 1];
-            load_mem(A.mem_off[cn], A.mem_off[cn + 1] - A.mem_off[cn], 0, nxt);
+        if (ci_i + 1 < nch) load_mem(e0_n1, len_n1, 0, nxt);
+        c_cur = c_n1;
+        e0_cur = e0_n1;
+        len_cur = len_n1;
+        if (ci_i + 2 < nch) {
+            c_n1 = c_n2;
+            e0_n1 = A.mem_off[c_n1];
+            len_n1 = A.mem_off[c_n1 + 1] - e0_n1;
         }
+        if (ci_i + 3 < nch) c_n2 = chosen[ci_i + 3];
         __syncthreads();
         if (tid < kWave) {
             // the bucket queue (src/index.rs:1712-1724): tau = min(tau, first u with #(h <= u) >= target)
@@ -2470,10 +2496,85 @@ __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work 
     // survivors h <= tau; the target smallest (d, slot) when more (src/index.rs:1743-1757; ties at
     // the cut by ascending slot)
     const uint32_t n = s_cnt, t = s_tau;
+    // the keys in LDS when they fit (every pass below reads them), with all of a thread's loads in flight
+    const bool staged = n <= kPqStage;
+    if (staged) {
+        constexpr uint32_t PER = kPqStage / kScanThreads;
+        uint64_t v[PER];
+#pragma unroll
+        for (uint32_t k = 0; k < PER; ++k) {
+            const uint32_t i = tid + k * nt;
+            v[k] = i < n ? cbuf[i] : 0ull;
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < PER; ++k) {
+            const uint32_t i = tid + k * nt;
+            if (i < n) stage[i] = v[k];
+        }
+        __syncthreads();
+    }
+    auto key = [&](uint32_t i) -> uint64_t { return staged ? stage[i] : cbuf[i]; };
     auto surv_d = [&](uint32_t i) -> uint32_t {
-        const uint32_t dv = static_cast<uint32_t>(cbuf[i] >> 32);
+        const uint32_t dv = static_cast<uint32_t>(key(i) >> 32);
         return (dv >> 6) <= t ? dv : 0xFFFFFFFFu;
     };
+    if (staged) {
+        // wave 0 alone: the survivors' d (and slots) in registers, KPL per lane for the smallest KPL
+        // that holds them, both cuts by ballot radix selects, and the compaction by ballots; the
+        // other waves are done
+        auto wave_end = [&](auto kpl) {
+            constexpr uint32_t KPL = decltype(kpl)::value;
+            uint32_t dv[KPL];
+            uint32_t m = 0;
+#pragma unroll
+            for (uint32_t r = 0; r < KPL; ++r) {
+                const uint32_t i = r * kWave + lane;
+                dv[r] = i < n ? surv_d(i) : 0xFFFFFFFFu;
+                m += static_cast<uint32_t>(__popcll(__ballot(dv[r] != 0xFFFFFFFFu)));
+            }
+            uint32_t dcut = 0xFFFFFFFFu, scut = 0xFFFFFFFFu;
+            if (m > target) {
+                dcut = wave_select_kth<KPL>(dv, target);
+                uint32_t below = 0, eq = 0;
+#pragma unroll
+                for (uint32_t r = 0; r < KPL; ++r) {
+                    below += static_cast<uint32_t>(__popcll(__ballot(dv[r] < dcut)));
+                    eq += static_cast<uint32_t>(__popcll(__ballot(dv[r] == dcut)));
+                }
+                if (eq > target - below) {
+                    // ties at the cut by ascending slot
+                    uint32_t sv[KPL];
+#pragma unroll
+                    for (uint32_t r = 0; r < KPL; ++r)
+                        sv[r] = dv[r] == dcut ? static_cast<uint32_t>(stage[r * kWave + lane]) : 0xFFFFFFFFu;
+                    scut = wave_select_kth<KPL, 32>(sv, target - below);
+                }
+            }
+            uint32_t w = 0;
+#pragma unroll
+            for (uint32_t r = 0; r < KPL; ++r) {
+                const uint32_t i = r * kWave + lane;
+                const uint32_t slot = i < n ? static_cast<uint32_t>(stage[i]) : 0u;
+                const bool take = dv[r] != 0xFFFFFFFFu && (dv[r] < dcut || (dv[r] == dcut && slot <= scut));
+                const uint64_t bm = __ballot(take);
+                if (take && w + lanes_below(bm) < K.cand_cap) cand[w + lanes_below(bm)] = make_uint2(dv[r], slot);
+                w += static_cast<uint32_t>(__popcll(bm));
+            }
+            if (lane == 0) {
+                Wk.cand_cnt[qi] = w;
+                Wk.seed_cnt[qi] = 0;
+            }
+        };
+        if (tid < kWave) {
+            if (n <= 4 * kWave)
+                wave_end(std::integral_constant<uint32_t, 4>{});
+            else if (n <= 16 * kWave)
+                wave_end(std::integral_constant<uint32_t, 16>{});
+            else
+                wave_end(std::integral_constant<uint32_t, kPqStage / kWave>{});
+        }
+        return;
+    }
     uint32_t m = 0;
     for (uint32_t i = tid; i < n; i += nt) m += surv_d(i) != 0xFFFFFFFFu;
     m = block_sum_u32(m, scratch);
@@ -2485,7 +2586,7 @@ __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work 
         for (uint32_t i = tid; i < n; i += nt) below += surv_d(i) < dcut;
         below = block_sum_u32(below, scratch);
         scut = select_kth_u32(n, target - below,
-                              [&](uint32_t i) { return surv_d(i) == dcut ? static_cast<uint32_t>(cbuf[i]) : 0xFFFFFFFFu; },
+                              [&](uint32_t i) { return surv_d(i) == dcut ? static_cast<uint32_t>(key(i)) : 0xFFFFFFFFu; },
                               hist2, scratch);
     }
     if (tid == 0) s_w = 0;
@@ -2496,7 +2597,7 @@ __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work 
         uint2 e = make_uint2(0, 0);
         if (i < n) {
             const uint32_t dv = surv_d(i);
-            const uint32_t slot = static_cast<uint32_t>(cbuf[i]);
+            const uint32_t slot = static_cast<uint32_t>(key(i));
             take = dv != 0xFFFFFFFFu && (dv < dcut || (dv == dcut && slot <= scut));
             e = make_uint2(dv, slot);
         }
