@@ -60,6 +60,7 @@ struct maivs_gpu_ctx {
     std::vector<void*> pq_allocs;
     uint32_t cap_pq_nq = 0, cap_tcap = 0, cap_pq = 0, pq_cap_min = 0;
     uint32_t* d_beams = nullptr;
+    std::vector<uint32_t> beams_on_device;  // what d_beams holds (empty: unknown)
     // the centroid tree (per-query path); n_levels 0 when the arena has none
     TreeDev tree{};
     std::vector<uint32_t> tree_level_n;

@@ -702,6 +702,7 @@ int ensure_pq(maivs_gpu_ctx* ctx, uint32_t nq, uint32_t tcap, uint32_t pq_cap) {
     rc |= dalloc(ctx, ctx->pq_allocs, &W.tcount, n);
     rc |= dalloc(ctx, ctx->pq_allocs, &W.pqc, static_cast<size_t>(n) * c);
     rc |= dalloc(ctx, ctx->pq_allocs, &ctx->d_beams, kPqMaxLevels);
+    ctx->beams_on_device.clear();
     if (rc) {
         free_all(ctx->pq_allocs);
         ctx->cap_pq_nq = ctx->cap_tcap = ctx->cap_pq = 0;
@@ -796,7 +797,12 @@ int run_search_pq(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs
         tree_beams(ctx->tree_level_n.data(), static_cast<uint32_t>(beams.size()), ctx->tree_beam_frac, ctx->tree_min_beam,
                    K.want_c, beams.data());
         for (uint32_t b : beams) cap = std::max(cap, b);
-        HIP_TRY(ctx, hipMemcpyAsync(ctx->d_beams, beams.data(), beams.size() * 4, hipMemcpyHostToDevice, ctx->stream));
+        // copied only when they change (they depend on the tree and want_c)
+        if (beams != ctx->beams_on_device) {
+            HIP_TRY(ctx, hipMemcpyAsync(ctx->d_beams, beams.data(), beams.size() * 4, hipMemcpyHostToDevice, ctx->stream));
+            HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));  // the host vector is about to go
+            ctx->beams_on_device = beams;
+        }
     }
     Work& W = ctx->Wk;
     HIP_TRY(ctx, hipEventRecord(ctx->ev[0], ctx->stream));
@@ -986,6 +992,7 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
     ctx->cap_nq = ctx->cap_nprobe = ctx->cap_k = ctx->cap_cand = ctx->cap_seed = ctx->cand_nq = 0;
     ctx->cap_pq_nq = ctx->cap_tcap = ctx->cap_pq = ctx->pq_cap_min = 0;
     ctx->d_beams = nullptr;
+    ctx->beams_on_device.clear();
     ctx->uploaded = false;
     ctx->last_nq = 0;
 
