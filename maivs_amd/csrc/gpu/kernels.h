@@ -2349,6 +2349,10 @@ __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work 
     }
     if (nch > 2) c_n2 = chosen[2];
     __syncthreads();
+    // #(h <= tau) over every admitted entry, and s_cnt when it was last counted in (wave 0 keeps
+    // both; s_cnt is read only where no admission is in flight: after a cell's barrier, after a
+    // compaction)
+    uint32_t cum = 0, cnt_prev = 0;
     for (uint32_t ci_i = 0; ci_i < nch; ++ci_i) {
         const uint32_t c = c_cur, e0 = e0_cur, len = len_cur;
         const uint32_t tau = s_tau;
@@ -2401,37 +2405,38 @@ __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work 
         if (ci_i + 3 < nch) c_n2 = chosen[ci_i + 3];
         __syncthreads();
         if (tid < kWave) {
-            // the bucket queue (src/index.rs:1712-1724): tau = min(tau, first u with #(h <= u) >= target)
-            const uint32_t nb = tau + 1, per = (nb + kWave - 1) / kWave;
-            const uint32_t b0 = min(lane * per, nb), b1 = min(b0 + per, nb);
-            uint32_t loc = 0;
-            for (uint32_t bb = b0; bb < b1; ++bb) loc += hist[bb];
-            uint32_t incl = loc;
-            for (int o = 1; o < kWave; o <<= 1) {
-                const uint32_t y = __shfl_up(incl, o, kWave);
-                if (lane >= static_cast<uint32_t>(o)) incl += y;
-            }
-            const uint32_t total = __shfl(incl, kWave - 1, kWave);  // #(h <= tau)
-            const uint32_t excl = incl - loc;
-            const bool here = excl < target && incl >= target;
-            uint32_t u = 0, cu = 0;
-            if (here) {
-                uint32_t cum = excl;
-                for (uint32_t bb = b0; bb < b1; ++bb) {
-                    cum += hist[bb];
-                    if (cum >= target) {
-                        u = bb;
-                        cu = cum;
+            // the bucket queue (src/index.rs:1712-1724): tau = min(tau, first u with #(h <= u) >= target).
+            // hist only grows by entries with h <= tau and tau only falls, so #(h <= tau) is carried
+            // from cell to cell (cum, plus this cell's admissions) and the new tau is found by walking
+            // down from the old one, 64 bins per step: lane l holds bin t - l, and an inclusive scan
+            // gives #(h <= t - l - 1) = c - (the bins t - l .. t).
+            cum += s_cnt - cnt_prev;
+            cnt_prev = s_cnt;
+            uint32_t t = tau, kept = cum;
+            if (cum >= target) {
+                uint32_t c = cum;  // #(h <= t)
+                for (;;) {
+                    const int32_t bi = static_cast<int32_t>(t) - static_cast<int32_t>(lane);
+                    const uint32_t hv = bi >= 0 ? hist[bi] : 0u;
+                    uint32_t incl = hv;
+                    for (int o = 1; o < kWave; o <<= 1) {
+                        const uint32_t y = __shfl_up(incl, o, kWave);
+                        if (lane >= static_cast<uint32_t>(o)) incl += y;
+                    }
+                    // the walk stops at the first bin u = t - l whose lower neighbour's count
+                    // #(h <= u - 1) falls below the target (bin 0's lower count is 0)
+                    const uint64_t stopm = __ballot(bi >= 0 && c - incl < target);
+                    if (stopm) {
+                        const int l = __ffsll(static_cast<long long>(stopm)) - 1;
+                        const uint32_t below = __shfl(incl - hv, l, kWave);  // the bins t - l + 1 .. t
+                        t = t - static_cast<uint32_t>(l);
+                        kept = c - below;
                         break;
                     }
+                    c -= __shfl(incl, kWave - 1, kWave);
+                    t -= kWave;
                 }
-            }
-            const uint64_t hm = __ballot(here);
-            uint32_t t = tau, kept = total;
-            if (hm) {
-                const int src = __ffsll(static_cast<long long>(hm)) - 1;
-                t = __shfl(u, src, kWave);
-                kept = __shfl(cu, src, kWave);
+                cum = kept;
             }
             uint32_t stop = 0;
             // the adaptive stop (:1727-1733)
@@ -2476,6 +2481,7 @@ __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work 
                 if (s_cnt + K.pq_room > K.pq_cap) s_stop = 2;  // the next cell might not fit
             }
             __syncthreads();
+            cnt_prev = s_cnt;  // the entries above tau are gone; cum is unchanged
             if (s_stop == 2) break;
         }
         if (s_stop) break;
