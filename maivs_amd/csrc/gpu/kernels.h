@@ -980,6 +980,26 @@ __device__ __forceinline__ uint32_t lut_sum1(const Code<NW>& c, const uint8_t* _
     return S;
 }
 
+// The same sum from a pair table in LDS: entry p*256 + (a | b << 4) = lut[2p][a] + lut[2p+1][b]
+// (u16; every sum stays below 65536), looked up by code byte p, which holds nibbles 2p (low) and
+// 2p + 1 (high). Half the lookups of lut_sum1; it wins where one workgroup has the CU's LDS to itself.
+template <int NW>
+__device__ __forceinline__ uint32_t lut_sum_pair(const Code<NW>& c, const uint16_t* __restrict__ pair) {
+    uint32_t S = 0;
+#pragma unroll
+    for (int k = 0; k < Code<NW>::NCH; ++k) {
+        const uint32_t dw[4] = {c.v[k].x, c.v[k].y, c.v[k].z, c.v[k].w};
+        constexpr int nbytes = NW == 1 ? 8 : 16;
+#pragma unroll
+        for (int t = 0; t < nbytes; ++t) {
+            const uint32_t byte = (dw[t >> 2] >> (8 * (t & 3))) & 0xFFu;
+            S += pair[(k * 16 + t) * 256 + byte];
+            if ((t & 15) == 15) asm volatile("" : "+v"(S));
+        }
+    }
+    return S;
+}
+
 // All canonical members of the first SEED_CELLS probed cells are scored
 // (src/index.rs:2150-2154); tau is their exact target-th smallest d (:2155-2160) and only
 // d <= tau is kept; then the adaptive cut (:2166-2188) from the route's bounds, and the per-cell
@@ -2245,9 +2265,12 @@ __device__ __forceinline__ bool pq_seen(const DevArena& A, uint64_t e, uint32_t 
 
 constexpr uint32_t kPqStage = 2048;  // survivor keys staged in LDS for the final selection
 
-__host__ __device__ inline uint32_t pq_scan_lds_words(uint32_t MW, uint32_t maxk, uint32_t nprobe) {
+// pair: the pair table's W * 1024 words (W * 4 KB) at the end
+__host__ __device__ inline uint32_t pq_scan_lds_words(uint32_t MW, uint32_t maxk, uint32_t nprobe, uint32_t W = 0,
+                                                      bool pair = false) {
     const uint32_t nbins = (maxk >> 6) + 1;
-    return ((MW + 3) & ~3u) + ((nbins + 3) & ~3u) + ((nprobe + 1 + 3) & ~3u) + kHistBins + 32 + 2 * kPqStage;
+    return ((MW + 3) & ~3u) + ((nbins + 3) & ~3u) + ((nprobe + 1 + 3) & ~3u) + kHistBins + 32 + 2 * kPqStage +
+           (pair ? W * 1024 : 0u);
 }
 
 // The FastScan scan of one query (src/index.rs:1689-1757), one workgroup: cells in probe order;
@@ -2258,7 +2281,8 @@ __host__ __device__ inline uint32_t pq_scan_lds_words(uint32_t MW, uint32_t maxk
 // The next cell's first round of member data is loaded before that barrier. Survivors h <= tau;
 // the target smallest (d, slot) of them go to the candidate list for finish.
 // LDS: static table[W*256] | scanned[MW4] | hist[bins4] | suffix[np4] | hist2[256] | scratch[32] |
-// stage[kPqStage] u64.
+// stage[kPqStage] u64 | pair[W*2048] u16 (K.pq_pair).
+// With K.pq_pair the lookups go through a table of position pairs built from the query's table.
 template <int NW>
 __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work Wk, KParams K) {
     constexpr uint32_t TB = NW * 256;
@@ -2275,9 +2299,20 @@ __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work 
     uint32_t* hist2 = reinterpret_cast<uint32_t*>(suffix + ((K.nprobe + 1 + 3) & ~3u));
     uint32_t* scratch = hist2 + kHistBins;
     uint64_t* stage = reinterpret_cast<uint64_t*>(scratch + 32);  // 8-byte aligned: every region is a multiple of 16 bytes
+    uint16_t* pair = reinterpret_cast<uint16_t*>(stage + kPqStage);
     {
         const uint4* src = reinterpret_cast<const uint4*>(Wk.lut + static_cast<uint64_t>(qi) * TB);
         for (uint32_t i = tid; i < TB / 16; i += nt) reinterpret_cast<uint4*>(table)[i] = src[i];
+    }
+    if (K.pq_pair) {
+        // entry p*256 + (a | b << 4) = table[2p][a] + table[2p+1][b], two entries per thread per step
+        __syncthreads();
+        for (uint32_t i = 2 * tid; i < NW * 2048; i += 2 * nt) {
+            const uint32_t pp = i >> 8, a = i & 15, b = (i >> 4) & 15;
+            const uint32_t hi = table[(2 * pp + 1) * 16 + b];
+            const uint32_t v0 = table[2 * pp * 16 + a] + hi, v1 = table[2 * pp * 16 + a + 1] + hi;
+            *reinterpret_cast<uint32_t*>(pair + i) = v0 | (v1 << 16);
+        }
     }
     for (uint32_t i = tid; i < A.MW; i += nt) scanned[i] = 0;
     for (uint32_t i = tid; i < nbins; i += nt) hist[i] = 0;
@@ -2366,7 +2401,7 @@ __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work 
             uint32_t dv = 0;
             if (m.have) {
                 const uint64_t e = static_cast<uint64_t>(e0) + base + tid;
-                dv = A.maxk - lut_sum1<NW>(m.code, table);
+                dv = A.maxk - (K.pq_pair ? lut_sum_pair<NW>(m.code, pair) : lut_sum1<NW>(m.code, table));
                 if ((dv >> 6) <= tau) {
                     ok = !K.filter || (m.tag >= K.tag_lo && m.tag <= K.tag_hi);
                     if (ok && A.ma > 1) {

@@ -686,6 +686,7 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
 
 // ---------------------------------------------------------------- the per-query path
 
+constexpr uint32_t kPqPairMaxQ = 256;   // batches up to this many queries use the pair tables in the per-query scan
 constexpr uint32_t kPqMaxProbe = 8192;  // probe-list bound of the per-query scan's on-chip suffix array
 constexpr uint32_t kPqMaxLevels = 64;
 
@@ -731,7 +732,7 @@ int launch_pq_tree(maivs_gpu_ctx* ctx, const KParams& K, uint32_t cap) {
 
 int launch_pq_scan(maivs_gpu_ctx* ctx, const KParams& K) {
     const DevArena& A = ctx->A;
-    const size_t lds = static_cast<size_t>(pq_scan_lds_words(A.MW, A.maxk, K.nprobe)) * 4;
+    const size_t lds = static_cast<size_t>(pq_scan_lds_words(A.MW, A.maxk, K.nprobe, A.W, K.pq_pair != 0)) * 4;
     if (lds + A.W * 256 + kScanThreads * 4 > kLdsBudget)
         return fail(ctx, MAIVS_ERR_UNSUPPORTED, "per-query scan needs %zu bytes of LDS", lds);
     DISPATCH_NW(A.W, {
@@ -782,6 +783,8 @@ int run_search_pq(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs
     if ((rc = ensure_pq(ctx, nq, K.tcap, pq_need))) return rc;
     K.pq_cap = ctx->cap_pq;
     K.pq_noflag = 0;
+    // small batches (at most one workgroup per CU) look up position pairs: half the LDS lookups
+    K.pq_pair = nq <= kPqPairMaxQ && pq_scan_lds_words(A.MW, A.maxk, K.nprobe, A.W, true) * 4 + A.W * 256 + kScanThreads * 4 <= kLdsBudget ? 1u : 0u;
     if (p->nprobe == 0) {
         std::vector<uint32_t> s(static_cast<size_t>(nq) * p->k, kNone);
         std::vector<float> f(static_cast<size_t>(nq) * p->k, -INFINITY);

@@ -138,6 +138,8 @@ struct KParams {
     uint32_t filter, tag_lo, tag_hi;  // keep!: tag in [tag_lo, tag_hi] (filter != 0 only with tags)
     // per-query path: routing from the tree's list, bounds from this probe rank on, buffer sizes
     uint32_t tree_list, bnd_from, tcap, pq_cap, pq_room, pq_noflag;
+    // per-query scan: look up byte pairs of positions in a 256-entry table per pair (small batches)
+    uint32_t pq_pair;
     // batched path: rest cells (probe ranks SEED_CELLS on) the seed stage scans itself, query-major
     uint32_t front_rest;
     // bucket work items with at least this many queries go to the matrix-core scan (0: none)

@@ -319,7 +319,8 @@ def test_scan_paths_match_oracle(quality50k, memory50k, churn50k, mix50k, monkey
 def test_other_code_widths_match_oracle(monkeypatch, d):
     """The batched pass at other dimensions, so that every code width the kernels are built for
     runs (padded dims 64, 128, 256, 1024: 1, 2, 4 and 16 words): seed, rest and cell-major scans on
-    the lookups and on the matrix cores, bit-exact with the oracle."""
+    the lookups and on the matrix cores, and the per-query scan on pair tables, bit-exact with the
+    oracle."""
     import maivs_amd as M
     from .conftest import small_clustered
     x = small_clustered(12400, d, 60, seed=31 + d)
@@ -330,7 +331,12 @@ def test_other_code_widths_match_oracle(monkeypatch, d):
         c = capi.Context(0)
         try:
             for nprobe in (10, 40):
-                _compare_search(c, ix, queries, _params(ix, 10, nprobe))
+                p = _params(ix, 10, nprobe)
+                _compare_search(c, ix, queries, p)
+                # the per-query path at this width (pair tables: at most 256 queries)
+                s, v = c.search_queries(queries[:100], p)
+                os_, ov = oracle.search_one(ix._arena_desc(), queries[:100], p, 8)
+                assert np.array_equal(s, os_) and v.tobytes() == ov.tobytes()
         finally:
             c.close()
 

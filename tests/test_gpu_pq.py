@@ -45,6 +45,17 @@ def test_pq_quality_two_stage_matches_oracle(ctx, quality50k, mix50k, nprobe, rf
         quality50k.set_rerank_factor(32)
 
 
+@pytest.mark.parametrize("nprobe", [8, 64])
+def test_pq_pair_tables_match_oracle(ctx, quality50k, memory50k, tree40k, mix50k, nprobe):
+    """Batches of at most 256 queries look up position pairs in the per-query scan (one 256-entry
+    table per pair of positions, built from the query's FastScan table): bit-exact with the oracle
+    for both presets and the tree route, for 200 queries and for one."""
+    _, queries, _ = mix50k
+    for ix in (quality50k, memory50k, tree40k):
+        _compare(ctx, ix, queries[:200], _params(ix, 10, nprobe))
+        _compare(ctx, ix, queries[200:201], _params(ix, 10, nprobe))
+
+
 @pytest.mark.parametrize("nprobe,tc", [(16, 0.95), (64, 0.5)])
 def test_pq_nucleus_matches_oracle(ctx, quality50k, mix50k, nprobe, tc):
     _, queries, _ = mix50k
