@@ -789,10 +789,25 @@ __device__ __forceinline__ void route_phase(const DevArena& A, const Work& Wk, c
         }
     } else {
     if constexpr (kRowsReady) {
-        const uint16_t* row = Wk.hs + static_cast<uint64_t>(qi) * Mp;
-        for (uint32_t c = tid; c < Mp; c += nt) {
-            const uint32_t h = row[c];
-            if (h != 0xFFFFu) atomicAdd(&hist[h], 1u);
+        // the row in 16-byte chunks (Mp is a multiple of 8), four per thread in flight
+        const uint4* row = reinterpret_cast<const uint4*>(Wk.hs + static_cast<uint64_t>(qi) * Mp);
+        const uint32_t nch8 = Mp / 8;
+        for (uint32_t c0 = tid; c0 < nch8; c0 += 4 * nt) {
+            uint4 v[4];
+#pragma unroll
+            for (uint32_t u = 0; u < 4; ++u) {
+                const uint32_t ch = c0 + u * nt;
+                v[u] = ch < nch8 ? row[ch] : make_uint4(0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu);
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < 4; ++u) {
+                const uint32_t w4[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+                for (uint32_t k = 0; k < 8; ++k) {
+                    const uint32_t h = (k & 1) ? (w4[k >> 1] >> 16) : (w4[k >> 1] & 0xFFFFu);
+                    if (h != 0xFFFFu) atomicAdd(&hist[h], 1u);
+                }
+            }
         }
         __syncthreads();
     } else if constexpr (!kFront) {
@@ -839,22 +854,33 @@ __device__ __forceinline__ void route_phase(const DevArena& A, const Work& Wk, c
             const uint32_t w = k < 2 ? v.x : k < 4 ? v.y : k < 6 ? v.z : v.w;
             return (k & 1) ? (w >> 16) : (w & 0xFFFFu);
         };
-        // each thread a run of consecutive chunks of 8 cells, so one block scan orders them all
+        // each thread a run of consecutive chunks of 8 cells, so one block scan orders them all;
+        // the chunks four at a time, their loads in flight together
         const uint32_t per = (nch8 + nt - 1) / nt, c0 = min(tid * per, nch8), c1 = min(c0 + per, nch8);
-        uint32_t cnt = 0;
-        for (uint32_t ch = c0; ch < c1; ++ch) {
-            const uint4 v = hrow[ch];
+        auto chunks4 = [&](uint32_t ch, uint4 (&v)[4]) {
 #pragma unroll
-            for (int k = 0; k < 8; ++k) cnt += h_at(v, k) <= cut;
+            for (uint32_t u = 0; u < 4; ++u) v[u] = ch + u < c1 ? hrow[ch + u] : make_uint4(0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu);
+        };
+        uint32_t cnt = 0;
+        for (uint32_t ch = c0; ch < c1; ch += 4) {
+            uint4 v[4];
+            chunks4(ch, v);
+#pragma unroll
+            for (uint32_t u = 0; u < 4; ++u)
+#pragma unroll
+                for (int k = 0; k < 8; ++k) cnt += h_at(v[u], k) <= cut;
         }
         uint32_t tot;
         uint32_t pos = block_excl_scan_u32(cnt, scratch, &tot);
         if (tot <= K.sort_cap) {
-            for (uint32_t ch = c0; ch < c1; ++ch) {
-                const uint4 v = hrow[ch];
+            for (uint32_t ch = c0; ch < c1; ch += 4) {
+                uint4 v[4];
+                chunks4(ch, v);
 #pragma unroll
-                for (int k = 0; k < 8; ++k)
-                    if (h_at(v, k) <= cut) keys[pos++] = ch * 8 + k;
+                for (uint32_t u = 0; u < 4; ++u)
+#pragma unroll
+                    for (int k = 0; k < 8; ++k)
+                        if (h_at(v[u], k) <= cut) keys[pos++] = (ch + u) * 8 + k;
             }
         }
         nsl = tot;
