@@ -753,6 +753,9 @@ __device__ __forceinline__ void dead_fixup(const DevArena& A, const Work& Wk, ui
 // kFront: the caller (front_kernel) already cleared the histogram, staged cqs and ran hamming_row,
 // and K.tree_list is 0. kRowsReady: hamming_kernel already wrote the query's row of Wk.hs (more
 // cells than the LDS row holds); the histogram is built from it.
+template <class Get>
+__device__ uint32_t select_kth_u32(uint32_t n, uint32_t want, Get get, uint32_t* hist, uint32_t* scratch);
+
 template <int NW, bool kFront = false, bool kRowsReady = false>
 __device__ __forceinline__ void route_phase(const DevArena& A, const Work& Wk, const KParams& K, uint32_t qi) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -937,7 +940,30 @@ __device__ __forceinline__ void route_phase(const DevArena& A, const Work& Wk, c
     } else {
         uint32_t n2 = 1;
         while (n2 < nsl) n2 <<= 1;
-        for (uint32_t i = nsl + tid; i < n2; i += nt) keys[i] = kKeyMax;
+        uint32_t m = nsl;  // keys that go to the sort
+        if (nbins >= kHistBins && K.nprobe <= 2 * nt && n2 > 2 * nt) {
+            // only keys[0 .. nprobe) are used: the nprobe-th smallest key's high word (the
+            // score), then the keys up to it compacted to the front in order (every write lands
+            // at or before an element already read), and only those sorted
+            const uint32_t hv = select_kth_u32(nsl, K.nprobe, [&](uint32_t i) { return static_cast<uint32_t>(keys[i] >> 32); },
+                                               hist, scratch);
+            uint32_t base = 0;
+            for (uint32_t r = 0; r < nsl; r += nt) {
+                const uint32_t i = r + tid;
+                const uint64_t key = i < nsl ? keys[i] : kKeyMax;
+                const bool take = i < nsl && static_cast<uint32_t>(key >> 32) <= hv;
+                uint32_t tot;
+                // the scan's barriers follow every read of this round, so the writes below are safe
+                const uint32_t off = block_excl_scan_u32(take ? 1u : 0u, scratch, &tot);
+                if (take) keys[base + off] = key;
+                base += tot;
+                __syncthreads();
+            }
+            m = base;
+            n2 = 1;
+            while (n2 < m) n2 <<= 1;
+        }
+        for (uint32_t i = m + tid; i < n2; i += nt) keys[i] = kKeyMax;
         bitonic_sort_u64(keys, n2);
     }
     __syncthreads();
