@@ -26,7 +26,9 @@
 #include <cstdio>
 #include <cstring>
 #include <functional>
+#include <map>
 #include <mutex>
+#include <utility>
 #include <string>
 #include <type_traits>
 #include <vector>
@@ -716,14 +718,27 @@ int ensure_pq(maivs_gpu_ctx* ctx, uint32_t nq, uint32_t tcap, uint32_t pq_cap) {
     return 0;
 }
 
+// A kernel's dynamic-LDS limit, raised only when a launch needs more than it was last raised to on
+// this device (the limit only grows): the attribute call costs a few µs of host time, which a
+// one-query search would otherwise spend while the GPU waits for its next launch.
+int raise_lds_limit(maivs_gpu_ctx* ctx, const void* fn, size_t lds) {
+    static std::mutex mu;
+    static std::map<std::pair<const void*, int>, size_t> raised;
+    std::lock_guard<std::mutex> lock(mu);
+    size_t& have = raised[{fn, ctx->device}];
+    if (lds <= have) return 0;
+    HIP_TRY(ctx, hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+    have = lds;
+    return 0;
+}
+
 int launch_pq_tree(maivs_gpu_ctx* ctx, const KParams& K, uint32_t cap) {
     const uint32_t words = pq_tree_lds_words(ctx->A.W, cap);
     const uint32_t per_wave = (words * 4 + 15) & ~15u;
     const size_t lds = static_cast<size_t>(per_wave) * kPqTreeWaves;
     if (lds > kLdsBudget) return fail(ctx, MAIVS_ERR_UNSUPPORTED, "tree descent needs %zu bytes of LDS", lds);
-    if (lds > 64 * 1024)
-        HIP_TRY(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(pq_tree_kernel),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+    int rc;
+    if (lds > 64 * 1024 && (rc = raise_lds_limit(ctx, reinterpret_cast<const void*>(pq_tree_kernel), lds))) return rc;
     hipLaunchKernelGGL(pq_tree_kernel, dim3((K.nq + kPqTreeWaves - 1) / kPqTreeWaves), dim3(kPqTreeWaves * kWave), lds,
                        ctx->stream, ctx->A, ctx->Wk, K, ctx->tree, ctx->d_beams, cap, per_wave);
     HIP_TRY(ctx, hipGetLastError());
@@ -736,9 +751,9 @@ int launch_pq_scan(maivs_gpu_ctx* ctx, const KParams& K) {
     if (lds + A.W * 256 + kScanThreads * 4 > kLdsBudget)
         return fail(ctx, MAIVS_ERR_UNSUPPORTED, "per-query scan needs %zu bytes of LDS", lds);
     DISPATCH_NW(A.W, {
-        if (lds > 48 * 1024)
-            HIP_TRY(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(pq_scan_kernel<NW>),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+        int rc;
+        if (lds > 48 * 1024 && (rc = raise_lds_limit(ctx, reinterpret_cast<const void*>(pq_scan_kernel<NW>), lds)))
+            return rc;
         hipLaunchKernelGGL(pq_scan_kernel<NW>, dim3(K.nq), dim3(kScanThreads), lds, ctx->stream, A, ctx->Wk, K);
     });
     HIP_TRY(ctx, hipGetLastError());
