@@ -823,7 +823,8 @@ int run_search_pq(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs
         }
     }
     Work& W = ctx->Wk;
-    HIP_TRY(ctx, hipEventRecord(ctx->ev[0], ctx->stream));
+    // timed only when the caller asks for measurements
+    if (st) HIP_TRY(ctx, hipEventRecord(ctx->ev[0], ctx->stream));
     ctx->counters_clean = false;  // cleared here by the prep, and again by the finish's epilogue
     if ((rc = launch_prep(ctx, K, d_q, kPrepReset))) return rc;
     for (;;) {
@@ -901,11 +902,13 @@ int run_search_pq(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs
         if (ctl.pq_overflow) return fail(ctx, MAIVS_ERR_HIP, "per-query candidate buffer still overflows");
         break;
     }
-    HIP_TRY(ctx, hipEventRecord(ctx->ev[6], ctx->stream));
-    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
-    float ms;
-    if (hipEventElapsedTime(&ms, ctx->ev[0], ctx->ev[6]) == hipSuccess) S.ms_total = ms;
-    (void)hipGetLastError();
+    if (st) {
+        HIP_TRY(ctx, hipEventRecord(ctx->ev[6], ctx->stream));
+        HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+        float ms;
+        if (hipEventElapsedTime(&ms, ctx->ev[0], ctx->ev[6]) == hipSuccess) S.ms_total = ms;
+        (void)hipGetLastError();
+    }
     ctx->last_nq = nq;
     ctx->last_K = K;
     return 0;
