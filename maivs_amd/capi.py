@@ -15,6 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("MAIVS_GPU_LIB", os.path.join(HERE, "libmaivs_gpu.so"))
 
 MAIVS_OK = 0
+OK, ERR_ARG, ERR_NOT_UPLOADED, ERR_HIP, ERR_OOM, ERR_UNSUPPORTED = 0, -1, -2, -3, -4, -5
 STATUS = {0: "ok", -1: "bad argument", -2: "arena not uploaded", -3: "HIP error", -4: "out of memory",
           -5: "unsupported"}
 RERANK_F32, RERANK_SQ8 = 0, 1

@@ -39,6 +39,7 @@ struct maivs_gpu_ctx {
     hipEvent_t ev[8] = {};
     // last call, for maivs_gpu_last_candidates / maivs_gpu_last_counters
     uint32_t last_nq = 0, last_fin_cap = 0;
+    bool last_pq = false;  // the last search ran the per-query path (no seed / rest-cut state kept)
     KParams last_K{};
     uint32_t initial_cand_cap = 4096;
     int front_rest_mode = -1;  // rest ranks the seed stage scans itself: -1 by cell sharing, else 0 or 8

@@ -403,6 +403,15 @@ __global__ void reset_kernel(Work Wk, uint32_t M, uint32_t nq) {
     for (uint32_t j = i; j < nq; j += stride) Wk.cand_cnt[j] = 0;
 }
 
+// Padded results (no cell probed): no slot, score -inf (src/index.rs:3353-3361).
+__global__ void pad_kernel(uint32_t* __restrict__ slots, float* __restrict__ scores, uint64_t n) {
+    for (uint64_t i = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
+        slots[i] = kNone;
+        scores[i] = -INFINITY;
+    }
+}
+
 // ---------------------------------------------------------------- prep + Hamming (one wave per query)
 
 // Rotation and sign code of one query, by one wave (src/quantize.rs:57-67,152-163;
@@ -2219,9 +2228,13 @@ __global__ void counters_kernel(DevArena A, Work Wk, KParams K) {
     unsigned long long v[5] = {0, 0, 0, 0, 0};
     for (uint32_t q = threadIdx.x; q < K.nq; q += blockDim.x) {
         const uint32_t* ch = Wk.chosen + static_cast<uint64_t>(q) * K.nprobe;
-        const uint32_t nch = Wk.nchosen[q], ns = min(kSeedCells, nch), re = Wk.rest_end[q];
-        for (uint32_t i = 0; i < max(ns, re); ++i) {
+        // rest_end lies in [ns, nch] after a batched pass; clamp anyway so that no value can index
+        // past the probe list, and skip unused (kNone) entries
+        const uint32_t nch = min(Wk.nchosen[q], K.nprobe), ns = min(kSeedCells, nch);
+        const uint32_t re = min(max(Wk.rest_end[q], ns), nch);
+        for (uint32_t i = 0; i < re; ++i) {
             const uint32_t c = ch[i];
+            if (c >= A.M) continue;
             const uint32_t nb = (A.mem_off[c + 1] - A.mem_off[c] + 31) / 32;
             v[i < ns ? 0 : 1] += nb;
         }

@@ -123,8 +123,6 @@ Chain make_chain(uint32_t d, uint32_t vec) {
     return c;
 }
 
-// Per-query and per-cell work buffers for (nq, nprobe, k); grows only. Candidate buffers are
-// separate (ensure_cand) so that growing them never moves the staged queries or outputs.
 // Per-cell query buckets: room for 4x the mean number of queries per live cell in the rest scan,
 // a power of two in [32, 4096]; a fuller cell sends the pass to the counting-sort inversion.
 uint32_t bucket_cap_for(const DevArena& A, uint32_t nq, uint32_t nprobe) {
@@ -135,6 +133,90 @@ uint32_t bucket_cap_for(const DevArena& A, uint32_t nq, uint32_t nprobe) {
     return cap;
 }
 
+// Lays buffers out back to back from a base address, each on a 256-byte boundary. With a null
+// base it only counts: the same walk sizes an allocation, then carves it (or a fixed array).
+struct Carver {
+    uint8_t* base;
+    size_t used = 0;
+    template <class T>
+    void take(T** p, uint64_t count) {
+        used = (used + 255) & ~size_t{255};
+        *p = base ? reinterpret_cast<T*>(base + used) : nullptr;
+        used += static_cast<size_t>(std::max<uint64_t>(count, 1)) * sizeof(T);
+    }
+};
+
+// The per-query and per-cell work buffers of a batched call of nq queries (everything but the
+// candidate lists). host_io: the staged queries and outputs of the host-buffer entry points.
+void carve_work(const DevArena& A, uint32_t nq, uint32_t nprobe, uint32_t k, uint32_t seed_cap, uint32_t bcap,
+                bool host_io, Carver& c, Work& W) {
+    const uint64_t nql = nq;
+    if (host_io) {
+        c.take(&W.q, nql * A.d);
+        c.take(&W.out_slots, nql * k);
+        c.take(&W.out_scores, nql * k);
+    } else {
+        W.q = nullptr;
+        W.out_slots = nullptr;
+        W.out_scores = nullptr;
+    }
+    c.take(&W.qbits, nql * A.W);
+    c.take(&W.lut, nql * A.npos * 16);
+    c.take(&W.delta, nql);
+    c.take(&W.bias, nql);
+    c.take(&W.cqs, nql * A.d);
+    c.take(&W.cqbase, nql);
+    c.take(&W.rbase, nql);
+    W.hs = nullptr;
+    if (A.Mp > kHdLdsCells) c.take(&W.hs, nql * A.Mp);
+    c.take(&W.bnd, nql * nprobe);
+    c.take(&W.chosen, nql * nprobe);
+    c.take(&W.cscore, nql * nprobe);
+    c.take(&W.nchosen, nql);
+    c.take(&W.probed, nql * A.MW);
+    c.take(&W.seed, nql * seed_cap);
+    c.take(&W.seed_cnt, nql);
+    c.take(&W.tau, nql);
+    c.take(&W.rest_end, nql);
+    c.take(&W.cand_cnt, nql);
+    c.take(&W.cut, nql);
+    c.take(&W.ncand, nql);
+    c.take(&W.cell_cnt, static_cast<uint64_t>(A.M) + 1);
+    c.take(&W.cell_off, static_cast<uint64_t>(A.M) + 1);
+    c.take(&W.cell_cur, static_cast<uint64_t>(A.M) + 1);
+    c.take(&W.qof, nql * nprobe);
+    c.take(&W.qbuck, static_cast<uint64_t>(A.M) * bcap);
+    // scan work items: at most one per kBucketQ (kItemQ) bucket entries plus one per cell
+    c.take(&W.active, static_cast<uint64_t>(A.M) + nql * nprobe / kBucketQ + 1);
+    c.take(&W.active8, static_cast<uint64_t>(A.M) + nql * nprobe / kItemQ + 1);
+    c.take(&W.flag_route, nql);
+    c.take(&W.flag_prune, nql);
+    c.take(&W.ctl, 1);
+    c.take(&W.cand_n, nql);
+    c.take(&W.done, 1);
+}
+
+// Room of the final list of one query (seed survivors + candidates) and of its sort keys.
+void cand_caps(uint32_t seed_cap, uint32_t cand_cap, uint32_t* fin_cap, uint32_t* key_cap) {
+    *fin_cap = seed_cap + cand_cap;
+    uint32_t kc = 1;
+    while (kc < *fin_cap) kc <<= 1;
+    *key_cap = kc;
+}
+
+// The candidate, final-list and sort-key buffers of nq queries.
+void carve_cand(uint32_t nq, uint32_t seed_cap, uint32_t cand_cap, Carver& c, Work& W) {
+    uint32_t fin_cap, key_cap;
+    cand_caps(seed_cap, cand_cap, &fin_cap, &key_cap);
+    const uint64_t nql = nq;
+    c.take(&W.cand, nql * cand_cap);
+    c.take(&W.fin, nql * fin_cap);
+    c.take(&W.keys, nql * key_cap);
+}
+
+// Per-query and per-cell work buffers for (nq, nprobe, k), one allocation; grows only. Candidate
+// buffers are a separate allocation (ensure_cand) so that growing them never moves the staged
+// queries or outputs.
 int ensure_work(maivs_gpu_ctx* ctx, uint32_t nq, uint32_t nprobe, uint32_t k) {
     const DevArena& A = ctx->A;
     const uint32_t seed_cap = ctx->seed_cap;
@@ -150,54 +232,20 @@ int ensure_work(maivs_gpu_ctx* ctx, uint32_t nq, uint32_t nprobe, uint32_t k) {
     nq = std::max(nq, ctx->cap_nq);
     nprobe = std::max(nprobe, ctx->cap_nprobe);
     k = std::max(k, ctx->cap_k);
-    Work& W = ctx->Wk;
-    auto& o = ctx->work_allocs;
-    const uint64_t nql = nq;
-    int rc = 0;
-    rc |= dalloc(ctx, o, &W.q, nql * A.d);
-    rc |= dalloc(ctx, o, &W.qbits, nql * A.W);
-    rc |= dalloc(ctx, o, &W.lut, nql * A.npos * 16);
-    rc |= dalloc(ctx, o, &W.delta, nql);
-    rc |= dalloc(ctx, o, &W.bias, nql);
-    rc |= dalloc(ctx, o, &W.cqs, nql * A.d);
-    rc |= dalloc(ctx, o, &W.cqbase, nql);
-    rc |= dalloc(ctx, o, &W.rbase, nql);
-    W.hs = nullptr;
-    if (A.Mp > kHdLdsCells) rc |= dalloc(ctx, o, &W.hs, nql * A.Mp);
-    rc |= dalloc(ctx, o, &W.bnd, nql * nprobe);
-    rc |= dalloc(ctx, o, &W.chosen, nql * nprobe);
-    rc |= dalloc(ctx, o, &W.cscore, nql * nprobe);
-    rc |= dalloc(ctx, o, &W.nchosen, nql);
-    rc |= dalloc(ctx, o, &W.probed, nql * A.MW);
-    rc |= dalloc(ctx, o, &W.seed, nql * seed_cap);
-    rc |= dalloc(ctx, o, &W.seed_cnt, nql);
-    rc |= dalloc(ctx, o, &W.tau, nql);
-    rc |= dalloc(ctx, o, &W.rest_end, nql);
-    rc |= dalloc(ctx, o, &W.cand_cnt, nql);
-    rc |= dalloc(ctx, o, &W.cut, nql);
-    rc |= dalloc(ctx, o, &W.ncand, nql);
-    rc |= dalloc(ctx, o, &W.out_slots, nql * k);
-    rc |= dalloc(ctx, o, &W.out_scores, nql * k);
-    rc |= dalloc(ctx, o, &W.cell_cnt, static_cast<uint64_t>(A.M) + 1);
-    rc |= dalloc(ctx, o, &W.cell_off, static_cast<uint64_t>(A.M) + 1);
-    rc |= dalloc(ctx, o, &W.cell_cur, static_cast<uint64_t>(A.M) + 1);
-    rc |= dalloc(ctx, o, &W.qof, nql * nprobe);
     const uint32_t bcap_all = std::max(bcap, ctx->cap_bucket);
-    rc |= dalloc(ctx, o, &W.qbuck, static_cast<uint64_t>(A.M) * bcap_all);
-    // scan work items: at most one per kBucketQ (kItemQ) bucket entries plus one per cell
-    rc |= dalloc(ctx, o, &W.active, static_cast<uint64_t>(A.M) + nql * nprobe / kBucketQ + 1);
-    rc |= dalloc(ctx, o, &W.active8, static_cast<uint64_t>(A.M) + nql * nprobe / kItemQ + 1);
-    rc |= dalloc(ctx, o, &W.flag_route, nql);
-    rc |= dalloc(ctx, o, &W.flag_prune, nql);
-    rc |= dalloc(ctx, o, &W.ctl, 1);
-    rc |= dalloc(ctx, o, &W.cand_n, nql);
-    rc |= dalloc(ctx, o, &W.done, 1);
+    Carver count{nullptr};
+    Work& W = ctx->Wk;
+    carve_work(A, nq, nprobe, k, seed_cap, bcap_all, true, count, W);
+    uint8_t* base = nullptr;
+    int rc = dalloc(ctx, ctx->work_allocs, &base, count.used);
     ctx->counters_clean = false;  // fresh buffers: the next pass clears them first
     if (rc) {
         free_all(ctx->work_allocs);
         ctx->cap_nq = ctx->cap_nprobe = ctx->cap_k = ctx->cap_seed = ctx->cap_bucket = 0;
         return rc;
     }
+    Carver cv{base};
+    carve_work(A, nq, nprobe, k, seed_cap, bcap_all, true, cv, W);
     ctx->cap_nq = nq;
     ctx->cap_nprobe = nprobe;
     ctx->cap_k = k;
@@ -213,26 +261,21 @@ int ensure_cand(maivs_gpu_ctx* ctx, uint32_t cand_cap) {
     drop_graph(ctx);
     free_all(ctx->cand_allocs);
     cand_cap = std::max(cand_cap, ctx->cap_cand);
-    uint32_t fin_cap = ctx->cap_seed + cand_cap;
-    uint32_t key_cap = 1;
-    while (key_cap < fin_cap) key_cap <<= 1;
-    Work& W = ctx->Wk;
-    auto& o = ctx->cand_allocs;
-    const uint64_t nql = ctx->cap_nq;
-    int rc = 0;
-    rc |= dalloc(ctx, o, &W.cand, nql * cand_cap);
-    rc |= dalloc(ctx, o, &W.fin, nql * fin_cap);
-    rc |= dalloc(ctx, o, &W.keys, nql * key_cap);
+    Carver count{nullptr};
+    carve_cand(ctx->cap_nq, ctx->cap_seed, cand_cap, count, ctx->Wk);
+    uint8_t* base = nullptr;
+    int rc = dalloc(ctx, ctx->cand_allocs, &base, count.used);
     if (rc) {
         free_all(ctx->cand_allocs);
         ctx->cand_nq = 0;
         ctx->cap_cand = 0;
         return rc;
     }
+    Carver cv{base};
+    carve_cand(ctx->cap_nq, ctx->cap_seed, cand_cap, cv, ctx->Wk);
     ctx->cand_nq = ctx->cap_nq;
     ctx->cap_cand = cand_cap;
-    ctx->cap_fin = fin_cap;
-    ctx->cap_key = key_cap;
+    cand_caps(ctx->cap_seed, cand_cap, &ctx->cap_fin, &ctx->cap_key);
     return 0;
 }
 
@@ -441,6 +484,13 @@ KParams csr(KParams K) {
     return K;
 }
 
+int launch_pad(maivs_gpu_ctx* ctx, uint32_t* d_slots, float* d_scores, uint64_t n) {
+    const uint32_t blocks = static_cast<uint32_t>(std::min<uint64_t>((n + 255) / 256, 1024));
+    hipLaunchKernelGGL(pad_kernel, dim3(std::max(blocks, 1u)), dim3(256), 0, ctx->stream, d_slots, d_scores, n);
+    HIP_TRY(ctx, hipGetLastError());
+    return 0;
+}
+
 int launch_finish(maivs_gpu_ctx* ctx, const KParams& K, const float* d_q, uint32_t* d_slots, float* d_scores) {
     hipLaunchKernelGGL(finish_kernel, dim3(K.nq), dim3(kFinishThreads), ctx->lds_finish, ctx->stream, ctx->A, ctx->Wk,
                        K, d_q, d_slots, d_scores);
@@ -478,16 +528,44 @@ int read_ctl_live(maivs_gpu_ctx* ctx, Ctl* ctl) {
     return 0;
 }
 
+// A fixed device region the work buffers are carved from instead of the context's allocations
+// (the no-allocation entry point): the candidate buffers start at cand_off.
+struct Scratch {
+    uint8_t* base;
+    size_t bytes;
+    size_t cand_off;
+};
+
+// Re-carve the candidate buffers of a scratch-backed call for cand_cap candidates per query.
+int recarve_cand(maivs_gpu_ctx* ctx, const Scratch& sc, uint32_t cand_cap) {
+    Carver c{nullptr};
+    c.used = sc.cand_off;
+    Work W = ctx->Wk;
+    carve_cand(ctx->cap_nq, ctx->cap_seed, cand_cap, c, W);
+    if (c.used > sc.bytes)
+        return fail(ctx, MAIVS_ERR_UNSUPPORTED,
+                    "%u candidates per query for %u queries need %zu bytes of scratch, more than its %zu", cand_cap,
+                    ctx->cap_nq, c.used, sc.bytes);
+    Carver cv{sc.base};
+    cv.used = sc.cand_off;
+    carve_cand(ctx->cap_nq, ctx->cap_seed, cand_cap, cv, ctx->Wk);
+    ctx->cap_cand = cand_cap;
+    cand_caps(ctx->cap_seed, cand_cap, &ctx->cap_fin, &ctx->cap_key);
+    return 0;
+}
+
 // The whole batch. Stages after the first pass only re-run when the control block asks:
 // (1) a nucleus decision within kNucleusBand of tc, (2) an adaptive cut within kPruneBand of its
 // threshold (both re-evaluated with the host libm the reference uses), (3) a candidate buffer
 // overflow (grown to the exact count), (4) a shortlist larger than the on-chip sort.
+// With a scratch region (sc), the work buffers were carved from it beforehand: nothing is
+// allocated, the stages run eagerly (no graph), and a candidate overflow re-carves within it.
 int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_search_params* p, uint32_t* d_slots,
-               float* d_scores, maivs_gpu_stats* st) {
+               float* d_scores, maivs_gpu_stats* st, const Scratch* sc = nullptr) {
     if (!ctx->uploaded) return fail(ctx, MAIVS_ERR_NOT_UPLOADED, "no arena uploaded");
     if (p->k == 0) return fail(ctx, MAIVS_ERR_ARG, "k must be > 0");
     const DevArena& A = ctx->A;
-    int rc = ensure_all(ctx, nq, p->nprobe, p->k);
+    int rc = sc ? 0 : ensure_all(ctx, nq, p->nprobe, p->k);
     if (rc) return rc;
     Work& W = ctx->Wk;
     maivs_gpu_stats local{};
@@ -498,10 +576,7 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
     KParams K = make_params(ctx, nq, p);
     if (p->nprobe == 0 || K.want_c == 0) {
         // route_batch returns empty probe lists (src/index.rs:1887-1889): padded results
-        std::vector<uint32_t> s(static_cast<size_t>(nq) * p->k, kNone);
-        std::vector<float> f(static_cast<size_t>(nq) * p->k, -INFINITY);
-        HIP_TRY(ctx, hipMemcpyAsync(d_slots, s.data(), s.size() * 4, hipMemcpyHostToDevice, ctx->stream));
-        HIP_TRY(ctx, hipMemcpyAsync(d_scores, f.data(), f.size() * 4, hipMemcpyHostToDevice, ctx->stream));
+        if ((rc = launch_pad(ctx, d_slots, d_scores, static_cast<uint64_t>(nq) * p->k))) return rc;
         HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
         return 0;
     }
@@ -539,7 +614,7 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
     // replayed as one captured graph when possible (one launch instead of a dozen); the capture
     // is keyed by the parameters and every buffer address it bakes in
     auto run_main = [&]() -> int {
-        if (ctx->use_graph) {
+        if (ctx->use_graph && !sc) {
             maivs_gpu_ctx::GraphKey key{};
             key.K = K;
             key.q = d_q;
@@ -668,7 +743,7 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
     if (ctl.max_cand > ctx->cap_cand) {
         uint32_t need = ctl.max_cand + ctl.max_cand / 4 + 64;
         ctx->initial_cand_cap = std::max(ctx->initial_cand_cap, need);
-        if ((rc = ensure_cand(ctx, need))) return rc;
+        if ((rc = sc ? recarve_cand(ctx, *sc, need) : ensure_cand(ctx, need))) return rc;
         const uint32_t sc = K.sort_cap;
         K = make_params(ctx, nq, p);
         K.sort_cap = sc;
@@ -683,6 +758,7 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
     }
     ctx->last_nq = nq;
     ctx->last_K = K;
+    ctx->last_pq = false;
     return 0;
 }
 
@@ -801,10 +877,7 @@ int run_search_pq(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs
     // small batches (at most one workgroup per CU) look up position pairs: half the LDS lookups
     K.pq_pair = nq <= kPqPairMaxQ && pq_scan_lds_words(A.MW, A.maxk, K.nprobe, A.W, true) * 4 + A.W * 256 + kScanThreads * 4 <= kLdsBudget ? 1u : 0u;
     if (p->nprobe == 0) {
-        std::vector<uint32_t> s(static_cast<size_t>(nq) * p->k, kNone);
-        std::vector<float> f(static_cast<size_t>(nq) * p->k, -INFINITY);
-        HIP_TRY(ctx, hipMemcpyAsync(d_slots, s.data(), s.size() * 4, hipMemcpyHostToDevice, ctx->stream));
-        HIP_TRY(ctx, hipMemcpyAsync(d_scores, f.data(), f.size() * 4, hipMemcpyHostToDevice, ctx->stream));
+        if ((rc = launch_pad(ctx, d_slots, d_scores, static_cast<uint64_t>(nq) * p->k))) return rc;
         HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
         return 0;
     }
@@ -911,6 +984,7 @@ int run_search_pq(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs
     }
     ctx->last_nq = nq;
     ctx->last_K = K;
+    ctx->last_pq = true;
     return 0;
 }
 
@@ -1182,24 +1256,21 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
     ctx->lds_prep = prep_lds(A);
     ctx->lds_seed = seed_lds(A, seed_cap);
     ctx->lds_finish = finish_lds(A);
-    hipFuncSetAttribute(reinterpret_cast<const void*>(finish_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                        static_cast<int>(ctx->lds_finish));
-    DISPATCH_EPL(A.P / 64, hipFuncSetAttribute(reinterpret_cast<const void*>(prep_kernel<EPL>),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize,
-                                               static_cast<int>(ctx->lds_prep)));
+    // every kernel's dynamic-LDS limit only grows (another context's smaller arena must not lower
+    // the limit this one's launches rely on), and a failure is an error
+    auto raise = [&](const void* fn, size_t lds) { return raise_lds_limit(ctx, fn, lds); };
+    if ((rc = raise(reinterpret_cast<const void*>(finish_kernel), ctx->lds_finish))) return rc;
+    DISPATCH_EPL(A.P / 64, rc = raise(reinterpret_cast<const void*>(prep_kernel<EPL>), ctx->lds_prep));
+    if (rc) return rc;
     DISPATCH_NW(A.W, {
-        hipFuncSetAttribute(reinterpret_cast<const void*>(route_kernel<NW>), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            static_cast<int>(route_lds(A, sc, sc)));
-        hipFuncSetAttribute(reinterpret_cast<const void*>(seed_kernel<NW>), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            static_cast<int>(ctx->lds_seed));
-        hipFuncSetAttribute(reinterpret_cast<const void*>(route_seed_kernel<NW, false>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize,
-                            static_cast<int>(std::max(route_lds(A, sc, sc), ctx->lds_seed)));
-        hipFuncSetAttribute(reinterpret_cast<const void*>(route_seed_kernel<NW, true>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize,
-                            static_cast<int>(std::max(route_lds(A, sc, sc), ctx->lds_seed)));
-        hipFuncSetAttribute(reinterpret_cast<const void*>(front_kernel<NW>), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            static_cast<int>(std::max(route_lds(A, sc, sc) + prep1_lds(A), ctx->lds_seed)));
+        const size_t rs = std::max(route_lds(A, sc, sc), ctx->lds_seed);
+        if ((rc = raise(reinterpret_cast<const void*>(route_kernel<NW>), route_lds(A, sc, sc))) ||
+            (rc = raise(reinterpret_cast<const void*>(seed_kernel<NW>), ctx->lds_seed)) ||
+            (rc = raise(reinterpret_cast<const void*>(route_seed_kernel<NW, false>), rs)) ||
+            (rc = raise(reinterpret_cast<const void*>(route_seed_kernel<NW, true>), rs)) ||
+            (rc = raise(reinterpret_cast<const void*>(front_kernel<NW>),
+                        std::max(route_lds(A, sc, sc) + prep1_lds(A), ctx->lds_seed))))
+            return rc;
     });
     ctx->uploaded = true;
     return 0;
@@ -1382,6 +1453,8 @@ int maivs_gpu_last_counters(maivs_gpu_ctx* ctx, maivs_gpu_stats* stats) {
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     stats->seed_blocks = stats->scan_blocks = stats->scan_pairs = stats->survivors = stats->rerank_rows = 0;
     if (ctx->last_nq == 0) return 0;
+    if (ctx->last_pq)
+        return fail(ctx, MAIVS_ERR_UNSUPPORTED, "the last search ran the per-query path, which keeps no work counters");
     hipLaunchKernelGGL(counters_kernel, dim3(1), dim3(1024), 0, ctx->stream, ctx->A, ctx->Wk, ctx->last_K);
     HIP_TRY(ctx, hipGetLastError());
     Ctl ctl{};
@@ -1402,6 +1475,8 @@ int maivs_gpu_last_candidates(maivs_gpu_ctx* ctx, uint32_t* tau, uint32_t* rest_
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     const uint32_t nq = ctx->last_nq;
     if (nq == 0) return 0;
+    if (ctx->last_pq)
+        return fail(ctx, MAIVS_ERR_UNSUPPORTED, "the last search ran the per-query path, which keeps no seed cut-offs");
     Work& W = ctx->Wk;
     std::vector<uint32_t> n(nq);
     HIP_TRY(ctx, hipMemcpy(n.data(), W.ncand, nq * 4, hipMemcpyDeviceToHost));

@@ -4,6 +4,7 @@
 #include <pybind11/pybind11.h>
 #include <pybind11/stl.h>
 
+#include <atomic>
 #include <cstring>
 #include <type_traits>
 
@@ -13,6 +14,10 @@ namespace py = pybind11;
 using maivs::FlatCellIndex;
 
 namespace {
+
+struct BorrowError : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
 
 // A float32 (n, d) C-contiguous view, with the reference's error messages.
 struct F32Rows {
@@ -60,8 +65,35 @@ py::dict stats_dict(const maivs_gpu_stats& s) {
 struct PyIndex {
     FlatCellIndex ix;
     maivs_gpu_stats last{};
+    // pyo3's borrow flag (src/concurrent.rs:3-5): > 0 shared borrows (searches), -1 one exclusive
+    // borrow (a mutation). Methods release the GIL, so two calls can overlap; a conflicting one
+    // raises as the reference's does instead of racing.
+    std::atomic<int> borrow{0};
     PyIndex(size_t dim, const std::string& mode, size_t rf, uint64_t seed, size_t code_bits)
         : ix(dim, mode, rf, seed, code_bits) {}
+};
+
+// A shared borrow (&self): fails while a mutation runs, with pyo3's PyBorrowError message.
+struct Ref {
+    std::atomic<int>& f;
+    explicit Ref(PyIndex& s) : f(s.borrow) {
+        int v = f.load();
+        do {
+            if (v < 0) throw BorrowError("Already mutably borrowed");
+        } while (!f.compare_exchange_weak(v, v + 1));
+    }
+    ~Ref() { f.fetch_sub(1); }
+};
+
+// An exclusive borrow (&mut self): fails while any other call holds the index, with pyo3's
+// PyBorrowMutError message.
+struct Mut {
+    std::atomic<int>& f;
+    explicit Mut(PyIndex& s) : f(s.borrow) {
+        int v = 0;
+        if (!f.compare_exchange_strong(v, -1)) throw BorrowError("Already borrowed");
+    }
+    ~Mut() { f.store(0); }
 };
 
 }  // namespace
@@ -77,6 +109,8 @@ PYBIND11_MODULE(_maivs, m) {
             PyErr_SetString(PyExc_NotImplementedError, e.what());
         } catch (const maivs::IoError& e) {
             PyErr_SetString(PyExc_OSError, e.what());
+        } catch (const BorrowError& e) {
+            PyErr_SetString(PyExc_RuntimeError, e.what());
         }
     });
 
@@ -89,7 +123,7 @@ PYBIND11_MODULE(_maivs, m) {
              py::arg("seed") = 0x5EEDull, py::arg("code_bits") = 0)
         .def(
             "train_centroids",
-            [](PyIndex& s, const py::array& vectors, size_t n_cells, size_t sample, uint64_t seed) {
+            [](PyIndex& s, const py::array& vectors, size_t n_cells, size_t sample, uint64_t seed) { Mut _b(s); 
                 F32Rows r = as_rows(vectors, "vectors", "vectors must be C-contiguous");
                 if (r.cols != s.ix.dim()) throw py::value_error("dim mismatch");
                 py::gil_scoped_release nogil;
@@ -97,65 +131,65 @@ PYBIND11_MODULE(_maivs, m) {
             },
             py::arg("vectors"), py::arg("n_cells"), py::arg("sample") = 262144, py::arg("seed") = 0x5EEDull)
         .def("set_centroids",
-             [](PyIndex& s, const py::array& c) {
+             [](PyIndex& s, const py::array& c) { Mut _b(s); 
                  F32Rows r = as_rows(c, "centroids", "centroids must be C-contiguous");
                  if (r.cols != s.ix.dim()) throw py::value_error("centroid dim mismatch");
                  translate([&] { s.ix.set_centroids(r.ptr, r.rows); });
              })
-        .def("set_i8_rerank", [](PyIndex& s, bool on) { s.ix.set_i8_rerank(on); })
+        .def("set_i8_rerank", [](PyIndex& s, bool on) { Mut _b(s);  s.ix.set_i8_rerank(on); })
         .def(
             "set_tree_route",
-            [](PyIndex& s, bool on, size_t min_cells, size_t fanout, float beam_frac) {
+            [](PyIndex& s, bool on, size_t min_cells, size_t fanout, float beam_frac) { Mut _b(s); 
                 py::gil_scoped_release nogil;
                 s.ix.set_tree_route(on, min_cells, fanout, beam_frac);
             },
             py::arg("on"), py::arg("min_cells") = 0, py::arg("fanout") = 0, py::arg("beam_frac") = 0.0f)
         .def(
-            "set_graph_route", [](PyIndex& s, bool on, size_t min_cells) { s.ix.set_graph_route(on, min_cells); },
+            "set_graph_route", [](PyIndex& s, bool on, size_t min_cells) { Mut _b(s);  s.ix.set_graph_route(on, min_cells); },
             py::arg("on"), py::arg("min_cells") = 0)
-        .def("set_centroid_sq8", [](PyIndex& s, bool on) { s.ix.set_centroid_sq8(on); })
-        .def("set_two_stage", [](PyIndex& s, bool on, size_t mult) { s.ix.set_two_stage(on, mult); })
-        .def("set_adaptive", [](PyIndex& s, bool on, float margin) { s.ix.set_adaptive(on, margin); })
-        .def("set_per_dim_sq", [](PyIndex& s, bool on) { s.ix.set_per_dim_sq(on); })
-        .def("set_f16_rerank", [](PyIndex& s, bool on) { translate([&] { s.ix.set_f16_rerank(on); }); })
-        .def("set_quant_scale", [](PyIndex& s, float v) { s.ix.set_quant_scale(v); })
-        .def("set_rerank_factor", [](PyIndex& s, size_t rf) { s.ix.set_rerank_factor(rf); })
-        .def("set_asym_cascade", [](PyIndex& s, size_t f) { s.ix.set_asym_cascade(f); })
-        .def("set_fastscan", [](PyIndex& s, bool on) { s.ix.set_fastscan(on); })
-        .def("set_replication", [](PyIndex& s, size_t ma, float margin) { s.ix.set_replication(ma, margin); })
+        .def("set_centroid_sq8", [](PyIndex& s, bool on) { Mut _b(s);  s.ix.set_centroid_sq8(on); })
+        .def("set_two_stage", [](PyIndex& s, bool on, size_t mult) { Mut _b(s);  s.ix.set_two_stage(on, mult); })
+        .def("set_adaptive", [](PyIndex& s, bool on, float margin) { Mut _b(s);  s.ix.set_adaptive(on, margin); })
+        .def("set_per_dim_sq", [](PyIndex& s, bool on) { Mut _b(s);  s.ix.set_per_dim_sq(on); })
+        .def("set_f16_rerank", [](PyIndex& s, bool on) { Mut _b(s);  translate([&] { s.ix.set_f16_rerank(on); }); })
+        .def("set_quant_scale", [](PyIndex& s, float v) { Mut _b(s);  s.ix.set_quant_scale(v); })
+        .def("set_rerank_factor", [](PyIndex& s, size_t rf) { Mut _b(s);  s.ix.set_rerank_factor(rf); })
+        .def("set_asym_cascade", [](PyIndex& s, size_t f) { Mut _b(s);  s.ix.set_asym_cascade(f); })
+        .def("set_fastscan", [](PyIndex& s, bool on) { Mut _b(s);  s.ix.set_fastscan(on); })
+        .def("set_replication", [](PyIndex& s, size_t ma, float margin) { Mut _b(s);  s.ix.set_replication(ma, margin); })
         .def(
-            "set_orthogonal_polysemy", [](PyIndex& s, size_t homes, float lam) { s.ix.set_orthogonal_polysemy(homes, lam); },
+            "set_orthogonal_polysemy", [](PyIndex& s, size_t homes, float lam) { Mut _b(s);  s.ix.set_orthogonal_polysemy(homes, lam); },
             py::arg("homes") = 2, py::arg("lam") = 1.0f)
-        .def("set_parallel_scan", [](PyIndex& s, bool on) { s.ix.set_parallel_scan(on); })
+        .def("set_parallel_scan", [](PyIndex& s, bool on) { Mut _b(s);  s.ix.set_parallel_scan(on); })
         .def("set_tags",
-             [](PyIndex& s, std::vector<uint64_t> ids, std::vector<uint32_t> tags) {
+             [](PyIndex& s, std::vector<uint64_t> ids, std::vector<uint32_t> tags) { Mut _b(s); 
                  translate([&] { s.ix.set_tags(ids, tags); });
              })
         .def(
             "set_filter",
-            [](PyIndex& s, std::optional<uint32_t> lo, std::optional<uint32_t> hi) { s.ix.set_filter(lo, hi); },
+            [](PyIndex& s, std::optional<uint32_t> lo, std::optional<uint32_t> hi) { Mut _b(s);  s.ix.set_filter(lo, hi); },
             py::arg("lo") = py::none(), py::arg("hi") = py::none())
         .def("rebuild_tree",
-             [](PyIndex& s) {
+             [](PyIndex& s) { Mut _b(s); 
                  py::gil_scoped_release nogil;
                  s.ix.rebuild_tree();
              })
         .def("add_batch",
-             [](PyIndex& s, std::vector<uint64_t> ids, const py::array& vectors) {
+             [](PyIndex& s, std::vector<uint64_t> ids, const py::array& vectors) { Mut _b(s); 
                  F32Rows r = as_rows(vectors, "vectors", "vectors must be C-contiguous (use np.ascontiguousarray)");
                  if (r.rows != ids.size() || r.cols != s.ix.dim()) throw py::value_error("shape mismatch");
                  py::gil_scoped_release nogil;
                  translate([&] { s.ix.add_batch(ids, r.ptr, r.rows); });
              })
-        .def("remove", [](PyIndex& s, uint64_t id) { return s.ix.remove(id); })
+        .def("remove", [](PyIndex& s, uint64_t id) { Mut _b(s);  return s.ix.remove(id); })
         .def("compact",
-             [](PyIndex& s) {
+             [](PyIndex& s) { Mut _b(s); 
                  py::gil_scoped_release nogil;
                  s.ix.compact();
              })
         .def(
             "search",
-            [](PyIndex& s, const py::array& query, size_t k, size_t nprobe, float tc, float beta) -> py::tuple {
+            [](PyIndex& s, const py::array& query, size_t k, size_t nprobe, float tc, float beta) -> py::tuple { Ref _b(s); 
                 if (!py::dtype::of<float>().is(query.dtype())) throw py::type_error("query must be a float32 array");
                 if (query.ndim() != 1) throw py::value_error("query must be 1-dimensional");
                 if (static_cast<size_t>(query.shape(0)) != s.ix.dim()) throw py::value_error("query dim mismatch");
@@ -174,7 +208,7 @@ PYBIND11_MODULE(_maivs, m) {
         .def(
             "search_batch",
             [](PyIndex& s, const py::array& queries, size_t k, size_t nprobe, float tc, float beta,
-               bool cell_major) {
+               bool cell_major) { Ref _b(s); 
                 if (!py::dtype::of<float>().is(queries.dtype()))
                     throw py::type_error("queries must be a float32 array");
                 if (queries.ndim() != 2) throw py::value_error("queries must be 2-dimensional");
@@ -195,7 +229,7 @@ PYBIND11_MODULE(_maivs, m) {
             py::arg("beta") = 8.0f, py::arg("cell_major") = true)
         .def(
             "save",
-            [](PyIndex& s, const std::string& path) {
+            [](PyIndex& s, const std::string& path) { Ref _b(s); 
                 py::gil_scoped_release nogil;
                 translate([&] { s.ix.save(path); });
             },
@@ -211,16 +245,16 @@ PYBIND11_MODULE(_maivs, m) {
                 return p;
             },
             py::arg("path"))
-        .def("stats", [](PyIndex& s) { return s.ix.stats(); })
-        .def("__len__", [](PyIndex& s) { return s.ix.len(); })
-        .def("recommend", [](PyIndex& s) { return s.ix.recommend(); })
+        .def("stats", [](PyIndex& s) { Ref _b(s);  return s.ix.stats(); })
+        .def("__len__", [](PyIndex& s) { Ref _b(s);  return s.ix.len(); })
+        .def("recommend", [](PyIndex& s) { Ref _b(s);  return s.ix.recommend(); })
         // ---- not in the reference: hooks for the C-ABI tests and the benchmark ----
-        .def("set_gpu_build", [](PyIndex& s, bool on) { s.ix.set_gpu_build(on); },
+        .def("set_gpu_build", [](PyIndex& s, bool on) { Mut _b(s);  s.ix.set_gpu_build(on); },
              "Run the index build's k-means (train_centroids, the centroid tree) on the GPU; the "
              "result is bit-identical to the CPU build.")
         .def("_kmeans",
              [](PyIndex& s, const py::array& x, std::vector<uint32_t> rows, std::vector<std::vector<uint64_t>> jobs,
-                bool gpu) {
+                bool gpu) { Ref _b(s); 
                  F32Rows r = as_rows(x, "x", "x must be C-contiguous");
                  std::vector<maivs::KMeansJob> js;
                  size_t total = 0;
@@ -244,46 +278,46 @@ PYBIND11_MODULE(_maivs, m) {
              },
              py::arg("x"), py::arg("rows"), py::arg("jobs"), py::arg("gpu"),
              "One batch of k-means jobs (first, n, k, iters, seed) on the CPU or the GPU (test hook).")
-        .def("last_search_stats", [](PyIndex& s) { return stats_dict(s.last); },
+        .def("last_search_stats", [](PyIndex& s) { Ref _b(s);  return stats_dict(s.last); },
              "Device timings and work counters of the last search_batch call.")
-        .def("cellmajor_blocker", [](PyIndex& s, bool cell_major) { return s.ix.cellmajor_blocker(cell_major); },
+        .def("cellmajor_blocker", [](PyIndex& s, bool cell_major) { Ref _b(s);  return s.ix.cellmajor_blocker(cell_major); },
              py::arg("cell_major") = true)
-        .def("perquery_blocker", [](PyIndex& s) { return s.ix.perquery_blocker(); })
-        .def("takes_cellmajor", [](PyIndex& s, size_t nq, bool cell_major) { return s.ix.takes_cellmajor(nq, cell_major); },
+        .def("perquery_blocker", [](PyIndex& s) { Ref _b(s);  return s.ix.perquery_blocker(); })
+        .def("takes_cellmajor", [](PyIndex& s, size_t nq, bool cell_major) { Ref _b(s);  return s.ix.takes_cellmajor(nq, cell_major); },
              py::arg("nq"), py::arg("cell_major") = true,
              "Whether search_batch(nq queries) takes the batched cell-major path (the reference's cm_ok).")
-        .def("set_batched_filter", [](PyIndex& s, bool on) { s.ix.set_batched_filter(on); },
+        .def("set_batched_filter", [](PyIndex& s, bool on) { Mut _b(s);  s.ix.set_batched_filter(on); },
              "Filtered searches take the batched path too (not in the reference; off by default).")
         .def("_arena_desc",
-             [](PyIndex& s) -> uintptr_t {
+             [](PyIndex& s) -> uintptr_t { Mut _b(s); 
                  const maivs_arena_desc* d = s.ix.arena_desc();
                  if (!d) throw py::value_error("index is not compacted");
                  return reinterpret_cast<uintptr_t>(d);
              },
              "Address of the maivs_arena_desc of the compacted arena (valid until the next mutation).")
         .def("_search_params",
-             [](PyIndex& s, size_t k, size_t nprobe, float tc, float beta) {
+             [](PyIndex& s, size_t k, size_t nprobe, float tc, float beta) { Ref _b(s); 
                  maivs_search_params p = s.ix.search_params(k, nprobe, tc, beta);
                  return py::bytes(reinterpret_cast<const char*>(&p), sizeof(p));
              },
              py::arg("k"), py::arg("nprobe"), py::arg("target_confidence") = 1.0f, py::arg("beta") = 8.0f,
              "The maivs_search_params struct search_batch would pass, as raw bytes.")
         .def("_ext_ids",
-             [](PyIndex& s) {
+             [](PyIndex& s) { Ref _b(s); 
                  const auto& e = s.ix.ext_ids();
                  py::array_t<uint64_t> a(static_cast<py::ssize_t>(e.size()));
                  std::memcpy(a.mutable_data(), e.data(), e.size() * sizeof(uint64_t));
                  return a;
              })
         .def("_codes",
-             [](PyIndex& s) {
+             [](PyIndex& s) { Ref _b(s); 
                  const auto& b = s.ix.bits();
                  py::array_t<uint64_t> a(static_cast<py::ssize_t>(b.size()));
                  std::memcpy(a.mutable_data(), b.data(), b.size() * sizeof(uint64_t));
                  return a;
              })
         .def("_arena_arrays",
-             [](PyIndex& s) {
+             [](PyIndex& s) { Ref _b(s); 
                  const maivs_arena_desc* a = s.ix.arena_desc();
                  if (!a) throw py::value_error("index is not compacted");
                  auto copy = [](const auto* p, size_t n) {
@@ -322,7 +356,7 @@ PYBIND11_MODULE(_maivs, m) {
              },
              "Copies of the compacted arena arrays (for brute-force checks).")
         .def("_tree_arrays",
-             [](PyIndex& s) -> py::object {
+             [](PyIndex& s) -> py::object { Ref _b(s); 
                  maivs::TreeFlat f;
                  if (!s.ix.tree_flat(f)) return py::none();
                  auto arr = [](const auto& v) {
@@ -343,7 +377,7 @@ PYBIND11_MODULE(_maivs, m) {
                  return d;
              },
              "The centroid tree as flat arrays (None without a tree).")
-        .def("_rot_signs", [](PyIndex& s) {
+        .def("_rot_signs", [](PyIndex& s) { Ref _b(s); 
             const auto& r = s.ix.rot_signs();
             py::array_t<float> a(static_cast<py::ssize_t>(r.size()));
             std::memcpy(a.mutable_data(), r.data(), r.size() * sizeof(float));

@@ -102,11 +102,17 @@ public:
     std::mutex mu;
 };
 
+// The GPU session, created once: concurrent searches (shared borrows) may both get here first.
+GpuSession* FlatCellIndex::session() {
+    std::lock_guard<std::mutex> lk(session_mu_);
+    if (!gpu_) gpu_ = std::make_unique<GpuSession>();
+    return gpu_.get();
+}
+
 // The k-means runner of the GPU build: every batch of jobs goes to maivs_gpu_kmeans, whose
 // results are bit-identical to run_kmeans_cpu's.
 KMeansRunner FlatCellIndex::gpu_kmeans_runner() {
-    if (!gpu_) gpu_ = std::make_unique<GpuSession>();
-    GpuSession* g = gpu_.get();
+    GpuSession* g = session();
     return [g](const float* x, size_t n_rows, size_t dim, const uint32_t* rows, const std::vector<KMeansJob>& jobs,
                std::vector<uint32_t>& assign, std::vector<float>& cents) {
         std::vector<maivs_kmeans_job> js;
@@ -580,7 +586,7 @@ void fill_tree_desc(const TreeFlat& tf, maivs_tree_desc& td) {
 // (assign_cells_routed), its 1-bit code and, when kept, its i8 / SQ8 copy.
 void FlatCellIndex::place_on_gpu(const float* data, size_t n, bool store_i8, std::vector<std::vector<uint32_t>>& asg,
                                  std::vector<uint64_t>& bits, std::vector<int8_t>& i8) {
-    if (!gpu_) gpu_ = std::make_unique<GpuSession>();
+    session();
     const size_t M = cells_.size(), ma = max_assign_;
     std::vector<float> cents(M * dim_);
     for (size_t c = 0; c < M; ++c) std::memcpy(&cents[c * dim_], cells_[c].centroid.data(), dim_ * sizeof(float));
@@ -1000,7 +1006,7 @@ std::string FlatCellIndex::perquery_blocker() const {
 }
 
 void FlatCellIndex::ensure_uploaded() {
-    if (!gpu_) gpu_ = std::make_unique<GpuSession>();
+    // called with the session's mutex held (searches serialise on it)
     if (gpu_->uploaded_gen != generation_) {
         gpu_->check(gpu_api().upload(gpu_->ctx_, arena_desc()), "maivs_gpu_upload_arena");
         gpu_->uploaded_gen = generation_;
@@ -1023,8 +1029,8 @@ void FlatCellIndex::search_batch(const float* q, size_t nq, size_t k, size_t npr
     const bool cm = takes_cellmajor(nq, cell_major);
     std::string why = cm ? cellmajor_blocker(true) : perquery_blocker();
     if (!why.empty()) throw Unsupported(why);
-    if (!gpu_) gpu_ = std::make_unique<GpuSession>();
-    std::lock_guard<std::mutex> lk(gpu_->mu);
+    GpuSession* g = session();
+    std::lock_guard<std::mutex> lk(g->mu);
     ensure_uploaded();
     maivs_search_params p = search_params(k, nprobe, tc, beta);
     std::vector<uint32_t> slots(nq * k);

@@ -10,6 +10,7 @@
 #include <cstdint>
 #include <map>
 #include <memory>
+#include <mutex>
 #include <optional>
 #include <stdexcept>
 #include <string>
@@ -208,6 +209,8 @@ private:
     bool gpu_build_ = false;
     bool batched_filter_ = false;
     std::unique_ptr<GpuSession> gpu_;
+    std::mutex session_mu_;  // guards the creation of gpu_ (searches share the index)
+    GpuSession* session();
 };
 
 }  // namespace maivs

@@ -364,3 +364,57 @@ def test_candidate_overflow_regrows(quality50k, mix50k, monkeypatch):
             assert st2.reruns == 0
     finally:
         c.close()
+
+
+def test_counters_after_a_per_query_call(quality50k, mix50k):
+    """After a per-query search the batched pass's seed cut-offs and work counters do not exist:
+    last_counters / last_candidates report that instead of reading stale per-batch state, and a
+    batched search afterwards reports its own counters again."""
+    _, queries, _ = mix50k
+    ix = quality50k
+    c = capi.Context(0)
+    try:
+        c.upload(ix._arena_desc())
+        p = _params(ix, 10, 16)
+        c.search(queries[:200], p)          # batched: sets rest_end and the counters
+        c.search_queries(queries[:7], _params(ix, 10, 600))  # per-query, a longer probe list
+        with pytest.raises(capi.GpuError) as e:
+            c.last_counters(capi.GpuStats())
+        assert e.value.status == capi.ERR_UNSUPPORTED
+        with pytest.raises(capi.GpuError):
+            c.last_candidates(7, 1024)
+        st = capi.GpuStats()
+        c.search(queries[:200], p)
+        c.last_counters(st)
+        assert st.seed_blocks > 0 and st.rerank_rows > 0
+    finally:
+        c.close()
+
+
+def test_small_arena_upload_keeps_larger_lds_limits(mix50k):
+    """Uploading an arena with a small dimension on a second context must not lower the kernels'
+    LDS limits that a larger arena's searches rely on: index A (d = 768) searched, index B (d = 64)
+    uploaded elsewhere, then A searched again without a re-upload, equal to the oracle."""
+    import maivs_amd as M
+    from .conftest import small_clustered
+    base, queries, _ = mix50k
+    xa = np.ascontiguousarray(np.concatenate([base[:6000], base[6000:12000]], axis=1))
+    xa /= np.linalg.norm(xa, axis=1, keepdims=True)
+    qa = np.ascontiguousarray(np.concatenate([queries[:300], queries[300:600]], axis=1))
+    qa /= np.linalg.norm(qa, axis=1, keepdims=True)
+    ia = M.build_preset(xa.astype(np.float32), "quality")
+    ib = M.build_preset(small_clustered(3000, 64), "quality")
+    ca, cb = capi.Context(0), capi.Context(0)
+    try:
+        ca.upload(ia._arena_desc())
+        p = _params(ia, 10, 24)
+        s1, v1 = ca.search(qa, p)
+        cb.upload(ib._arena_desc())
+        cb.search(small_clustered(64, 64, seed=3), _params(ib, 10, 8))
+        s2, v2 = ca.search(qa, p)
+        o_s, o_v = oracle.search_batch(ia._arena_desc(), qa, p, 8)
+        assert np.array_equal(s1, o_s) and v1.tobytes() == o_v.tobytes()
+        assert np.array_equal(s2, o_s) and v2.tobytes() == o_v.tobytes()
+    finally:
+        ca.close()
+        cb.close()

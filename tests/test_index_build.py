@@ -218,3 +218,43 @@ def test_mixture_generator_is_deterministic():
     assert np.allclose(np.linalg.norm(a1, axis=1), 1.0, atol=1e-5)
     b, s = mixture.workload("mix500k-shift", n=1000, nq=20)
     assert b.shape == (1000, 384) and s.shape == (20, 384)
+
+
+def test_overlapping_calls_follow_the_borrow_rules():
+    """A mutation that released the GIL holds the index exclusively: a search, a read or another
+    mutation that overlaps it raises RuntimeError with pyo3's messages (src/concurrent.rs:3-5),
+    and the index works again once the mutation ends. Runs on the CPU: add_batch of 200k vectors
+    keeps the exclusive borrow for long enough to be seen from the main thread."""
+    import threading
+
+    x = small_clustered(200_000, 64, 50, seed=7)
+    ix = M.FlatCellIndex(64, "binary", 8)
+    ix.train_centroids(x[:20_000], 64)
+    errs, done = [], threading.Event()
+
+    def mutate():
+        try:
+            ix.add_batch(list(range(len(x))), x)
+        except Exception as e:  # pragma: no cover - reported below
+            errs.append(e)
+        finally:
+            done.set()
+
+    t = threading.Thread(target=mutate)
+    t.start()
+    seen_read = seen_mut = None
+    while not done.is_set() and (seen_read is None or seen_mut is None):
+        try:
+            len(ix)
+        except RuntimeError as e:
+            seen_read = str(e)
+        try:
+            ix.set_adaptive(True, 0.02)
+        except RuntimeError as e:
+            seen_mut = str(e)
+    t.join()
+    assert not errs, errs
+    assert seen_read == "Already mutably borrowed"
+    assert seen_mut == "Already borrowed"
+    assert len(ix) == len(x)
+    ix.set_adaptive(True, 0.02)  # free again

@@ -149,6 +149,122 @@ def test_fs_query_estimator_bound():
             assert abs(est - exact) <= 64.0 * float(delta) + 1e-4
 
 
+def _fwht_textbook_f32(x):
+    """The textbook iterative FWHT in float32: levels h = 1, 2, 4, ..., n/2 in ascending order,
+    butterflies (u + v, u - v), then one multiply by 1/sqrt(n) computed in f32. Butterflies of one
+    level are independent, so only the level order fixes the rounding; the reference states its
+    8-block form is bit-identical to this loop (src/quantize.rs:73-75, 103-121)."""
+    a = np.array(x, np.float32).copy()
+    n = len(a)
+    h = 1
+    while h < n:
+        v = a.reshape(-1, 2, h)
+        u, w = v[:, 0, :].copy(), v[:, 1, :].copy()
+        v[:, 0, :] = u + w
+        v[:, 1, :] = u - w
+        h *= 2
+    s = np.float32(1.0) / np.sqrt(np.float32(n))
+    return a * s
+
+
+def _fwht_descending_f32(x):
+    a = np.array(x, np.float32).copy()
+    n = len(a)
+    h = n // 2
+    while h >= 1:
+        v = a.reshape(-1, 2, h)
+        u, w = v[:, 0, :].copy(), v[:, 1, :].copy()
+        v[:, 0, :] = u + w
+        v[:, 1, :] = u - w
+        h //= 2
+    return a * (np.float32(1.0) / np.sqrt(np.float32(n)))
+
+
+@pytest.mark.parametrize("n", [8, 16, 64, 512, 1024])
+def test_fht_bit_identical_to_textbook_level_order(n):
+    rs = np.random.RandomState(100 + n)
+    for trial in range(8):
+        x = (rs.standard_normal(n) * (10.0 ** rs.randint(-3, 4))).astype(np.float32)
+        got = oracle.fht(x)
+        want = _fwht_textbook_f32(x)
+        assert got.tobytes() == want.tobytes(), (n, trial)
+    # the check can tell level orders apart: on these inputs a descending-level transform,
+    # equal in exact arithmetic, rounds differently somewhere
+    if n >= 64:
+        x = rs.standard_normal(n).astype(np.float32)
+        assert _fwht_descending_f32(x).tobytes() != oracle.fht(x).tobytes()
+
+
+def test_rotate_is_two_rounds_of_textbook_fwht():
+    """rotate = copy + zero-pad, then twice (multiply by the round's signs, FWHT)
+    (src/quantize.rs:152-163), bit for bit."""
+    signs = oracle.make_signs(512, 0x5EED)
+    rs = np.random.RandomState(17)
+    for _ in range(4):
+        q = rs.standard_normal(384).astype(np.float32)
+        x = np.zeros(512, np.float32)
+        x[:384] = q
+        for r in range(2):
+            x = _fwht_textbook_f32(x * signs[r * 512:(r + 1) * 512])
+        assert oracle.rotate(q, signs, 512).tobytes() == x.tobytes()
+
+
+def test_fs_query_every_entry_within_half_a_step():
+    """Every table entry is the nearest integer to (raw - min_j) / delta: |lut * delta - (raw - min_j)|
+    <= delta / 2 (with the division's own rounding as slack), raw being the 4-term sign sum of the
+    position (src/quantize.rs:279-308), recomputed here in float64 from rq."""
+    rs = np.random.RandomState(19)
+    signs = oracle.make_signs(512, 0x5EED)
+    for _ in range(10):
+        q = rs.standard_normal(384).astype(np.float32)
+        rq = oracle.rotate(q, signs, 512)
+        lut, delta, bias = oracle.fs_query(rq, 8)
+        d = float(delta)
+        tab = lut.reshape(128, 16).astype(np.float64)
+        x = rq.astype(np.float64).reshape(128, 4)
+        e = np.arange(16)
+        sgn = np.where(((e[:, None] >> np.arange(4)[None, :]) & 1) == 1, -1.0, 1.0)  # (16, 4)
+        raw = x @ sgn.T  # (128, 16)
+        mins = raw.min(axis=1, keepdims=True)
+        err = np.abs(tab * d - (raw - mins))
+        assert err.max() <= 0.5 * d * (1 + 1e-5) + 1e-6
+        # bias = the sum of the per-position minima, to within an f32 running sum's error bound
+        bound = 128 * np.finfo(np.float32).eps * float(np.abs(mins).sum())
+        assert abs(float(bias) - float(mins.sum())) <= bound
+
+
+def test_fs_query_rounds_half_away_from_zero():
+    """(raw - min) / delta exactly k + 1/2 rounds up (Rust's f32::round, src/quantize.rs:302), which
+    a round-half-to-even (rint) slip would not. Position 0 spans 255 (x = 127.5), so delta = 1.0
+    exactly; position 1 holds x = (1.25, 0.25), whose raw - min values are 0, 0.5, 2.5 and 3.0."""
+    rq = np.zeros(64, np.float32)
+    rq[0] = 127.5
+    rq[4], rq[5] = 1.25, 0.25
+    lut, delta, bias = oracle.fs_query(rq, 1)
+    assert float(delta) == 1.0
+    tab = lut.reshape(16, 16)  # nw = 1: 16 positions; position j = 2p + half at p*32 + half*16
+    # position 0: raw = +-127.5 -> entries 0 / 255
+    assert tab[0, 0] == 255 and tab[0, 1] == 0
+    # position 1, e = bits of (t0, t1): raw = (+-1.25) + (+-0.25), min = -1.5
+    want = {0: 3, 1: 1, 2: 3, 3: 0}  # 3.0 -> 3, 0.5 -> 1 (rint: 0), 2.5 -> 3 (rint: 2), 0 -> 0
+    for e_lo, v in want.items():
+        for hi in range(4):  # t2, t3 carry x = 0
+            assert tab[1, e_lo | (hi << 2)] == v, (e_lo, hi)
+    assert float(bias) == -127.5 - 1.5
+
+
+def test_product_signs_are_the_splitmix64_stream():
+    """The index's own rotation signs (what the product uploads and the GPU rotates with) are
+    splitmix64's stream from the index seed: +1 for an even output, -1 for an odd one, two rounds
+    of dim_pad (src/quantize.rs:132-148)."""
+    import maivs_amd as M
+    for seed, dim, pad in ((0x5EED, 384, 512), (7, 64, 64), (123456789, 100, 128)):
+        ix = M.FlatCellIndex(dim, "binary", 8, seed)
+        got = np.asarray(ix._rot_signs(), np.float32)
+        want = np.array([1.0 if (z & 1) == 0 else -1.0 for z in splitmix64(seed, 2 * pad)], np.float32)
+        assert got.shape == want.shape and np.array_equal(got, want), seed
+
+
 # ---- exact-rational emulation of the 8-lane FMA dots ----
 
 def _f32_round(v: Fraction) -> np.float32:
