@@ -164,6 +164,27 @@ int maivs_gpu_search_batch_device(maivs_gpu_ctx* ctx, const float* d_queries, ui
                                   const maivs_search_params* params, uint32_t* d_out_slots,
                                   float* d_out_scores, maivs_gpu_stats* stats);
 
+/* Bytes of the fixed device array maivs_gpu_search_batch_device_noalloc works in (one per GPU). */
+#define MAIVS_GPU_SCRATCH_BYTES ((size_t)128 << 20)
+
+/*
+ * No counterpart in the reference. For callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): the same search as
+ * maivs_gpu_search_batch_device, with identical results, that allocates nothing. Every work buffer
+ * is carved from a fixed array of MAIVS_GPU_SCRATCH_BYTES that the library holds on each GPU it
+ * runs on until the process ends; queries and outputs stay the caller's. A batch whose buffers do
+ * not fit runs as equal chunks of the largest size that does (queries are independent, so results
+ * do not change); MAIVS_ERR_UNSUPPORTED when even one query does not fit (very long probe lists or
+ * indexes of more than 8,192 cells, whose Hamming rows live in global memory). Calls on one GPU
+ * share its array and keep the last call's contents: the library runs them one at a time within a
+ * process, and each call clears what must start at zero. The call runs its stages without a HIP
+ * graph and leaves the context's own buffers, and what maivs_gpu_last_candidates /
+ * maivs_gpu_last_counters read, untouched (they report nothing after it).
+ */
+int maivs_gpu_search_batch_device_noalloc(maivs_gpu_ctx* ctx, const float* d_queries, uint32_t nq,
+                                          const maivs_search_params* params, uint32_t* d_out_slots,
+                                          float* d_out_scores, maivs_gpu_stats* stats);
+
 /*
  * The per-query path: the reference's search_one (src/index.rs:1381-1864) for every query on its
  * own, as its search() and its search_batch for small batches, filtered searches and

@@ -65,6 +65,7 @@ SIGNATURES = {
     "maivs_gpu_upload_arena": (I32, [P, P]),
     "maivs_gpu_search_batch": (I32, [P, P, U32, C.POINTER(SearchParams), P, P, C.POINTER(GpuStats)]),
     "maivs_gpu_search_batch_device": (I32, [P, P, U32, C.POINTER(SearchParams), P, P, C.POINTER(GpuStats)]),
+    "maivs_gpu_search_batch_device_noalloc": (I32, [P, P, U32, C.POINTER(SearchParams), P, P, C.POINTER(GpuStats)]),
     "maivs_gpu_query_prep": (I32, [P, P, U32, P, P, P, P]),
     "maivs_gpu_block_sums": (I32, [P, U32, P, P, U32, P]),
     "maivs_gpu_route": (I32, [P, P, U32, C.POINTER(SearchParams), P, P, P]),
@@ -149,6 +150,14 @@ class Context:
                                                            C.c_void_p(slots_ptr), C.c_void_p(scores_ptr),
                                                            C.byref(stats) if stats is not None else None),
                     "maivs_gpu_search_batch_device")
+
+    def search_device_noalloc(self, q_ptr: int, nq: int, params: SearchParams, slots_ptr: int, scores_ptr: int,
+                              stats: GpuStats | None = None) -> None:
+        """maivs_gpu_search_batch_device_noalloc: device buffers, no device allocation."""
+        self._check(self.lib.maivs_gpu_search_batch_device_noalloc(self.h, C.c_void_p(q_ptr), nq, C.byref(params),
+                                                                   C.c_void_p(slots_ptr), C.c_void_p(scores_ptr),
+                                                                   C.byref(stats) if stats is not None else None),
+                    "maivs_gpu_search_batch_device_noalloc")
 
     def search_queries(self, q: np.ndarray, params: SearchParams, stats: GpuStats | None = None):
         """The per-query path (maivs_gpu_search_queries)."""

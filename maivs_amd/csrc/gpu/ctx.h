@@ -67,6 +67,8 @@ struct maivs_gpu_ctx {
     std::vector<uint32_t> tree_level_n;
     float tree_beam_frac = 0.5f;
     uint32_t tree_min_beam = 32;
+    // this device's fixed scratch array (ScratchSlot, maivs_gpu.hip), set at create
+    void* scratch = nullptr;
 };
 
 namespace maivs_host {

@@ -990,6 +990,42 @@ int run_search_pq(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs
 
 }  // namespace
 
+// ================================================================ the fixed scratch array
+
+// The work area of maivs_gpu_search_batch_device_noalloc: every work buffer of a batched call is
+// carved from it, so that entry point allocates nothing. Each GPU the library runs on holds its
+// own copy at its own address, from the code object's load until the process ends. In host code
+// the name is only a stand-in for the symbol: kernels and copies get the per-device address that
+// hipGetSymbolAddress returns (kept in ScratchSlot::ptr), never `scratch` itself.
+static __device__ __align__(256) uint8_t scratch[MAIVS_GPU_SCRATCH_BYTES];
+
+namespace {
+
+struct ScratchSlot {
+    uint8_t* ptr = nullptr;  // this device's copy of `scratch`
+    hipError_t lookup = hipSuccess;
+    std::mutex run;          // calls on one GPU share the array: they run one at a time
+};
+
+// This device's scratch slot; the symbol's address is looked up once per device, with that device
+// current (maivs_gpu_create calls this after hipSetDevice).
+ScratchSlot* scratch_slot(int device) {
+    static std::mutex mu;
+    static std::map<int, ScratchSlot*> slots;  // never freed: the array lives as long as the process
+    std::lock_guard<std::mutex> lk(mu);
+    ScratchSlot*& s = slots[device];
+    if (!s) {
+        s = new ScratchSlot();
+        void* p = nullptr;
+        s->lookup = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        s->ptr = s->lookup == hipSuccess ? static_cast<uint8_t*>(p) : nullptr;
+        (void)hipGetLastError();
+    }
+    return s;
+}
+
+}  // namespace
+
 // ================================================================ C ABI
 
 extern "C" {
@@ -1032,6 +1068,8 @@ int maivs_gpu_create(int device, maivs_gpu_ctx** out) {
     }
     std::memset(ctx->h_ctl, 0, sizeof(Ctl));
     ctx->Wk.h_ctl = static_cast<Ctl*>(dev_ctl);
+    // the no-allocation entry point's array on this device (device current)
+    ctx->scratch = scratch_slot(device);
     *out = ctx;
     return 0;
 }
@@ -1282,6 +1320,118 @@ int maivs_gpu_search_batch_device(maivs_gpu_ctx* ctx, const float* d_q, uint32_t
     std::lock_guard<std::mutex> lk(ctx->mu);
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     return run_search(ctx, d_q, nq, p, d_slots, d_scores, st);
+}
+
+int maivs_gpu_search_batch_device_noalloc(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq,
+                                          const maivs_search_params* p, uint32_t* d_slots, float* d_scores,
+                                          maivs_gpu_stats* st) {
+    if (!ctx || !p || (nq && (!d_q || !d_slots || !d_scores))) return MAIVS_ERR_ARG;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    if (!ctx->uploaded) return fail(ctx, MAIVS_ERR_NOT_UPLOADED, "no arena uploaded");
+    if (p->k == 0) return fail(ctx, MAIVS_ERR_ARG, "k must be > 0");
+    ScratchSlot* slot = static_cast<ScratchSlot*>(ctx->scratch);
+    if (!slot || !slot->ptr)
+        return fail(ctx, MAIVS_ERR_HIP, "the scratch array of device %d is unavailable: hipGetSymbolAddress: %s",
+                    ctx->device, hipGetErrorString(slot ? slot->lookup : hipErrorInvalidValue));
+    if (st) *st = maivs_gpu_stats{};
+    if (nq == 0) return 0;
+    const DevArena& A = ctx->A;
+    const uint32_t nprobe = std::max<uint32_t>(p->nprobe, 1), k = std::max<uint32_t>(p->k, 1);
+    const size_t bytes = MAIVS_GPU_SCRATCH_BYTES;
+    const uint32_t cand_cap = std::max<uint32_t>(ctx->initial_cand_cap, 64);
+    // Bytes of one chunk of n queries: its work buffers, then its candidate buffers at the room
+    // the context starts with (an overflow re-carves them within the array).
+    auto need = [&](uint32_t n, size_t* cand_off) {
+        Work tmp{};
+        Carver c{nullptr};
+        carve_work(A, n, nprobe, k, ctx->seed_cap, bucket_cap_for(A, n, nprobe), false, c, tmp);
+        if (cand_off) *cand_off = c.used;
+        carve_cand(n, ctx->seed_cap, cand_cap, c, tmp);
+        return c.used;
+    };
+    // Queries are independent, so a batch larger than the array holds runs as equal chunks of the
+    // largest size that fits, with results identical to one pass.
+    uint32_t chunk = nq;
+    if (need(chunk, nullptr) > bytes) {
+        uint32_t lo = 0, hi = nq;  // need(lo) fits (lo = 0 meaning none), need(hi) does not
+        while (hi - lo > 1) {
+            const uint32_t mid = lo + (hi - lo) / 2;
+            (need(mid, nullptr) <= bytes ? lo : hi) = mid;
+        }
+        if (lo == 0)
+            return fail(ctx, MAIVS_ERR_UNSUPPORTED,
+                        "one query at nprobe %u needs %zu bytes of work buffers, more than the %zu-byte scratch "
+                        "(use maivs_gpu_search_batch_device)",
+                        nprobe, need(1, nullptr), bytes);
+        const uint32_t parts = (nq + lo - 1) / lo;
+        chunk = (nq + parts - 1) / parts;
+    }
+
+    // one call at a time on this GPU's array; the call returns only after its kernels are done
+    std::lock_guard<std::mutex> run(slot->run);
+    // the context's own buffers and their state are set aside and restored afterwards
+    const Work own = ctx->Wk;
+    const uint32_t s_nq = ctx->cap_nq, s_np = ctx->cap_nprobe, s_k = ctx->cap_k, s_cand = ctx->cap_cand,
+                   s_seed = ctx->cap_seed, s_fin = ctx->cap_fin, s_key = ctx->cap_key, s_b = ctx->cap_bucket,
+                   s_cnq = ctx->cand_nq;
+    const bool s_clean = ctx->counters_clean;
+    int rc = 0;
+    for (uint32_t q0 = 0; q0 < nq && rc == 0; q0 += chunk) {
+        const uint32_t n = std::min(chunk, nq - q0);
+        const uint32_t bcap = bucket_cap_for(A, n, nprobe);
+        size_t cand_off = 0;
+        need(n, &cand_off);
+        Work W = own;  // keeps the pinned control-block mirror and the per-query path's fields
+        Carver cw{slot->ptr};
+        carve_work(A, n, nprobe, k, ctx->seed_cap, bcap, false, cw, W);
+        Carver cc{slot->ptr};
+        cc.used = cand_off;
+        carve_cand(n, ctx->seed_cap, cand_cap, cc, W);
+        ctx->Wk = W;
+        ctx->cap_nq = n;
+        ctx->cap_nprobe = nprobe;
+        ctx->cap_k = k;
+        ctx->cap_seed = ctx->seed_cap;
+        ctx->cap_bucket = bcap;
+        ctx->cap_cand = cand_cap;
+        ctx->cand_nq = n;
+        cand_caps(ctx->cap_seed, cand_cap, &ctx->cap_fin, &ctx->cap_key);
+        ctx->counters_clean = false;  // the array holds the last call's contents: clear the counters first
+        const Scratch sc{slot->ptr, bytes, cand_off};
+        maivs_gpu_stats part{};
+        rc = run_search(ctx, d_q + static_cast<uint64_t>(q0) * A.d, n, p, d_slots + static_cast<uint64_t>(q0) * p->k,
+                        d_scores + static_cast<uint64_t>(q0) * p->k, st ? &part : nullptr, &sc);
+        if (st && rc == 0) {
+            st->ms_total += part.ms_total;
+            st->ms_prep += part.ms_prep;
+            st->ms_route += part.ms_route;
+            st->ms_seed += part.ms_seed;
+            st->ms_invert += part.ms_invert;
+            st->ms_scan += part.ms_scan;
+            st->ms_select += part.ms_select;
+            st->ms_rerank += part.ms_rerank;
+            st->host_checks += part.host_checks;
+            st->host_fixes += part.host_fixes;
+            st->reruns += part.reruns;
+        }
+    }
+    const hipError_t sync = hipStreamSynchronize(ctx->stream);
+    ctx->Wk = own;
+    ctx->cap_nq = s_nq;
+    ctx->cap_nprobe = s_np;
+    ctx->cap_k = s_k;
+    ctx->cap_cand = s_cand;
+    ctx->cap_seed = s_seed;
+    ctx->cap_fin = s_fin;
+    ctx->cap_key = s_key;
+    ctx->cap_bucket = s_b;
+    ctx->cand_nq = s_cnq;
+    ctx->counters_clean = s_clean;
+    ctx->last_nq = 0;  // the stage read-backs read the context's own buffers, which this call left alone
+    if (rc) return rc;
+    if (sync != hipSuccess) return fail(ctx, MAIVS_ERR_HIP, "hipStreamSynchronize: %s", hipGetErrorString(sync));
+    return 0;
 }
 
 int maivs_gpu_search_batch(maivs_gpu_ctx* ctx, const float* q, uint32_t nq, const maivs_search_params* p,
