@@ -35,6 +35,7 @@ _SIGS = {
     "orc_search_batch": (C.c_int, [P, P, U32, C.POINTER(SearchParams), U32, P, P]),
     "orc_last_candidates": (C.c_int, [P, P, P, P, P, P, U64]),
     "orc_last_total_candidates": (U64, []),
+    "orc_set_record": (None, [C.c_int]),
     "orc_search_one": (C.c_int, [P, P, U32, C.POINTER(SearchParams), U32, P, P]),
     "orc_route_query": (C.c_int, [P, P, U32, C.POINTER(SearchParams), U32, P, P, P]),
 }
@@ -198,3 +199,9 @@ def last_candidates(nq: int):
     if rc != 0:
         raise RuntimeError("orc_last_candidates failed")
     return tau, rest_end, cut, ncand, slots[:total], dd[:total]
+
+
+def set_record(on: bool) -> None:
+    """Keep (True, the default) or skip each query's candidate list for last_candidates; the CPU
+    baseline's timing runs skip it, as the reference keeps nothing of the kind."""
+    lib().orc_set_record(1 if on else 0)

@@ -62,6 +62,9 @@ struct LastRun {
     std::vector<uint32_t> tau, rest_end, cut;
     std::vector<std::vector<Cand>> cands;
 } g_last;
+// whether orc_search_batch keeps each query's candidates for orc_last_candidates (the timing
+// runs of the CPU baseline switch it off: the reference keeps nothing of the kind)
+bool g_record = true;
 
 }  // namespace
 
@@ -595,10 +598,11 @@ int orc_search_batch(const maivs_arena_desc* a, const float* data, uint32_t nq, 
         }
     });
     // 5. merge, exact tie-inclusive cut at target, rerank (src/index.rs:2277-2311, 1309-1378)
-    g_last.tau.assign(nq, 0);
-    g_last.rest_end.assign(nq, 0);
-    g_last.cut.assign(nq, 0);
-    g_last.cands.assign(nq, {});
+    const bool record = g_record;
+    g_last.tau.assign(record ? nq : 0, 0);
+    g_last.rest_end.assign(record ? nq : 0, 0);
+    g_last.cut.assign(record ? nq : 0, 0);
+    g_last.cands.assign(record ? nq : 0, {});
     par_for(nthreads, nq, [&](size_t qi) {
         uint32_t t = gtau[qi].load(std::memory_order_relaxed);
         std::vector<Cand> v;
@@ -636,6 +640,7 @@ int orc_search_batch(const maivs_arena_desc* a, const float* data, uint32_t nq, 
             out_slots[qi * k + i] = i < kk ? scored[i].first : UINT32_MAX;
             out_scores[qi * k + i] = i < kk ? scored[i].second : -INFINITY;
         }
+        if (!record) return;
         std::sort(v.begin(), v.end(), [](const Cand& x, const Cand& y) { return x.d != y.d ? x.d < y.d : x.slot < y.slot; });
         g_last.tau[qi] = st[qi].tau;
         g_last.rest_end[qi] = st[qi].rest_end;
@@ -644,6 +649,8 @@ int orc_search_batch(const maivs_arena_desc* a, const float* data, uint32_t nq, 
     }, 4);
     return 0;
 }
+
+void orc_set_record(int on) { g_record = on != 0; }
 
 uint64_t orc_last_total_candidates(void) {
     uint64_t n = 0;
