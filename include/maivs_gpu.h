@@ -52,7 +52,7 @@ enum {
 };
 
 /*
- * The compacted index, as host pointers. Caller-owned; maivs_gpu_upload_arena copies every
+ * The index, as host pointers (compacted with FastScan blocks, or else with per-slot codes). Caller-owned; maivs_gpu_upload_arena copies every
  * array to HBM and keeps nothing of the caller's. Shapes use d = dim, P = dim_pad,
  * W = n_words, M = n_cells, N = n_slots, E = mem_off[M], B = fs_off[M].
  */
@@ -89,6 +89,11 @@ typedef struct maivs_arena_desc {
     const uint32_t* tags;       /* N */
     /* the centroid tree the per-query path routes with (n_levels 0: none); defined below */
     const struct maivs_tree_desc* tree;
+    /* Per-slot sign codes, N * W. An index that is not compacted, or has no FastScan blocks, is
+     * uploaded with fs_codes and fs_off NULL and these instead: its cells' members are then in any
+     * order, and only the per-query path runs, scanning them with Hamming distances (search_one's
+     * Hamming branch, src/index.rs:1694-1760). Ignored when fs_codes is given. */
+    const uint64_t* slot_codes;
 } maivs_arena_desc;
 
 /* Query-time settings of search_batch (src/index.rs:3316-3326 and the index setters). */

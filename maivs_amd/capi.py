@@ -30,7 +30,7 @@ class ArenaDesc(C.Structure):
         ("slot_cells", C.c_void_p), ("cent_bits", C.c_void_p), ("cent_sq8", C.c_void_p),
         ("centroids", C.c_void_p), ("csq_min", C.c_void_p), ("csq_step", C.c_void_p), ("r_bound", C.c_void_p),
         ("rot_signs", C.c_void_p), ("vecs_f32", C.c_void_p), ("sq8_codes", C.c_void_p), ("sq_min", C.c_void_p),
-        ("sq_step", C.c_void_p), ("tags", C.c_void_p), ("tree", C.c_void_p),
+        ("sq_step", C.c_void_p), ("tags", C.c_void_p), ("tree", C.c_void_p), ("slot_codes", C.c_void_p),
     ]
 
 

@@ -160,6 +160,21 @@ struct Code {
     }
 };
 
+// Hamming distance of a member's code to the query's code words (qd: the query's 2 * NW dwords).
+template <int NW>
+__device__ __forceinline__ uint32_t code_hamming(const Code<NW>& c, const uint32_t (&qd)[2 * NW]) {
+    if constexpr (NW == 1) {
+        return __popc(c.v[0].x ^ qd[0]) + __popc(c.v[0].y ^ qd[1]);
+    } else {
+        uint32_t h = 0;
+#pragma unroll
+        for (int k = 0; k < Code<NW>::NCH; ++k)
+            h += __popc(c.v[k].x ^ qd[4 * k]) + __popc(c.v[k].y ^ qd[4 * k + 1]) + __popc(c.v[k].z ^ qd[4 * k + 2]) +
+                 __popc(c.v[k].w ^ qd[4 * k + 3]);
+        return h;
+    }
+}
+
 template <int NW, int G>
 __device__ __forceinline__ void lut_sums(const Code<NW>& c, const uint8_t* table, uint32_t (&sum)[G]) {
     static_assert(G == 1 || G == 4, "G is 1 or 4");
@@ -401,6 +416,16 @@ __global__ void reset_kernel(Work Wk, uint32_t M, uint32_t nq) {
     if (i == 0) *Wk.done = 0;
     for (uint32_t j = i; j <= M; j += stride) Wk.cell_cnt[j] = 0;
     for (uint32_t j = i; j < nq; j += stride) Wk.cand_cnt[j] = 0;
+}
+
+// Entry-major codes of an index without FastScan blocks: entry e gets its slot's code words.
+__global__ void gather_codes_kernel(const uint64_t* __restrict__ slot_codes, const uint32_t* __restrict__ members,
+                                    uint64_t E, uint32_t W, uint64_t* __restrict__ codes) {
+    for (uint64_t i = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x; i < E * W;
+         i += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
+        const uint64_t e = i / W, w = i - e * W;
+        codes[i] = slot_codes[static_cast<uint64_t>(members[e]) * W + w];
+    }
 }
 
 // Padded results (no cell probed): no slot, score -inf (src/index.rs:3353-3361).
@@ -2331,9 +2356,15 @@ __device__ __forceinline__ bool pq_seen(const DevArena& A, uint64_t e, uint32_t 
 constexpr uint32_t kPqStage = 2048;  // survivor keys staged in LDS for the final selection
 
 // pair: the pair table's W * 1024 words (W * 4 KB) at the end
+// Bucket-queue bins of the per-query scan: h = d >> 6 of the FastScan distance, or (ham) the
+// Hamming distance itself, 0 .. W * 64.
+__host__ __device__ inline uint32_t pq_bins(uint32_t maxk, uint32_t W, bool ham) {
+    return ham ? W * 64 + 1 : (maxk >> 6) + 1;
+}
+
 __host__ __device__ inline uint32_t pq_scan_lds_words(uint32_t MW, uint32_t maxk, uint32_t nprobe, uint32_t W = 0,
-                                                      bool pair = false) {
-    const uint32_t nbins = (maxk >> 6) + 1;
+                                                      bool pair = false, bool ham = false) {
+    const uint32_t nbins = pq_bins(maxk, W, ham);
     return ((MW + 3) & ~3u) + ((nbins + 3) & ~3u) + ((nprobe + 1 + 3) & ~3u) + kHistBins + 32 + 2 * kPqStage +
            (pair ? W * 1024 : 0u);
 }
@@ -2348,7 +2379,11 @@ __host__ __device__ inline uint32_t pq_scan_lds_words(uint32_t MW, uint32_t maxk
 // LDS: static table[W*256] | scanned[MW4] | hist[bins4] | suffix[np4] | hist2[256] | scratch[32] |
 // stage[kPqStage] u64 | pair[W*2048] u16 (K.pq_pair).
 // With K.pq_pair the lookups go through a table of position pairs built from the query's table.
-template <int NW>
+// HAM: the Hamming branch instead (src/index.rs:1694-1760; an index without FastScan blocks): the
+// distance of a member is its Hamming distance h to the query's code, the bucket queue runs on h
+// itself from tau = W * 64, the adaptive stop compares with cos(pi * tau / dp) (the host's libm
+// value, A.ham_cos[tau]), and every survivor h <= tau, ties included, goes to the rerank.
+template <int NW, bool HAM = false>
 __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work Wk, KParams K) {
     constexpr uint32_t TB = NW * 256;
     __shared__ __align__(16) uint8_t table[TB];
@@ -2357,7 +2392,14 @@ __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work 
     const uint32_t qi = blockIdx.x;
     if (qi >= K.nq) return;
     const uint32_t tid = threadIdx.x, nt = blockDim.x, lane = lane_id();
-    const uint32_t nbins = (A.maxk >> 6) + 1;
+    const uint32_t nbins = pq_bins(A.maxk, NW, HAM);
+    auto bucket = [](uint32_t dv) { return HAM ? dv : dv >> 6; };
+    uint32_t qd[2 * NW];
+    if constexpr (HAM) {
+        const uint32_t* qb = reinterpret_cast<const uint32_t*>(Wk.qbits + static_cast<uint64_t>(qi) * NW);
+#pragma unroll
+        for (int j = 0; j < 2 * NW; ++j) qd[j] = qb[j];
+    }
     uint32_t* scanned = pq_smem;
     uint32_t* hist = scanned + ((A.MW + 3) & ~3u);
     float* suffix = reinterpret_cast<float*>(hist + ((nbins + 3) & ~3u));
@@ -2365,11 +2407,11 @@ __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work 
     uint32_t* scratch = hist2 + kHistBins;
     uint64_t* stage = reinterpret_cast<uint64_t*>(scratch + 32);  // 8-byte aligned: every region is a multiple of 16 bytes
     uint16_t* pair = reinterpret_cast<uint16_t*>(stage + kPqStage);
-    {
+    if (!HAM) {
         const uint4* src = reinterpret_cast<const uint4*>(Wk.lut + static_cast<uint64_t>(qi) * TB);
         for (uint32_t i = tid; i < TB / 16; i += nt) reinterpret_cast<uint4*>(table)[i] = src[i];
     }
-    if (K.pq_pair) {
+    if (!HAM && K.pq_pair) {
         // entry p*256 + (a | b << 4) = table[2p][a] + table[2p+1][b], two entries per thread per step
         __syncthreads();
         for (uint32_t i = 2 * tid; i < NW * 2048; i += 2 * nt) {
@@ -2404,7 +2446,7 @@ __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work 
     }
     if (tid == 0) {
         s_cnt = 0;
-        s_tau = A.maxk >> 6;
+        s_tau = HAM ? NW * 64 : A.maxk >> 6;
         s_kept = 0;
         s_stop = 0;
     }
@@ -2466,8 +2508,11 @@ __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work 
             uint32_t dv = 0;
             if (m.have) {
                 const uint64_t e = static_cast<uint64_t>(e0) + base + tid;
-                dv = A.maxk - (K.pq_pair ? lut_sum_pair<NW>(m.code, pair) : lut_sum1<NW>(m.code, table));
-                if ((dv >> 6) <= tau) {
+                if constexpr (HAM)
+                    dv = code_hamming<NW>(m.code, qd);
+                else
+                    dv = A.maxk - (K.pq_pair ? lut_sum_pair<NW>(m.code, pair) : lut_sum1<NW>(m.code, table));
+                if (bucket(dv) <= tau) {
                     ok = !K.filter || (m.tag >= K.tag_lo && m.tag <= K.tag_hi);
                     if (ok && A.ma > 1) {
                         if (A.ma == 2)
@@ -2486,7 +2531,7 @@ __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work 
                 if (ok) {
                     const uint32_t pos = wb + lanes_below(bm);
                     if (pos < K.pq_cap) cbuf[pos] = (static_cast<uint64_t>(dv) << 32) | m.slot;
-                    atomicAdd(&hist[dv >> 6], 1u);
+                    atomicAdd(&hist[bucket(dv)], 1u);
                 }
             }
         }
@@ -2541,10 +2586,15 @@ __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work 
             uint32_t stop = 0;
             // the adaptive stop (:1727-1733)
             if (K.adaptive && kept >= target) {
-                const uint32_t top = ((t + 1) << 6) - 1;
-                const uint32_t worst = A.maxk > top ? A.maxk - top : 0u;
-                const float est = delta * static_cast<float>(worst) + bias;
-                const float thr = fminf(fmaxf(est / K.norm, -1.0f), 1.0f);
+                float thr;
+                if constexpr (HAM) {
+                    thr = A.ham_cos[t];  // score_to_cos(hamming_score(tau)), src/index.rs:1782-1786
+                } else {
+                    const uint32_t top = ((t + 1) << 6) - 1;
+                    const uint32_t worst = A.maxk > top ? A.maxk - top : 0u;
+                    const float est = delta * static_cast<float>(worst) + bias;
+                    thr = fminf(fmaxf(est / K.norm, -1.0f), 1.0f);
+                }
                 const float T = thr - K.at_margin;
                 const float sx = suffix[ci_i + 1];
                 if (!K.pq_noflag && fabsf(sx - T) <= K.prune_band) flagged = true;
@@ -2568,7 +2618,7 @@ __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work 
             for (uint32_t base = 0; base < n; base += nt) {
                 const uint32_t i = base + tid;
                 const uint64_t key = i < n ? cbuf[i] : 0ull;
-                const bool keepit = i < n && (static_cast<uint32_t>(key >> 32) >> 6) <= t;
+                const bool keepit = i < n && bucket(static_cast<uint32_t>(key >> 32)) <= t;
                 uint32_t tot;
                 const uint32_t off = block_excl_scan_u32(keepit ? 1u : 0u, scratch, &tot);
                 if (keepit) cbuf[s_w + off] = key;
@@ -2622,7 +2672,7 @@ __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work 
     auto key = [&](uint32_t i) -> uint64_t { return staged ? stage[i] : cbuf[i]; };
     auto surv_d = [&](uint32_t i) -> uint32_t {
         const uint32_t dv = static_cast<uint32_t>(key(i) >> 32);
-        return (dv >> 6) <= t ? dv : 0xFFFFFFFFu;
+        return bucket(dv) <= t ? dv : 0xFFFFFFFFu;
     };
     if (staged) {
         // wave 0 alone: the survivors' d (and slots) in registers, KPL per lane for the smallest KPL
@@ -2639,7 +2689,7 @@ __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work 
                 m += static_cast<uint32_t>(__popcll(__ballot(dv[r] != 0xFFFFFFFFu)));
             }
             uint32_t dcut = 0xFFFFFFFFu, scut = 0xFFFFFFFFu;
-            if (m > target) {
+            if (!HAM && m > target) {
                 dcut = wave_select_kth<KPL>(dv, target);
                 uint32_t below = 0, eq = 0;
 #pragma unroll
@@ -2685,7 +2735,7 @@ __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work 
     for (uint32_t i = tid; i < n; i += nt) m += surv_d(i) != 0xFFFFFFFFu;
     m = block_sum_u32(m, scratch);
     uint32_t dcut = 0xFFFFFFFFu, scut = 0xFFFFFFFFu;
-    if (m > target) {
+    if (!HAM && m > target) {
         dcut = select_kth(n, target, [&](uint32_t i) { const uint32_t v = surv_d(i); return v == 0xFFFFFFFFu ? 0xFFFFu : v; },
                           hist2, scratch);
         uint32_t below = 0;

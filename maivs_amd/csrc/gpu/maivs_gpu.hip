@@ -565,6 +565,9 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
     if (!ctx->uploaded) return fail(ctx, MAIVS_ERR_NOT_UPLOADED, "no arena uploaded");
     if (p->k == 0) return fail(ctx, MAIVS_ERR_ARG, "k must be > 0");
     const DevArena& A = ctx->A;
+    if (!A.fs)
+        return fail(ctx, MAIVS_ERR_UNSUPPORTED,
+                    "the batched path scans FastScan blocks; this arena has per-slot codes only (not compacted)");
     int rc = sc ? 0 : ensure_all(ctx, nq, p->nprobe, p->k);
     if (rc) return rc;
     Work& W = ctx->Wk;
@@ -823,15 +826,23 @@ int launch_pq_tree(maivs_gpu_ctx* ctx, const KParams& K, uint32_t cap) {
 
 int launch_pq_scan(maivs_gpu_ctx* ctx, const KParams& K) {
     const DevArena& A = ctx->A;
-    const size_t lds = static_cast<size_t>(pq_scan_lds_words(A.MW, A.maxk, K.nprobe, A.W, K.pq_pair != 0)) * 4;
+    const size_t lds =
+        static_cast<size_t>(pq_scan_lds_words(A.MW, A.maxk, K.nprobe, A.W, K.pq_pair != 0, K.pq_ham != 0)) * 4;
     if (lds + A.W * 256 + kScanThreads * 4 > kLdsBudget)
         return fail(ctx, MAIVS_ERR_UNSUPPORTED, "per-query scan needs %zu bytes of LDS", lds);
-    DISPATCH_NW(A.W, {
+    auto go = [&](const void* fn, auto kernel) -> int {
         int rc;
-        if (lds > 48 * 1024 && (rc = raise_lds_limit(ctx, reinterpret_cast<const void*>(pq_scan_kernel<NW>), lds)))
-            return rc;
-        hipLaunchKernelGGL(pq_scan_kernel<NW>, dim3(K.nq), dim3(kScanThreads), lds, ctx->stream, A, ctx->Wk, K);
-    });
+        if (lds > 48 * 1024 && (rc = raise_lds_limit(ctx, fn, lds))) return rc;
+        hipLaunchKernelGGL(kernel, dim3(K.nq), dim3(kScanThreads), lds, ctx->stream, A, ctx->Wk, K);
+        return 0;
+    };
+    int rc = 0;
+    if (K.pq_ham) {
+        DISPATCH_NW(A.W, rc = go(reinterpret_cast<const void*>(pq_scan_kernel<NW, true>), pq_scan_kernel<NW, true>));
+    } else {
+        DISPATCH_NW(A.W, rc = go(reinterpret_cast<const void*>(pq_scan_kernel<NW, false>), pq_scan_kernel<NW, false>));
+    }
+    if (rc) return rc;
     HIP_TRY(ctx, hipGetLastError());
     return 0;
 }
@@ -874,8 +885,13 @@ int run_search_pq(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs
     if ((rc = ensure_pq(ctx, nq, K.tcap, pq_need))) return rc;
     K.pq_cap = ctx->cap_pq;
     K.pq_noflag = 0;
+    // without FastScan blocks: search_one's Hamming branch (src/index.rs:1694-1760)
+    K.pq_ham = A.fs ? 0u : 1u;
     // small batches (at most one workgroup per CU) look up position pairs: half the LDS lookups
-    K.pq_pair = nq <= kPqPairMaxQ && pq_scan_lds_words(A.MW, A.maxk, K.nprobe, A.W, true) * 4 + A.W * 256 + kScanThreads * 4 <= kLdsBudget ? 1u : 0u;
+    K.pq_pair = !K.pq_ham && nq <= kPqPairMaxQ &&
+                        pq_scan_lds_words(A.MW, A.maxk, K.nprobe, A.W, true) * 4 + A.W * 256 + kScanThreads * 4 <= kLdsBudget
+                    ? 1u
+                    : 0u;
     if (p->nprobe == 0) {
         if ((rc = launch_pad(ctx, d_slots, d_scores, static_cast<uint64_t>(nq) * p->k))) return rc;
         HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
@@ -965,6 +981,14 @@ int run_search_pq(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs
                 K.pq_cap = ctx->cap_pq;
                 rerun = true;
             }
+            if (ctl.max_cand > ctx->cap_cand) {
+                // the Hamming branch keeps every tie at tau, possibly more than the candidate room
+                if ((rc = ensure_cand(ctx, ctl.max_cand + ctl.max_cand / 4 + 64))) return rc;
+                K.cand_cap = ctx->cap_cand;
+                K.fin_cap = ctx->cap_fin;
+                K.key_cap = ctx->cap_key;
+                rerun = true;
+            }
             if (!rerun) break;
             S.reruns++;
             if ((rc = launch_reset(ctx, nq)) || (rc = launch_pq_scan(ctx, K)) ||
@@ -972,7 +996,8 @@ int run_search_pq(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs
                 return rc;
             ctl.nflag_route = 0;  // decided above; nucleus flags are raised only by the route
         }
-        if (ctl.pq_overflow) return fail(ctx, MAIVS_ERR_HIP, "per-query candidate buffer still overflows");
+        if (ctl.pq_overflow || ctl.max_cand > ctx->cap_cand)
+            return fail(ctx, MAIVS_ERR_HIP, "per-query candidate buffer still overflows");
         break;
     }
     if (st) {
@@ -1096,8 +1121,10 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
     if (!ctx || !a) return MAIVS_ERR_ARG;
     std::lock_guard<std::mutex> lk(ctx->mu);
     HIP_TRY(ctx, hipSetDevice(ctx->device));
-    if (!a->fs_codes || !a->fs_off || !a->mem_off || !a->members || !a->cent_bits || !a->rot_signs || !a->r_bound)
-        return fail(ctx, MAIVS_ERR_ARG, "arena is missing FastScan blocks, members, centroid codes or radii");
+    const bool fs_arena = a->fs_codes && a->fs_off;
+    if (!(fs_arena || a->slot_codes) || !a->mem_off || !a->members || !a->cent_bits || !a->rot_signs || !a->r_bound)
+        return fail(ctx, MAIVS_ERR_ARG, "arena is missing its codes (FastScan blocks or per-slot codes), members, "
+                                        "centroid codes or radii");
     if (!supported_nw(a->n_words)) return fail(ctx, MAIVS_ERR_UNSUPPORTED, "n_words %u not in {1,2,4,8,16}", a->n_words);
     if (a->max_assign > 1 && !a->slot_cells) return fail(ctx, MAIVS_ERR_ARG, "slot_cells missing");
     if (a->max_assign > 1) {
@@ -1153,9 +1180,14 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
         if (len == 0) dead.push_back(c);
         n_live += len > 0;
         max_len = std::max(max_len, len);
-        if (a->fs_off[c + 1] - a->fs_off[c] != (len + 31) / 32)
+        if (fs_arena && a->fs_off[c + 1] - a->fs_off[c] != (len + 31) / 32)
             return fail(ctx, MAIVS_ERR_ARG, "fs_off does not match the member lists at cell %u", c);
     }
+    // members index per-slot arrays on the device (codes, rows, homes, tags)
+    for (uint64_t e = 0; e < A.E; ++e)
+        if (a->members[e] >= A.N) return fail(ctx, MAIVS_ERR_ARG, "member %llu names slot %u of %u",
+                                              static_cast<unsigned long long>(e), a->members[e], A.N);
+    A.fs = fs_arena ? 1u : 0u;
     A.n_live = n_live;
     A.n_dead = static_cast<uint32_t>(dead.size());
     A.max_cell_len = max_len;
@@ -1170,7 +1202,7 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
         for (uint32_t i = 0; i < top; ++i) sum += lens[i];
         seed_cap = static_cast<uint32_t>(std::min<uint64_t>(std::max<uint64_t>(sum, 1), 1ull << 20));
     }
-    if (seed_cap > 65536 || seed_lds(A, seed_cap) + A.W * 256 > kLdsBudget)
+    if (fs_arena && (seed_cap > 65536 || seed_lds(A, seed_cap) + A.W * 256 > kLdsBudget))
         return fail(ctx, MAIVS_ERR_UNSUPPORTED, "the %u largest cells (%u members) exceed the on-chip seed set", kSeedCells,
                     seed_cap);
     if (prep_lds(A) > kLdsBudget) return fail(ctx, MAIVS_ERR_UNSUPPORTED, "dim_pad %u too large for query prep", A.P);
@@ -1191,10 +1223,32 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
         uint64_t* cent_bits = nullptr;
         float *csq_min = nullptr, *csq_step = nullptr, *r_bound = nullptr, *signs = nullptr, *sq_min = nullptr,
               *sq_step = nullptr;
-        const uint64_t nblocks = a->fs_off[A.M];
-        if ((rc = stage(a->fs_codes, nblocks * A.W * 256, &fs))) return rc;
-        if ((rc = stage(a->fs_off, static_cast<uint64_t>(A.M) + 1, &fs_off))) return rc;
+        uint64_t* scodes = nullptr;
+        if (fs_arena) {
+            const uint64_t nblocks = a->fs_off[A.M];
+            if ((rc = stage(a->fs_codes, nblocks * A.W * 256, &fs))) return rc;
+            if ((rc = stage(a->fs_off, static_cast<uint64_t>(A.M) + 1, &fs_off))) return rc;
+        } else if ((rc = stage(a->slot_codes, static_cast<uint64_t>(A.N) * A.W, &scodes))) {
+            return rc;
+        }
         if ((rc = dalloc(ctx, ctx->arena_allocs, &codes, A.E * 2 * A.W))) return rc;
+        // cos(pi * t / dp) for t = 0 .. dp with the f32 operations of score_to_cos(hamming_score(t))
+        // (src/index.rs:1139-1158, src/quantize.rs:206) and this host's libm: the Hamming branch's
+        // adaptive-stop threshold, exact on the device
+        {
+            const uint32_t dp = A.W * 64;
+            std::vector<float> hc(dp + 1);
+            const float dpf = static_cast<float>(dp);
+            for (uint32_t t = 0; t <= dp; ++t) {
+                const float sc = dpf - 2.0f * static_cast<float>(t);
+                const float hh = (dpf - sc) * 0.5f;
+                hc[t] = std::cos(static_cast<float>(M_PI) * hh / dpf);
+            }
+            float* dhc = nullptr;
+            if ((rc = dupload(ctx, hc.data(), hc.size(), &dhc))) return rc;
+            HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));  // hc is about to go
+            A.ham_cos = dhc;
+        }
         if ((rc = dupload(ctx, a->members, A.E, &members))) return rc;
         if ((rc = dupload(ctx, a->mem_off, static_cast<uint64_t>(A.M) + 1, &mem_off))) return rc;
         if ((rc = dalloc(ctx, ctx->arena_allocs, &alt, A.E))) return rc;
@@ -1203,8 +1257,14 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
         if ((rc = dupload(ctx, a->r_bound, A.M, &r_bound))) return rc;
         if ((rc = dupload(ctx, a->rot_signs, 2ull * A.P, &signs))) return rc;
         if (!dead.empty() && (rc = dupload(ctx, dead.data(), dead.size(), &ddead))) return rc;
-        hipLaunchKernelGGL(fs_to_codes_kernel, dim3(std::max<uint32_t>(A.M, 1)), dim3(256), 0, ctx->stream, fs, fs_off,
-                           mem_off, A.M, A.W, codes);
+        if (fs_arena) {
+            hipLaunchKernelGGL(fs_to_codes_kernel, dim3(std::max<uint32_t>(A.M, 1)), dim3(256), 0, ctx->stream, fs,
+                               fs_off, mem_off, A.M, A.W, codes);
+        } else if (A.E) {
+            const uint32_t blocks = static_cast<uint32_t>(std::min<uint64_t>((A.E * A.W + 255) / 256, 65535));
+            hipLaunchKernelGGL(gather_codes_kernel, dim3(blocks), dim3(256), 0, ctx->stream, scodes, members, A.E, A.W,
+                               reinterpret_cast<uint64_t*>(codes));
+        }
         if (A.ma == 2)
             hipLaunchKernelGGL(entry_alt_kernel, dim3(std::max<uint32_t>(A.M, 1)), dim3(256), 0, ctx->stream, mem_off,
                                members, slot_cells, A.M, alt);

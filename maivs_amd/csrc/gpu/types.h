@@ -59,6 +59,8 @@ struct DevArena {
     const float* sq_step;
     const uint32_t* dead;       // n_dead: the cells with no members, ascending
     const uint32_t* entry_tag;  // E: the tag of the entry's slot (null without tags)
+    uint32_t fs;                // 1: codes came from FastScan blocks (compacted); 0: from per-slot codes
+    const float* ham_cos;       // W*64 + 1: cos(pi * t / dp) in f32 by the host's libm (Hamming branch)
 };
 
 struct Ctl {
@@ -144,6 +146,8 @@ struct KParams {
     uint32_t front_rest;
     // bucket work items with at least this many queries go to the matrix-core scan (0: none)
     uint32_t mma_min;
+    // per-query path: the Hamming branch (no FastScan blocks)
+    uint32_t pq_ham;
     float tc, beta, at_margin, norm, prune_band, nucleus_band;
 };
 

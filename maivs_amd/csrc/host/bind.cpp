@@ -291,10 +291,10 @@ PYBIND11_MODULE(_maivs, m) {
         .def("_arena_desc",
              [](PyIndex& s) -> uintptr_t { Mut _b(s); 
                  const maivs_arena_desc* d = s.ix.arena_desc();
-                 if (!d) throw py::value_error("index is not compacted");
+                 if (!d) throw py::value_error("index has no cells");
                  return reinterpret_cast<uintptr_t>(d);
              },
-             "Address of the maivs_arena_desc of the compacted arena (valid until the next mutation).")
+             "Address of the maivs_arena_desc of the arena (valid until the next mutation).")
         .def("_search_params",
              [](PyIndex& s, size_t k, size_t nprobe, float tc, float beta) { Ref _b(s); 
                  maivs_search_params p = s.ix.search_params(k, nprobe, tc, beta);
@@ -317,9 +317,9 @@ PYBIND11_MODULE(_maivs, m) {
                  return a;
              })
         .def("_arena_arrays",
-             [](PyIndex& s) { Ref _b(s); 
+             [](PyIndex& s) { Mut _b(s); 
                  const maivs_arena_desc* a = s.ix.arena_desc();
-                 if (!a) throw py::value_error("index is not compacted");
+                 if (!a) throw py::value_error("index has no cells");
                  auto copy = [](const auto* p, size_t n) {
                      using T = std::remove_cv_t<std::remove_pointer_t<decltype(p)>>;
                      py::array_t<T> out(static_cast<py::ssize_t>(p ? n : 0));

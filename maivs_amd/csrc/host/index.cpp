@@ -920,8 +920,18 @@ std::string FlatCellIndex::cellmajor_blocker(bool cell_major) const {
 }
 
 const maivs_arena_desc* FlatCellIndex::arena_desc() {
-    if (!compacted_) return nullptr;
+    if (cells_.empty()) return nullptr;
     size_t M = cells_.size();
+    if (!compacted_) {
+        // the member lists as they stand, in any order after deletes and inserts: only the per-query
+        // path's Hamming branch runs on them, over the per-slot codes
+        mem_off_.assign(M + 1, 0);
+        for (size_t c = 0; c < M; ++c) mem_off_[c + 1] = mem_off_[c] + static_cast<uint32_t>(cells_[c].members.size());
+        members_flat_.resize(mem_off_.back());
+        for (size_t c = 0; c < M; ++c)
+            std::copy(cells_[c].members.begin(), cells_[c].members.end(), members_flat_.begin() + mem_off_[c]);
+    }
+    const bool fs = compacted_ && fastscan_ && !fs_off_.empty();
     cents_flat_.resize(M * dim_);
     r_bound_flat_.resize(M);
     for (size_t c = 0; c < M; ++c) {
@@ -937,8 +947,9 @@ const maivs_arena_desc* FlatCellIndex::arena_desc() {
     a.n_slots = static_cast<uint32_t>(ext_ids_.size());
     a.max_assign = static_cast<uint32_t>(max_assign_);
     a.rerank_mode = per_dim_sq_ ? MAIVS_RERANK_SQ8 : MAIVS_RERANK_F32;
-    a.fs_codes = fs_codes_.empty() ? nullptr : fs_codes_.data();
-    a.fs_off = fs_off_.empty() ? nullptr : fs_off_.data();
+    a.fs_codes = fs && !fs_codes_.empty() ? fs_codes_.data() : nullptr;
+    a.fs_off = fs ? fs_off_.data() : nullptr;
+    a.slot_codes = bits_.size() >= ext_ids_.size() * n_words_ && !bits_.empty() ? bits_.data() : nullptr;
     a.mem_off = mem_off_.data();
     a.members = members_flat_.data();
     a.slot_cells = slot_cells_.data();
@@ -990,8 +1001,12 @@ std::string FlatCellIndex::perquery_blocker() const {
     // what the GPU per-query path runs: search_one's FastScan branch (src/index.rs:1689-1757) with
     // route_query's tree or two-stage router (:1185-1257)
     if (scan_mode_ != ScanMode::Binary) return "the per-query path needs scan_mode='binary'";
-    if (!fastscan_ || !compacted_ || fs_off_.empty())
-        return "the per-query path runs the FastScan scan: set_fastscan(True) and compact() first";
+    if (!(fastscan_ && compacted_ && !fs_off_.empty())) {
+        // the Hamming branch (src/index.rs:1694-1760)
+        if (asym_cascade_ > 0) return "the asymmetric cascade (set_asym_cascade) is not part of this build";
+        if (bits_.size() < ext_ids_.size() * n_words_ || bits_.empty())
+            return "the Hamming scan needs the per-slot sign codes";
+    }
     if (!tree_ && graph_route_ && cells_.size() >= graph_min_cells_)
         return "the centroid-graph router is not part of this build (set_graph_route(False, ...))";
     if (!tree_ && (!two_stage_ || cent_bits_.empty()))

@@ -864,10 +864,13 @@ int orc_route_query(const maivs_arena_desc* a, const float* q, uint32_t nq, cons
     return 0;
 }
 
-// search_one, src/index.rs:1381-1864, binary mode with FastScan on a compacted index (:1689-1742).
+// search_one, src/index.rs:1381-1864, binary mode: the FastScan branch on a compacted index with
+// FastScan blocks (:1689-1742), else the Hamming branch over per-slot codes (:1694-1760).
 int orc_search_one(const maivs_arena_desc* a, const float* data, uint32_t nq, const maivs_search_params* p,
                    uint32_t nthreads, uint32_t* out_slots, float* out_scores) {
-    if (!a || !p || (!data && nq) || !a->fs_codes || !a->fs_off || p->k == 0) return MAIVS_ERR_ARG;
+    if (!a || !p || (!data && nq) || p->k == 0) return MAIVS_ERR_ARG;
+    const bool fs_on = a->fs_codes && a->fs_off;
+    if (!fs_on && !a->slot_codes) return MAIVS_ERR_ARG;
     Arena A(a);
     const uint32_t d = A.d, nw = A.nw, M = A.M, maxk = A.maxk, k = p->k;
     const uint32_t ma = a->max_assign;
@@ -916,6 +919,49 @@ int orc_search_one(const maivs_arena_desc* a, const float* data, uint32_t nq, co
                 bounds[i] = std::cos(std::fmax(ang - a->r_bound[r.chosen[i]], 0.0f));
             }
             for (size_t i = n; i-- > 0;) suffix[i] = std::fmax(bounds[i], suffix[i + 1]);
+        }
+        if (!fs_on) {
+            // Hamming branch (:1694-1760), asymmetric cascade off: every member of the probed cells
+            // in member order, keep! and the exactly-once rule, then the bucket queue on the
+            // Hamming distance h in [0, dp]; after a cell, the adaptive stop on
+            // score_to_cos(hamming_score(tau)) = cos(pi * tau / dp) in f32 (:1139-1158, quantize.rs:206).
+            const uint32_t dp = nw * 64;
+            std::vector<uint32_t> hist(dp + 1, 0);
+            std::vector<std::pair<uint32_t, uint32_t>> hc;  // (h, slot)
+            uint32_t tau = dp;
+            size_t kept = 0;
+            for (size_t ci_i = 0; ci_i < n; ++ci_i) {
+                const uint32_t ci = r.chosen[ci_i];
+                const uint32_t len = A.mem_len(ci);
+                const uint32_t* mem = a->members + a->mem_off[ci];
+                for (uint32_t i = 0; i < len; ++i) {
+                    const uint32_t slot = mem[i];
+                    if (!keep(slot) || seen(slot, ci)) continue;
+                    const uint32_t h = orc_hamming(r.bits.data(), a->slot_codes + static_cast<size_t>(slot) * nw, nw);
+                    if (h <= tau) {
+                        hc.emplace_back(h, slot);
+                        hist[h] += 1;
+                        kept += 1;
+                        while (tau > 0 && kept - hist[tau] >= target) {
+                            kept -= hist[tau];
+                            tau -= 1;
+                        }
+                    }
+                }
+                if (p->adaptive && kept >= target) {
+                    const float dpf = static_cast<float>(dp);
+                    const float sc = dpf - 2.0f * static_cast<float>(tau);  // hamming_score
+                    const float hh = (dpf - sc) * 0.5f;
+                    const float thr = std::cos(static_cast<float>(M_PI) * hh / dpf);
+                    if (suffix[ci_i + 1] < thr - p->at_margin) break;
+                }
+            }
+            // every survivor h <= tau, ties included, goes to the rerank (:1761-1775, 1840-1850)
+            std::vector<uint32_t> slots;
+            for (auto& e : hc)
+                if (e.first <= tau) slots.push_back(e.second);
+            rerank_top(A, q, slots, k, os, osc);
+            return;
         }
         // FastScan scan with the bucket queue on d >> 6 (:1689-1742)
         std::vector<uint8_t> lut(A.npos * 16);

@@ -141,10 +141,17 @@ def test_binding_errors_and_padding():
         ix.search_batch(np.zeros((64, 4), np.float32).T, 5)  # not C-contiguous
     with pytest.raises(TypeError):
         ix.search_batch(np.zeros((4, 64), np.float64), 5)
+    # not compacted, no FastScan: the per-query path's Hamming branch runs (src/index.rs:1694-1760),
+    # routed by the two-stage shortlist (the flat all-cells router is not part of this build)
+    assert "two_stage" in ix.perquery_blocker()
+    ix.set_two_stage(True, 2)
+    assert ix.perquery_blocker() == ""
+    assert not ix.takes_cellmajor(64, True)
+    ix.set_asym_cascade(4)
+    assert "cascade" in ix.perquery_blocker()
     with pytest.raises(NotImplementedError):
-        ix.search_batch(q, 5)  # not compacted, no FastScan: the per-query path is not built
-    with pytest.raises(NotImplementedError):
-        ix.search(q[0], 5)
+        ix.search_batch(q, 5)
+    ix.set_asym_cascade(0)
     with pytest.raises(NotImplementedError):
         ix.set_f16_rerank(True)
     with pytest.raises(ValueError):

@@ -220,9 +220,182 @@ def test_search_binding_errors():
     assert ix.search(x[0], 5) == ([], [])  # empty index (src/index.rs:3295-3297)
     ix.train_centroids(x, 8)
     ix.add_batch(list(range(len(x))), x)
-    with pytest.raises(NotImplementedError):
-        ix.search(x[0], 5)  # not compacted: the FastScan arena is not built
+    # not compacted: search() takes the Hamming branch over the per-slot codes (no blocker)
+    assert ix.perquery_blocker() == ""
     with pytest.raises(ValueError):
         ix.search(np.zeros(31, np.float32), 5)
     with pytest.raises(TypeError):
         ix.search(np.zeros(32, np.float64), 5)
+
+
+@pytest.fixture(scope="module")
+def churned_uncompacted(mix50k):
+    """20k vectors, 156 cells, then 3 rounds of (delete 1,000 random ids, insert 1,000 new ones) and
+    no compact(): member lists in swap_remove order, per-slot codes, no FastScan blocks."""
+    base, _, _ = mix50k
+    x = np.ascontiguousarray(base[:20000])
+    ix = M.preset(384, len(x))
+    ix.train_centroids(x, 156)
+    ix.add_batch(list(range(len(x))), x)
+    ix.compact()
+    rs = np.random.RandomState(11)
+    dele = rs.choice(20000, 3000, replace=False)
+    for r in range(3):
+        for i in dele[r * 1000:(r + 1) * 1000]:
+            assert ix.remove(int(i))
+        lo = 20000 + r * 1000
+        ix.add_batch(list(range(lo, lo + 1000)), np.ascontiguousarray(base[lo:lo + 1000]))
+    arr = ix._arena_arrays()
+    assert len(arr["fs_codes"]) == 0 and len(arr["fs_off"]) == 0  # the Hamming branch's arena
+    assert not ix.takes_cellmajor(10 ** 6, True)
+    return ix
+
+
+def _popcounts(x):
+    """Per-row popcount of a (n, W) uint64 array."""
+    b = np.ascontiguousarray(x).view(np.uint8)
+    return np.unpackbits(b, axis=1).sum(axis=1).astype(np.int64)
+
+
+def _hamming_branch_closed_form(ix, q, p, chosen, tags=None, filt=None, upto=None):
+    """search_one's Hamming branch over the first `upto` probed cells (all when None), restated in
+    numpy from its definition: the canonical entries (tag filter, first-ranked probed home), their
+    Hamming distances h to the query's code, the final bucket-queue threshold
+    tau = min{t : #(h <= t) >= target} (W * 64 when fewer than target entries), every entry with
+    h <= tau reranked exactly in float64. Returns (tau, kept count, [(score, slot)] sorted)."""
+    arr = ix._arena_arrays()
+    W = arr["n_words"]
+    dp = W * 64
+    target = p.k * max(p.rerank_factor, 1)
+    codes = ix._codes().reshape(-1, W)
+    rq = oracle.rotate(q, arr["rot_signs"], arr["dim_pad"])
+    qb = oracle.pack_signs(rq, W)
+    sc = arr["slot_cells"].reshape(-1, arr["max_assign"])
+    rank = {c: r for r, c in enumerate(chosen)}
+    U = []
+    for r, c in enumerate(chosen[: upto if upto is not None else len(chosen)]):
+        mem = arr["members"][arr["mem_off"][c]: arr["mem_off"][c + 1]].astype(np.int64)
+        h = _popcounts(codes[mem] ^ qb[None, :])
+        for slot, hh in zip(mem.tolist(), h.tolist()):
+            if filt is not None and not (filt[0] <= tags[slot] <= filt[1]):
+                continue
+            if any(x != 0xFFFFFFFF and x != c and x in rank and rank[x] < r for x in sc[slot].tolist()):
+                continue
+            U.append((hh, slot))
+    hs = np.array([h for h, _ in U], np.int64)
+    cnt = np.bincount(hs, minlength=dp + 1).cumsum() if len(hs) else np.zeros(dp + 1, np.int64)
+    reach = np.nonzero(cnt >= target)[0]
+    tau = int(reach[0]) if len(reach) else dp
+    kept = [s for h, s in U if h <= tau]
+    vecs = arr["vecs_f32"].reshape(-1, arr["dim"]).astype(np.float64)
+    ex = sorted(((float(vecs[s] @ q.astype(np.float64)), s) for s in kept), key=lambda t: (-t[0], t[1]))
+    return tau, int(cnt[tau]), ex
+
+
+@pytest.mark.parametrize("nprobe,rf,filt", [(8, 8, None), (24, 4, None), (156, 2, None), (16, 8, (0, 99))])
+def test_search_one_hamming_branch_closed_form(churned_uncompacted, mix50k, nprobe, rf, filt):
+    """With adaptive stopping off, the oracle's Hamming branch equals the closed form over every
+    probed cell: the same reranked survivors, ties at tau included."""
+    _, queries, _ = mix50k
+    ix = churned_uncompacted
+    ix.set_rerank_factor(rf)
+    ix.set_adaptive(False, 0.02)
+    ext = ix._ext_ids()
+    tags = np.random.RandomState(502).randint(0, 1000, len(ext)).astype(np.uint32)
+    if filt is not None:
+        # every slot is live here (the inserts reused the deleted slots): slot i gets tags[i]
+        ix.set_tags([int(e) for e in ext], [int(t) for t in tags])
+        ix.set_filter(*filt)
+    try:
+        p = _params(ix, 10, nprobe)
+        qs = queries[:12]
+        slots, scores = oracle.search_one(ix._arena_desc(), qs, p, nthreads=4)
+        ch, _, nch = oracle.route_query(ix._arena_desc(), qs, p, nthreads=4)
+        for i, q in enumerate(qs):
+            chosen = [int(c) for c in ch[i, : nch[i]]]
+            _, _, ex = _hamming_branch_closed_form(ix, q, p, chosen, tags, filt)
+            kk = min(10, len(ex))
+            got = [int(s) for s in slots[i] if s != 0xFFFFFFFF]
+            assert len(got) == kk and len(set(got)) == kk
+            assert np.allclose([e for e, _ in ex[:kk]], scores[i][:kk], rtol=1e-5, atol=1e-6)
+            if kk == len(ex) or ex[kk - 1][0] - ex[kk][0] > 1e-5:
+                assert set(got) == {s for _, s in ex[:kk]}, i
+            if filt is not None:
+                assert all(filt[0] <= tags[s] <= filt[1] for s in got)
+    finally:
+        ix.set_rerank_factor(32)
+        ix.set_adaptive(True, 0.02)
+        ix.set_filter()
+
+
+def tight_clusters(n=12000, d=64, n_clusters=16, seed=5):
+    """Unit vectors in 16 tight clusters (noise 0.08 / sqrt(d)): cells cut from one cluster have
+    small radii, so the reachability bounds of the other clusters' cells fall far below the
+    Hamming branch's stop threshold and its adaptive stop fires after a cluster's cells."""
+    rs = np.random.RandomState(seed)
+    cent = rs.standard_normal((n_clusters, d))
+    cent /= np.linalg.norm(cent, axis=1, keepdims=True)
+    x = cent[rs.randint(0, n_clusters, n)] + 0.08 * rs.standard_normal((n, d)) / np.sqrt(d)
+    x /= np.linalg.norm(x, axis=1, keepdims=True)
+    return x.astype(np.float32)
+
+
+@pytest.fixture(scope="module")
+def tight_uncompacted():
+    """10k tight-cluster vectors in 128 cells, 300 deletes and 2,000 inserts, no compact()."""
+    x = tight_clusters()
+    ix = M.preset(64, 10000)
+    ix.train_centroids(x[:10000], 128)
+    ix.add_batch(list(range(10000)), x[:10000])
+    ix.compact()
+    for i in range(300):
+        assert ix.remove(i)
+    ix.add_batch(list(range(10000, 12000)), x[10000:])
+    return ix, x
+
+
+def test_search_one_hamming_branch_adaptive_stop(tight_uncompacted):
+    """With adaptive stopping on, the oracle's answer is the closed form over the first L probed
+    cells, where L is the first prefix whose stop test fires: kept >= target and the best remaining
+    reachability bound below cos(pi * tau / dp) - margin (src/index.rs:1779-1788), evaluated here in
+    float64 (prefixes within 1e-5 of the threshold are skipped as libm-dependent)."""
+    ix, x = tight_uncompacted
+    queries = x[:64] + 0.0
+    ix.set_rerank_factor(2)
+    p = _params(ix, 10, 64)
+    assert p.adaptive == 1
+    arr = ix._arena_arrays()
+    dp = arr["n_words"] * 64
+    qs = queries[:16]
+    slots, _ = oracle.search_one(ix._arena_desc(), qs, p, nthreads=4)
+    ch, cs, nch = oracle.route_query(ix._arena_desc(), qs, p, nthreads=4)
+    stopped_early = 0
+    try:
+        for i, q in enumerate(qs):
+            chosen = [int(c) for c in ch[i, : nch[i]]]
+            n = len(chosen)
+            b = np.cos(np.maximum(np.arccos(np.clip(cs[i, :n].astype(np.float64), -1, 1))
+                                  - arr["r_bound"][chosen].astype(np.float64), 0.0))
+            suffix = np.append(np.maximum.accumulate(b[::-1])[::-1], -np.inf)
+            L, ambiguous = n, False
+            for upto in range(1, n + 1):
+                tau, kept, _ = _hamming_branch_closed_form(ix, q, p, chosen, upto=upto)
+                if kept >= p.k * p.rerank_factor:
+                    thr = np.cos(np.pi * tau / dp) - p.at_margin
+                    if abs(suffix[upto] - thr) <= 1e-5:
+                        ambiguous = True
+                        break
+                    if suffix[upto] < thr:
+                        L = upto
+                        break
+            if ambiguous:
+                continue
+            stopped_early += L < n
+            _, _, ex = _hamming_branch_closed_form(ix, q, p, chosen, upto=L)
+            got = [int(s) for s in slots[i] if s != 0xFFFFFFFF]
+            kk = min(10, len(ex))
+            if kk == len(ex) or ex[kk - 1][0] - ex[kk][0] > 1e-5:
+                assert set(got) == {s for _, s in ex[:kk]}, i
+        assert stopped_early > 0  # the stop is exercised
+    finally:
+        ix.set_rerank_factor(32)
