@@ -1850,6 +1850,24 @@ typedef int mma_v16 __attribute__((ext_vector_type(16)));
 // settled (keep!, exactly-once, one append per query) at the item's end, or earlier when it could
 // not take another tile, so these global round trips are paid per item, not per tile.
 constexpr uint32_t kMmaQueue = kBucketQ * 32;  // one tile's worst case of (member, d | query << 16)
+constexpr uint32_t kXcds = 8;                  // MI355X: workgroup b runs on XCD b % 8
+
+// The matrix-core scan's work items in cell order: cell c's items c * kItemGroups + g for
+// g < ceil(min(count_c, bucket_cap) / kBucketQ), the same set the seed stage opened in arrival
+// order. One workgroup: a block scan of the cells' item counts, then each thread writes its cells'.
+__global__ void __launch_bounds__(1024) order_items_kernel(Work Wk, KParams K, uint32_t M) {
+    __shared__ uint32_t scratch[32];
+    const uint32_t t = threadIdx.x, nt = blockDim.x;
+    const uint32_t per = (M + nt - 1) / nt, c0 = min(t * per, M), c1 = min(c0 + per, M);
+    uint32_t loc = 0;
+    for (uint32_t c = c0; c < c1; ++c) loc += (min(Wk.cell_cnt[c], K.bucket_cap) + kBucketQ - 1) / kBucketQ;
+    uint32_t tot;
+    uint32_t pos = block_excl_scan_u32(loc, scratch, &tot);
+    for (uint32_t c = c0; c < c1; ++c) {
+        const uint32_t n = (min(Wk.cell_cnt[c], K.bucket_cap) + kBucketQ - 1) / kBucketQ;
+        for (uint32_t g = 0; g < n; ++g) Wk.active_cs[pos++] = c * kItemGroups + g;
+    }
+}
 
 template <int NW>
 __global__ void __launch_bounds__(kScanThreads, NW >= 16 ? 2 : 4)
@@ -1913,10 +1931,23 @@ cell_mma_kernel(DevArena A, Work Wk, KParams K) {
         __syncthreads();
     };
     const uint32_t items = Wk.ctl->n_active;
-    uint32_t itn = blockIdx.x < items ? Wk.active[blockIdx.x] : 0u;  // the next item's id, one item ahead
-    for (uint32_t b = blockIdx.x; b < items; b += gridDim.x) {
+    // With K.xcd_order the items come in cell order and each XCD takes a contiguous chunk of them:
+    // the items one XCD runs together are then neighbouring cells, whose probing queries overlap, so
+    // their tables and codes are reused from that XCD's L2. Else the grid strides over the
+    // arrival-order list.
+    const uint32_t* list = K.xcd_order ? Wk.active_cs : Wk.active;
+    uint32_t lo = 0, hi = items, first = blockIdx.x, step = gridDim.x;
+    if (K.xcd_order && gridDim.x >= kXcds) {
+        const uint32_t x = blockIdx.x % kXcds;
+        lo = static_cast<uint32_t>(static_cast<uint64_t>(items) * x / kXcds);
+        hi = static_cast<uint32_t>(static_cast<uint64_t>(items) * (x + 1) / kXcds);
+        first = lo + blockIdx.x / kXcds;
+        step = (gridDim.x - x + kXcds - 1) / kXcds;  // the workgroups on this XCD
+    }
+    uint32_t itn = first < hi ? list[first] : 0u;  // the next item's id, one item ahead
+    for (uint32_t b = first; b < hi; b += step) {
         const uint32_t it = itn;
-        if (b + gridDim.x < items) itn = Wk.active[b + gridDim.x];
+        if (b + step < hi) itn = list[b + step];
         const uint32_t c = it / kItemGroups, g0 = (it % kItemGroups) * kBucketQ;
         const uint32_t cnt = min(Wk.cell_cnt[c], K.bucket_cap);
         const uint32_t nqi = min(kBucketQ, cnt - g0);

@@ -189,6 +189,7 @@ void carve_work(const DevArena& A, uint32_t nq, uint32_t nprobe, uint32_t k, uin
     // scan work items: at most one per kBucketQ (kItemQ) bucket entries plus one per cell
     c.take(&W.active, static_cast<uint64_t>(A.M) + nql * nprobe / kBucketQ + 1);
     c.take(&W.active8, static_cast<uint64_t>(A.M) + nql * nprobe / kItemQ + 1);
+    c.take(&W.active_cs, static_cast<uint64_t>(A.M) + nql * nprobe / kBucketQ + 1);
     c.take(&W.flag_route, nql);
     c.take(&W.flag_prune, nql);
     c.take(&W.ctl, 1);
@@ -320,6 +321,7 @@ KParams make_params(maivs_gpu_ctx* ctx, uint32_t nq, const maivs_search_params* 
     K.cand_cap = ctx->cap_cand;
     K.fin_cap = ctx->cap_fin;
     K.key_cap = ctx->cap_key;
+    K.xcd_order = ctx->xcd_order ? 1u : 0u;
     K.tc = p->target_confidence;
     K.beta = p->beta;
     K.at_margin = p->at_margin;
@@ -466,8 +468,12 @@ int launch_scan(maivs_gpu_ctx* ctx, const KParams& K, bool recount, bool events 
                                             ctx->stream, A, W, K));
         HIP_TRY(ctx, hipGetLastError());
     }
-    // the items with many queries, on the matrix cores
+    // the items with many queries, on the matrix cores (in cell order, by XCD)
     if (K.bucket_cap && K.mma_min) {
+        if (K.xcd_order) {
+            hipLaunchKernelGGL(order_items_kernel, dim3(1), dim3(1024), 0, ctx->stream, W, K, A.M);
+            HIP_TRY(ctx, hipGetLastError());
+        }
         DISPATCH_NW(A.W, hipLaunchKernelGGL(cell_mma_kernel<NW>, dim3(std::max(grid, 1u)), dim3(kScanThreads), 0,
                                             ctx->stream, A, W, K));
         HIP_TRY(ctx, hipGetLastError());
@@ -1070,6 +1076,8 @@ int maivs_gpu_create(int device, maivs_gpu_ctx** out) {
     if (const char* f = std::getenv("MAIVS_GPU_FRONT_REST")) ctx->front_rest_mode = std::max(0, std::atoi(f));
     // the matrix-core scan: unset = by cell sharing, 0 = off, else the least queries of its work items
     if (const char* m = std::getenv("MAIVS_GPU_MMA_MIN")) ctx->mma_min_mode = std::max(0, std::atoi(m));
+    // the matrix-core scan's items in cell order, a contiguous chunk per XCD: 1 (default) or 0
+    if (const char* x = std::getenv("MAIVS_GPU_XCD_ORDER")) ctx->xcd_order = std::strcmp(x, "0") != 0;
     if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
         delete ctx;
         return MAIVS_ERR_HIP;

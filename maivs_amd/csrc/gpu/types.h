@@ -124,6 +124,7 @@ struct Work {
     uint32_t* qbuck;       // M x bucket_cap: the queries probing each cell (bucket mode)
     uint32_t* active;      // scan work items, cell * kItemGroups + group of kBucketQ, in arrival order (bucket mode)
     uint32_t* active8;     // the same by groups of kItemQ (cell * kItemGroups + group)
+    uint32_t* active_cs;   // the kBucketQ items again, in cell order (order_items_kernel)
     uint32_t* flag_route;  // nq
     uint32_t* flag_prune;  // nq
     // per-query path
@@ -148,6 +149,8 @@ struct KParams {
     uint32_t mma_min;
     // per-query path: the Hamming branch (no FastScan blocks)
     uint32_t pq_ham;
+    // matrix-core scan: items in cell order, a contiguous chunk per XCD (else arrival order)
+    uint32_t xcd_order;
     float tc, beta, at_margin, norm, prune_band, nucleus_band;
 };
 
