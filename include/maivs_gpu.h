@@ -117,11 +117,11 @@ typedef struct maivs_search_params {
 } maivs_search_params;
 
 /* Per-call measurements. maivs_gpu_search_batch* fills the times and host_* / reruns fields
- * (HIP events on the context's stream; no extra device work). The main pass is normally replayed
- * as one captured HIP graph, which is timed as a whole (ms_total; the stage fields stay 0); a
- * context created with the environment variable MAIVS_GPU_GRAPH=0 launches the stages one by one
- * and times each. The work counters (the *_blocks, scan_pairs, survivors, rerank_rows fields) are
- * filled on demand by maivs_gpu_last_counters. */
+ * (HIP events on the context's stream, recorded only when a stats struct is passed; no extra
+ * device work). The main pass is launched stage by stage and each stage is timed; a context
+ * created with the environment variable MAIVS_GPU_GRAPH=1 replays it as one captured HIP graph
+ * instead, timed as a whole (ms_total; the stage fields stay 0). The work counters (the *_blocks,
+ * scan_pairs, survivors, rerank_rows fields) are filled on demand by maivs_gpu_last_counters. */
 typedef struct maivs_gpu_stats {
     float ms_total;       /* device time of the whole pipeline (hipEvents) */
     float ms_prep;        /* per-call counter reset; with the query prep (rotation, sign codes,

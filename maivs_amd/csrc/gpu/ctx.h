@@ -53,7 +53,7 @@ struct maivs_gpu_ctx {
         float* scores;
         uint64_t gen;
     };
-    bool use_graph = true;
+    bool use_graph = false;  // MAIVS_GPU_GRAPH=1: replay the main pass as one captured graph
     bool counters_clean = false;  // ctl / cell_cnt / cand_cnt / done are zero (a pass needs no clear first)
     uint64_t buf_gen = 0;  // bumped whenever a buffer the graph references is reallocated
     hipGraphExec_t gexec = nullptr;

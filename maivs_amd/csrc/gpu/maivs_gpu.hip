@@ -647,7 +647,8 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
                     if (ctx->gexec) (void)hipGraphExecDestroy(ctx->gexec);
                     ctx->gexec = nullptr;
                     ctx->use_graph = false;
-                    return enqueue_main(true);
+                    staged = st != nullptr;
+                    return enqueue_main(staged);
                 }
                 ctx->gkey = key;
             }
@@ -659,8 +660,9 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
             if (st) HIP_TRY(ctx, hipEventRecord(ctx->ev[6], ctx->stream));
             return 0;
         }
-        staged = true;
-        return enqueue_main(true);
+        // eager launches; the per-stage events only when the caller asks for measurements
+        staged = st != nullptr;
+        return enqueue_main(staged);
     };
     for (;;) {
         if (!ctx->counters_clean && (rc = launch_reset(ctx, nq))) return rc;
@@ -1069,7 +1071,9 @@ int maivs_gpu_create(int device, maivs_gpu_ctx** out) {
     auto* ctx = new (std::nothrow) maivs_gpu_ctx();
     if (!ctx) return MAIVS_ERR_OOM;
     ctx->device = device;
-    if (const char* g = std::getenv("MAIVS_GPU_GRAPH")) ctx->use_graph = std::strcmp(g, "0") != 0;
+    // the main pass launched kernel by kernel (default: two to five launches cost less than one
+    // graph replay here), or replayed as one captured HIP graph (MAIVS_GPU_GRAPH=1)
+    if (const char* g = std::getenv("MAIVS_GPU_GRAPH")) ctx->use_graph = std::strcmp(g, "1") == 0;
     // the first candidate buffer's room per query (it grows to the exact need on overflow)
     if (const char* c = std::getenv("MAIVS_GPU_CAND_CAP")) ctx->initial_cand_cap = std::max(16, std::atoi(c));
     // the seed stage's own rest scan: unset = by cell sharing, else a fixed count of ranks (0 or 8)
