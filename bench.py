@@ -366,7 +366,10 @@ def main() -> int:
                           f"best point with R@10 >= {args.target}: nprobe={cop['nprobe']} rf={cop['rf']} "
                           f"R@10={cop['recall']:.4f}"),
                "gpu_equal_points": f"{n_equal}/{len(cpu_pts)}",
-               "cpu_model": _cpu_model()}
+               "cpu_model": _cpu_model(),
+               # the CPU grid itself (nprobe, rerank_factor, R@10, QPS), e.g. for the order-of-magnitude
+               # check against the reference's published 500k grid (rf 32)
+               "grid": [[q["nprobe"], q["rf"], round(q["recall"], 4), round(q["qps"], 1)] for q in cpu_pts]}
         log(f"cpu baseline: {cop['qps']:.0f} QPS at np{cop['nprobe']}/rf{cop['rf']} on {threads} threads "
             f"({time.time() - t_all:.1f}s)")
 
