@@ -73,7 +73,7 @@ typedef struct maivs_arena_desc {
     const uint32_t* members;    /* E slots */
     const uint32_t* slot_cells; /* N * max_assign, UINT32_MAX = unused */
     /* routing */
-    const uint64_t* cent_bits;  /* M * W */
+    const uint64_t* cent_bits;  /* M * W, or NULL when two-stage routing is off (route_mode 1 only) */
     const uint8_t* cent_sq8;    /* M * d, or NULL to score the f32 centroids */
     const float* centroids;     /* M * d (used when cent_sq8 is NULL) */
     const float* csq_min;       /* d */
@@ -114,6 +114,12 @@ typedef struct maivs_search_params {
     uint32_t filter;
     uint32_t tag_lo;
     uint32_t tag_hi;
+    /* Routing (src/index.rs:1168-1305, 1873-1877). 0: two-stage routing is on (set_two_stage with
+     * centroid codes): the batched path routes with route_batch's Hamming shortlist and exact
+     * rescore; the per-query path with the tree when the arena has one, else route_query's
+     * two-stage shortlist. 1: two-stage routing is off: both paths route as route_query does, with
+     * the tree when the arena has one, else over every live cell scored exactly. */
+    uint32_t route_mode;
 } maivs_search_params;
 
 /* Per-call measurements. maivs_gpu_search_batch* fills the times and host_* / reruns fields

@@ -39,6 +39,7 @@ class SearchParams(C.Structure):
         ("k", C.c_uint32), ("nprobe", C.c_uint32), ("target_confidence", C.c_float), ("beta", C.c_float),
         ("rerank_factor", C.c_uint32), ("shortlist_mult", C.c_uint32), ("adaptive", C.c_uint32),
         ("at_margin", C.c_float), ("filter", C.c_uint32), ("tag_lo", C.c_uint32), ("tag_hi", C.c_uint32),
+        ("route_mode", C.c_uint32),
     ]
 
 

@@ -785,7 +785,7 @@ __device__ __forceinline__ void dead_fixup(const DevArena& A, const Work& Wk, ui
 }
 
 // kFront: the caller (front_kernel) already cleared the histogram, staged cqs and ran hamming_row,
-// and K.tree_list is 0. kRowsReady: hamming_kernel already wrote the query's row of Wk.hs (more
+// and K.tree_list and K.flat_route are 0. kRowsReady: hamming_kernel already wrote the query's row of Wk.hs (more
 // cells than the LDS row holds); the histogram is built from it.
 template <class Get>
 __device__ uint32_t select_kth_u32(uint32_t n, uint32_t want, Get get, uint32_t* hist, uint32_t* scratch);
@@ -803,7 +803,6 @@ __device__ __forceinline__ void route_phase(const DevArena& A, const Work& Wk, c
     uint32_t* hist = reinterpret_cast<uint32_t*>(keys + K.sort_cap);
     uint32_t* scratch = hist + ((nbins + 3) & ~3u);
     __shared__ uint32_t s_cut;
-    (void)M;
 
     if constexpr (!kFront) {
         for (uint32_t i = tid; i < nbins; i += nt) hist[i] = 0;
@@ -819,6 +818,17 @@ __device__ __forceinline__ void route_phase(const DevArena& A, const Work& Wk, c
             const uint32_t i = r0 + tid;
             const uint32_t c = i < nt_list ? tl[i] : 0u;
             const bool live = i < nt_list && A.mem_off[c + 1] > A.mem_off[c];
+            uint32_t tot;
+            const uint32_t pos = nsl + block_excl_scan_u32(live ? 1u : 0u, scratch, &tot);
+            if (live && pos < K.sort_cap) keys[pos] = c;
+            nsl += tot;
+        }
+    } else if (!kFront && K.flat_route) {
+        // every live cell, ascending id (route_query without a tree or two-stage routing,
+        // src/index.rs:1260-1269)
+        for (uint32_t r0 = 0; r0 < M; r0 += nt) {
+            const uint32_t c = r0 + tid;
+            const bool live = c < M && A.mem_off[c + 1] > A.mem_off[c];
             uint32_t tot;
             const uint32_t pos = nsl + block_excl_scan_u32(live ? 1u : 0u, scratch, &tot);
             if (live && pos < K.sort_cap) keys[pos] = c;

@@ -286,6 +286,65 @@ int ensure_all(maivs_gpu_ctx* ctx, uint32_t nq, uint32_t nprobe, uint32_t k) {
     return ensure_cand(ctx, std::max(ctx->cap_cand, ctx->initial_cand_cap));
 }
 
+// ---------------------------------------------------------------- the centroid tree's buffers and descent
+
+constexpr uint32_t kPqPairMaxQ = 256;   // batches up to this many queries use the pair tables in the per-query scan
+constexpr uint32_t kPqMaxProbe = 8192;  // probe-list bound of the per-query scan's on-chip suffix array
+constexpr uint32_t kPqMaxLevels = 64;
+
+// Tree lists (nq x tcap), scan candidate buffers (nq x pq_cap) and the beams; grow only.
+int ensure_pq(maivs_gpu_ctx* ctx, uint32_t nq, uint32_t tcap, uint32_t pq_cap) {
+    if (nq <= ctx->cap_pq_nq && tcap <= ctx->cap_tcap && pq_cap <= ctx->cap_pq && ctx->d_beams) return 0;
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    drop_graph(ctx);
+    free_all(ctx->pq_allocs);
+    const uint32_t n = std::max(nq, ctx->cap_pq_nq), t = std::max(tcap, ctx->cap_tcap), c = std::max(pq_cap, ctx->cap_pq);
+    Work& W = ctx->Wk;
+    int rc = 0;
+    rc |= dalloc(ctx, ctx->pq_allocs, &W.tlist, static_cast<size_t>(n) * t);
+    rc |= dalloc(ctx, ctx->pq_allocs, &W.tcount, n);
+    rc |= dalloc(ctx, ctx->pq_allocs, &W.pqc, static_cast<size_t>(n) * c);
+    rc |= dalloc(ctx, ctx->pq_allocs, &ctx->d_beams, kPqMaxLevels);
+    ctx->beams_on_device.clear();
+    if (rc) {
+        free_all(ctx->pq_allocs);
+        ctx->cap_pq_nq = ctx->cap_tcap = ctx->cap_pq = 0;
+        ctx->d_beams = nullptr;
+        return rc;
+    }
+    ctx->cap_pq_nq = n;
+    ctx->cap_tcap = t;
+    ctx->cap_pq = c;
+    return 0;
+}
+
+// A kernel's dynamic-LDS limit, raised only when a launch needs more than it was last raised to on
+// this device (the limit only grows): the attribute call costs a few µs of host time, which a
+// one-query search would otherwise spend while the GPU waits for its next launch.
+int raise_lds_limit(maivs_gpu_ctx* ctx, const void* fn, size_t lds) {
+    static std::mutex mu;
+    static std::map<std::pair<const void*, int>, size_t> raised;
+    std::lock_guard<std::mutex> lock(mu);
+    size_t& have = raised[{fn, ctx->device}];
+    if (lds <= have) return 0;
+    HIP_TRY(ctx, hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+    have = lds;
+    return 0;
+}
+
+int launch_pq_tree(maivs_gpu_ctx* ctx, const KParams& K, uint32_t cap) {
+    const uint32_t words = pq_tree_lds_words(ctx->A.W, cap);
+    const uint32_t per_wave = (words * 4 + 15) & ~15u;
+    const size_t lds = static_cast<size_t>(per_wave) * kPqTreeWaves;
+    if (lds > kLdsBudget) return fail(ctx, MAIVS_ERR_UNSUPPORTED, "tree descent needs %zu bytes of LDS", lds);
+    int rc;
+    if (lds > 64 * 1024 && (rc = raise_lds_limit(ctx, reinterpret_cast<const void*>(pq_tree_kernel), lds))) return rc;
+    hipLaunchKernelGGL(pq_tree_kernel, dim3((K.nq + kPqTreeWaves - 1) / kPqTreeWaves), dim3(kPqTreeWaves * kWave), lds,
+                       ctx->stream, ctx->A, ctx->Wk, K, ctx->tree, ctx->d_beams, cap, per_wave);
+    HIP_TRY(ctx, hipGetLastError());
+    return 0;
+}
+
 KParams make_params(maivs_gpu_ctx* ctx, uint32_t nq, const maivs_search_params* p) {
     const DevArena& A = ctx->A;
     KParams K{};
@@ -335,6 +394,69 @@ KParams make_params(maivs_gpu_ctx* ctx, uint32_t nq, const maivs_search_params* 
     K.bnd_from = kSeedCells;
     K.tcap = 1;
     return K;
+}
+
+// The routing of a call (src/index.rs:1168-1305, 1873-1877), into K's routing fields. Batched
+// (search_batch_cellmajor): the two-stage shortlist when p->route_mode is 0 (route_batch), else
+// route_query's routing, the tree when the arena has one, else every live cell. Per query
+// (search_one, route_query): the tree first, then the two-stage shortlist (route_mode 0), then every
+// live cell. With the tree, *beams receives the descent's beam per level.
+int route_setup(maivs_gpu_ctx* ctx, const maivs_search_params* p, bool batched, KParams& K,
+                std::vector<uint32_t>* beams) {
+    const DevArena& A = ctx->A;
+    const bool tree = ctx->tree.n_levels > 0 && (!batched || p->route_mode != 0);
+    const bool two = !tree && p->route_mode == 0;
+    if (beams) beams->clear();
+    K.tree_list = 0;
+    K.flat_route = 0;
+    K.tcap = 1;
+    auto sort_room = [&](uint32_t need) {
+        uint32_t sc = 1024;
+        while (sc < need && sc < ctx->max_sort_cap_route) sc <<= 1;
+        K.sort_cap = std::min(sc, ctx->max_sort_cap_route);
+    };
+    if (two) {
+        if (!A.cent_bits)
+            return fail(ctx, MAIVS_ERR_ARG, "route_mode 0 (two-stage routing) needs the arena's centroid codes");
+        // route_batch keeps nprobe * max(mult, 2) cells, route_query's branch nprobe * mult (:1886, 1245)
+        K.want_c = std::min<uint32_t>(p->nprobe * (batched ? std::max<uint32_t>(p->shortlist_mult, 2u) : p->shortlist_mult),
+                                      A.n_live);
+        sort_room(4u * K.want_c);
+        return 0;
+    }
+    if (tree) {
+        // the tree keeps nprobe * max(mult, 2) leaves (:1194)
+        K.want_c = std::min<uint32_t>(p->nprobe * std::max<uint32_t>(p->shortlist_mult, 2u), ctx->tree.n_leaf);
+        sort_room(4u * K.want_c);
+        K.tree_list = 1;
+        K.tcap = std::max(K.want_c, 1u);
+        if (ctx->tree_level_n.size() > kPqMaxLevels) return fail(ctx, MAIVS_ERR_UNSUPPORTED, "tree deeper than %u", kPqMaxLevels);
+        if (beams) {
+            beams->resize(ctx->tree_level_n.size());
+            tree_beams(ctx->tree_level_n.data(), static_cast<uint32_t>(beams->size()), ctx->tree_beam_frac,
+                       ctx->tree_min_beam, K.want_c, beams->data());
+        }
+        return 0;
+    }
+    // every live cell is rescored and sorted on chip
+    if (A.n_live > ctx->max_sort_cap_route)
+        return fail(ctx, MAIVS_ERR_UNSUPPORTED,
+                    "routing over every live cell sorts at most %u cells on chip, this arena has %u (use two-stage "
+                    "routing or a centroid tree)",
+                    ctx->max_sort_cap_route, A.n_live);
+    K.want_c = A.n_live;
+    K.flat_route = 1;
+    sort_room(A.n_live);
+    return 0;
+}
+
+// Copies the tree descent's beams to d_beams when they differ from what it holds.
+int upload_beams(maivs_gpu_ctx* ctx, const std::vector<uint32_t>& beams) {
+    if (beams.empty() || beams == ctx->beams_on_device) return 0;
+    HIP_TRY(ctx, hipMemcpyAsync(ctx->d_beams, beams.data(), beams.size() * 4, hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));  // the host vector is about to go
+    ctx->beams_on_device = beams;
+    return 0;
 }
 
 // ---- host re-evaluation of libm-sensitive decisions (the reference's libm, same host) ----
@@ -583,11 +705,21 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
     ctx->last_nq = 0;
     if (nq == 0) return 0;
     KParams K = make_params(ctx, nq, p);
+    std::vector<uint32_t> beams;
+    if ((rc = route_setup(ctx, p, true, K, &beams))) return rc;
+    const bool two_stage = !K.tree_list && !K.flat_route;
+    uint32_t tree_cap = 1;
+    for (uint32_t b : beams) tree_cap = std::max(tree_cap, b);
     if (p->nprobe == 0 || K.want_c == 0) {
         // route_batch returns empty probe lists (src/index.rs:1887-1889): padded results
         if ((rc = launch_pad(ctx, d_slots, d_scores, static_cast<uint64_t>(nq) * p->k))) return rc;
         HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
         return 0;
+    }
+    if (K.tree_list) {
+        // the descent's leaf lists (a scratch-backed call has them carved already) and beams
+        if (!sc && (rc = ensure_pq(ctx, nq, K.tcap, 0))) return rc;
+        if ((rc = upload_beams(ctx, beams))) return rc;
     }
     Ctl ctl{};
     // the main pass; run eagerly it has an event between stages (the per-stage device times)
@@ -597,7 +729,13 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
             if (events) HIP_TRY(ctx, hipEventRecord(ctx->ev[i], ctx->stream));
             return 0;
         };
-        if (ctx->A.Mp > kHdLdsCells) {
+        if (!two_stage) {
+            // route_query's routing (src/index.rs:2105-2124): prep, the tree's descent, then route
+            // (the tree's leaves or every live cell, rescored) and seed
+            if ((r = mark(0)) || (r = launch_prep(ctx, K, d_q, kPrepReset))) return r;
+            if (K.tree_list && (r = launch_pq_tree(ctx, K, tree_cap))) return r;
+            if ((r = mark(3)) || (r = launch_route_seed(ctx, K)) || (r = mark(2))) return r;
+        } else if (ctx->A.Mp > kHdLdsCells) {
             // many cells: Hamming rows by query tiles, then route and seed from them
             if ((r = mark(0)) || (r = launch_prep(ctx, K, d_q, 0)) || (r = launch_hamming(ctx, K.nq)) || (r = mark(3)))
                 return r;
@@ -755,9 +893,9 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
         uint32_t need = ctl.max_cand + ctl.max_cand / 4 + 64;
         ctx->initial_cand_cap = std::max(ctx->initial_cand_cap, need);
         if ((rc = sc ? recarve_cand(ctx, *sc, need) : ensure_cand(ctx, need))) return rc;
-        const uint32_t sc = K.sort_cap;
-        K = make_params(ctx, nq, p);
-        K.sort_cap = sc;
+        K.cand_cap = ctx->cap_cand;
+        K.fin_cap = ctx->cap_fin;
+        K.key_cap = ctx->cap_key;
         rerun_scan = true;
     }
     if (rerun_scan) {
@@ -774,63 +912,6 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
 }
 
 // ---------------------------------------------------------------- the per-query path
-
-constexpr uint32_t kPqPairMaxQ = 256;   // batches up to this many queries use the pair tables in the per-query scan
-constexpr uint32_t kPqMaxProbe = 8192;  // probe-list bound of the per-query scan's on-chip suffix array
-constexpr uint32_t kPqMaxLevels = 64;
-
-// Tree lists (nq x tcap), scan candidate buffers (nq x pq_cap) and the beams; grow only.
-int ensure_pq(maivs_gpu_ctx* ctx, uint32_t nq, uint32_t tcap, uint32_t pq_cap) {
-    if (nq <= ctx->cap_pq_nq && tcap <= ctx->cap_tcap && pq_cap <= ctx->cap_pq && ctx->d_beams) return 0;
-    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
-    drop_graph(ctx);
-    free_all(ctx->pq_allocs);
-    const uint32_t n = std::max(nq, ctx->cap_pq_nq), t = std::max(tcap, ctx->cap_tcap), c = std::max(pq_cap, ctx->cap_pq);
-    Work& W = ctx->Wk;
-    int rc = 0;
-    rc |= dalloc(ctx, ctx->pq_allocs, &W.tlist, static_cast<size_t>(n) * t);
-    rc |= dalloc(ctx, ctx->pq_allocs, &W.tcount, n);
-    rc |= dalloc(ctx, ctx->pq_allocs, &W.pqc, static_cast<size_t>(n) * c);
-    rc |= dalloc(ctx, ctx->pq_allocs, &ctx->d_beams, kPqMaxLevels);
-    ctx->beams_on_device.clear();
-    if (rc) {
-        free_all(ctx->pq_allocs);
-        ctx->cap_pq_nq = ctx->cap_tcap = ctx->cap_pq = 0;
-        ctx->d_beams = nullptr;
-        return rc;
-    }
-    ctx->cap_pq_nq = n;
-    ctx->cap_tcap = t;
-    ctx->cap_pq = c;
-    return 0;
-}
-
-// A kernel's dynamic-LDS limit, raised only when a launch needs more than it was last raised to on
-// this device (the limit only grows): the attribute call costs a few µs of host time, which a
-// one-query search would otherwise spend while the GPU waits for its next launch.
-int raise_lds_limit(maivs_gpu_ctx* ctx, const void* fn, size_t lds) {
-    static std::mutex mu;
-    static std::map<std::pair<const void*, int>, size_t> raised;
-    std::lock_guard<std::mutex> lock(mu);
-    size_t& have = raised[{fn, ctx->device}];
-    if (lds <= have) return 0;
-    HIP_TRY(ctx, hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
-    have = lds;
-    return 0;
-}
-
-int launch_pq_tree(maivs_gpu_ctx* ctx, const KParams& K, uint32_t cap) {
-    const uint32_t words = pq_tree_lds_words(ctx->A.W, cap);
-    const uint32_t per_wave = (words * 4 + 15) & ~15u;
-    const size_t lds = static_cast<size_t>(per_wave) * kPqTreeWaves;
-    if (lds > kLdsBudget) return fail(ctx, MAIVS_ERR_UNSUPPORTED, "tree descent needs %zu bytes of LDS", lds);
-    int rc;
-    if (lds > 64 * 1024 && (rc = raise_lds_limit(ctx, reinterpret_cast<const void*>(pq_tree_kernel), lds))) return rc;
-    hipLaunchKernelGGL(pq_tree_kernel, dim3((K.nq + kPqTreeWaves - 1) / kPqTreeWaves), dim3(kPqTreeWaves * kWave), lds,
-                       ctx->stream, ctx->A, ctx->Wk, K, ctx->tree, ctx->d_beams, cap, per_wave);
-    HIP_TRY(ctx, hipGetLastError());
-    return 0;
-}
 
 int launch_pq_scan(maivs_gpu_ctx* ctx, const KParams& K) {
     const DevArena& A = ctx->A;
@@ -875,19 +956,11 @@ int run_search_pq(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs
         if ((rc = ensure_cand(ctx, K.target))) return rc;
         K = make_params(ctx, nq, p);
     }
-    const bool tree = ctx->tree.n_levels > 0;
-    // route_query's shortlist size: the tree keeps nprobe * max(mult, 2) leaves; the two-stage
-    // branch nprobe * mult live cells (src/index.rs:1194, 1245)
-    K.want_c = tree ? std::min<uint32_t>(p->nprobe * std::max<uint32_t>(p->shortlist_mult, 2u), ctx->tree.n_leaf)
-                    : std::min<uint32_t>(p->nprobe * p->shortlist_mult, A.n_live);
-    {
-        uint32_t sc = 1024;
-        while (sc < 4u * K.want_c && sc < ctx->max_sort_cap_route) sc <<= 1;
-        K.sort_cap = std::min(sc, ctx->max_sort_cap_route);
-    }
-    K.tree_list = tree ? 1u : 0u;
+    // route_query: the tree, else the two-stage shortlist, else every live cell
+    std::vector<uint32_t> beams;
+    if ((rc = route_setup(ctx, p, false, K, &beams))) return rc;
+    const bool tree = K.tree_list != 0;
     K.bnd_from = 0;
-    K.tcap = tree ? std::max(K.want_c, 1u) : 1u;
     K.pq_room = std::max(A.max_cell_len, 1u);
     const uint32_t pq_need = std::max({4u * K.target + 1024u, 2u * K.pq_room + K.target, ctx->pq_cap_min});
     if ((rc = ensure_pq(ctx, nq, K.tcap, pq_need))) return rc;
@@ -906,19 +979,9 @@ int run_search_pq(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs
         return 0;
     }
     uint32_t cap = 1;
-    if (tree) {
-        if (ctx->tree_level_n.size() > kPqMaxLevels) return fail(ctx, MAIVS_ERR_UNSUPPORTED, "tree deeper than %u", kPqMaxLevels);
-        std::vector<uint32_t> beams(ctx->tree_level_n.size());
-        tree_beams(ctx->tree_level_n.data(), static_cast<uint32_t>(beams.size()), ctx->tree_beam_frac, ctx->tree_min_beam,
-                   K.want_c, beams.data());
-        for (uint32_t b : beams) cap = std::max(cap, b);
-        // copied only when they change (they depend on the tree and want_c)
-        if (beams != ctx->beams_on_device) {
-            HIP_TRY(ctx, hipMemcpyAsync(ctx->d_beams, beams.data(), beams.size() * 4, hipMemcpyHostToDevice, ctx->stream));
-            HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));  // the host vector is about to go
-            ctx->beams_on_device = beams;
-        }
-    }
+    for (uint32_t b : beams) cap = std::max(cap, b);
+    // copied only when they change (they depend on the tree and want_c)
+    if (tree && (rc = upload_beams(ctx, beams))) return rc;
     Work& W = ctx->Wk;
     // timed only when the caller asks for measurements
     if (st) HIP_TRY(ctx, hipEventRecord(ctx->ev[0], ctx->stream));
@@ -1134,9 +1197,9 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
     std::lock_guard<std::mutex> lk(ctx->mu);
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     const bool fs_arena = a->fs_codes && a->fs_off;
-    if (!(fs_arena || a->slot_codes) || !a->mem_off || !a->members || !a->cent_bits || !a->rot_signs || !a->r_bound)
+    if (!(fs_arena || a->slot_codes) || !a->mem_off || !a->members || !a->rot_signs || !a->r_bound)
         return fail(ctx, MAIVS_ERR_ARG, "arena is missing its codes (FastScan blocks or per-slot codes), members, "
-                                        "centroid codes or radii");
+                                        "rotation or radii");
     if (!supported_nw(a->n_words)) return fail(ctx, MAIVS_ERR_UNSUPPORTED, "n_words %u not in {1,2,4,8,16}", a->n_words);
     if (a->max_assign > 1 && !a->slot_cells) return fail(ctx, MAIVS_ERR_ARG, "slot_cells missing");
     if (a->max_assign > 1) {
@@ -1265,7 +1328,7 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
         if ((rc = dupload(ctx, a->mem_off, static_cast<uint64_t>(A.M) + 1, &mem_off))) return rc;
         if ((rc = dalloc(ctx, ctx->arena_allocs, &alt, A.E))) return rc;
         if (A.ma > 1 && (rc = dupload(ctx, a->slot_cells, static_cast<uint64_t>(A.N) * A.ma, &slot_cells))) return rc;
-        if ((rc = dupload(ctx, a->cent_bits, static_cast<uint64_t>(A.M) * A.W, &cent_bits))) return rc;
+        if (a->cent_bits && (rc = dupload(ctx, a->cent_bits, static_cast<uint64_t>(A.M) * A.W, &cent_bits))) return rc;
         if ((rc = dupload(ctx, a->r_bound, A.M, &r_bound))) return rc;
         if ((rc = dupload(ctx, a->rot_signs, 2ull * A.P, &signs))) return rc;
         if (!dead.empty() && (rc = dupload(ctx, dead.data(), dead.size(), &ddead))) return rc;
@@ -1412,12 +1475,26 @@ int maivs_gpu_search_batch_device_noalloc(maivs_gpu_ctx* ctx, const float* d_q, 
     const uint32_t nprobe = std::max<uint32_t>(p->nprobe, 1), k = std::max<uint32_t>(p->k, 1);
     const size_t bytes = MAIVS_GPU_SCRATCH_BYTES;
     const uint32_t cand_cap = std::max<uint32_t>(ctx->initial_cand_cap, 64);
-    // Bytes of one chunk of n queries: its work buffers, then its candidate buffers at the room
-    // the context starts with (an overflow re-carves them within the array).
+    // routing through the centroid tree also needs the descent's leaf lists and beams
+    KParams Kr = make_params(ctx, 1, p);
+    int rc = route_setup(ctx, p, true, Kr, nullptr);
+    if (rc) return rc;
+    const uint32_t tcap = Kr.tree_list ? Kr.tcap : 0u;
+    // A chunk of n queries: its work buffers (and the tree's), then its candidate buffers at the
+    // room the context starts with (an overflow re-carves them within the array).
+    auto carve_front = [&](uint32_t n, Carver& c, Work& w, uint32_t** beams) {
+        carve_work(A, n, nprobe, k, ctx->seed_cap, bucket_cap_for(A, n, nprobe), false, c, w);
+        if (tcap) {
+            c.take(&w.tlist, static_cast<uint64_t>(n) * tcap);
+            c.take(&w.tcount, n);
+            c.take(beams, kPqMaxLevels);
+        }
+    };
     auto need = [&](uint32_t n, size_t* cand_off) {
         Work tmp{};
         Carver c{nullptr};
-        carve_work(A, n, nprobe, k, ctx->seed_cap, bucket_cap_for(A, n, nprobe), false, c, tmp);
+        uint32_t* b = nullptr;
+        carve_front(n, c, tmp, &b);
         if (cand_off) *cand_off = c.used;
         carve_cand(n, ctx->seed_cap, cand_cap, c, tmp);
         return c.used;
@@ -1448,7 +1525,8 @@ int maivs_gpu_search_batch_device_noalloc(maivs_gpu_ctx* ctx, const float* d_q, 
                    s_seed = ctx->cap_seed, s_fin = ctx->cap_fin, s_key = ctx->cap_key, s_b = ctx->cap_bucket,
                    s_cnq = ctx->cand_nq;
     const bool s_clean = ctx->counters_clean;
-    int rc = 0;
+    uint32_t* const s_beams = ctx->d_beams;
+    const std::vector<uint32_t> s_beams_dev = ctx->beams_on_device;
     for (uint32_t q0 = 0; q0 < nq && rc == 0; q0 += chunk) {
         const uint32_t n = std::min(chunk, nq - q0);
         const uint32_t bcap = bucket_cap_for(A, n, nprobe);
@@ -1456,7 +1534,12 @@ int maivs_gpu_search_batch_device_noalloc(maivs_gpu_ctx* ctx, const float* d_q, 
         need(n, &cand_off);
         Work W = own;  // keeps the pinned control-block mirror and the per-query path's fields
         Carver cw{slot->ptr};
-        carve_work(A, n, nprobe, k, ctx->seed_cap, bcap, false, cw, W);
+        uint32_t* beams = nullptr;
+        carve_front(n, cw, W, &beams);
+        if (tcap) {
+            ctx->d_beams = beams;  // the array's beams: unknown contents, copied by the pass
+            ctx->beams_on_device.clear();
+        }
         Carver cc{slot->ptr};
         cc.used = cand_off;
         carve_cand(n, ctx->seed_cap, cand_cap, cc, W);
@@ -1490,6 +1573,8 @@ int maivs_gpu_search_batch_device_noalloc(maivs_gpu_ctx* ctx, const float* d_q, 
     }
     const hipError_t sync = hipStreamSynchronize(ctx->stream);
     ctx->Wk = own;
+    ctx->d_beams = s_beams;
+    ctx->beams_on_device = s_beams_dev;
     ctx->cap_nq = s_nq;
     ctx->cap_nprobe = s_np;
     ctx->cap_k = s_k;
@@ -1635,6 +1720,11 @@ int maivs_gpu_route(maivs_gpu_ctx* ctx, const float* q, uint32_t nq, const maivs
     int rc = ensure_all(ctx, nq, p->nprobe, p->k);
     if (rc) return rc;
     KParams K = make_params(ctx, nq, p);
+    std::vector<uint32_t> beams;
+    if ((rc = route_setup(ctx, p, true, K, &beams))) return rc;
+    uint32_t tree_cap = 1;
+    for (uint32_t b : beams) tree_cap = std::max(tree_cap, b);
+    if (K.tree_list && ((rc = ensure_pq(ctx, nq, K.tcap, 0)) || (rc = upload_beams(ctx, beams)))) return rc;
     Work& W = ctx->Wk;
     if (K.want_c == 0) {
         std::fill(out_chosen, out_chosen + static_cast<size_t>(nq) * p->nprobe, kNone);
@@ -1645,6 +1735,7 @@ int maivs_gpu_route(maivs_gpu_ctx* ctx, const float* q, uint32_t nq, const maivs
     HIP_TRY(ctx, hipMemcpyAsync(W.q, q, static_cast<size_t>(nq) * ctx->A.d * 4, hipMemcpyHostToDevice, ctx->stream));
     ctx->counters_clean = false;  // the route sets control counters that no epilogue clears
     if ((rc = launch_prep(ctx, K, W.q, kPrepReset))) return rc;
+    if (K.tree_list && (rc = launch_pq_tree(ctx, K, tree_cap))) return rc;
     if ((rc = launch_route(ctx, K))) return rc;
     Ctl ctl{};
     HIP_TRY(ctx, hipMemcpyAsync(&ctl, W.ctl, sizeof(Ctl), hipMemcpyDeviceToHost, ctx->stream));

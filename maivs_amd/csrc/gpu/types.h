@@ -46,7 +46,7 @@ struct DevArena {
     const uint32_t* entry_alt;  // E: the entry's other home (max_assign == 2), kNoAlt if none
     const uint32_t* mem_off;    // M + 1
     const uint32_t* slot_cells; // N x ma
-    const uint64_t* cent_bits;  // M x W
+    const uint64_t* cent_bits;  // M x W (null: the arena routes by the tree or every live cell only)
     const uint8_t* cent_sq8;    // M x cu.stride (chain-major) or null
     const float* cents;         // M x cf.stride (chain-major f32 centroids, when cent_sq8 is null)
     const float* csq_min;
@@ -151,6 +151,8 @@ struct KParams {
     uint32_t pq_ham;
     // matrix-core scan: items in cell order, a contiguous chunk per XCD (else arrival order)
     uint32_t xcd_order;
+    // routing: every live cell is rescored (no tree, no two-stage shortlist)
+    uint32_t flat_route;
     float tc, beta, at_margin, norm, prune_band, nucleus_band;
 };
 

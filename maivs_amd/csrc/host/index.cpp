@@ -167,9 +167,12 @@ void FlatCellIndex::set_tree_route(bool on, size_t min_cells, size_t fanout, flo
 }
 
 void FlatCellIndex::set_graph_route(bool on, size_t min_cells) {  // :2860-2866
-    // The centroid HNSW only serves the per-query router, which this build does not include.
+    // The centroid HNSW itself is not part of this build; only whether the reference would hold
+    // one (rebuild_centroid_graph, :625-636) is tracked, so that searches it would route refuse.
     graph_route_ = on;
     if (min_cells > 0) graph_min_cells_ = min_cells;
+    graph_built_ = graph_route_ && live_cell_count() >= graph_min_cells_;
+    ++generation_;
 }
 
 void FlatCellIndex::set_centroid_sq8(bool on) {  // :2873-2880
@@ -402,6 +405,7 @@ void FlatCellIndex::refresh_derived() {  // src/index.rs:864-878
     recompute_radii();
     if (two_stage_) rebuild_centroid_codes();
     if (centroid_sq8_) rebuild_centroid_sq8();
+    graph_built_ = graph_route_ && live_cell_count() >= graph_min_cells_;  // rebuild_centroid_graph
     maybe_rebuild_centroid_tree();
     ++generation_;
 }
@@ -911,7 +915,8 @@ std::string FlatCellIndex::cellmajor_blocker(bool cell_major) const {
     if (!compacted_) return "the index is not compacted (call compact() after add_batch/remove)";
     if (!(max_assign_ == 1 || !rep_off_.empty())) return "polysemic runs are missing (compact() again)";
     if (!fastscan_ || fs_off_.empty()) return "the MI355X scan needs set_fastscan(True) before compact()";
-    if (!two_stage_ || cent_bits_.empty()) return "the MI355X router needs set_two_stage(True, mult)";
+    if (!(two_stage_ && !cent_bits_.empty()) && !tree_ && graph_built_)
+        return "the centroid-graph router is not part of this build (set_graph_route(False, ...))";
     if (f16_rerank_) return "the f16 rerank store is not part of this build";
     if (!per_dim_sq_ && (!keep_f32_ || vecs_f32_.empty()))
         return "the rerank needs the f32 rows or the per-dimension SQ8 store";
@@ -953,7 +958,9 @@ const maivs_arena_desc* FlatCellIndex::arena_desc() {
     a.mem_off = mem_off_.data();
     a.members = members_flat_.data();
     a.slot_cells = slot_cells_.data();
-    a.cent_bits = cent_bits_.empty() ? nullptr : cent_bits_.data();
+    // centroid codes only while two-stage routing keeps them current (set_two_stage(False) leaves
+    // the last ones behind, src/index.rs:2882-2888)
+    a.cent_bits = two_stage_ && cent_bits_.size() == M * n_words_ ? cent_bits_.data() : nullptr;
     a.cent_sq8 = (centroid_sq8_ && !cent_sq8_.empty()) ? cent_sq8_.data() : nullptr;
     a.centroids = cents_flat_.data();
     a.csq_min = csq_min_.empty() ? nullptr : csq_min_.data();
@@ -988,6 +995,9 @@ maivs_search_params FlatCellIndex::search_params(size_t k, size_t nprobe, float 
     p.shortlist_mult = static_cast<uint32_t>(shortlist_mult_);
     p.adaptive = adaptive_ ? 1u : 0u;
     p.at_margin = at_margin_;
+    // route_batch only with two-stage routing and centroid codes, else route_query's routing
+    // (src/index.rs:1241, 1875)
+    p.route_mode = (two_stage_ && !cent_bits_.empty()) ? 0u : 1u;
     // filtering = tag_filter.is_some() && !tags.is_empty() (src/index.rs:1430-1431)
     if (tag_filter_ && !tags_.empty()) {
         p.filter = 1;
@@ -1007,10 +1017,8 @@ std::string FlatCellIndex::perquery_blocker() const {
         if (bits_.size() < ext_ids_.size() * n_words_ || bits_.empty())
             return "the Hamming scan needs the per-slot sign codes";
     }
-    if (!tree_ && graph_route_ && cells_.size() >= graph_min_cells_)
+    if (!tree_ && graph_built_)
         return "the centroid-graph router is not part of this build (set_graph_route(False, ...))";
-    if (!tree_ && (!two_stage_ || cent_bits_.empty()))
-        return "the per-query path routes with the centroid tree or set_two_stage(True, mult)";
     if (par_scan_ && !adaptive_ && max_assign_ <= 1)
         return "set_parallel_scan's within-query parallel scan is not part of this build";
     if (f16_rerank_) return "the f16 rerank store is not part of this build";

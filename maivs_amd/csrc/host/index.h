@@ -178,6 +178,9 @@ private:
     bool par_scan_ = false;
     bool graph_route_ = true;
     size_t graph_min_cells_ = 65536;
+    // the reference's cent_graph is Some: rebuilt by refresh_derived and set_graph_route when graph
+    // routing is on and enough cells are live, never by a load (src/index.rs:625-636)
+    bool graph_built_ = false;
     bool two_stage_ = false;
     size_t shortlist_mult_ = 4;
     float quant_scale_ = 0.0f;

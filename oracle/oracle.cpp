@@ -332,6 +332,15 @@ struct Routed {
     std::vector<float> cscore;
 };
 
+struct QRoute {
+    std::vector<uint64_t> bits;
+    std::vector<float> rot;
+    std::vector<uint32_t> chosen;
+    std::vector<float> cscore;
+};
+
+QRoute route_query(const Arena& A, const float* q, const maivs_search_params* p);
+
 // route_batch, src/index.rs:1873-1980
 std::vector<Routed> route_batch(const Arena& A, const float* data, uint32_t nq, const maivs_search_params* p,
                                 uint32_t nthreads) {
@@ -440,7 +449,8 @@ int orc_route_batch(const maivs_arena_desc* a, const float* q, uint32_t nq, cons
 // search_batch_cellmajor (src/index.rs:1999-2311) with the FastScan scan and rerank_exact.
 int orc_search_batch(const maivs_arena_desc* a, const float* data, uint32_t nq, const maivs_search_params* p,
                      uint32_t nthreads, uint32_t* out_slots, float* out_scores) {
-    if (!a || !p || (!data && nq) || !a->cent_bits || !a->fs_codes || !a->fs_off || p->k == 0) return MAIVS_ERR_ARG;
+    if (!a || !p || (!data && nq) || (p->route_mode == 0 && !a->cent_bits) || !a->fs_codes || !a->fs_off || p->k == 0)
+        return MAIVS_ERR_ARG;
     Arena A(a);
     const uint32_t d = A.d, nw = A.nw, M = A.M, dp = A.maxk, k = p->k;
     const uint32_t target = std::max<uint32_t>(k * std::max<uint32_t>(p->rerank_factor, 1), 1);
@@ -489,7 +499,20 @@ int orc_search_batch(const maivs_arena_desc* a, const float* data, uint32_t nq, 
     };
 
     // 1. route, then per query: FastScan table, seed scan, tau, adaptive cut (src/index.rs:2126-2191)
-    std::vector<Routed> probes = route_batch(A, data, nq, p, nthreads);
+    // route_batch returns None without two-stage routing: each query routed by route_query instead
+    // (src/index.rs:2105-2124)
+    std::vector<Routed> probes;
+    if (p->route_mode == 0) {
+        probes = route_batch(A, data, nq, p, nthreads);
+    } else {
+        probes.resize(nq);
+        par_for(nthreads, nq, [&](size_t qi) {
+            QRoute r = route_query(A, data + qi * d, p);
+            probes[qi].bits = std::move(r.bits);
+            probes[qi].chosen = std::move(r.chosen);
+            probes[qi].cscore = std::move(r.cscore);
+        }, 4);
+    }
     std::vector<QState> st(nq);
     const float norm = std::sqrt(2.0f * static_cast<float>(A.P) / static_cast<float>(M_PI));
     par_for(nthreads, nq, [&](size_t qi) {
@@ -751,13 +774,6 @@ std::vector<uint32_t> tree_search(const maivs_tree_desc& T, uint32_t nw, const u
     return out;
 }
 
-struct QRoute {
-    std::vector<uint64_t> bits;
-    std::vector<float> rot;
-    std::vector<uint32_t> chosen;
-    std::vector<float> cscore;
-};
-
 // route_query, src/index.rs:1168-1305 (the tree, two-stage and flat branches; no graph router)
 QRoute route_query(const Arena& A, const float* q, const maivs_search_params* p) {
     const maivs_arena_desc* a = A.a;
@@ -781,7 +797,8 @@ QRoute route_query(const Arena& A, const float* q, const maivs_search_params* p)
         size_t want_c = std::min<size_t>(static_cast<size_t>(p->nprobe) * std::max<uint32_t>(p->shortlist_mult, 2), T->n_leaf);
         for (uint32_t ci : tree_search(*T, nw, r.bits.data(), want_c))
             if (A.live[ci]) cs.emplace_back(ci, cent_score(A, ci, q, cqs.data(), cqbase));
-    } else if (a->cent_bits) {
+    } else if (p->route_mode == 0 && a->cent_bits) {
+        // the two-stage branch runs only with two_stage on and centroid codes present (:1241)
         std::vector<uint16_t> hs(M);
         for (uint32_t c = 0; c < M; ++c)
             hs[c] = static_cast<uint16_t>(orc_hamming(r.bits.data(), a->cent_bits + static_cast<size_t>(c) * nw, nw));

@@ -39,14 +39,17 @@ int orc_route_batch(const maivs_arena_desc* a, const float* q, uint32_t nq, cons
                     uint32_t nthreads, uint64_t* qbits, uint32_t* chosen, float* cscore, uint32_t* nchosen);
 
 /* search_batch_cellmajor + rerank_exact, src/index.rs:1999-2311, 1309-1378.
- * out nq x k slots / scores, best first, ties by ascending slot, padded UINT32_MAX / -inf. */
+ * out nq x k slots / scores, best first, ties by ascending slot, padded UINT32_MAX / -inf.
+ * p->route_mode 0 routes with route_batch; 1 routes each query with route_query (tree, else every
+ * live cell), as the reference does when route_batch returns None (:2105-2124). */
 int orc_search_batch(const maivs_arena_desc* a, const float* q, uint32_t nq, const maivs_search_params* p,
                      uint32_t nthreads, uint32_t* out_slots, float* out_scores);
 
 /* The per-query path: route_query + search_one + rerank_exact (src/index.rs:1168-1305,
  * 1381-1864, 1309-1378) for the binary FastScan configuration, every query on its own. Routing
- * uses a->tree when it has levels (src/tree.rs:559-628), else the two-stage shortlist with
- * want = nprobe * shortlist_mult. out nq x k as orc_search_batch. */
+ * uses a->tree when it has levels (src/tree.rs:559-628), else (p->route_mode 0 with a->cent_bits)
+ * the two-stage shortlist with want = nprobe * shortlist_mult, else every live cell. out nq x k as
+ * orc_search_batch. */
 int orc_search_one(const maivs_arena_desc* a, const float* q, uint32_t nq, const maivs_search_params* p,
                    uint32_t nthreads, uint32_t* out_slots, float* out_scores);
 

@@ -142,10 +142,20 @@ def test_binding_errors_and_padding():
     with pytest.raises(TypeError):
         ix.search_batch(np.zeros((4, 64), np.float64), 5)
     # not compacted, no FastScan: the per-query path's Hamming branch runs (src/index.rs:1694-1760),
-    # routed by the two-stage shortlist (the flat all-cells router is not part of this build)
-    assert "two_stage" in ix.perquery_blocker()
+    # routed over every live cell without two-stage routing (:1260-1269)
+    assert ix.perquery_blocker() == ""
+    p = np.frombuffer(ix._search_params(5, 8, 1.0, 1.0), np.uint32)
+    assert p[-1] == 1  # route_mode 1: route_query's routing
+    # a centroid graph exists once graph routing is on past min_cells live cells (src/index.rs:625-636);
+    # the graph router is not part of this build, so a search it would route refuses
+    ix.set_graph_route(True, 8)
+    assert "graph" in ix.perquery_blocker()
+    ix.set_graph_route(False, 0)
+    assert ix.perquery_blocker() == ""
     ix.set_two_stage(True, 2)
     assert ix.perquery_blocker() == ""
+    p = np.frombuffer(ix._search_params(5, 8, 1.0, 1.0), np.uint32)
+    assert p[-1] == 0  # two-stage routing with centroid codes
     assert not ix.takes_cellmajor(64, True)
     ix.set_asym_cascade(4)
     assert "cascade" in ix.perquery_blocker()
