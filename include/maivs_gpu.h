@@ -24,7 +24,11 @@
  *   maivs_gpu_place          add_batch's per-vector work, src/index.rs:2442-2610: rotation and
  *                            sign code, the centroid-tree descent (src/tree.rs:120-159, 559-628),
  *                            exact centroid scores and the home choice (assign_cells,
- *                            pick_orthogonal, :2480-2560), the i8 / SQ8 copy (:3083-3123)
+ *                            pick_orthogonal, :2480-2560), the i8 / SQ8 copy (:3083-3123),
+ *                            and the primary cell sums (:2643-2667, 3186-3196)
+ *   maivs_gpu_store_radii    recompute_radii, src/index.rs:817-861 (the dots and order statistics)
+ *   maivs_gpu_store_compact  compact_arena's row moves and FastScan packing, src/index.rs:929-1112
+ *   maivs_gpu_store_reset / _info: the row store those two read (no counterpart: see below)
  */
 #ifndef MAIVS_GPU_H
 #define MAIVS_GPU_H
@@ -94,6 +98,12 @@ typedef struct maivs_arena_desc {
      * order, and only the per-query path runs, scanning them with Hamming distances (search_one's
      * Hamming branch, src/index.rs:1694-1760). Ignored when fs_codes is given. */
     const uint64_t* slot_codes;
+    /* Nonzero: the token maivs_gpu_store_info gave for this context's row store, which holds this
+     * arena's N rows in slot order. The f32 rows, the SQ8 rows and the sign codes are then read from
+     * that store in HBM instead of from vecs_f32, sq8_codes and fs_codes / slot_codes (which may
+     * still be given and are ignored). A token of another store, or of an older state of this one,
+     * is ignored and the host arrays are used. */
+    uint64_t store_token;
 } maivs_arena_desc;
 
 /* Query-time settings of search_batch (src/index.rs:3316-3326 and the index setters). */
@@ -305,6 +315,14 @@ typedef struct maivs_place_desc {
     const float* sq_min;          /* dim (code_mode 1) */
     const float* sq_step;         /* dim (code_mode 1) */
     maivs_tree_desc tree;         /* n_levels 0: every cell is a candidate */
+    /* Optional, n entries: vector i's rows (the f32 row, the sign code and the i8 / SQ8 copy, as
+     * the context's row store keeps them) are also written to the store at slot store_slots[i],
+     * the slot add_batch gives it (src/index.rs:3077-3199, 2566-2667). */
+    const uint32_t* store_slots;
+    /* Optional, n_cells x dim, in and out: vector i's f32 row is added to the sum of its primary
+     * home (homes[i * max_assign]), the vectors of a cell in input order (add_batch's primary
+     * sums, src/index.rs:2643-2667, 3186-3196). */
+    float* sums;
 } maivs_place_desc;
 
 /*
@@ -314,6 +332,58 @@ typedef struct maivs_place_desc {
  */
 int maivs_gpu_place(maivs_gpu_ctx* ctx, const maivs_place_desc* desc, const float* x, uint32_t n,
                     uint32_t* homes, uint64_t* bits, int8_t* codes);
+
+/*
+ * The row store: the index's per-slot rows kept in HBM through the build. No counterpart in the
+ * reference, whose rows live in host memory only. Placement writes each vector's rows once
+ * (maivs_place_desc.store_slots); the cell radii, the compaction and the arena upload then read
+ * them where they are, so the build moves each row over PCIe once instead of at every step.
+ * One store per context; its layout is fixed by maivs_gpu_store_reset.
+ */
+enum {
+    MAIVS_STORE_F32 = 1,    /* f32 rows, dim floats per slot (keep_f32) */
+    MAIVS_STORE_CODES = 2,  /* i8 / SQ8 rows, dim bytes per slot (scan_i8) */
+    MAIVS_STORE_BITS = 4,   /* sign codes, n_words u64 per slot (bits) */
+};
+
+/* Empties the store and sets its layout (flags: MAIVS_STORE_*). */
+int maivs_gpu_store_reset(maivs_gpu_ctx* ctx, uint32_t dim, uint32_t n_words, uint32_t flags);
+
+/* The store's token (nonzero after a reset, new after every write) and its slot count. */
+int maivs_gpu_store_info(maivs_gpu_ctx* ctx, uint64_t* token, uint32_t* n_slots);
+
+/* What recompute_radii reads (src/index.rs:817-861), besides the store's rows. */
+typedef struct maivs_radii_desc {
+    uint32_t n_cells, dim;
+    uint32_t mode;            /* 0: f32 rows, 1: per-dimension SQ8 rows, 2: global int8 rows */
+    float inv_scale;          /* mode 2: 1 / quant_scale */
+    const uint32_t* mem_off;  /* n_cells + 1 */
+    const uint32_t* members;  /* mem_off[n_cells] slots of the store, any order within a cell */
+    const float* centroids;   /* n_cells x dim */
+    const float* sq_min;      /* dim (mode 1) */
+    const float* sq_step;     /* dim (mode 1) */
+} maivs_radii_desc;
+
+/*
+ * recompute_radii's order statistics (src/index.rs:817-861): for every cell with members, the
+ * member dots with its centroid clamped to [-1, 1] (the reference's arithmetic for each mode),
+ * and of those p99_dot = the (p99 + 1)-th largest, p99 = min(ceil(len * 0.99) - 1, len - 1) in
+ * f32, and min_dot = the smallest. acos is non-increasing on [-1, 1] (checked for every f32 input
+ * of the host's libm by the tests), so r_bound = acos(p99_dot) and r_max = acos(min_dot) are the
+ * reference's select_nth_unstable and max over the angles. Cells without members get 0.
+ */
+int maivs_gpu_store_radii(maivs_gpu_ctx* ctx, const maivs_radii_desc* desc, float* p99_dot, float* min_dot);
+
+/*
+ * compact_arena's row moves and FastScan packing (src/index.rs:929-1112) in the store: slot s of
+ * the compacted store is old slot old_of_new[s]; then, when fs_codes is given, every cell's members
+ * (mem_off / members, in compacted slots and final member order) are packed into FastScan blocks
+ * from the store's sign codes (fs_pack_block, src/quantize.rs:238-265), cell c's blocks at
+ * fs_off[c]. The compacted rows are also copied to rows_out / codes_out / bits_out where given.
+ */
+int maivs_gpu_store_compact(maivs_gpu_ctx* ctx, const uint32_t* old_of_new, uint32_t n_new, uint32_t n_cells,
+                            const uint32_t* mem_off, const uint32_t* members, const uint32_t* fs_off,
+                            uint8_t* fs_codes, float* rows_out, int8_t* codes_out, uint64_t* bits_out);
 
 #ifdef __cplusplus
 }

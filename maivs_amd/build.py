@@ -16,7 +16,7 @@ import sysconfig
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 HOST_SRC = [os.path.join(HERE, "csrc", "host", f) for f in ("bind.cpp", "index.cpp", "tree.cpp", "persist.cpp")]
-GPU_SRC = [os.path.join(HERE, "csrc", "gpu", f) for f in ("maivs_gpu.hip", "build.hip")]
+GPU_SRC = [os.path.join(HERE, "csrc", "gpu", f) for f in ("maivs_gpu.hip", "build.hip", "store.hip")]
 GPU_LIB = os.path.join(HERE, "libmaivs_gpu.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # Device code: no FMA contraction (bit-exact parity with the reference's f32 arithmetic), no

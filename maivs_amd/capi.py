@@ -31,6 +31,7 @@ class ArenaDesc(C.Structure):
         ("centroids", C.c_void_p), ("csq_min", C.c_void_p), ("csq_step", C.c_void_p), ("r_bound", C.c_void_p),
         ("rot_signs", C.c_void_p), ("vecs_f32", C.c_void_p), ("sq8_codes", C.c_void_p), ("sq_min", C.c_void_p),
         ("sq_step", C.c_void_p), ("tags", C.c_void_p), ("tree", C.c_void_p), ("slot_codes", C.c_void_p),
+        ("store_token", C.c_uint64),
     ]
 
 
@@ -76,6 +77,10 @@ SIGNATURES = {
     "maivs_gpu_search_queries_device": (I32, [P, P, U32, C.POINTER(SearchParams), P, P, C.POINTER(GpuStats)]),
     "maivs_gpu_kmeans": (I32, [P, P, U64, U32, P, P, U32, P, P]),
     "maivs_gpu_place": (I32, [P, P, P, U32, P, P, P]),
+    "maivs_gpu_store_reset": (I32, [P, U32, U32, U32]),
+    "maivs_gpu_store_info": (I32, [P, P, P]),
+    "maivs_gpu_store_radii": (I32, [P, P, P, P]),
+    "maivs_gpu_store_compact": (I32, [P, P, U32, U32, P, P, P, P, P, P, P]),
 }
 
 _lib = None

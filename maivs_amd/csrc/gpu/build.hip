@@ -20,6 +20,7 @@
 
 #include "build_kernels.h"
 #include "ctx.h"
+#include "store.h"
 
 using namespace maivs_host;
 
@@ -271,5 +272,12 @@ extern "C" int maivs_gpu_place(maivs_gpu_ctx* ctx, const maivs_place_desc* pd, c
     if (D.code_mode)
         HIP_TRY(ctx, hipMemcpyAsync(codes, d_codes, static_cast<size_t>(n) * d, hipMemcpyDeviceToHost, ctx->stream));
     HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    // the rows into the row store, and the primary sums, while the batch is on the device
+    if (D.store_slots && (rc = store_write(ctx, D.store_slots, n, d_x, d_bits, d_codes, D.code_mode != 0))) return rc;
+    if (D.sums) {
+        for (uint32_t i = 0; i < n; ++i)
+            if (homes[static_cast<size_t>(i) * ma] >= M) return fail(ctx, MAIVS_ERR_HIP, "maivs_gpu_place: vector %u has no home", i);
+        if ((rc = cell_sums(ctx, d_x, d_homes, ma, n, M, d, D.sums))) return rc;
+    }
     return 0;
 }

@@ -16,6 +16,19 @@
 
 using namespace maivs_dev;
 
+// The index's per-slot rows in HBM through the build (maivs_gpu_store_*): f32 rows, i8 / SQ8
+// rows and sign codes in slot order, the arrays the layout flags name. `token` changes with every
+// write, so an arena description can name the exact state it was made from.
+struct RowStore {
+    uint32_t dim = 0, W = 0, flags = 0;
+    uint32_t n = 0, cap = 0;
+    float* f32 = nullptr;
+    int8_t* codes = nullptr;
+    uint64_t* bits = nullptr;
+    uint64_t token = 0;  // 0: never reset
+    std::vector<void*> allocs;
+};
+
 struct maivs_gpu_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
@@ -70,6 +83,7 @@ struct maivs_gpu_ctx {
     uint32_t tree_min_beam = 32;
     // this device's fixed scratch array (ScratchSlot, maivs_gpu.hip), set at create
     void* scratch = nullptr;
+    RowStore store;
 };
 
 namespace maivs_host {

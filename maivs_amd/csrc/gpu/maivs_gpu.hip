@@ -1183,6 +1183,7 @@ void maivs_gpu_destroy(maivs_gpu_ctx* ctx) {
     free_all(ctx->cand_allocs);
     free_all(ctx->pq_allocs);
     free_all(ctx->arena_allocs);
+    free_all(ctx->store.allocs);
     for (auto& e : ctx->ev)
         if (e) (void)hipEventDestroy(e);
     if (ctx->h_ctl) (void)hipHostFree(ctx->h_ctl);
@@ -1196,8 +1197,15 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
     if (!ctx || !a) return MAIVS_ERR_ARG;
     std::lock_guard<std::mutex> lk(ctx->mu);
     HIP_TRY(ctx, hipSetDevice(ctx->device));
-    const bool fs_arena = a->fs_codes && a->fs_off;
-    if (!(fs_arena || a->slot_codes) || !a->mem_off || !a->members || !a->rot_signs || !a->r_bound)
+    // this context's row store holds the arena's rows in slot order: they are read there (no H2D),
+    // and the description may then leave vecs_f32, sq8_codes, fs_codes and slot_codes out
+    const RowStore& R = ctx->store;
+    const bool from_store = a->store_token != 0 && a->store_token == R.token && R.n == a->n_slots &&
+                            R.dim == a->dim && R.W == a->n_words && (R.flags & MAIVS_STORE_BITS) &&
+                            (a->rerank_mode == MAIVS_RERANK_F32 ? (R.flags & MAIVS_STORE_F32) != 0
+                                                                : (R.flags & MAIVS_STORE_CODES) != 0);
+    const bool fs_arena = a->fs_off && (a->fs_codes || from_store);
+    if (!(fs_arena || a->slot_codes || from_store) || !a->mem_off || !a->members || !a->rot_signs || !a->r_bound)
         return fail(ctx, MAIVS_ERR_ARG, "arena is missing its codes (FastScan blocks or per-slot codes), members, "
                                         "rotation or radii");
     if (!supported_nw(a->n_words)) return fail(ctx, MAIVS_ERR_UNSUPPORTED, "n_words %u not in {1,2,4,8,16}", a->n_words);
@@ -1211,8 +1219,8 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
     }
     if (!a->cent_sq8 && !a->centroids) return fail(ctx, MAIVS_ERR_ARG, "no centroid store for the rescore");
     if (a->cent_sq8 && (!a->csq_min || !a->csq_step)) return fail(ctx, MAIVS_ERR_ARG, "csq_min/csq_step missing");
-    if (a->rerank_mode == MAIVS_RERANK_F32 && !a->vecs_f32) return fail(ctx, MAIVS_ERR_ARG, "f32 rows missing");
-    if (a->rerank_mode == MAIVS_RERANK_SQ8 && (!a->sq8_codes || !a->sq_min || !a->sq_step))
+    if (a->rerank_mode == MAIVS_RERANK_F32 && !a->vecs_f32 && !from_store) return fail(ctx, MAIVS_ERR_ARG, "f32 rows missing");
+    if (a->rerank_mode == MAIVS_RERANK_SQ8 && ((!a->sq8_codes && !from_store) || !a->sq_min || !a->sq_step))
         return fail(ctx, MAIVS_ERR_ARG, "SQ8 rows missing");
     if (a->rerank_mode > MAIVS_RERANK_SQ8) return fail(ctx, MAIVS_ERR_UNSUPPORTED, "rerank mode %u", a->rerank_mode);
     if (a->dim == 0 || a->dim > a->dim_pad || a->dim_pad > 4096 || (a->dim_pad & (a->dim_pad - 1)))
@@ -1299,7 +1307,9 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
         float *csq_min = nullptr, *csq_step = nullptr, *r_bound = nullptr, *signs = nullptr, *sq_min = nullptr,
               *sq_step = nullptr;
         uint64_t* scodes = nullptr;
-        if (fs_arena) {
+        if (from_store) {
+            scodes = R.bits;  // the members' codes are gathered from the store's sign codes
+        } else if (fs_arena) {
             const uint64_t nblocks = a->fs_off[A.M];
             if ((rc = stage(a->fs_codes, nblocks * A.W * 256, &fs))) return rc;
             if ((rc = stage(a->fs_off, static_cast<uint64_t>(A.M) + 1, &fs_off))) return rc;
@@ -1332,7 +1342,7 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
         if ((rc = dupload(ctx, a->r_bound, A.M, &r_bound))) return rc;
         if ((rc = dupload(ctx, a->rot_signs, 2ull * A.P, &signs))) return rc;
         if (!dead.empty() && (rc = dupload(ctx, dead.data(), dead.size(), &ddead))) return rc;
-        if (fs_arena) {
+        if (fs_arena && !from_store) {
             hipLaunchKernelGGL(fs_to_codes_kernel, dim3(std::max<uint32_t>(A.M, 1)), dim3(256), 0, ctx->stream, fs,
                                fs_off, mem_off, A.M, A.W, codes);
         } else if (A.E) {
@@ -1358,20 +1368,21 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
         ctx->tree_min_beam = a->tree ? a->tree->min_beam : 32u;
         HIP_TRY(ctx, hipGetLastError());
         // chain-major copies of the rows the 8-lane dots read
-        auto chain_f32 = [&](const float* src, uint64_t rows, const float** out) -> int {
-            float *raw = nullptr, *cm = nullptr;
+        // dev: the rows already in HBM (the row store), else src is staged
+        auto chain_f32 = [&](const float* src, uint64_t rows, const float** out, const float* dev = nullptr) -> int {
+            float *raw = const_cast<float*>(dev), *cm = nullptr;
             int r;
-            if ((r = stage(src, rows * A.d, &raw))) return r;
+            if (!raw && (r = stage(src, rows * A.d, &raw))) return r;
             if ((r = dalloc(ctx, ctx->arena_allocs, &cm, rows * A.cf.stride))) return r;
             hipLaunchKernelGGL(to_chain_kernel<float>, dim3(static_cast<uint32_t>(std::min<uint64_t>(rows, 65535))),
                                dim3(256), 0, ctx->stream, raw, rows, A.d, A.cf, cm);
             *out = cm;
             return 0;
         };
-        auto chain_u8 = [&](const uint8_t* src, uint64_t rows, const uint8_t** out) -> int {
-            uint8_t *raw = nullptr, *cm = nullptr;
+        auto chain_u8 = [&](const uint8_t* src, uint64_t rows, const uint8_t** out, const uint8_t* dev = nullptr) -> int {
+            uint8_t *raw = const_cast<uint8_t*>(dev), *cm = nullptr;
             int r;
-            if ((r = stage(src, rows * A.d, &raw))) return r;
+            if (!raw && (r = stage(src, rows * A.d, &raw))) return r;
             if ((r = dalloc(ctx, ctx->arena_allocs, &cm, rows * A.cu.stride))) return r;
             hipLaunchKernelGGL(to_chain_kernel<uint8_t>, dim3(static_cast<uint32_t>(std::min<uint64_t>(rows, 65535))),
                                dim3(256), 0, ctx->stream, raw, rows, A.d, A.cu, cm);
@@ -1386,9 +1397,10 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
             if ((rc = chain_f32(a->centroids, A.M, &A.cents))) return rc;
         }
         if (A.rerank_mode == MAIVS_RERANK_F32) {
-            if ((rc = chain_f32(a->vecs_f32, A.N, &A.vecs))) return rc;
+            if ((rc = chain_f32(a->vecs_f32, A.N, &A.vecs, from_store ? R.f32 : nullptr))) return rc;
         } else {
-            if ((rc = chain_u8(a->sq8_codes, A.N, &A.sq8))) return rc;
+            if ((rc = chain_u8(a->sq8_codes, A.N, &A.sq8, from_store ? reinterpret_cast<const uint8_t*>(R.codes) : nullptr)))
+                return rc;
             if ((rc = dupload(ctx, a->sq_min, A.d, &sq_min))) return rc;
             if ((rc = dupload(ctx, a->sq_step, A.d, &sq_step))) return rc;
         }

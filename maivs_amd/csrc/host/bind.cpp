@@ -295,6 +295,8 @@ PYBIND11_MODULE(_maivs, m) {
                  return reinterpret_cast<uintptr_t>(d);
              },
              "Address of the maivs_arena_desc of the arena (valid until the next mutation).")
+        .def("_store_mirrors", [](PyIndex& s) { Ref _b(s); return s.ix.store_mirrors(); },
+             "Whether the GPU session's row store holds this index's rows (a GPU build keeps it).")
         .def("_search_params",
              [](PyIndex& s, size_t k, size_t nprobe, float tc, float beta) { Ref _b(s); 
                  maivs_search_params p = s.ix.search_params(k, nprobe, tc, beta);

@@ -31,6 +31,11 @@ struct GpuApi {
                   uint32_t, uint32_t*, float*) = nullptr;
     int (*place)(maivs_gpu_ctx*, const maivs_place_desc*, const float*, uint32_t, uint32_t*, uint64_t*,
                  int8_t*) = nullptr;
+    int (*store_reset)(maivs_gpu_ctx*, uint32_t, uint32_t, uint32_t) = nullptr;
+    int (*store_info)(maivs_gpu_ctx*, uint64_t*, uint32_t*) = nullptr;
+    int (*store_radii)(maivs_gpu_ctx*, const maivs_radii_desc*, float*, float*) = nullptr;
+    int (*store_compact)(maivs_gpu_ctx*, const uint32_t*, uint32_t, uint32_t, const uint32_t*, const uint32_t*,
+                         const uint32_t*, uint8_t*, float*, int8_t*, uint64_t*) = nullptr;
     std::string error;
 };
 
@@ -71,6 +76,10 @@ const GpuApi& gpu_api() {
         api.search_pq = reinterpret_cast<decltype(api.search_pq)>(sym("maivs_gpu_search_queries"));
         api.kmeans = reinterpret_cast<decltype(api.kmeans)>(sym("maivs_gpu_kmeans"));
         api.place = reinterpret_cast<decltype(api.place)>(sym("maivs_gpu_place"));
+        api.store_reset = reinterpret_cast<decltype(api.store_reset)>(sym("maivs_gpu_store_reset"));
+        api.store_info = reinterpret_cast<decltype(api.store_info)>(sym("maivs_gpu_store_info"));
+        api.store_radii = reinterpret_cast<decltype(api.store_radii)>(sym("maivs_gpu_store_radii"));
+        api.store_compact = reinterpret_cast<decltype(api.store_compact)>(sym("maivs_gpu_store_compact"));
     });
     return api;
 }
@@ -156,6 +165,7 @@ FlatCellIndex::~FlatCellIndex() = default;
 void FlatCellIndex::set_i8_rerank(bool on) {  // src/index.rs:2827-2832
     i8_rerank_ = on;
     keep_f32_ = !on;
+    store_ok_ = false;  // the rows' layout changes
 }
 
 void FlatCellIndex::set_tree_route(bool on, size_t min_cells, size_t fanout, float beam_frac) {  // :2840-2853
@@ -198,6 +208,7 @@ void FlatCellIndex::set_adaptive(bool on, float margin) {  // :2899-2902
 
 void FlatCellIndex::set_per_dim_sq(bool on) {  // :2908-2915
     per_dim_sq_ = on;
+    store_ok_ = false;  // the rows' layout changes
     if (on) {
         i8_rerank_ = true;
         f16_rerank_ = false;
@@ -357,7 +368,67 @@ void FlatCellIndex::rebuild_centroid_sq8() {  // src/index.rs:730-775
         }
 }
 
+// The session's row store's current token (the arena description names it, so the upload reads
+// the rows where they are).
+void FlatCellIndex::refresh_store_token() {
+    uint32_t n = 0;
+    gpu_->check(gpu_api().store_info(gpu_->ctx_, &store_token_, &n), "maivs_gpu_store_info");
+    if (n != ext_ids_.size()) {
+        store_ok_ = false;
+        throw std::runtime_error("the GPU row store holds " + std::to_string(n) + " slots, the index " +
+                                 std::to_string(ext_ids_.size()));
+    }
+}
+
+// recompute_radii on the GPU, from the row store: the device returns each cell's (p99 + 1)-th
+// largest and smallest clamped member dot, and the angles are their acos here. acosf is
+// non-increasing on [-1, 1], so these are the reference's p99-th smallest and largest angle.
+bool FlatCellIndex::gpu_radii() {
+    if (!gpu_build_ || !store_ok_ || !gpu_ || f16_rerank_) return false;
+    uint32_t mode;
+    if (per_dim_sq_)
+        mode = 1;
+    else if (keep_f32_)
+        mode = 0;
+    else
+        mode = 2;
+    if (mode == 0 ? vecs_f32_.empty() : scan_i8_.empty()) return false;
+    const size_t M = cells_.size();
+    std::vector<uint32_t> off(M + 1, 0), mem;
+    for (size_t c = 0; c < M; ++c) off[c + 1] = off[c] + static_cast<uint32_t>(cells_[c].members.size());
+    mem.resize(off[M]);
+    std::vector<float> cents(M * dim_);
+    for (size_t c = 0; c < M; ++c) {
+        std::copy(cells_[c].members.begin(), cells_[c].members.end(), mem.begin() + off[c]);
+        std::memcpy(&cents[c * dim_], cells_[c].centroid.data(), dim_ * sizeof(float));
+    }
+    maivs_radii_desc D{};
+    D.n_cells = static_cast<uint32_t>(M);
+    D.dim = static_cast<uint32_t>(dim_);
+    D.mode = mode;
+    D.inv_scale = quant_scale_ > 0.0f ? 1.0f / quant_scale_ : 1.0f;
+    D.mem_off = off.data();
+    D.members = mem.data();
+    D.centroids = cents.data();
+    D.sq_min = sq_min_.empty() ? nullptr : sq_min_.data();
+    D.sq_step = sq_step_.empty() ? nullptr : sq_step_.data();
+    std::vector<float> p99(M), mn(M);
+    gpu_->check(gpu_api().store_radii(gpu_->ctx_, &D, p99.data(), mn.data()), "maivs_gpu_store_radii");
+    for (size_t c = 0; c < M; ++c) {
+        Cell& cell = cells_[c];
+        if (cell.members.empty()) {
+            cell.r_bound = 0.0f;
+            cell.r_max = 0.0f;
+        } else {
+            cell.r_bound = std::acos(p99[c]);
+            cell.r_max = std::acos(mn[c]);
+        }
+    }
+    return true;
+}
+
 void FlatCellIndex::recompute_radii() {  // src/index.rs:817-861
+    if (gpu_radii()) return;
     float inv = quant_scale_ > 0.0f ? 1.0f / quant_scale_ : 1.0f;
     size_t d = dim_;
     parallel_for(cells_.size(), [&](size_t ci) {
@@ -589,7 +660,8 @@ void fill_tree_desc(const TreeFlat& tf, maivs_tree_desc& td) {
 // add_batch's per-vector work on the GPU (maivs_gpu_place): the homes of every input vector
 // (assign_cells_routed), its 1-bit code and, when kept, its i8 / SQ8 copy.
 void FlatCellIndex::place_on_gpu(const float* data, size_t n, bool store_i8, std::vector<std::vector<uint32_t>>& asg,
-                                 std::vector<uint64_t>& bits, std::vector<int8_t>& i8) {
+                                 std::vector<uint64_t>& bits, std::vector<int8_t>& i8, const uint32_t* slots,
+                                 float* sums) {
     session();
     const size_t M = cells_.size(), ma = max_assign_;
     std::vector<float> cents(M * dim_);
@@ -621,8 +693,10 @@ void FlatCellIndex::place_on_gpu(const float* data, size_t n, bool store_i8, std
     if (store_i8) i8.assign(n * dim_, 0);
     // batches of at most 2^20 vectors keep the device copy of the inputs bounded
     const size_t step = size_t{1} << 20;
+    D.sums = sums;  // in and out: the chunks add in input order
     for (size_t b = 0; b < n; b += step) {
         const size_t m = std::min(step, n - b);
+        D.store_slots = slots ? slots + b : nullptr;
         gpu_->check(gpu_api().place(gpu_->ctx_, &D, data + b * dim_, static_cast<uint32_t>(m), &homes[b * ma],
                                     &bits[b * n_words_], store_i8 ? &i8[b * dim_] : nullptr),
                     "maivs_gpu_place");
@@ -665,8 +739,32 @@ void FlatCellIndex::add_batch(const std::vector<uint64_t>& ids, const float* dat
     std::vector<int8_t> g_i8;
     const bool on_gpu = gpu_build_ && n > 0;
     if (on_gpu) {
-        place_on_gpu(data, n, store_i8, asg, g_bits, g_i8);
+        // The session's row store: started by the first GPU add_batch of an empty index and kept
+        // up by the following ones. Each input's slot is the one the loops below give it: free
+        // slots from the back of the list first, then appended ones.
+        session();
+        if (ext_ids_.empty()) {
+            const uint32_t flags = (keep_f32_ ? MAIVS_STORE_F32 : 0u) | (store_i8 ? MAIVS_STORE_CODES : 0u) |
+                                   (store_bits ? MAIVS_STORE_BITS : 0u);
+            gpu_->check(gpu_api().store_reset(gpu_->ctx_, static_cast<uint32_t>(dim_), static_cast<uint32_t>(nw), flags),
+                        "maivs_gpu_store_reset");
+            store_ok_ = true;
+        }
+        std::vector<uint32_t> slots;
+        if (store_ok_) {
+            slots.resize(n);
+            const size_t nr = std::min(free_slots_.size(), n);
+            for (size_t i = 0; i < n; ++i)
+                slots[i] = static_cast<uint32_t>(i < nr ? free_slots_[free_slots_.size() - 1 - i] : ext_ids_.size() + (i - nr));
+        }
+        // the primary sums on the device too (the same adds in the same order)
+        const size_t M = cells_.size();
+        std::vector<float> sums(M * dim_);
+        for (size_t c = 0; c < M; ++c) std::memcpy(&sums[c * dim_], cells_[c].sum.data(), dim_ * sizeof(float));
+        place_on_gpu(data, n, store_i8, asg, g_bits, g_i8, store_ok_ ? slots.data() : nullptr, sums.data());
+        for (size_t c = 0; c < M; ++c) std::memcpy(cells_[c].sum.data(), &sums[c * dim_], dim_ * sizeof(float));
     } else {
+        store_ok_ = false;  // the rows are written by the host alone
         // one scratch per chunk of 256 vectors keeps allocation out of the inner loop
         size_t nchunk = (n + 255) / 256;
         parallel_for(nchunk, [&](size_t ch) {
@@ -701,7 +799,7 @@ void FlatCellIndex::add_batch(const std::vector<uint64_t>& ids, const float* dat
         for (size_t j = 0; j < asg[i].size(); ++j) {
             Cell& c = cells_[asg[i][j]];
             c.members.push_back(s);
-            if (j == 0)
+            if (j == 0 && !on_gpu)
                 for (size_t d = 0; d < dim_; ++d) c.sum[d] += v[d];
         }
         id_to_slot_[ids[i]] = s;
@@ -731,6 +829,10 @@ void FlatCellIndex::add_batch(const std::vector<uint64_t>& ids, const float* dat
             id_to_slot_[ids[n_reuse + i]] = slot;
         }
         n_live_ += m;
+    }
+    if (n_reuse < n && !on_gpu) {
+        const size_t m = n - n_reuse;
+        const float* dat = data + n_reuse * dim_;
         // primary sums, parallel over cells, input order within a cell
         size_t M = cells_.size();
         std::vector<size_t> start(M + 1, 0);
@@ -746,6 +848,7 @@ void FlatCellIndex::add_batch(const std::vector<uint64_t>& ids, const float* dat
             }
         }, 16);
     }
+    if (on_gpu && store_ok_) refresh_store_token();
     for (auto& c : cells_) recompute_centroid(c);
     refresh_derived();
 }
@@ -815,19 +918,21 @@ void FlatCellIndex::compact_arena() {  // src/index.rs:929-1112
         old_of_new.push_back(s);
     }
     size_t n_new = old_of_new.size();
-    if (keep_f32_ && !vecs_f32_.empty()) {
+    // with a mirroring row store the rows move on the GPU (below, after the member lists)
+    const bool on_gpu = gpu_build_ && store_ok_ && gpu_;
+    if (keep_f32_ && !vecs_f32_.empty() && !on_gpu) {
         std::vector<float> v(n_new * d);
         for (size_t ns = 0; ns < n_new; ++ns)
             std::memcpy(&v[ns * d], &vecs_f32_[static_cast<size_t>(old_of_new[ns]) * d], d * sizeof(float));
         vecs_f32_.swap(v);
     }
-    if (!scan_i8_.empty()) {
+    if (!scan_i8_.empty() && !on_gpu) {
         std::vector<int8_t> v(n_new * d);
         for (size_t ns = 0; ns < n_new; ++ns)
             std::memcpy(&v[ns * d], &scan_i8_[static_cast<size_t>(old_of_new[ns]) * d], d);
         scan_i8_.swap(v);
     }
-    if (!bits_.empty() && nw > 0) {
+    if (!bits_.empty() && nw > 0 && !on_gpu) {
         std::vector<uint64_t> v(n_new * nw);
         for (size_t ns = 0; ns < n_new; ++ns)
             std::memcpy(&v[ns * nw], &bits_[static_cast<size_t>(old_of_new[ns]) * nw], nw * 8);
@@ -878,12 +983,38 @@ void FlatCellIndex::compact_arena() {  // src/index.rs:929-1112
     }
     fs_codes_.clear();
     fs_off_.clear();
-    if (fastscan_ && scan_mode_ == ScanMode::Binary && nw > 0) {
-        size_t bb = fs_block_bytes(nw);
+    const bool pack = fastscan_ && scan_mode_ == ScanMode::Binary && nw > 0;
+    const size_t bb = fs_block_bytes(nw);
+    if (pack) {
         fs_off_.assign(cells_.size() + 1, 0);
         for (size_t ci = 0; ci < cells_.size(); ++ci)
             fs_off_[ci + 1] = fs_off_[ci] + static_cast<uint32_t>((cells_[ci].members.size() + kFsBlock - 1) / kFsBlock);
         fs_codes_.assign(static_cast<size_t>(fs_off_.back()) * bb, 0);
+    }
+    // flattened CSR for the arena descriptor
+    mem_off_.assign(cells_.size() + 1, 0);
+    for (size_t ci = 0; ci < cells_.size(); ++ci)
+        mem_off_[ci + 1] = mem_off_[ci] + static_cast<uint32_t>(cells_[ci].members.size());
+    members_flat_.resize(mem_off_.back());
+    for (size_t ci = 0; ci < cells_.size(); ++ci)
+        std::copy(cells_[ci].members.begin(), cells_[ci].members.end(), members_flat_.begin() + mem_off_[ci]);
+    if (on_gpu) {
+        // the store's rows move to their new slots, the FastScan blocks are packed from its codes,
+        // and the compacted rows come back for the index's own arrays
+        std::vector<float> v32(keep_f32_ && !vecs_f32_.empty() ? n_new * d : 0);
+        std::vector<int8_t> v8(!scan_i8_.empty() ? n_new * d : 0);
+        std::vector<uint64_t> vb(!bits_.empty() && nw > 0 ? n_new * nw : 0);
+        const uint32_t M = static_cast<uint32_t>(cells_.size());
+        gpu_->check(gpu_api().store_compact(gpu_->ctx_, old_of_new.data(), static_cast<uint32_t>(n_new), M, mem_off_.data(),
+                                            members_flat_.data(), pack ? fs_off_.data() : nullptr,
+                                            pack ? fs_codes_.data() : nullptr, v32.empty() ? nullptr : v32.data(),
+                                            v8.empty() ? nullptr : v8.data(), vb.empty() ? nullptr : vb.data()),
+                    "maivs_gpu_store_compact");
+        if (!v32.empty()) vecs_f32_.swap(v32);
+        if (!v8.empty()) scan_i8_.swap(v8);
+        if (!vb.empty()) bits_.swap(vb);
+        refresh_store_token();
+    } else if (pack) {
         parallel_for(cells_.size(), [&](size_t ci) {
             const auto& mem = cells_[ci].members;
             size_t nb = fs_off_[ci + 1] - fs_off_[ci];
@@ -895,13 +1026,6 @@ void FlatCellIndex::compact_arena() {  // src/index.rs:929-1112
             }
         }, 16);
     }
-    // flattened CSR for the arena descriptor
-    mem_off_.assign(cells_.size() + 1, 0);
-    for (size_t ci = 0; ci < cells_.size(); ++ci)
-        mem_off_[ci + 1] = mem_off_[ci] + static_cast<uint32_t>(cells_[ci].members.size());
-    members_flat_.resize(mem_off_.back());
-    for (size_t ci = 0; ci < cells_.size(); ++ci)
-        std::copy(cells_[ci].members.begin(), cells_[ci].members.end(), members_flat_.begin() + mem_off_[ci]);
     ++generation_;
     compacted_ = true;
 }
@@ -955,6 +1079,7 @@ const maivs_arena_desc* FlatCellIndex::arena_desc() {
     a.fs_codes = fs && !fs_codes_.empty() ? fs_codes_.data() : nullptr;
     a.fs_off = fs ? fs_off_.data() : nullptr;
     a.slot_codes = bits_.size() >= ext_ids_.size() * n_words_ && !bits_.empty() ? bits_.data() : nullptr;
+    a.store_token = store_ok_ ? store_token_ : 0;
     a.mem_off = mem_off_.data();
     a.members = members_flat_.data();
     a.slot_cells = slot_cells_.data();
@@ -1031,7 +1156,18 @@ std::string FlatCellIndex::perquery_blocker() const {
 void FlatCellIndex::ensure_uploaded() {
     // called with the session's mutex held (searches serialise on it)
     if (gpu_->uploaded_gen != generation_) {
-        gpu_->check(gpu_api().upload(gpu_->ctx_, arena_desc()), "maivs_gpu_upload_arena");
+        const maivs_arena_desc* desc = arena_desc();
+        if (!desc) throw std::runtime_error("the index has no cells");
+        maivs_arena_desc a = *desc;
+        if (store_ok_) {
+            // the rows are in the session's row store: the upload reads them there, and fails
+            // rather than falling back to a host copy if the store and the index ever disagree
+            a.vecs_f32 = nullptr;
+            a.sq8_codes = nullptr;
+            a.fs_codes = nullptr;
+            a.slot_codes = nullptr;
+        }
+        gpu_->check(gpu_api().upload(gpu_->ctx_, &a), "maivs_gpu_upload_arena");
         gpu_->uploaded_gen = generation_;
     }
 }

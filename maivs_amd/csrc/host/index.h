@@ -73,6 +73,7 @@ public:
     void rebuild_tree() { rebuild_centroid_tree(); }
     // Not in the reference: run the index build's heavy steps on the GPU (bit-identical results).
     void set_gpu_build(bool on) { gpu_build_ = on; }
+    bool store_mirrors() const { return store_ok_; }
     bool gpu_build() const { return gpu_build_; }
     // One batch of k-means jobs through the CPU or the GPU runner (test hook).
     void run_kmeans(const float* x, size_t n_rows, size_t dim, const uint32_t* rows, const std::vector<KMeansJob>& jobs,
@@ -149,7 +150,9 @@ private:
     KMeansRunner gpu_kmeans_runner();
     void ensure_uploaded();
     void place_on_gpu(const float* data, size_t n, bool store_i8, std::vector<std::vector<uint32_t>>& asg,
-                      std::vector<uint64_t>& bits, std::vector<int8_t>& i8);
+                      std::vector<uint64_t>& bits, std::vector<int8_t>& i8, const uint32_t* slots, float* sums);
+    bool gpu_radii();
+    void refresh_store_token();
 
     size_t dim_, rerank_factor_, dim_pad_, n_words_;
     ScanMode scan_mode_;
@@ -210,6 +213,11 @@ private:
     maivs_tree_desc tree_desc_{};
     uint64_t generation_ = 0;
     bool gpu_build_ = false;
+    // The GPU session's row store mirrors bits_, scan_i8_ and vecs_f32_ slot for slot: set by a GPU
+    // build's first add_batch, kept by later GPU add_batch / remove / compact, cleared by anything
+    // that writes those arrays otherwise (a CPU add_batch, a load, a change of their layout).
+    bool store_ok_ = false;
+    uint64_t store_token_ = 0;
     bool batched_filter_ = false;
     std::unique_ptr<GpuSession> gpu_;
     std::mutex session_mu_;  // guards the creation of gpu_ (searches share the index)

@@ -256,6 +256,7 @@ void FlatCellIndex::load_file(const std::string& path) {  // src/persist.rs:145-
     graph_route_ = true;
     graph_min_cells_ = 65536;
     graph_built_ = false;  // a load builds no centroid graph (src/persist.rs:228)
+    store_ok_ = false;     // the loaded rows are not in the GPU session's row store
     tag_filter_.reset();
     tree_.reset();
     tree_route_ = h[13] != 0;

@@ -38,6 +38,7 @@ _SIGS = {
     "orc_set_record": (None, [C.c_int]),
     "orc_search_one": (C.c_int, [P, P, U32, C.POINTER(SearchParams), U32, P, P]),
     "orc_route_query": (C.c_int, [P, P, U32, C.POINTER(SearchParams), U32, P, P, P]),
+    "orc_acosf_violations": (U64, [U32, P]),
 }
 
 
@@ -205,3 +206,11 @@ def set_record(on: bool) -> None:
     """Keep (True, the default) or skip each query's candidate list for last_candidates; the CPU
     baseline's timing runs skip it, as the reference keeps nothing of the kind."""
     lib().orc_set_record(1 if on else 0)
+
+
+def acosf_violations(nthreads: int = 8):
+    """(count, first x) of the f32 inputs in [-1, 1] where the host libm's acosf increases from one
+    input to the next (none expected: the GPU radii rely on acosf being non-increasing)."""
+    first = C.c_uint64(0)
+    n = lib().orc_acosf_violations(nthreads, C.byref(first))
+    return int(n), int(first.value)

@@ -1039,3 +1039,44 @@ int orc_search_one(const maivs_arena_desc* a, const float* data, uint32_t nq, co
 }
 
 }  // extern "C"
+
+// ---- the host libm (not a restatement): what the GPU radii rely on ----
+
+extern "C" uint64_t orc_acosf_violations(uint32_t nthreads, uint64_t* first_bad_bits) {
+    // Every f32 in [-1, 1] in increasing order: -1 .. -0 (bit patterns 0xBF800000 down to
+    // 0x80000000), then +0 .. 1 (0x00000000 up to 0x3F800000). Counts the x whose successor y has
+    // acosf(y) > acosf(x), i.e. where acosf fails to be non-increasing.
+    const uint64_t n_neg = 0xBF800000ull - 0x80000000ull + 1, N = 2 * n_neg;
+    auto at = [&](uint64_t k) -> float {
+        const uint32_t b = static_cast<uint32_t>(k < n_neg ? 0xBF800000ull - k : k - n_neg);
+        float f;
+        std::memcpy(&f, &b, 4);
+        return f;
+    };
+    const size_t chunks = 4096;
+    std::vector<uint64_t> bad(chunks, 0), first(chunks, UINT64_MAX);
+    par_for(nthreads, chunks, [&](size_t ch) {
+        const uint64_t lo = 1 + (N - 1) * ch / chunks, hi = 1 + (N - 1) * (ch + 1) / chunks;
+        float prev = std::acos(at(lo - 1));
+        for (uint64_t k = lo; k < hi; ++k) {
+            const float cur = std::acos(at(k));
+            if (cur > prev) {
+                if (!bad[ch]) first[ch] = k - 1;
+                ++bad[ch];
+            }
+            prev = cur;
+        }
+    });
+    uint64_t total = 0, f = UINT64_MAX;
+    for (size_t ch = 0; ch < chunks; ++ch) {
+        total += bad[ch];
+        f = std::min(f, first[ch]);
+    }
+    if (first_bad_bits) {
+        float x = f == UINT64_MAX ? 0.0f : at(f);
+        uint32_t b;
+        std::memcpy(&b, &x, 4);
+        *first_bad_bits = f == UINT64_MAX ? UINT64_MAX : b;
+    }
+    return total;
+}

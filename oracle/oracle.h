@@ -64,6 +64,11 @@ int orc_last_candidates(uint32_t* tau, uint32_t* rest_end, uint32_t* cut, uint32
 /* Total candidates of the last call (to size the arrays above). */
 uint64_t orc_last_total_candidates(void);
 
+/* Not a restatement: checks the host libm that the GPU build's radii rely on. Number of f32 x in
+ * [-1, 1) whose successor y has acosf(y) > acosf(x) (0: acosf is non-increasing there);
+ * *first_bad_bits = the first such x's bit pattern, or UINT64_MAX. */
+uint64_t orc_acosf_violations(uint32_t nthreads, uint64_t* first_bad_bits);
+
 #ifdef __cplusplus
 }
 #endif

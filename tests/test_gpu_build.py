@@ -167,12 +167,8 @@ def test_gpu_build_matches_cpu_build(mix50k):
         ix.add_batch(list(range(len(base))), base)
         ix.compact()
         built.append(ix)
-    a, b = built[0]._arena_arrays(), built[1]._arena_arrays()
-    for key in a:
-        if isinstance(a[key], np.ndarray):
-            assert a[key].tobytes() == b[key].tobytes(), key
-        else:
-            assert a[key] == b[key], key
+    assert built[1]._store_mirrors() and not built[0]._store_mirrors()
+    _same_arena(*built)
     assert built[0].stats()["tree_depth"] == built[1].stats()["tree_depth"] >= 1
     q = np.ascontiguousarray(queries[:200])
     assert built[0].search_batch(q, 10, 16, 1.0, 8.0, True) == built[1].search_batch(q, 10, 16, 1.0, 8.0, True)
@@ -192,12 +188,25 @@ def _configure(ix, case):
         ix.set_i8_rerank(True)
 
 
+def _same_arena(a, b):
+    """Two indexes' arena arrays (every array the upload reads, radii and FastScan blocks included)
+    byte for byte."""
+    x, y = a._arena_arrays(), b._arena_arrays()
+    assert x.keys() == y.keys()
+    for key in x:
+        if isinstance(x[key], np.ndarray):
+            assert x[key].tobytes() == y[key].tobytes(), key
+        else:
+            assert x[key] == y[key], key
+
+
 def _pair(x, n_cells, case, tree_min=2048, churn=False):
-    """Two identical indexes (CPU-trained centroids); one places with the GPU. Returns the saved
-    files' bytes of both after add_batch (+ churn) + compact."""
+    """Two identical indexes (CPU-trained centroids); one builds with the GPU (placement, sums,
+    radii and compaction through its row store). Checks their arenas byte for byte and returns
+    the saved files' bytes of both after add_batch (+ churn) + compact."""
     import os
     import tempfile
-    out = []
+    out, built = [], []
     for gpu in (False, True):
         ix = M.preset(x.shape[1], len(x))
         _configure(ix, case)
@@ -211,10 +220,13 @@ def _pair(x, n_cells, case, tree_min=2048, churn=False):
                 assert ix.remove(v)
             ix.add_batch(list(range(n0, len(x))), np.ascontiguousarray(x[n0:]))  # reuses free slots
         ix.compact()
+        assert ix._store_mirrors() == gpu
+        built.append(ix)
         with tempfile.TemporaryDirectory() as td:
             p = os.path.join(td, "ix.maivs")
             ix.save(p)
             out.append(open(p, "rb").read())
+    _same_arena(*built)
     return out
 
 
@@ -242,3 +254,54 @@ def test_gpu_placement_odd_dim_and_churn():
     x = small_clustered(6000, 37, 40, seed=13)
     a, b = _pair(x, 46, "quality", churn=True)
     assert a == b
+
+
+# ---------------------------------------------------------------- the row store (sums, radii, compaction)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("profile", ["quality", "memory"])
+def test_gpu_build_500k_matches_cpu_build(profile):
+    """The 500k mixture, both presets: the GPU build (k-means, placement, primary sums, radii, row
+    moves and FastScan packing on the device) gives the CPU build's arena byte for byte, and its
+    searches (uploaded from the row store) return the same ids and score bits."""
+    from maivs_amd import mixture
+    base, queries = mixture.workload("mix500k")
+    built = [M.build_preset(base, profile, gpu_build=g) for g in (False, True)]
+    assert built[1]._store_mirrors() and not built[0]._store_mirrors()
+    _same_arena(*built)
+    q = np.ascontiguousarray(queries[:300])
+    assert built[0].search_batch(q, 10, 24, 1.0, 8.0, True) == built[1].search_batch(q, 10, 24, 1.0, 8.0, True)
+
+
+@pytest.mark.gpu
+def test_store_follows_removes_and_reuse_then_stops_at_a_cpu_write(mix50k):
+    """The row store mirrors the index through GPU add_batch, remove (slots freed) and a second
+    GPU add_batch reusing them; a CPU add_batch ends the mirror (the host steps run again), and
+    every stage stays identical to an all-CPU build."""
+    base, queries, _ = mix50k
+    x = np.ascontiguousarray(base[:30000])
+    built = []
+    for gpu in (False, True):
+        ix = M.preset(384, len(x))
+        ix.set_tree_route(True, 256, 16)
+        ix.train_centroids(x[:20000], 156)
+        ix.set_gpu_build(gpu)
+        ix.add_batch(list(range(20000)), np.ascontiguousarray(x[:20000]))
+        for v in range(0, 20000, 5):
+            assert ix.remove(v)
+        ix.add_batch(list(range(20000, 25000)), np.ascontiguousarray(x[20000:25000]))
+        assert ix._store_mirrors() == gpu
+        ix.compact()
+        assert ix._store_mirrors() == gpu
+        built.append(ix)
+    _same_arena(*built)
+    q = np.ascontiguousarray(queries[:200])
+    assert built[0].search_batch(q, 10, 16, 1.0, 8.0, True) == built[1].search_batch(q, 10, 16, 1.0, 8.0, True)
+    for ix in built:
+        ix.set_gpu_build(False)
+        ix.add_batch(list(range(25000, 30000)), np.ascontiguousarray(x[25000:]))
+        assert not ix._store_mirrors()
+        ix.compact()
+    _same_arena(*built)
+    assert built[0].search_batch(q, 10, 16, 1.0, 8.0, True) == built[1].search_batch(q, 10, 16, 1.0, 8.0, True)

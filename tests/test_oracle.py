@@ -509,3 +509,11 @@ def test_adaptive_cut_matches_double_precision(quality50k, mix50k):
             assert rest_end[i] == rest, i
             checked += 1
     assert checked > 100
+
+
+def test_host_acosf_is_non_increasing_on_every_f32_in_unit_interval():
+    """The GPU build's radii select the p99-th largest member dot on the device and take acos of it
+    on the host; that equals the reference's p99-th smallest angle exactly when the host's acosf is
+    non-increasing on [-1, 1]. Checked for every f32 there (2.1e9 inputs)."""
+    n, first = oracle.acosf_violations(8)
+    assert n == 0, hex(first)
