@@ -246,8 +246,7 @@ void FlatCellIndex::set_tags(const std::vector<uint64_t>& ids, const std::vector
     if (ids.size() != tags.size()) throw ValueError("ids/tags length mismatch");
     if (tags_.size() < ext_ids_.size()) tags_.resize(ext_ids_.size(), 0);
     for (size_t i = 0; i < ids.size(); ++i) {
-        auto it = id_to_slot_.find(ids[i]);
-        if (it != id_to_slot_.end()) tags_[it->second] = tags[i];
+        if (const uint32_t* slot = id_to_slot_.find(ids[i])) tags_[*slot] = tags[i];
     }
     ++generation_;  // the uploaded arena carries the tags
 }
@@ -713,18 +712,38 @@ void FlatCellIndex::add_batch(const std::vector<uint64_t>& ids, const float* dat
     if (cells_.empty()) throw ValueError("call set_centroids() before add_batch()");
     if (ids.size() != n) throw ValueError("shape mismatch");
     touch();
+    // max |x| and the per-dimension ranges are order-free, so they are taken over chunks of rows
+    // on several threads and then combined
+    const size_t rows_per = 4096, nch = (n + rows_per - 1) / rows_per;
     if (quant_scale_ == 0.0f) {
+        std::vector<float> part(nch, 0.0f);
+        parallel_for(nch, [&](size_t ch) {
+            float m = 0.0f;
+            for (size_t i = ch * rows_per * dim_, e = std::min(n, (ch + 1) * rows_per) * dim_; i < e; ++i)
+                m = std::max(m, std::fabs(data[i]));
+            part[ch] = m;
+        });
         float max_abs = 0.0f;
-        for (size_t i = 0; i < n * dim_; ++i) max_abs = std::max(max_abs, std::fabs(data[i]));
+        for (float m : part) max_abs = std::max(max_abs, m);
         quant_scale_ = max_abs > 0.0f ? 127.0f / max_abs : 1.0f;
     }
     if (per_dim_sq_ && sq_min_.empty() && n > 0) {
+        std::vector<float> plo(nch * dim_, INFINITY), phi(nch * dim_, -INFINITY);
+        parallel_for(nch, [&](size_t ch) {
+            float* lo = &plo[ch * dim_];
+            float* hi = &phi[ch * dim_];
+            for (size_t i = ch * rows_per, e = std::min(n, (ch + 1) * rows_per); i < e; ++i)
+                for (size_t j = 0; j < dim_; ++j) {
+                    float x = data[i * dim_ + j];
+                    if (x < lo[j]) lo[j] = x;
+                    if (x > hi[j]) hi[j] = x;
+                }
+        });
         std::vector<float> lo(dim_, INFINITY), hi(dim_, -INFINITY);
-        for (size_t i = 0; i < n; ++i)
+        for (size_t ch = 0; ch < nch; ++ch)
             for (size_t j = 0; j < dim_; ++j) {
-                float x = data[i * dim_ + j];
-                if (x < lo[j]) lo[j] = x;
-                if (x > hi[j]) hi[j] = x;
+                if (plo[ch * dim_ + j] < lo[j]) lo[j] = plo[ch * dim_ + j];
+                if (phi[ch * dim_ + j] > hi[j]) hi[j] = phi[ch * dim_ + j];
             }
         sq_step_.resize(dim_);
         for (size_t j = 0; j < dim_; ++j) sq_step_[j] = std::max(hi[j] - lo[j], 1e-9f) / 255.0f;
@@ -802,7 +821,7 @@ void FlatCellIndex::add_batch(const std::vector<uint64_t>& ids, const float* dat
             if (j == 0 && !on_gpu)
                 for (size_t d = 0; d < dim_; ++d) c.sum[d] += v[d];
         }
-        id_to_slot_[ids[i]] = s;
+        id_to_slot_.set(ids[i], s);
         n_live_ += 1;
     }
     if (n_reuse < n) {
@@ -810,10 +829,12 @@ void FlatCellIndex::add_batch(const std::vector<uint64_t>& ids, const float* dat
         size_t m = n - n_reuse;
         const float* dat = data + n_reuse * dim_;
         size_t base = ext_ids_.size();
-        if (keep_f32_) vecs_f32_.insert(vecs_f32_.end(), dat, dat + m * dim_);
-        if (store_bits) bits_.resize((base + m) * nw, 0);
-        if (store_i8) scan_i8_.resize((base + m) * dim_, 0);
+        // the new rows are written by several threads; every one is written in full
+        if (keep_f32_) vecs_f32_.resize((base + m) * dim_);
+        if (store_bits) bits_.resize((base + m) * nw);
+        if (store_i8) scan_i8_.resize((base + m) * dim_);
         parallel_for(m, [&](size_t i) {
+            if (keep_f32_) std::memcpy(&vecs_f32_[(base + i) * dim_], dat + i * dim_, dim_ * sizeof(float));
             encode_input(n_reuse + i, store_bits ? &bits_[(base + i) * nw] : nullptr,
                          store_i8 ? &scan_i8_[(base + i) * dim_] : nullptr);
         }, 512);
@@ -823,10 +844,11 @@ void FlatCellIndex::add_batch(const std::vector<uint64_t>& ids, const float* dat
             slot_cell_.push_back(a[0]);
             for (size_t j = 0; j < ma; ++j) slot_cells_.push_back(j < a.size() ? a[j] : UINT32_MAX);
         }
+        id_to_slot_.reserve(id_to_slot_.size() + m);
         for (size_t i = 0; i < m; ++i) {
             uint32_t slot = static_cast<uint32_t>(base + i);
             for (uint32_t ci : asg[n_reuse + i]) cells_[ci].members.push_back(slot);
-            id_to_slot_[ids[n_reuse + i]] = slot;
+            id_to_slot_.set(ids[n_reuse + i], slot);
         }
         n_live_ += m;
     }
@@ -854,10 +876,10 @@ void FlatCellIndex::add_batch(const std::vector<uint64_t>& ids, const float* dat
 }
 
 bool FlatCellIndex::remove(uint64_t id) {  // src/index.rs:3223-3276
-    auto it = id_to_slot_.find(id);
-    if (it == id_to_slot_.end()) return false;
-    uint32_t slot = it->second;
-    id_to_slot_.erase(it);
+    const uint32_t* found = id_to_slot_.find(id);
+    if (!found) return false;
+    const uint32_t slot = *found;
+    id_to_slot_.erase(id);
     touch();
     uint32_t primary = slot_cell_[slot];
     size_t v0 = static_cast<size_t>(slot) * dim_;
@@ -910,8 +932,9 @@ void FlatCellIndex::compact_arena() {  // src/index.rs:929-1112
         }
     // live slots no primary cell lists keep their data (slot order, deterministic)
     std::vector<uint32_t> missed;
-    for (auto& kv : id_to_slot_)
-        if (new_of_old[kv.second] == UINT32_MAX) missed.push_back(kv.second);
+    id_to_slot_.for_each([&](uint64_t, uint32_t s) {
+        if (new_of_old[s] == UINT32_MAX) missed.push_back(s);
+    });
     std::sort(missed.begin(), missed.end());
     for (uint32_t s : missed) {
         new_of_old[s] = static_cast<uint32_t>(old_of_new.size());
@@ -921,19 +944,19 @@ void FlatCellIndex::compact_arena() {  // src/index.rs:929-1112
     // with a mirroring row store the rows move on the GPU (below, after the member lists)
     const bool on_gpu = gpu_build_ && store_ok_ && gpu_;
     if (keep_f32_ && !vecs_f32_.empty() && !on_gpu) {
-        std::vector<float> v(n_new * d);
+        RowVec<float> v(n_new * d);
         for (size_t ns = 0; ns < n_new; ++ns)
             std::memcpy(&v[ns * d], &vecs_f32_[static_cast<size_t>(old_of_new[ns]) * d], d * sizeof(float));
         vecs_f32_.swap(v);
     }
     if (!scan_i8_.empty() && !on_gpu) {
-        std::vector<int8_t> v(n_new * d);
+        RowVec<int8_t> v(n_new * d);
         for (size_t ns = 0; ns < n_new; ++ns)
             std::memcpy(&v[ns * d], &scan_i8_[static_cast<size_t>(old_of_new[ns]) * d], d);
         scan_i8_.swap(v);
     }
     if (!bits_.empty() && nw > 0 && !on_gpu) {
-        std::vector<uint64_t> v(n_new * nw);
+        RowVec<uint64_t> v(n_new * nw);
         for (size_t ns = 0; ns < n_new; ++ns)
             std::memcpy(&v[ns * nw], &bits_[static_cast<size_t>(old_of_new[ns]) * nw], nw * 8);
         bits_.swap(v);
@@ -963,7 +986,8 @@ void FlatCellIndex::compact_arena() {  // src/index.rs:929-1112
         c.members.swap(m2);
     }
     id_to_slot_.clear();
-    for (size_t ns = 0; ns < ext_ids_.size(); ++ns) id_to_slot_[ext_ids_[ns]] = static_cast<uint32_t>(ns);
+    id_to_slot_.reserve(ext_ids_.size());
+    for (size_t ns = 0; ns < ext_ids_.size(); ++ns) id_to_slot_.set(ext_ids_[ns], static_cast<uint32_t>(ns));
     free_slots_.clear();
 
     prim_len_.clear();
@@ -1000,19 +1024,20 @@ void FlatCellIndex::compact_arena() {  // src/index.rs:929-1112
         std::copy(cells_[ci].members.begin(), cells_[ci].members.end(), members_flat_.begin() + mem_off_[ci]);
     if (on_gpu) {
         // the store's rows move to their new slots, the FastScan blocks are packed from its codes,
-        // and the compacted rows come back for the index's own arrays
-        std::vector<float> v32(keep_f32_ && !vecs_f32_.empty() ? n_new * d : 0);
-        std::vector<int8_t> v8(!scan_i8_.empty() ? n_new * d : 0);
-        std::vector<uint64_t> vb(!bits_.empty() && nw > 0 ? n_new * nw : 0);
+        // and the compacted rows come back over the index's own arrays (each holds old_n >= n_new
+        // rows, none of which is read again), which then shrink to n_new rows
+        const bool f32 = keep_f32_ && !vecs_f32_.empty(), i8 = !scan_i8_.empty(), b = !bits_.empty() && nw > 0;
+        if ((f32 && vecs_f32_.size() < n_new * d) || (i8 && scan_i8_.size() < n_new * d) || (b && bits_.size() < n_new * nw))
+            throw std::runtime_error("compact: a row array is shorter than the slot count");
         const uint32_t M = static_cast<uint32_t>(cells_.size());
         gpu_->check(gpu_api().store_compact(gpu_->ctx_, old_of_new.data(), static_cast<uint32_t>(n_new), M, mem_off_.data(),
                                             members_flat_.data(), pack ? fs_off_.data() : nullptr,
-                                            pack ? fs_codes_.data() : nullptr, v32.empty() ? nullptr : v32.data(),
-                                            v8.empty() ? nullptr : v8.data(), vb.empty() ? nullptr : vb.data()),
+                                            pack ? fs_codes_.data() : nullptr, f32 ? vecs_f32_.data() : nullptr,
+                                            i8 ? scan_i8_.data() : nullptr, b ? bits_.data() : nullptr),
                     "maivs_gpu_store_compact");
-        if (!v32.empty()) vecs_f32_.swap(v32);
-        if (!v8.empty()) scan_i8_.swap(v8);
-        if (!vb.empty()) bits_.swap(vb);
+        if (f32) vecs_f32_.resize(n_new * d);
+        if (i8) scan_i8_.resize(n_new * d);
+        if (b) bits_.resize(n_new * nw);
         refresh_store_token();
     } else if (pack) {
         parallel_for(cells_.size(), [&](size_t ci) {

@@ -34,6 +34,130 @@ struct IoError : std::runtime_error {
 
 enum class ScanMode { F32, I8, Binary };
 
+// Allocator whose value-initialisation leaves elements default-initialised (for these row arrays:
+// unset), so a row array can grow by millions of rows and then be filled by several threads,
+// instead of first being zeroed by one. resize(n, value) and assign still write their value.
+template <class T>
+struct NoInitAlloc : std::allocator<T> {
+    template <class U>
+    struct rebind {
+        using other = NoInitAlloc<U>;
+    };
+    NoInitAlloc() = default;
+    template <class U>
+    NoInitAlloc(const NoInitAlloc<U>&) noexcept {}
+    template <class U>
+    void construct(U* p) noexcept {
+        ::new (static_cast<void*>(p)) U;
+    }
+    template <class U, class... Args>
+    void construct(U* p, Args&&... args) {
+        ::new (static_cast<void*>(p)) U(std::forward<Args>(args)...);
+    }
+};
+template <class T>
+using RowVec = std::vector<T, NoInitAlloc<T>>;
+
+// External id -> slot, the reference's id_to_slot HashMap (src/index.rs:431-566): open addressing
+// with linear probing over a power-of-two table kept at most half full, erased entries marked so
+// probes pass over them. One flat allocation instead of a node per id, so rebuilding it for
+// millions of ids (add_batch, compact) costs a fraction of a node-based map.
+class IdMap {
+public:
+    size_t size() const { return n_; }
+    void clear() {
+        keys_.clear();
+        vals_.clear();
+        state_.clear();
+        n_ = used_ = 0;
+    }
+    void reserve(size_t n) {
+        if (2 * n >= state_.size()) rehash(n);
+    }
+    // the slot of id k, or nullptr
+    const uint32_t* find(uint64_t k) const {
+        if (state_.empty()) return nullptr;
+        for (size_t i = hash(k) & mask(), step = 0; step <= mask(); i = (i + 1) & mask(), ++step) {
+            if (state_[i] == kEmpty) return nullptr;
+            if (state_[i] == kFull && keys_[i] == k) return &vals_[i];
+        }
+        return nullptr;
+    }
+    // inserts k or overwrites its slot
+    void set(uint64_t k, uint32_t v) {
+        if (2 * (used_ + 1) > state_.size()) rehash(n_ + 1);
+        size_t tomb = SIZE_MAX;
+        for (size_t i = hash(k) & mask();; i = (i + 1) & mask()) {
+            if (state_[i] == kFull && keys_[i] == k) {
+                vals_[i] = v;
+                return;
+            }
+            if (state_[i] == kTomb && tomb == SIZE_MAX) tomb = i;
+            if (state_[i] == kEmpty) {
+                if (tomb != SIZE_MAX) {
+                    i = tomb;
+                } else {
+                    ++used_;
+                }
+                keys_[i] = k;
+                vals_[i] = v;
+                state_[i] = kFull;
+                ++n_;
+                return;
+            }
+        }
+    }
+    bool erase(uint64_t k) {
+        const uint32_t* v = find(k);
+        if (!v) return false;
+        const size_t i = static_cast<size_t>(v - vals_.data());
+        state_[i] = kTomb;
+        --n_;
+        return true;
+    }
+    template <class F>
+    void for_each(F f) const {
+        for (size_t i = 0; i < state_.size(); ++i)
+            if (state_[i] == kFull) f(keys_[i], vals_[i]);
+    }
+
+private:
+    static constexpr uint8_t kEmpty = 0, kFull = 1, kTomb = 2;
+    static size_t hash(uint64_t k) {  // splitmix64's finaliser
+        k ^= k >> 30;
+        k *= 0xBF58476D1CE4E5B9ull;
+        k ^= k >> 27;
+        k *= 0x94D049BB133111EBull;
+        k ^= k >> 31;
+        return static_cast<size_t>(k);
+    }
+    size_t mask() const { return state_.size() - 1; }
+    void rehash(size_t n) {
+        size_t cap = 16;
+        while (cap < 2 * n + 2) cap <<= 1;
+        std::vector<uint64_t> keys(cap);
+        std::vector<uint32_t> vals(cap);
+        std::vector<uint8_t> state(cap, kEmpty);
+        const size_t m = cap - 1;
+        for (size_t j = 0; j < state_.size(); ++j) {
+            if (state_[j] != kFull) continue;
+            size_t i = hash(keys_[j]) & m;
+            while (state[i] == kFull) i = (i + 1) & m;
+            keys[i] = keys_[j];
+            vals[i] = vals_[j];
+            state[i] = kFull;
+        }
+        keys_.swap(keys);
+        vals_.swap(vals);
+        state_.swap(state);
+        used_ = n_;
+    }
+    std::vector<uint64_t> keys_;
+    std::vector<uint32_t> vals_;
+    std::vector<uint8_t> state_;
+    size_t n_ = 0, used_ = 0;  // live entries; live + erased (slots no longer empty)
+};
+
 struct Cell {
     std::vector<uint32_t> members;
     std::vector<float> sum, centroid;
@@ -121,7 +245,7 @@ public:
     const maivs_arena_desc* arena_desc();
     maivs_search_params search_params(size_t k, size_t nprobe, float tc, float beta) const;
     const std::vector<uint64_t>& ext_ids() const { return ext_ids_; }
-    const std::vector<uint64_t>& bits() const { return bits_; }
+    const RowVec<uint64_t>& bits() const { return bits_; }
     const std::vector<float>& rot_signs() const { return rot_signs_; }
     uint64_t generation() const { return generation_; }
     // The centroid tree's flat arrays (false when there is no tree).
@@ -159,13 +283,13 @@ private:
     uint64_t seed_;
     std::vector<float> rot_signs_;
 
-    std::vector<uint64_t> bits_;
-    std::vector<int8_t> scan_i8_;
-    std::vector<float> vecs_f32_;
+    RowVec<uint64_t> bits_;
+    RowVec<int8_t> scan_i8_;
+    RowVec<float> vecs_f32_;
     std::vector<uint64_t> ext_ids_;
     std::vector<uint32_t> slot_cell_;
     std::vector<uint32_t> free_slots_;
-    std::unordered_map<uint64_t, uint32_t> id_to_slot_;
+    IdMap id_to_slot_;
 
     std::vector<Cell> cells_;
     std::vector<uint64_t> cent_bits_;

@@ -54,8 +54,8 @@ public:
     }
     void u64(uint64_t v) { bytes(&v, 8); }
     void f32(float v) { bytes(&v, 4); }
-    template <class T>
-    void pod(const std::vector<T>& v) {
+    template <class T, class A>
+    void pod(const std::vector<T, A>& v) {
         u64(v.size());
         bytes(v.data(), v.size() * sizeof(T));
     }
@@ -96,12 +96,12 @@ public:
         bytes(&v, 4);
         return v;
     }
-    template <class T>
-    std::vector<T> pod() {
+    template <class T, class V = std::vector<T>>
+    V pod() {
         uint64_t n = u64();
         // a length the rest of the file cannot hold is a truncated or corrupt file
         if (n > left() / sizeof(T)) throw IoError("failed to fill whole buffer");
-        std::vector<T> v(n);
+        V v(n);
         bytes(v.data(), n * sizeof(T));
         return v;
     }
@@ -167,12 +167,12 @@ void FlatCellIndex::load_file(const std::string& path) {  // src/persist.rs:145-
     uint64_t h[16];
     for (uint64_t& v : h) v = r.u64();
     const float quant_scale = r.f32(), spill_margin = r.f32(), at_margin = r.f32(), tree_beam_frac = r.f32();
-    auto bits = r.pod<uint64_t>();
-    auto scan_i8 = r.pod<int8_t>();
+    auto bits = r.pod<uint64_t, RowVec<uint64_t>>();
+    auto scan_i8 = r.pod<int8_t, RowVec<int8_t>>();
     auto rr_f16 = r.pod<uint16_t>();
     auto sq_min = r.pod<float>();
     auto sq_step = r.pod<float>();
-    auto vecs_f32 = r.pod<float>();
+    auto vecs_f32 = r.pod<float, RowVec<float>>();
     auto ext_ids = r.pod<uint64_t>();
     auto slot_cell = r.pod<uint32_t>();
     auto free_slots = r.pod<uint32_t>();
@@ -247,8 +247,9 @@ void FlatCellIndex::load_file(const std::string& path) {  // src/persist.rs:145-
     cells_.swap(cells);
     std::unordered_set<uint32_t> free(free_slots_.begin(), free_slots_.end());
     id_to_slot_.clear();
+    id_to_slot_.reserve(ext_ids_.size());
     for (size_t s = 0; s < ext_ids_.size(); ++s)
-        if (!free.count(static_cast<uint32_t>(s))) id_to_slot_[ext_ids_[s]] = static_cast<uint32_t>(s);
+        if (!free.count(static_cast<uint32_t>(s))) id_to_slot_.set(ext_ids_[s], static_cast<uint32_t>(s));
     cent_bits_.clear();
     cent_sq8_.clear();
     csq_min_.clear();

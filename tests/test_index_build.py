@@ -275,3 +275,34 @@ def test_overlapping_calls_follow_the_borrow_rules():
     assert seen_mut == "Already borrowed"
     assert len(ix) == len(x)
     ix.set_adaptive(True, 0.02)  # free again
+
+
+def test_id_map_through_churn():
+    """The id -> slot map under repeated deletes and re-inserts of the same ids (erased entries
+    reused, the table rebuilt by compact): every present id removes once, absent ids never, and
+    the slots' ids stay a permutation of the live ids."""
+    rs = np.random.RandomState(5)
+    x = small_clustered(2000, 64, 10, seed=9)
+    ix = M.FlatCellIndex(64, "binary", 8)
+    ix.train_centroids(x, 16)
+    ids = list(range(10**12, 10**12 + 2000))
+    ix.add_batch(ids, x)
+    live = set(ids)
+    for rnd in range(6):
+        gone = rs.choice(sorted(live), 400, replace=False).tolist()
+        for i in gone:
+            assert ix.remove(i)
+            assert not ix.remove(i)
+            live.discard(i)
+        back = gone[: 200 + 20 * rnd]
+        ix.add_batch(back, np.ascontiguousarray(x[: len(back)]))
+        live.update(back)
+        assert len(ix) == len(live)
+        if rnd % 2:
+            ix.compact()
+            ext = ix._ext_ids()
+            assert sorted(ext.tolist()) == sorted(live)
+    assert not ix.remove(7)
+    for i in sorted(live):
+        assert ix.remove(i)
+    assert len(ix) == 0
