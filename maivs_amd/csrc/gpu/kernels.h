@@ -286,13 +286,31 @@ __device__ __forceinline__ bool canonical(const DevArena& A, uint64_t e, uint32_
     return true;
 }
 
+// f(get(i)) for i in [0, n), each thread taking i = tid, tid + nt, ...: eight values are loaded
+// before any is used, so a long list in global memory has eight loads per thread in flight.
+template <class Get, class F>
+__device__ __forceinline__ void for_each_value8(uint32_t n, Get get, F f) {
+    constexpr uint32_t U = 8;
+    for (uint32_t base = threadIdx.x; base < n; base += U * blockDim.x) {
+        uint32_t v[U];
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u) {
+            const uint32_t i = base + u * blockDim.x;
+            v[u] = i < n ? get(i) : 0u;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u)
+            if (base + u * blockDim.x < n) f(v[u]);
+    }
+}
+
 // Exact `want`-th smallest (1-based) of n values d < 65536 from get(i). Two 256-bin LDS histogram
 // passes; every thread returns the value. Block-uniform call.
 template <class Get>
 __device__ uint32_t select_kth(uint32_t n, uint32_t want, Get get, uint32_t* hist, uint32_t* scratch) {
     for (uint32_t i = threadIdx.x; i < kHistBins; i += blockDim.x) hist[i] = 0;
     __syncthreads();
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) atomicAdd(&hist[get(i) >> 8], 1u);
+    for_each_value8(n, get, [&](uint32_t d) { atomicAdd(&hist[d >> 8], 1u); });
     __syncthreads();
     uint32_t hb, below;
     {
@@ -305,10 +323,9 @@ __device__ uint32_t select_kth(uint32_t n, uint32_t want, Get get, uint32_t* his
     }
     for (uint32_t i = threadIdx.x; i < kHistBins; i += blockDim.x) hist[i] = 0;
     __syncthreads();
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
-        uint32_t d = get(i);
+    for_each_value8(n, get, [&](uint32_t d) {
         if ((d >> 8) == hb) atomicAdd(&hist[d & 0xFFu], 1u);
-    }
+    });
     __syncthreads();
     const uint32_t need = want - below;
     uint32_t v = threadIdx.x < kHistBins ? hist[threadIdx.x] : 0u;
@@ -1306,6 +1323,15 @@ __device__ __forceinline__ void seed_phase(const DevArena& A, const Work& Wk, co
         }
     }
     __syncthreads();  // every wave's kept count is in misc[kKeep]
+    // ---- the scans' running cut starts at tau, its histogram with the scored seed members
+    if (K.run_thr == 1) {
+        uint32_t* dh = Wk.dhist + static_cast<uint64_t>(qi) * kThrBins;
+        for (uint32_t i = tid; i < kThrBins; i += nt) dh[i] = coarse[i];
+        if (tid == 0) {
+            Wk.thr[qi] = tau;
+            Wk.thr_at[qi] = 0;
+        }
+    }
     // ---- adaptive cut: suffix maxima of the route's bounds, first i >= ns below thr - margin
     uint32_t rest_end = nch;
     if (K.adaptive && cnt >= K.target && ns < nch) {
@@ -1610,6 +1636,43 @@ __global__ void invert_fill_kernel(Work Wk, KParams K) {
 
 // ---------------------------------------------------------------- the cell-major scan
 
+
+// Lowers query q's running cut to the upper edge of the d >> 8 bin holding the target-th smallest
+// counted entry (one thread). Counts it reads may lag atomics still in flight; fewer counts give
+// a higher edge, never one below the final cut.
+__device__ __forceinline__ void thr_lower(const Work& Wk, const KParams& K, uint32_t q) {
+    const uint4* h = reinterpret_cast<const uint4*>(Wk.dhist + static_cast<uint64_t>(q) * kThrBins);
+    uint32_t cum = 0;
+#pragma unroll 1
+    for (uint32_t i = 0; i < kThrBins / 4; ++i) {
+        const uint4 v = h[i];
+        const uint32_t s4 = v.x + v.y + v.z + v.w;
+        if (cum + s4 >= K.target) {
+            const uint32_t b = 4 * i + (cum + v.x >= K.target ? 0u : cum + v.x + v.y >= K.target ? 1u
+                                                                  : cum + v.x + v.y + v.z >= K.target ? 2u : 3u);
+            atomicMin(&Wk.thr[q], b * 256 + 255);
+            return;
+        }
+        cum += s4;
+    }
+}
+
+// A query's cut for a work item of the scans (K.run_thr: tau, or the running cut), read when the
+// item starts. With K.run_thr 1, the cut is first lowered from the histogram when the query has
+// appended kThrEvery candidates since its last update (the item start, not the append, does it:
+// there the scans hold no tables or codes in registers).
+__device__ __forceinline__ uint32_t scan_cut(const Work& Wk, const KParams& K, uint32_t q, bool update = true) {
+    if (!K.run_thr) return Wk.tau[q];
+    if (K.run_thr == 1 && update) {
+        const uint32_t c = Wk.cand_cnt[q];
+        if (c >= Wk.thr_at[q] + kThrEvery) {
+            Wk.thr_at[q] = c;
+            thr_lower(Wk, K, q);
+        }
+    }
+    return Wk.thr[q];
+}
+
 // One workgroup per cell (the CPU loop this replaces is src/index.rs:2231-2275). Lanes own
 // members; each lane's code is loaded once per pass while groups of kG probing queries stream
 // through the LDS table; survivors d <= tau of canonical members are appended per query.
@@ -1732,9 +1795,12 @@ __device__ __forceinline__ void scan_item(const DevArena& A, const Work& Wk, con
             for (uint32_t g = 0; g < kG; ++g) {
                 const uint32_t base = __shfl(wb, static_cast<int>(g), kWave);
                 const uint32_t pos = base + lanes_below(bm[g]);
+                const uint32_t qq = s_q[h * kG + g];
                 if (pass[g] && pos < K.cand_cap)
-                    Wk.cand[static_cast<uint64_t>(s_q[h * kG + g]) * K.cand_cap + pos] = make_uint2(dv[g], m.slot);
+                    Wk.cand[static_cast<uint64_t>(qq) * K.cand_cap + pos] = make_uint2(dv[g], m.slot);
+                if (pass[g] && K.run_thr == 1) atomicAdd(&Wk.dhist[static_cast<uint64_t>(qq) * kThrBins + (dv[g] >> 8)], 1u);
             }
+
         }
     }
     __syncthreads();  // the table and s_q / s_t are reused by the next item
@@ -1768,7 +1834,7 @@ cell_scan_kernel(DevArena A, Work Wk, KParams K) {
                 if (tid < kItemQ) {
                     const bool ok = tid < nqi;
                     s_q[tid] = ok ? qv : kNone;
-                    s_t[tid] = ok ? Wk.tau[qv] : 0u;
+                    s_t[tid] = ok ? scan_cut(Wk, K, qv) : 0u;
                 }
                 __syncthreads();
                 scan_item<NW>(A, Wk, K, c, e0, e1 - e0, nqi, table, s_q, s_t);
@@ -1814,7 +1880,7 @@ cell_scan_kernel(DevArena A, Work Wk, KParams K) {
                 if (tid < kItemQ) {
                     const bool ok = tid < nqi;
                     s_q[tid] = ok ? qv : kNone;
-                    s_t[tid] = ok ? Wk.tau[qv] : 0u;
+                    s_t[tid] = ok ? scan_cut(Wk, K, qv) : 0u;
                 }
                 __syncthreads();
                 scan_item<NW>(A, Wk, K, c, e0, e1 - e0, nqi, table, s_q, s_t);
@@ -1833,7 +1899,7 @@ cell_scan_kernel(DevArena A, Work Wk, KParams K) {
                 const bool ok = tid < nqi;
                 const uint32_t qv = ok ? Wk.qof[q0 + g0 + tid] : kNone;
                 s_q[tid] = qv;
-                s_t[tid] = ok ? Wk.tau[qv] : 0u;
+                s_t[tid] = ok ? scan_cut(Wk, K, qv) : 0u;
             }
             __syncthreads();
             scan_item<NW>(A, Wk, K, c, e0, len, nqi, table, s_q, s_t);
@@ -1928,7 +1994,8 @@ cell_mma_kernel(DevArena A, Work Wk, KParams K) {
         __syncthreads();
         if (tid < kBucketQ) {
             const uint32_t m = s_cnt[tid];
-            s_base[tid] = m ? atomicAdd(&Wk.cand_cnt[s_q[tid]], m) : 0u;
+            const uint32_t b = m ? atomicAdd(&Wk.cand_cnt[s_q[tid]], m) : 0u;
+            s_base[tid] = b;
             s_cnt[tid] = 0;
         }
         __syncthreads();
@@ -1936,7 +2003,9 @@ cell_mma_kernel(DevArena A, Work Wk, KParams K) {
         for (uint32_t k = 0; k < PER; ++k) {
             if (off[k] == kNone) continue;
             const uint32_t jj = dq[k] >> 16, pos = s_base[jj] + off[k];
-            if (pos < K.cand_cap) Wk.cand[static_cast<uint64_t>(s_q[jj]) * K.cand_cap + pos] = make_uint2(dq[k] & 0xFFFFu, slot[k]);
+            const uint32_t dd = dq[k] & 0xFFFFu;
+            if (pos < K.cand_cap) Wk.cand[static_cast<uint64_t>(s_q[jj]) * K.cand_cap + pos] = make_uint2(dd, slot[k]);
+            if (K.run_thr == 1) atomicAdd(&Wk.dhist[static_cast<uint64_t>(s_q[jj]) * kThrBins + (dd >> 8)], 1u);
         }
         __syncthreads();
     };
@@ -1977,7 +2046,7 @@ cell_mma_kernel(DevArena A, Work Wk, KParams K) {
                                static_cast<int>(v.z ^ 0x80808080u), static_cast<int>(v.w ^ 0x80808080u)};
             }
         }
-        const uint32_t tj = qj != kNone ? Wk.tau[qj] : 0u;
+        const uint32_t tj = qj != kNone ? scan_cut(Wk, K, qj, w == 0) : 0u;  // wave 0 lowers the cuts
         if (tid < kBucketQ) s_q[tid] = qj;
         // this wave's code dwords of member t*32 + j (zero past the cell's end)
         auto load_codes = [&](uint32_t t, uint32_t (&dw)[CDW]) {
@@ -2163,23 +2232,27 @@ __device__ __forceinline__ uint32_t finish_phase(const DevArena& A, const Work& 
     uint2* fin = Wk.fin + static_cast<uint64_t>(qi) * K.fin_cap;
     auto tail = [&](uint64_t* kk) -> uint32_t {
         // compact the survivors into fin[] (global, read back by the debug entry point); their
-        // slots go into the key list
-        for (uint32_t base = 0; base < total; base += nt) {
-            const uint32_t i = base + tid;
-            uint2 e = make_uint2(0, 0);
-            bool pass = false;
-            if (i < total) {
-                e = entry(i);
-                pass = e.x <= cutv;
+        // slots go into the key list. Four rounds' entries are loaded before the first is used.
+        constexpr uint32_t U = 4;
+        for (uint32_t base = 0; base < total; base += U * nt) {
+            uint2 e[U];
+#pragma unroll
+            for (uint32_t u = 0; u < U; ++u) {
+                const uint32_t i = base + u * nt + tid;
+                e[u] = i < total ? entry(i) : make_uint2(0, 0);
             }
-            const uint64_t m = __ballot(pass);
-            uint32_t wb = 0;
-            if (lane == 0 && m) wb = atomicAdd(&s_n, static_cast<uint32_t>(__popcll(m)));
-            wb = __shfl(wb, 0, kWave);
-            if (pass) {
-                const uint32_t pos = wb + lanes_below(m);
-                fin[pos] = e;
-                kk[pos] = e.y;
+#pragma unroll
+            for (uint32_t u = 0; u < U; ++u) {
+                const bool pass = base + u * nt + tid < total && e[u].x <= cutv;
+                const uint64_t m = __ballot(pass);
+                uint32_t wb = 0;
+                if (lane == 0 && m) wb = atomicAdd(&s_n, static_cast<uint32_t>(__popcll(m)));
+                wb = __shfl(wb, 0, kWave);
+                if (pass) {
+                    const uint32_t pos = wb + lanes_below(m);
+                    fin[pos] = e[u];
+                    kk[pos] = e[u].y;
+                }
             }
         }
         __syncthreads();

@@ -192,6 +192,9 @@ void carve_work(const DevArena& A, uint32_t nq, uint32_t nprobe, uint32_t k, uin
     c.take(&W.active_cs, static_cast<uint64_t>(A.M) + nql * nprobe / kBucketQ + 1);
     c.take(&W.flag_route, nql);
     c.take(&W.flag_prune, nql);
+    c.take(&W.thr, nql);
+    c.take(&W.dhist, nql * kThrBins);
+    c.take(&W.thr_at, nql);
     c.take(&W.ctl, 1);
     c.take(&W.cand_n, nql);
     c.take(&W.done, 1);
@@ -381,6 +384,8 @@ KParams make_params(maivs_gpu_ctx* ctx, uint32_t nq, const maivs_search_params* 
     K.fin_cap = ctx->cap_fin;
     K.key_cap = ctx->cap_key;
     K.xcd_order = ctx->xcd_order ? 1u : 0u;
+    // the running cut only where a cell-major scan runs after the seed stage
+    K.run_thr = p->nprobe > kSeedCells + K.front_rest ? 1u : 0u;
     K.tc = p->target_confidence;
     K.beta = p->beta;
     K.at_margin = p->at_margin;
@@ -864,6 +869,7 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
     // (2) adaptive cuts near their threshold; a full query bucket re-runs the scan from the
     // counting-sort inversion
     bool rerun_scan = ctl.bucket_overflow != 0;
+    bool cells_changed = false;  // a re-run scans other cells than the running cuts were counted on
     if (ctl.nflag_prune) {
         std::vector<uint32_t> fl(ctl.nflag_prune);
         HIP_TRY(ctx, hipMemcpy(fl.data(), W.flag_prune, fl.size() * 4, hipMemcpyDeviceToHost));
@@ -885,6 +891,7 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
                 S.host_fixes++;
                 HIP_TRY(ctx, hipMemcpy(W.rest_end + qi, &exact, 4, hipMemcpyHostToDevice));
                 rerun_scan = true;
+                cells_changed = true;
             }
         }
     }
@@ -899,11 +906,23 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
         rerun_scan = true;
     }
     if (rerun_scan) {
-        S.reruns++;
-        if ((rc = launch_scan(ctx, csr(K), true))) return rc;
-        if ((rc = launch_finish(ctx, csr(K), d_q, d_slots, d_scores))) return rc;
-        if ((rc = read_ctl(ctx, &ctl))) return rc;
-        if (ctl.max_cand > ctx->cap_cand) return fail(ctx, MAIVS_ERR_HIP, "candidate count changed between passes");
+        // the same cells: the running cuts as they stand (their entries were counted); other cells:
+        // tau. A re-run under a higher cut may append more than the buffer took: it grows once more.
+        K.run_thr = K.run_thr && !cells_changed ? 2u : 0u;
+        for (int attempt = 0;; ++attempt) {
+            S.reruns++;
+            if ((rc = launch_scan(ctx, csr(K), true))) return rc;
+            if ((rc = launch_finish(ctx, csr(K), d_q, d_slots, d_scores))) return rc;
+            if ((rc = read_ctl(ctx, &ctl))) return rc;
+            if (ctl.max_cand <= ctx->cap_cand) break;
+            if (attempt > 0) return fail(ctx, MAIVS_ERR_HIP, "candidate count changed between passes");
+            const uint32_t need = ctl.max_cand + ctl.max_cand / 4 + 64;
+            ctx->initial_cand_cap = std::max(ctx->initial_cand_cap, need);
+            if ((rc = sc ? recarve_cand(ctx, *sc, need) : ensure_cand(ctx, need))) return rc;
+            K.cand_cap = ctx->cap_cand;
+            K.fin_cap = ctx->cap_fin;
+            K.key_cap = ctx->cap_key;
+        }
     }
     ctx->last_nq = nq;
     ctx->last_K = K;

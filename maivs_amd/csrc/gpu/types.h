@@ -28,6 +28,8 @@ constexpr uint32_t kHistBins = 256;
 constexpr uint32_t kFinishLdsCap = 2048; // final candidates kept and sorted in LDS up to this many
 constexpr uint32_t kNoAlt = 0xFFFFFFFEu; // entry_alt: the slot has no other home
 constexpr uint32_t kNoD = 0xFFFFu;        // seed score buffer: member not scored here (d <= 255 * 256 < kNoD)
+constexpr uint32_t kThrBins = 256;       // a query's running-cut histogram: bins of d >> 8 (d < 65536)
+constexpr uint32_t kThrEvery = 512;      // its cut is recomputed each time this many more candidates are appended
 
 // Chain-major row layout for the 8-lane FMA dots: element 8t + l (t < T) of a row is stored at
 // l*Tp + t, the d - 8T tail elements at 8*Tp + i. Lane l of a group of 8 then reads its whole
@@ -131,6 +133,14 @@ struct Work {
     uint32_t* tlist;       // nq x tcap: the centroid tree's leaf cells for each query
     uint32_t* tcount;      // nq
     uint64_t* pqc;         // nq x pq_cap: scanned candidates (d << 32 | slot)
+    // The cell-major scans' running cut of each query: starts at tau, and drops to the upper edge of
+    // the d >> 8 bin holding the target-th smallest d among the entries counted so far in dhist
+    // (the seed's scored members, then every appended candidate). Those are entries of the query's
+    // scanned cells, so the cut never falls below the final cut G and the candidate set at G is
+    // unchanged; it only stops the scans appending entries G would drop.
+    uint32_t* thr;         // nq
+    uint32_t* dhist;       // nq x kThrBins
+    uint32_t* thr_at;      // nq: the query's candidate count when its running cut was last lowered
     Ctl* ctl;
     Ctl* h_ctl;            // pinned host mirror of ctl, written by pass_epilogue (device address)
 };
@@ -153,6 +163,10 @@ struct KParams {
     uint32_t xcd_order;
     // routing: every live cell is rescored (no tree, no two-stage shortlist)
     uint32_t flat_route;
+    // the scans' cut: 0 tau; 1 the running cut Wk.thr, counted and lowered as candidates are
+    // appended (the seed stage starts it); 2 the running cut as it stands, not updated (a re-run
+    // over the same cells, whose entries were counted already)
+    uint32_t run_thr;
     float tc, beta, at_margin, norm, prune_band, nucleus_band;
 };
 
