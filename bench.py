@@ -31,6 +31,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "batch QPS at R@10 0.95/0.99, 500k×384 f32, 1 MI355X; scan HBM GB/s"
 HBM_PEAK_GBS = 8000.0
+MFMA_I8_PEAK_TOPS = 5000.0  # MI355X dense int8 matrix-core peak, 5.0 POP/s
 NPROBE_GRID = (1, 2, 3, 4, 6, 8, 10, 12, 16, 20, 24, 32, 48, 64, 96, 128)
 RF_GRID = (8, 16, 32)
 TARGETS = (0.95, 0.99, 0.995)
@@ -328,6 +329,19 @@ def main() -> int:
                 "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": traffic["bytes_per_launch"] if traffic else None, "kernel": dom,
                 "kernel_ms": round(ms_dom, 4), "bytes_per_launch": int(bytes_dom), "bytes_are": what}
+    if dom == "cell_mma_kernel" and ms_dom > 0:
+        # the matrix-core scan reads each cell's codes once per 32-query work item, so its
+        # algorithmic bytes exceed what HBM moves; its bound is the int8 matrix cores. A 32-member
+        # block against one query is 32 x 2,048 one-hot multiply-adds (2 ops each).
+        ops = avg["scan_blocks"] * 32 * 2048 * 2
+        tops = ops / (ms_dom * 1e-3) / 1e12
+        roofline = {"bound": "mfma", "achieved": round(tops, 1), "peak": MFMA_I8_PEAK_TOPS, "unit": "TFLOP/s",
+                    "frac": round(tops / MFMA_I8_PEAK_TOPS, 4),
+                    "traffic": traffic["bytes_per_launch"] if traffic else None, "kernel": dom,
+                    "kernel_ms": round(ms_dom, 4), "ops_per_launch": int(ops),
+                    "ops_are": "int8 one-hot multiply-adds of every (query, 32-member block) pair scanned, "
+                               "2 ops each, against the dense int8 peak (5.0 POP/s)",
+                    "bytes_per_launch": int(bytes_dom), "bytes_are": what}
     log(f"stages (avg ms): " + ", ".join(f"{s_}={stages[s_][0]:.4f}" for s_ in stages))
 
     # ---- CPU baseline: the oracle on the host cores, same index, same grid
