@@ -369,14 +369,12 @@ void FlatCellIndex::rebuild_centroid_sq8() {  // src/index.rs:730-775
 
 // The session's row store's current token (the arena description names it, so the upload reads
 // the rows where they are).
+// A store whose slot count differs from the index's no longer mirrors it: the mirror ends and the
+// host steps (exact restatements too) take over, so the index stays usable.
 void FlatCellIndex::refresh_store_token() {
     uint32_t n = 0;
     gpu_->check(gpu_api().store_info(gpu_->ctx_, &store_token_, &n), "maivs_gpu_store_info");
-    if (n != ext_ids_.size()) {
-        store_ok_ = false;
-        throw std::runtime_error("the GPU row store holds " + std::to_string(n) + " slots, the index " +
-                                 std::to_string(ext_ids_.size()));
-    }
+    if (n != ext_ids_.size()) store_ok_ = false;
 }
 
 // recompute_radii on the GPU, from the row store: the device returns each cell's (p99 + 1)-th
