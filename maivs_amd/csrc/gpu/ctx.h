@@ -48,6 +48,7 @@ struct maivs_gpu_ctx {
     uint32_t max_sort_cap_route = 0;  // largest shortlist sort the route kernel's LDS can hold
     uint32_t seed_cap = 0;            // sum of the SEED_CELLS largest cells: bound of one seed set
     size_t lds_prep = 0, lds_seed = 0, lds_finish = 0;
+    uint32_t pq_tree_block_max_q = 1000000;  // the block-wide tree descent up to this many queries
     Ctl* h_ctl = nullptr;  // pinned host copy of the control block (read after each pass)
     hipEvent_t ev[8] = {};
     // last call, for maivs_gpu_last_candidates / maivs_gpu_last_counters

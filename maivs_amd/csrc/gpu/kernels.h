@@ -2423,6 +2423,35 @@ pq_tree_kernel(DevArena A, Work Wk, KParams K, TreeDev T, const uint32_t* __rest
     if (lane == 0) Wk.tcount[qi] = n;
 }
 
+// The same descent by a whole workgroup per query (block_tree_descent), for small batches: the
+// frontier's code loads and the selections spread over kPqTreeBlock threads instead of one wave.
+// LDS: qb[W] u64 | hist[W*64 + 1 (4)] | rbase[cap + 1] | rpre[cap + 2] | knodes[cap] | scratch[32] |
+// hcache[kTreeHCache] u16.
+constexpr uint32_t kPqTreeBlock = 256;
+
+__host__ __device__ inline uint32_t pq_tree_block_lds_words(uint32_t W, uint32_t cap) {
+    return pq_tree_lds_words(W, cap) + 32;
+}
+
+__global__ void __launch_bounds__(kPqTreeBlock)
+pq_tree_block_kernel(DevArena A, Work Wk, KParams K, TreeDev T, const uint32_t* __restrict__ beams, uint32_t cap) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const uint32_t qi = blockIdx.x;
+    if (qi >= K.nq) return;  // uniform over the workgroup
+    uint64_t* qb = reinterpret_cast<uint64_t*>(smem);
+    uint32_t* hist = reinterpret_cast<uint32_t*>(qb + A.W);
+    uint32_t* rbase = hist + ((A.W * 64 + 1 + 3) & ~3u);
+    uint32_t* rpre = rbase + cap + 1;
+    uint32_t* knodes = rpre + cap + 2;
+    uint32_t* scratch = knodes + cap;
+    uint16_t* hcache = reinterpret_cast<uint16_t*>(scratch + 32);
+    for (uint32_t w = threadIdx.x; w < A.W; w += blockDim.x) qb[w] = Wk.qbits[static_cast<uint64_t>(qi) * A.W + w];
+    __syncthreads();
+    const uint32_t n = block_tree_descent(T, beams, K.want_c, qb, A.W, hist, rbase, rpre, knodes,
+                                          Wk.tlist + static_cast<uint64_t>(qi) * K.tcap, hcache, kTreeHCache, scratch);
+    if (threadIdx.x == 0) Wk.tcount[qi] = n;
+}
+
 // want-th smallest (1-based) of the n u32 values get(i), block-wide, four 8-bit radix passes.
 // Values of 0xFFFFFFFF stand for absent entries; want must not exceed the present ones.
 template <class Get>

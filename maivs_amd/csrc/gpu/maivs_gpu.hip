@@ -336,6 +336,18 @@ int raise_lds_limit(maivs_gpu_ctx* ctx, const void* fn, size_t lds) {
 }
 
 int launch_pq_tree(maivs_gpu_ctx* ctx, const KParams& K, uint32_t cap) {
+    if (K.nq <= ctx->pq_tree_block_max_q) {
+        // small batches: a workgroup per query
+        const size_t lds = static_cast<size_t>(pq_tree_block_lds_words(ctx->A.W, cap)) * 4;
+        if (lds > kLdsBudget) return fail(ctx, MAIVS_ERR_UNSUPPORTED, "tree descent needs %zu bytes of LDS", lds);
+        int rc;
+        if (lds > 64 * 1024 && (rc = raise_lds_limit(ctx, reinterpret_cast<const void*>(pq_tree_block_kernel), lds)))
+            return rc;
+        hipLaunchKernelGGL(pq_tree_block_kernel, dim3(K.nq), dim3(kPqTreeBlock), lds, ctx->stream, ctx->A, ctx->Wk, K,
+                           ctx->tree, ctx->d_beams, cap);
+        HIP_TRY(ctx, hipGetLastError());
+        return 0;
+    }
     const uint32_t words = pq_tree_lds_words(ctx->A.W, cap);
     const uint32_t per_wave = (words * 4 + 15) & ~15u;
     const size_t lds = static_cast<size_t>(per_wave) * kPqTreeWaves;
@@ -1162,6 +1174,8 @@ int maivs_gpu_create(int device, maivs_gpu_ctx** out) {
     if (const char* f = std::getenv("MAIVS_GPU_FRONT_REST")) ctx->front_rest_mode = std::max(0, std::atoi(f));
     // the matrix-core scan: unset = by cell sharing, 0 = off, else the least queries of its work items
     if (const char* m = std::getenv("MAIVS_GPU_MMA_MIN")) ctx->mma_min_mode = std::max(0, std::atoi(m));
+    // the per-query tree descent by a workgroup per query up to this many queries (else a wave each)
+    if (const char* t = std::getenv("MAIVS_GPU_PQ_TREE_BLOCK")) ctx->pq_tree_block_max_q = static_cast<uint32_t>(std::max(0, std::atoi(t)));
     // the matrix-core scan's items in cell order, a contiguous chunk per XCD: 1 (default) or 0
     if (const char* x = std::getenv("MAIVS_GPU_XCD_ORDER")) ctx->xcd_order = std::strcmp(x, "0") != 0;
     if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {

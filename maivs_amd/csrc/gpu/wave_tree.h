@@ -208,6 +208,138 @@ __device__ inline uint32_t tree_descent(const TreeDev& T, const uint32_t* beams,
     return nout;
 }
 
+// wave_keep_smallest by the whole workgroup (every thread calls it; blockDim.x a multiple of 64, at
+// most 1024): the same kept entries, emitted with the same ranks k. hist: bits + 1 counters;
+// scratch: 18 words (block scans, then the threshold and its count below).
+template <class HD, class EMIT>
+__device__ uint32_t block_keep_smallest(uint32_t F, uint32_t keep, uint32_t bits, uint32_t* hist, uint32_t* scratch,
+                                        HD hd, EMIT emit, uint16_t* hcache, uint32_t hcap) {
+    const uint32_t tid = threadIdx.x, nt = blockDim.x;
+    if (keep >= F) {
+        for (uint32_t p = tid; p < F; p += nt) emit(p, p);
+        return F;
+    }
+    for (uint32_t j = tid; j <= bits; j += nt) hist[j] = 0;
+    __syncthreads();
+    for (uint32_t p0 = tid; p0 < F; p0 += 4 * nt) {
+        uint32_t hv[4];
+#pragma unroll
+        for (uint32_t u = 0; u < 4; ++u) {
+            const uint32_t p = p0 + u * nt;
+            hv[u] = p < F ? hd(p) : 0u;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < 4; ++u) {
+            const uint32_t p = p0 + u * nt;
+            if (p < F) {
+                atomicAdd(&hist[hv[u]], 1u);
+                if (p < hcap) hcache[p] = static_cast<uint16_t>(hv[u]);
+            }
+        }
+    }
+    __syncthreads();
+    // t = the smallest distance with count(h <= t) >= keep; below = count(h < t)
+    const uint32_t nb = bits + 1, bpt = (nb + nt - 1) / nt;
+    const uint32_t b0 = min(tid * bpt, nb), b1 = min(b0 + bpt, nb);
+    uint32_t mine = 0;
+    for (uint32_t b = b0; b < b1; ++b) mine += hist[b];
+    uint32_t total;
+    const uint32_t excl = block_excl_scan_u32(mine, scratch, &total);
+    if (excl < keep && excl + mine >= keep) {
+        uint32_t cum = excl;
+        for (uint32_t b = b0; b < b1; ++b) {
+            if (cum + hist[b] >= keep) {
+                scratch[16] = b;
+                scratch[17] = cum;
+                break;
+            }
+            cum += hist[b];
+        }
+    }
+    __syncthreads();
+    const uint32_t t = scratch[16], below = scratch[17];
+    const uint32_t need_eq = keep - below;
+    // encounter order, a chunk of nt positions at a time: one scan counts both the entries below t
+    // (low half) and those at t (high half) before each position
+    uint32_t eq_seen = 0, kept = 0;
+    for (uint32_t c0 = 0; c0 < F; c0 += nt) {
+        const uint32_t p = c0 + tid;
+        const bool valid = p < F;
+        const uint32_t h = valid ? (p < hcap ? static_cast<uint32_t>(hcache[p]) : hd(p)) : 0xFFFFFFFFu;
+        const bool lt = valid && h < t, eq = valid && h == t;
+        uint32_t tot;
+        const uint32_t ex = block_excl_scan_u32((lt ? 1u : 0u) | (eq ? 0x10000u : 0u), scratch, &tot);
+        const uint32_t rem = need_eq > eq_seen ? need_eq - eq_seen : 0u;
+        const uint32_t eq_before = ex >> 16;
+        if (lt || (eq && eq_before < rem)) emit(kept + (ex & 0xFFFFu) + min(eq_before, rem), p);
+        kept += (tot & 0xFFFFu) + min(tot >> 16, rem);
+        eq_seen += tot >> 16;
+    }
+    return kept;
+}
+
+// tree_descent by the whole workgroup (every thread calls it): the same leaves in the same order.
+// LDS as tree_descent's, plus scratch (18 words).
+__device__ inline uint32_t block_tree_descent(const TreeDev& T, const uint32_t* beams, uint32_t want, const uint64_t* qb,
+                                              uint32_t W, uint32_t* hist, uint32_t* rbase, uint32_t* rpre,
+                                              uint32_t* knodes, uint32_t* out, uint16_t* hcache, uint32_t hcap,
+                                              uint32_t* scratch) {
+    const uint32_t tid = threadIdx.x, nt = blockDim.x, bits = W * 64;
+    if (T.n_levels == 0) return 0;
+    uint32_t nr = 1;
+    if (tid == 0) {
+        rbase[0] = 0;
+        rpre[0] = 0;
+        rpre[1] = T.lv_off[1] - T.lv_off[0];
+    }
+    __syncthreads();
+    uint32_t F = T.lv_off[1] - T.lv_off[0];
+    for (uint32_t li = 0; li < T.n_levels; ++li) {
+        const uint64_t* codes = T.lv_codes + static_cast<uint64_t>(T.lv_off[li]) * W;
+        const uint32_t keep = min(beams[li], F);
+        if (keep == 0) return 0;
+        const uint32_t nk = block_keep_smallest(
+            F, keep, bits, hist, scratch,
+            [&](uint32_t p) {
+                const uint32_t node = frontier_node(rbase, rpre, nr, p);
+                return hamming_lds(qb, codes + static_cast<uint64_t>(node) * W, W);
+            },
+            [&](uint32_t k, uint32_t p) { knodes[k] = frontier_node(rbase, rpre, nr, p); }, hcache, hcap);
+        __syncthreads();
+        // children of the kept nodes, in order: the next frontier's ranges
+        const uint32_t* cs = T.lv_cs + T.lv_off[li];
+        const uint32_t* cl = T.lv_cl + T.lv_off[li];
+        uint32_t carry = 0;
+        for (uint32_t k0 = 0; k0 < nk; k0 += nt) {
+            const uint32_t k = k0 + tid;
+            const uint32_t node = k < nk ? knodes[k] : 0u;
+            const uint32_t len = k < nk ? cl[node] : 0u;
+            uint32_t tot;
+            const uint32_t ex = block_excl_scan_u32(len, scratch, &tot);
+            if (k < nk) {
+                rbase[k] = cs[node];
+                rpre[k] = carry + ex;
+            }
+            carry += tot;
+        }
+        if (tid == 0) rpre[nk] = carry;
+        __syncthreads();
+        nr = nk;
+        F = carry;
+    }
+    const uint32_t keep = min(want, F);
+    if (keep == 0) return 0;
+    const uint32_t nout = block_keep_smallest(
+        F, keep, bits, hist, scratch,
+        [&](uint32_t p) {
+            const uint32_t leaf = frontier_node(rbase, rpre, nr, p);
+            return hamming_lds(qb, T.leaf_codes + static_cast<uint64_t>(leaf) * W, W);
+        },
+        [&](uint32_t k, uint32_t p) { out[k] = T.leaf_ids[frontier_node(rbase, rpre, nr, p)]; }, hcache, hcap);
+    __syncthreads();
+    return nout;
+}
+
 // beams of the descent (src/tree.rs:559-570): from the finest level up, clamp(ceil(need * frac),
 // min_beam, level size), need starting at max(want, 1).
 __host__ inline void tree_beams(const uint32_t* level_n, uint32_t n_levels, float frac, uint32_t min_beam, uint32_t want,

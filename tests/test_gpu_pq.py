@@ -129,3 +129,34 @@ def test_binding_search_and_small_batches(quality50k, tree40k, mix50k):
         assert not ix.takes_cellmajor(3, True)
         ids, sc = ix.search_batch(queries[:3], 10, 16, 0.95, 8.0, True)
         assert ids == [int(ext[s]) if s != 0xFFFFFFFF else 2 ** 64 - 1 for s in oslots.reshape(-1)]
+
+
+@pytest.fixture(scope="module")
+def tree2lvl(mix50k):
+    """40k vectors, 600 cells and fanout 2: a two-level centroid tree (300 and 150 nodes)."""
+    base, _, _ = mix50k
+    x = np.ascontiguousarray(base[:40000])
+    ix = M.preset(384, len(x))
+    ix.set_tree_route(True, 256, 2)
+    ix.train_centroids(x, 600)
+    ix.add_batch(list(range(len(x))), x)
+    ix.compact()
+    assert len(ix._tree_arrays()["level_n"]) == 2
+    return ix
+
+
+@pytest.mark.parametrize("block_max_q", ["0", "1000000"])
+def test_pq_tree_descent_kernels_match_oracle(monkeypatch, tree40k, tree2lvl, mix50k, block_max_q):
+    """The tree descent one wave per query (MAIVS_GPU_PQ_TREE_BLOCK=0) and one workgroup per query:
+    the same leaves, so slots and score bits identical to the oracle, for one- and two-level trees,
+    300 queries and one."""
+    _, queries, _ = mix50k
+    monkeypatch.setenv("MAIVS_GPU_PQ_TREE_BLOCK", block_max_q)
+    c = capi.Context(0)
+    try:
+        for ix in (tree40k, tree2lvl):
+            for nprobe in (4, 40):
+                _compare(c, ix, queries[:300], _params(ix, 10, nprobe))
+                _compare(c, ix, queries[300:301], _params(ix, 10, nprobe))
+    finally:
+        c.close()
