@@ -49,6 +49,7 @@ struct maivs_gpu_ctx {
     uint32_t seed_cap = 0;            // sum of the SEED_CELLS largest cells: bound of one seed set
     size_t lds_prep = 0, lds_seed = 0, lds_finish = 0;
     uint32_t pq_tree_block_max_q = 1000000;  // the block-wide tree descent up to this many queries
+    uint32_t pq_rounds_max_q = 64;           // the per-query scan in rounds of cells up to this many queries
     Ctl* h_ctl = nullptr;  // pinned host copy of the control block (read after each pass)
     hipEvent_t ev[8] = {};
     // last call, for maivs_gpu_last_candidates / maivs_gpu_last_counters

@@ -2505,11 +2505,19 @@ __host__ __device__ inline uint32_t pq_bins(uint32_t maxk, uint32_t W, bool ham)
     return ham ? W * 64 + 1 : (maxk >> 6) + 1;
 }
 
+// The rounds variant of the scan (small batches): up to kRoundCells probed cells at a time, with
+// at most 2 * kScanRoundThreads entries together (a single larger cell makes a round of its own).
+constexpr uint32_t kScanRoundThreads = 1024;
+constexpr uint32_t kRoundCells = 8;
+constexpr uint32_t kRoundBudget = 2 * kScanRoundThreads;
+constexpr uint32_t kRoundPre = 64;  // probe ranks whose cell and member range are staged in LDS
+
 __host__ __device__ inline uint32_t pq_scan_lds_words(uint32_t MW, uint32_t maxk, uint32_t nprobe, uint32_t W = 0,
-                                                      bool pair = false, bool ham = false) {
+                                                      bool pair = false, bool ham = false, bool rounds = false) {
     const uint32_t nbins = pq_bins(maxk, W, ham);
-    return ((MW + 3) & ~3u) + ((nbins + 3) & ~3u) + ((nprobe + 1 + 3) & ~3u) + kHistBins + 32 + 2 * kPqStage +
-           (pair ? W * 1024 : 0u);
+    const uint32_t nb4 = (nbins + 3) & ~3u;
+    return ((MW + 3) & ~3u) + nb4 + ((nprobe + 1 + 3) & ~3u) + kHistBins + 32 + 2 * kPqStage + (pair ? W * 1024 : 0u) +
+           (rounds ? ((MW + 3) & ~3u) + kRoundCells * nb4 + 72 + 3 * kRoundPre : 0u);
 }
 
 // The FastScan scan of one query (src/index.rs:1689-1757), one workgroup: cells in probe order;
@@ -2526,12 +2534,21 @@ __host__ __device__ inline uint32_t pq_scan_lds_words(uint32_t MW, uint32_t maxk
 // distance of a member is its Hamming distance h to the query's code, the bucket queue runs on h
 // itself from tau = W * 64, the adaptive stop compares with cos(pi * tau / dp) (the host's libm
 // value, A.ham_cos[tau]), and every survivor h <= tau, ties included, goes to the rerank.
-template <int NW, bool HAM = false>
-__global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work Wk, KParams K) {
+// RND (small batches, kScanRoundThreads threads): the probed cells in rounds of up to kRoundCells
+// scanned together. Each round admits the entries with h <= tau as it stood before the round and
+// counts them per cell; the cumulative counts give each cell's tau and adaptive decision exactly
+// as the cell-by-cell loop would (tau after a cell depends only on the entries of the cells up to
+// it, and an entry above the round's starting tau is above every later one). The first cell that
+// stops ends the scan, and the round's entries of the cells after it are dropped. The keys of a
+// round carry the cell's place in the round in bits 48-55. Extra LDS after pair: rbits[MW4] (the
+// round's cells) | rhist[kRoundCells * bins4] | rinfo[72] | the first kRoundPre probe ranks'
+// cell, first entry and length.
+template <int NW, bool HAM = false, bool RND = false>
+__global__ void __launch_bounds__(RND ? kScanRoundThreads : kScanThreads) pq_scan_kernel(DevArena A, Work Wk, KParams K) {
     constexpr uint32_t TB = NW * 256;
     __shared__ __align__(16) uint8_t table[TB];
     extern __shared__ __align__(16) uint32_t pq_smem[];
-    __shared__ uint32_t s_cnt, s_tau, s_kept, s_stop, s_w;
+    __shared__ uint32_t s_cnt, s_tau, s_kept, s_stop, s_w, s_round, s_over;
     const uint32_t qi = blockIdx.x;
     if (qi >= K.nq) return;
     const uint32_t tid = threadIdx.x, nt = blockDim.x, lane = lane_id();
@@ -2550,6 +2567,21 @@ __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work 
     uint32_t* scratch = hist2 + kHistBins;
     uint64_t* stage = reinterpret_cast<uint64_t*>(scratch + 32);  // 8-byte aligned: every region is a multiple of 16 bytes
     uint16_t* pair = reinterpret_cast<uint16_t*>(stage + kPqStage);
+    const uint32_t nb4 = (nbins + 3) & ~3u;
+    uint32_t* rbits = reinterpret_cast<uint32_t*>(pair) + (K.pq_pair ? NW * 1024 : 0u);
+    uint32_t* rhist = rbits + ((A.MW + 3) & ~3u);
+    uint32_t* rinfo = rhist + kRoundCells * nb4;
+    uint32_t* rc = rinfo;         // the round's cells
+    uint32_t* re0 = rinfo + 8;    // their first entries
+    uint32_t* roff = rinfo + 16;  // their offsets in the round's entry order (9)
+    uint32_t* rn = rinfo + 25;    // entries admitted per cell
+    uint32_t* rtau = rinfo + 33;
+    uint32_t* rkept = rinfo + 41;
+    uint32_t* rstop = rinfo + 49;
+    uint32_t* rflag = rinfo + 57;
+    uint32_t* pc = rinfo + 72;    // probe ranks < kRoundPre: cell, first entry, length
+    uint32_t* pe0 = pc + kRoundPre;
+    uint32_t* plen = pe0 + kRoundPre;
     if (!HAM) {
         const uint4* src = reinterpret_cast<const uint4*>(Wk.lut + static_cast<uint64_t>(qi) * TB);
         for (uint32_t i = tid; i < TB / 16; i += nt) reinterpret_cast<uint4*>(table)[i] = src[i];
@@ -2568,6 +2600,19 @@ __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work 
     for (uint32_t i = tid; i < nbins; i += nt) hist[i] = 0;
     const uint32_t nch = Wk.nchosen[qi];
     const uint32_t* chosen = Wk.chosen + static_cast<uint64_t>(qi) * K.nprobe;
+    if constexpr (RND) {
+        for (uint32_t i = tid; i < A.MW; i += nt) rbits[i] = 0;
+        if (tid >= kWave && tid < kWave + kRoundPre) {
+            const uint32_t r = tid - kWave;
+            if (r < nch) {
+                const uint32_t c = chosen[r];
+                const uint32_t e0 = A.mem_off[c];
+                pc[r] = c;
+                pe0[r] = e0;
+                plen[r] = A.mem_off[c + 1] - e0;
+            }
+        }
+    }
     const float delta = Wk.delta[qi], bias = Wk.bias[qi];
     // suffix maxima of the reachability bounds (src/index.rs:1466-1489), suffix[nch] = -inf: wave 0,
     // 64 probe ranks at a time from the end
@@ -2596,6 +2641,76 @@ __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work 
     uint64_t* cbuf = Wk.pqc + static_cast<uint64_t>(qi) * K.pq_cap;
     const uint32_t target = K.target;
     bool flagged = false;
+    // The bucket queue (src/index.rs:1712-1724), by one wave: from c = #(h <= t0) and the counts
+    // h[0 .. t0], tau = min(t0, the first u with #(h <= u) >= target) and #(h <= tau). The walk
+    // goes down from t0, 64 bins per step: lane l holds bin t - l, and an inclusive scan gives
+    // #(h <= t - l - 1) = c - (the bins t - l .. t).
+    auto walk = [&](const uint32_t* h, uint32_t t0, uint32_t c, uint32_t& t_out, uint32_t& kept_out) {
+        uint32_t t = t0, kept = c;
+        if (c >= target) {
+            for (;;) {
+                const int32_t bi = static_cast<int32_t>(t) - static_cast<int32_t>(lane);
+                const uint32_t hv = bi >= 0 ? h[bi] : 0u;
+                uint32_t incl = hv;
+                for (int o = 1; o < kWave; o <<= 1) {
+                    const uint32_t y = __shfl_up(incl, o, kWave);
+                    if (lane >= static_cast<uint32_t>(o)) incl += y;
+                }
+                // the walk stops at the first bin u = t - l whose lower neighbour's count
+                // #(h <= u - 1) falls below the target (bin 0's lower count is 0)
+                const uint64_t stopm = __ballot(bi >= 0 && c - incl < target);
+                if (stopm) {
+                    const int l = __ffsll(static_cast<long long>(stopm)) - 1;
+                    const uint32_t below = __shfl(incl - hv, l, kWave);  // the bins t - l + 1 .. t
+                    t = t - static_cast<uint32_t>(l);
+                    kept = c - below;
+                    break;
+                }
+                c -= __shfl(incl, kWave - 1, kWave);
+                t -= kWave;
+            }
+        }
+        t_out = t;
+        kept_out = kept;
+    };
+    // the adaptive stop after a cell (:1727-1733), tau t with kept entries at or below it, and the
+    // suffix maximum sx of the bounds of the cells after it; flag: the comparison is within the
+    // host-check band
+    auto adaptive_stop = [&](uint32_t t, uint32_t kept, float sx, bool& flag) -> bool {
+        if (!K.adaptive || kept < target) return false;
+        float thr;
+        if constexpr (HAM) {
+            thr = A.ham_cos[t];  // score_to_cos(hamming_score(tau)), src/index.rs:1782-1786
+        } else {
+            const uint32_t top = ((t + 1) << 6) - 1;
+            const uint32_t worst = A.maxk > top ? A.maxk - top : 0u;
+            const float est = delta * static_cast<float>(worst) + bias;
+            thr = fminf(fmaxf(est / K.norm, -1.0f), 1.0f);
+        }
+        const float T = thr - K.at_margin;
+        if (!K.pq_noflag && fabsf(sx - T) <= K.prune_band) flag = true;
+        return sx < T;
+    };
+    // keeps the entries with h <= t (in place, in order) and sets s_cnt to their number
+    auto compact_to = [&](uint32_t t) {
+        const uint32_t n = s_cnt;
+        __syncthreads();
+        if (tid == 0) s_w = 0;
+        __syncthreads();
+        for (uint32_t base = 0; base < n; base += nt) {
+            const uint32_t i = base + tid;
+            const uint64_t key = i < n ? cbuf[i] : 0ull;
+            const bool keepit = i < n && bucket(static_cast<uint32_t>(key >> 32) & 0xFFFFu) <= t;
+            uint32_t tot;
+            const uint32_t off = block_excl_scan_u32(keepit ? 1u : 0u, scratch, &tot);
+            if (keepit) cbuf[s_w + off] = key;
+            __syncthreads();
+            if (tid == 0) s_w += tot;
+            __syncthreads();
+        }
+        if (tid == 0) s_cnt = s_w;
+        __syncthreads();
+    };
     // one member's data; the first round of the next cell is loaded ahead
     struct Mem {
         Code<NW> code;
@@ -2621,23 +2736,228 @@ __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work 
     uint32_t c_cur = 0, e0_cur = 0, len_cur = 0;  // this cell
     uint32_t c_n1 = 0, e0_n1 = 0, len_n1 = 0;     // the next one
     uint32_t c_n2 = 0;                            // the one after
-    if (nch > 0) {
+    if (!RND && nch > 0) {
         c_cur = chosen[0];
         e0_cur = A.mem_off[c_cur];
         len_cur = A.mem_off[c_cur + 1] - e0_cur;
         load_mem(e0_cur, len_cur, 0, nxt);
     }
-    if (nch > 1) {
+    if (!RND && nch > 1) {
         c_n1 = chosen[1];
         e0_n1 = A.mem_off[c_n1];
         len_n1 = A.mem_off[c_n1 + 1] - e0_n1;
     }
-    if (nch > 2) c_n2 = chosen[2];
+    if (!RND && nch > 2) c_n2 = chosen[2];
     __syncthreads();
     // #(h <= tau) over every admitted entry, and s_cnt when it was last counted in (wave 0 keeps
     // both; s_cnt is read only where no admission is in flight: after a cell's barrier, after a
     // compaction)
     uint32_t cum = 0, cnt_prev = 0;
+    if constexpr (RND) {
+        // ---- rounds of up to kRoundCells cells (cum: #(h <= s_tau) over every admitted entry)
+        const uint32_t wv = tid / kWave;
+        uint32_t r0 = 0;
+        while (r0 < nch) {
+            // the round: the cells from rank r0 whose entries stay within the budget (at least one)
+            if (tid < kWave) {
+                const uint32_t j = lane, rk = r0 + j;
+                const bool have = j < kRoundCells && rk < nch;
+                uint32_t c = 0, e0 = 0, len = 0;
+                if (have) {
+                    if (rk < kRoundPre) {
+                        c = pc[rk];
+                        e0 = pe0[rk];
+                        len = plen[rk];
+                    } else {
+                        c = chosen[rk];
+                        e0 = A.mem_off[c];
+                        len = A.mem_off[c + 1] - e0;
+                    }
+                }
+                uint32_t incl = len;
+                for (int o = 1; o < static_cast<int>(kRoundCells); o <<= 1) {
+                    const uint32_t y = __shfl_up(incl, o, kWave);
+                    if (lane >= static_cast<uint32_t>(o)) incl += y;
+                }
+                // a prefix of the lanes: have and the running total are both monotone in j
+                const bool fits = have && (j == 0 || incl <= kRoundBudget);
+                const uint32_t nr = static_cast<uint32_t>(__popcll(__ballot(fits)));
+                if (j < nr) {
+                    rc[j] = c;
+                    re0[j] = e0;
+                    roff[j] = incl - len;
+                    rn[j] = 0;
+                    atomicOr(&rbits[c >> 5], 1u << (c & 31));
+                }
+                if (j + 1 == nr) roff[nr] = incl;
+                if (lane == 0) s_round = nr;
+            }
+            for (uint32_t i = tid; i < kRoundCells * nb4; i += nt) rhist[i] = 0;
+            __syncthreads();
+            const uint32_t nr = s_round, total = roff[nr], tau0 = s_tau;
+            // room for the round's entries: drop the entries above tau, else the buffer grows (host)
+            if (s_cnt + total > K.pq_cap) {
+                compact_to(tau0);
+                if (s_cnt + total > K.pq_cap) {
+                    if (tid == 0) {
+                        s_stop = 2;
+                        s_over = s_cnt + total;
+                    }
+                    break;
+                }
+            }
+            const uint32_t round_base = s_cnt;
+            // the round's entries, concatenated in rank order, nt at a time; admitted: h <= tau0.
+            // Two chunks' member data are loaded before the first is used (a round has at most two
+            // chunks unless one cell alone is larger); one for the widest codes (registers).
+            constexpr uint32_t kCh = NW >= 16 ? 1 : 2;
+            for (uint32_t base0 = 0; base0 < total; base0 += kCh * nt) {
+                Code<NW> code[kCh];
+                uint32_t jv[kCh], slot[kCh], alt[kCh], tag[kCh];
+#pragma unroll
+                for (uint32_t u = 0; u < kCh; ++u) {
+                    const uint32_t i = base0 + u * nt + tid;
+                    uint32_t j = 0;
+#pragma unroll
+                    for (uint32_t r = 1; r < kRoundCells; ++r) j += (r < nr && roff[r] <= i) ? 1u : 0u;
+                    jv[u] = j;
+                    slot[u] = alt[u] = tag[u] = 0u;
+                    if (i < total) {
+                        const uint64_t e = static_cast<uint64_t>(re0[j]) + (i - roff[j]);
+                        code[u].load(A.codes + e * (2 * NW));
+                        slot[u] = A.members[e];
+                        alt[u] = A.ma == 2 ? A.entry_alt[e] : 0u;
+                        tag[u] = K.filter ? A.entry_tag[e] : 0u;
+                    }
+                }
+#pragma unroll
+                for (uint32_t u = 0; u < kCh; ++u) {
+                    const uint32_t i = base0 + u * nt + tid;
+                    const uint32_t j = jv[u];
+                    bool ok = false;
+                    uint32_t dv = 0;
+                    if (i < total) {
+                        const uint32_t c = rc[j];
+                        if constexpr (HAM)
+                            dv = code_hamming<NW>(code[u], qd);
+                        else
+                            dv = A.maxk - (K.pq_pair ? lut_sum_pair<NW>(code[u], pair) : lut_sum1<NW>(code[u], table));
+                        if (bucket(dv) <= tau0) {
+                            ok = !K.filter || (tag[u] >= K.tag_lo && tag[u] <= K.tag_hi);
+                            // the first-ranked probed home counts (src/index.rs:1433-1447): homes in
+                            // earlier rounds, or earlier in this one
+                            auto seen = [&](uint32_t h) {
+                                if (h == c) return false;
+                                if ((scanned[h >> 5] >> (h & 31)) & 1u) return true;
+                                if (!((rbits[h >> 5] >> (h & 31)) & 1u)) return false;
+                                for (uint32_t r = 0; r < j; ++r)
+                                    if (rc[r] == h) return true;
+                                return false;
+                            };
+                            if (ok && A.ma == 2) {
+                                ok = !(alt[u] != kNoAlt && seen(alt[u]));
+                            } else if (ok && A.ma > 2) {
+                                for (uint32_t hj = 0; hj < A.ma && ok; ++hj) {
+                                    const uint32_t h = A.slot_cells[static_cast<uint64_t>(slot[u]) * A.ma + hj];
+                                    if (h != kNone && seen(h)) ok = false;
+                                }
+                            }
+                        }
+                    }
+                    const uint64_t bm = __ballot(ok);
+                    if (bm) {
+                        uint32_t wb = 0;
+                        if (lane == 0) wb = atomicAdd(&s_cnt, static_cast<uint32_t>(__popcll(bm)));
+                        wb = __shfl(wb, 0, kWave);
+                        if (ok) {
+                            const uint32_t pos = wb + lanes_below(bm);
+                            if (pos < K.pq_cap)
+                                cbuf[pos] = (static_cast<uint64_t>(j) << 48) | (static_cast<uint64_t>(dv) << 32) | slot[u];
+                            atomicAdd(&rhist[j * nb4 + bucket(dv)], 1u);
+                        }
+                        // admissions per cell: j does not decrease over the wave's lanes
+                        const uint32_t jlo = __shfl(j, 0, kWave), jhi = __shfl(j, kWave - 1, kWave);
+                        for (uint32_t jj = jlo; jj <= jhi; ++jj) {
+                            const uint32_t cnt = static_cast<uint32_t>(__popcll(__ballot(ok && j == jj)));
+                            if (lane == 0 && cnt) atomicAdd(&rn[jj], cnt);
+                        }
+                    }
+                }
+            }
+            __syncthreads();
+            // cumulative counts through each cell of the round: rhist[j][b] = hist[b] + the round's
+            // cells 0 .. j
+            for (uint32_t b = tid; b < nbins; b += nt) {
+                uint32_t acc = hist[b];
+                for (uint32_t r = 0; r < nr; ++r) {
+                    acc += rhist[r * nb4 + b];
+                    rhist[r * nb4 + b] = acc;
+                }
+            }
+            __syncthreads();
+            // each cell's tau and adaptive decision, one wave per cell
+            for (uint32_t j = wv; j < nr; j += nt / kWave) {
+                uint32_t c = cum;
+                for (uint32_t r = 0; r <= j; ++r) c += rn[r];
+                uint32_t t, kept;
+                walk(rhist + j * nb4, tau0, c, t, kept);
+                bool flag = false;
+                const bool stp = adaptive_stop(t, kept, suffix[r0 + j + 1], flag);
+                if (lane == 0) {
+                    rtau[j] = t;
+                    rkept[j] = kept;
+                    rstop[j] = stp ? 1u : 0u;
+                    rflag[j] = flag ? 1u : 0u;
+                }
+            }
+            __syncthreads();
+            // the first cell that stops is the last one scanned
+            uint32_t js = nr - 1, stp = 0;
+            for (uint32_t r = 0; r < nr; ++r) {
+                if (rstop[r]) {
+                    js = r;
+                    stp = 1;
+                    break;
+                }
+            }
+            if (tid == 0) {
+                for (uint32_t r = 0; r <= js; ++r) flagged = flagged || rflag[r] != 0;
+                s_tau = rtau[js];
+                s_stop = stp;
+            }
+            cum = rkept[js];
+            for (uint32_t b = tid; b < nbins; b += nt) hist[b] = rhist[js * nb4 + b];
+            if (tid < nr) {
+                const uint32_t c = rc[tid];
+                atomicAnd(&rbits[c >> 5], ~(1u << (c & 31)));
+                if (tid <= js) atomicOr(&scanned[c >> 5], 1u << (c & 31));
+            }
+            if (stp && js + 1 < nr) {
+                // drop the round's entries of the cells after js (the round has two cells or more,
+                // so at most kRoundBudget entries: two per thread)
+                const uint32_t n_r = s_cnt - round_base;
+                uint64_t v[2];
+                bool kp[2];
+#pragma unroll
+                for (uint32_t u = 0; u < 2; ++u) {
+                    const uint32_t i = tid + u * nt;
+                    v[u] = i < n_r ? cbuf[round_base + i] : 0ull;
+                    kp[u] = i < n_r && static_cast<uint32_t>(v[u] >> 48) <= js;
+                }
+                __syncthreads();
+                if (tid == 0) s_w = round_base;
+                __syncthreads();
+#pragma unroll
+                for (uint32_t u = 0; u < 2; ++u)
+                    if (kp[u]) cbuf[atomicAdd(&s_w, 1u)] = v[u];
+                __syncthreads();
+                if (tid == 0) s_cnt = s_w;
+            }
+            __syncthreads();
+            if (s_stop) break;
+            r0 += nr;
+        }
+    } else {
     for (uint32_t ci_i = 0; ci_i < nch; ++ci_i) {
         const uint32_t c = c_cur, e0 = e0_cur, len = len_cur;
         const uint32_t tau = s_tau;
@@ -2693,56 +3013,14 @@ __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work 
         if (ci_i + 3 < nch) c_n2 = chosen[ci_i + 3];
         __syncthreads();
         if (tid < kWave) {
-            // the bucket queue (src/index.rs:1712-1724): tau = min(tau, first u with #(h <= u) >= target).
             // hist only grows by entries with h <= tau and tau only falls, so #(h <= tau) is carried
-            // from cell to cell (cum, plus this cell's admissions) and the new tau is found by walking
-            // down from the old one, 64 bins per step: lane l holds bin t - l, and an inclusive scan
-            // gives #(h <= t - l - 1) = c - (the bins t - l .. t).
+            // from cell to cell (cum, plus this cell's admissions)
             cum += s_cnt - cnt_prev;
             cnt_prev = s_cnt;
-            uint32_t t = tau, kept = cum;
-            if (cum >= target) {
-                uint32_t c = cum;  // #(h <= t)
-                for (;;) {
-                    const int32_t bi = static_cast<int32_t>(t) - static_cast<int32_t>(lane);
-                    const uint32_t hv = bi >= 0 ? hist[bi] : 0u;
-                    uint32_t incl = hv;
-                    for (int o = 1; o < kWave; o <<= 1) {
-                        const uint32_t y = __shfl_up(incl, o, kWave);
-                        if (lane >= static_cast<uint32_t>(o)) incl += y;
-                    }
-                    // the walk stops at the first bin u = t - l whose lower neighbour's count
-                    // #(h <= u - 1) falls below the target (bin 0's lower count is 0)
-                    const uint64_t stopm = __ballot(bi >= 0 && c - incl < target);
-                    if (stopm) {
-                        const int l = __ffsll(static_cast<long long>(stopm)) - 1;
-                        const uint32_t below = __shfl(incl - hv, l, kWave);  // the bins t - l + 1 .. t
-                        t = t - static_cast<uint32_t>(l);
-                        kept = c - below;
-                        break;
-                    }
-                    c -= __shfl(incl, kWave - 1, kWave);
-                    t -= kWave;
-                }
-                cum = kept;
-            }
-            uint32_t stop = 0;
-            // the adaptive stop (:1727-1733)
-            if (K.adaptive && kept >= target) {
-                float thr;
-                if constexpr (HAM) {
-                    thr = A.ham_cos[t];  // score_to_cos(hamming_score(tau)), src/index.rs:1782-1786
-                } else {
-                    const uint32_t top = ((t + 1) << 6) - 1;
-                    const uint32_t worst = A.maxk > top ? A.maxk - top : 0u;
-                    const float est = delta * static_cast<float>(worst) + bias;
-                    thr = fminf(fmaxf(est / K.norm, -1.0f), 1.0f);
-                }
-                const float T = thr - K.at_margin;
-                const float sx = suffix[ci_i + 1];
-                if (!K.pq_noflag && fabsf(sx - T) <= K.prune_band) flagged = true;
-                if (sx < T) stop = 1;
-            }
+            uint32_t t, kept;
+            walk(hist, tau, cum, t, kept);
+            cum = kept;
+            uint32_t stop = adaptive_stop(t, kept, suffix[ci_i + 1], flagged) ? 1u : 0u;
             if (s_cnt > K.pq_cap) stop = 2;
             if (lane == 0) {
                 s_tau = t;
@@ -2755,33 +3033,18 @@ __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work 
         if (s_stop == 2) break;
         // room for the next cell: drop the entries above tau
         if (s_stop == 0 && ci_i + 1 < nch && s_cnt + K.pq_room > K.pq_cap) {
-            const uint32_t n = s_cnt, t = s_tau;
-            if (tid == 0) s_w = 0;
-            __syncthreads();
-            for (uint32_t base = 0; base < n; base += nt) {
-                const uint32_t i = base + tid;
-                const uint64_t key = i < n ? cbuf[i] : 0ull;
-                const bool keepit = i < n && bucket(static_cast<uint32_t>(key >> 32)) <= t;
-                uint32_t tot;
-                const uint32_t off = block_excl_scan_u32(keepit ? 1u : 0u, scratch, &tot);
-                if (keepit) cbuf[s_w + off] = key;
-                __syncthreads();
-                if (tid == 0) s_w += tot;
-                __syncthreads();
-            }
-            if (tid == 0) {
-                s_cnt = s_w;
-                if (s_cnt + K.pq_room > K.pq_cap) s_stop = 2;  // the next cell might not fit
-            }
+            compact_to(s_tau);
+            if (tid == 0 && s_cnt + K.pq_room > K.pq_cap) s_stop = 2;  // the next cell might not fit
             __syncthreads();
             cnt_prev = s_cnt;  // the entries above tau are gone; cum is unchanged
             if (s_stop == 2) break;
         }
         if (s_stop) break;
     }
+    }
     __syncthreads();
     if (tid == 0) {
-        if (s_stop == 2) atomicMax(&Wk.ctl->pq_overflow, s_cnt + K.pq_room);
+        if (s_stop == 2) atomicMax(&Wk.ctl->pq_overflow, RND ? s_over : s_cnt + K.pq_room);
     }
     if (tid == 0 && flagged) Wk.flag_prune[atomicAdd(&Wk.ctl->nflag_prune, 1u)] = qi;
     uint2* cand = Wk.cand + static_cast<uint64_t>(qi) * K.cand_cap;
@@ -2791,6 +3054,11 @@ __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work 
             Wk.seed_cnt[qi] = 0;
         }
         return;
+    }
+    if constexpr (RND) {
+        // a round admits against the tau before it: keep the survivors (h <= tau) alone, so the
+        // selection below sees about as many entries as the cell-by-cell loop leaves
+        if (s_cnt > target) compact_to(s_tau);
     }
     // survivors h <= tau; the target smallest (d, slot) when more (src/index.rs:1743-1757; ties at
     // the cut by ascending slot)
@@ -2814,7 +3082,7 @@ __global__ void __launch_bounds__(kScanThreads) pq_scan_kernel(DevArena A, Work 
     }
     auto key = [&](uint32_t i) -> uint64_t { return staged ? stage[i] : cbuf[i]; };
     auto surv_d = [&](uint32_t i) -> uint32_t {
-        const uint32_t dv = static_cast<uint32_t>(key(i) >> 32);
+        const uint32_t dv = static_cast<uint32_t>(key(i) >> 32) & 0xFFFFu;
         return bucket(dv) <= t ? dv : 0xFFFFFFFFu;
     };
     if (staged) {

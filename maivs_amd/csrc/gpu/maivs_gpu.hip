@@ -946,19 +946,24 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
 
 int launch_pq_scan(maivs_gpu_ctx* ctx, const KParams& K) {
     const DevArena& A = ctx->A;
-    const size_t lds =
-        static_cast<size_t>(pq_scan_lds_words(A.MW, A.maxk, K.nprobe, A.W, K.pq_pair != 0, K.pq_ham != 0)) * 4;
-    if (lds + A.W * 256 + kScanThreads * 4 > kLdsBudget)
+    const size_t lds = static_cast<size_t>(pq_scan_lds_words(A.MW, A.maxk, K.nprobe, A.W, K.pq_pair != 0,
+                                                             K.pq_ham != 0, K.pq_rounds != 0)) * 4;
+    const uint32_t threads = K.pq_rounds ? kScanRoundThreads : kScanThreads;
+    if (lds + A.W * 256 + threads * 4 > kLdsBudget)
         return fail(ctx, MAIVS_ERR_UNSUPPORTED, "per-query scan needs %zu bytes of LDS", lds);
     auto go = [&](const void* fn, auto kernel) -> int {
         int rc;
         if (lds > 48 * 1024 && (rc = raise_lds_limit(ctx, fn, lds))) return rc;
-        hipLaunchKernelGGL(kernel, dim3(K.nq), dim3(kScanThreads), lds, ctx->stream, A, ctx->Wk, K);
+        hipLaunchKernelGGL(kernel, dim3(K.nq), dim3(threads), lds, ctx->stream, A, ctx->Wk, K);
         return 0;
     };
     int rc = 0;
-    if (K.pq_ham) {
+    if (K.pq_ham && K.pq_rounds) {
+        DISPATCH_NW(A.W, rc = go(reinterpret_cast<const void*>(pq_scan_kernel<NW, true, true>), pq_scan_kernel<NW, true, true>));
+    } else if (K.pq_ham) {
         DISPATCH_NW(A.W, rc = go(reinterpret_cast<const void*>(pq_scan_kernel<NW, true>), pq_scan_kernel<NW, true>));
+    } else if (K.pq_rounds) {
+        DISPATCH_NW(A.W, rc = go(reinterpret_cast<const void*>(pq_scan_kernel<NW, false, true>), pq_scan_kernel<NW, false, true>));
     } else {
         DISPATCH_NW(A.W, rc = go(reinterpret_cast<const void*>(pq_scan_kernel<NW, false>), pq_scan_kernel<NW, false>));
     }
@@ -993,15 +998,26 @@ int run_search_pq(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs
     const bool tree = K.tree_list != 0;
     K.bnd_from = 0;
     K.pq_room = std::max(A.max_cell_len, 1u);
-    const uint32_t pq_need = std::max({4u * K.target + 1024u, 2u * K.pq_room + K.target, ctx->pq_cap_min});
+    // small batches scan their probed cells in rounds (a round appends up to kRoundBudget entries,
+    // or one larger cell)
+    // (codes of up to 512 bits: the widest codes would spill registers at 1024 threads)
+    K.pq_rounds = nq <= ctx->pq_rounds_max_q && A.W <= 8 ? 1u : 0u;
+    const uint32_t pq_need = std::max({4u * K.target + 1024u, 2u * K.pq_room + K.target, ctx->pq_cap_min,
+                                       K.pq_rounds ? 2u * kRoundBudget + K.target : 0u});
     if ((rc = ensure_pq(ctx, nq, K.tcap, pq_need))) return rc;
     K.pq_cap = ctx->cap_pq;
     K.pq_noflag = 0;
     // without FastScan blocks: search_one's Hamming branch (src/index.rs:1694-1760)
     K.pq_ham = A.fs ? 0u : 1u;
+    if (K.pq_rounds && pq_scan_lds_words(A.MW, A.maxk, K.nprobe, A.W, false, K.pq_ham != 0, true) * 4 + A.W * 256 +
+                               kScanRoundThreads * 4 >
+                           kLdsBudget)
+        K.pq_rounds = 0;
     // small batches (at most one workgroup per CU) look up position pairs: half the LDS lookups
     K.pq_pair = !K.pq_ham && nq <= kPqPairMaxQ &&
-                        pq_scan_lds_words(A.MW, A.maxk, K.nprobe, A.W, true) * 4 + A.W * 256 + kScanThreads * 4 <= kLdsBudget
+                        pq_scan_lds_words(A.MW, A.maxk, K.nprobe, A.W, true, false, K.pq_rounds != 0) * 4 + A.W * 256 +
+                                (K.pq_rounds ? kScanRoundThreads : kScanThreads) * 4 <=
+                            kLdsBudget
                     ? 1u
                     : 0u;
     if (p->nprobe == 0) {
@@ -1176,6 +1192,8 @@ int maivs_gpu_create(int device, maivs_gpu_ctx** out) {
     if (const char* m = std::getenv("MAIVS_GPU_MMA_MIN")) ctx->mma_min_mode = std::max(0, std::atoi(m));
     // the per-query tree descent by a workgroup per query up to this many queries (else a wave each)
     if (const char* t = std::getenv("MAIVS_GPU_PQ_TREE_BLOCK")) ctx->pq_tree_block_max_q = static_cast<uint32_t>(std::max(0, std::atoi(t)));
+    // the per-query scan in rounds of cells (a 1024-thread workgroup per query) up to this many queries
+    if (const char* r = std::getenv("MAIVS_GPU_PQ_ROUNDS")) ctx->pq_rounds_max_q = static_cast<uint32_t>(std::max(0, std::atoi(r)));
     // the matrix-core scan's items in cell order, a contiguous chunk per XCD: 1 (default) or 0
     if (const char* x = std::getenv("MAIVS_GPU_XCD_ORDER")) ctx->xcd_order = std::strcmp(x, "0") != 0;
     if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {

@@ -159,6 +159,8 @@ struct KParams {
     uint32_t mma_min;
     // per-query path: the Hamming branch (no FastScan blocks)
     uint32_t pq_ham;
+    // per-query scan: probed cells in rounds scanned together (small batches)
+    uint32_t pq_rounds;
     // matrix-core scan: items in cell order, a contiguous chunk per XCD (else arrival order)
     uint32_t xcd_order;
     // routing: every live cell is rescored (no tree, no two-stage shortlist)
