@@ -50,6 +50,7 @@ struct maivs_gpu_ctx {
     size_t lds_prep = 0, lds_seed = 0, lds_finish = 0;
     uint32_t pq_tree_block_max_q = 1000000;  // the block-wide tree descent up to this many queries
     uint32_t pq_rounds_max_q = 64;           // the per-query scan in rounds of cells up to this many queries
+    uint32_t pq_split_max_q = 64;            // the split per-query scan up to this many queries
     Ctl* h_ctl = nullptr;  // pinned host copy of the control block (read after each pass)
     hipEvent_t ev[8] = {};
     // last call, for maivs_gpu_last_candidates / maivs_gpu_last_counters
@@ -76,6 +77,8 @@ struct maivs_gpu_ctx {
     // the per-query path's buffers (tree lists, scan candidates, beams), sized by (nq, tcap, pq_cap)
     std::vector<void*> pq_allocs;
     uint32_t cap_pq_nq = 0, cap_tcap = 0, cap_pq = 0, pq_cap_min = 0;
+    std::vector<void*> split_allocs;  // the split per-query scan's per-cell entries, histograms and counts
+    uint64_t cap_split_e = 0, cap_split_h = 0, cap_split_n = 0;
     uint32_t* d_beams = nullptr;
     std::vector<uint32_t> beams_on_device;  // what d_beams holds (empty: unknown)
     // the centroid tree (per-query path); n_levels 0 when the arena has none

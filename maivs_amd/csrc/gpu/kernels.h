@@ -2512,12 +2512,22 @@ constexpr uint32_t kRoundCells = 8;
 constexpr uint32_t kRoundBudget = 2 * kScanRoundThreads;
 constexpr uint32_t kRoundPre = 64;  // probe ranks whose cell and member range are staged in LDS
 
+constexpr uint32_t kSplitCells = 16;  // probe ranks replayed together by the split scan's second kernel
+
+// mode 0: cell by cell; 1: rounds; 2: the split scan's second kernel (no tables, no pair table)
 __host__ __device__ inline uint32_t pq_scan_lds_words(uint32_t MW, uint32_t maxk, uint32_t nprobe, uint32_t W = 0,
-                                                      bool pair = false, bool ham = false, bool rounds = false) {
+                                                      bool pair = false, bool ham = false, uint32_t mode = 0) {
     const uint32_t nbins = pq_bins(maxk, W, ham);
     const uint32_t nb4 = (nbins + 3) & ~3u;
-    return ((MW + 3) & ~3u) + nb4 + ((nprobe + 1 + 3) & ~3u) + kHistBins + 32 + 2 * kPqStage + (pair ? W * 1024 : 0u) +
-           (rounds ? ((MW + 3) & ~3u) + kRoundCells * nb4 + 72 + 3 * kRoundPre : 0u);
+    const uint32_t np4 = (nprobe + 1 + 3) & ~3u;
+    return ((MW + 3) & ~3u) + nb4 + np4 + kHistBins + 32 + 2 * kPqStage + (pair && mode != 2 ? W * 1024 : 0u) +
+           (mode == 1 ? ((MW + 3) & ~3u) + kRoundCells * nb4 + 72 + 3 * kRoundPre : 0u) +
+           (mode == 2 ? kSplitCells * nb4 + np4 + 4 * kSplitCells : 0u);
+}
+
+// LDS of pq_cells_kernel: earlier[MW4] | hist[bins4] (plus its static table)
+__host__ __device__ inline uint32_t pq_cells_lds_words(uint32_t MW, uint32_t maxk, uint32_t W, bool ham) {
+    return ((MW + 3) & ~3u) + ((pq_bins(maxk, W, ham) + 3) & ~3u);
 }
 
 // The FastScan scan of one query (src/index.rs:1689-1757), one workgroup: cells in probe order;
@@ -2543,8 +2553,14 @@ __host__ __device__ inline uint32_t pq_scan_lds_words(uint32_t MW, uint32_t maxk
 // round carry the cell's place in the round in bits 48-55. Extra LDS after pair: rbits[MW4] (the
 // round's cells) | rhist[kRoundCells * bins4] | rinfo[72] | the first kRoundPre probe ranks'
 // cell, first entry and length.
-template <int NW, bool HAM = false, bool RND = false>
-__global__ void __launch_bounds__(RND ? kScanRoundThreads : kScanThreads) pq_scan_kernel(DevArena A, Work Wk, KParams K) {
+// MODE 2 (SPLIT, kScanRoundThreads threads): pq_cells_kernel scored every probed cell; the bucket
+// queue is replayed from the cells' histograms in probe order (kSplitCells ranks at a time, one
+// wave per rank), then the survivors of the ranks up to the stop are gathered from Wk.pqe into the
+// stage (and the candidate buffer). Extra LDS after stage: C[kSplitCells * bins4] | the ranks'
+// entry counts[np4] | decisions[4 * kSplitCells].
+template <int NW, bool HAM = false, int MODE = 0>
+__global__ void __launch_bounds__(MODE ? kScanRoundThreads : kScanThreads) pq_scan_kernel(DevArena A, Work Wk, KParams K) {
+    constexpr bool RND = MODE == 1, SPLIT = MODE == 2;
     constexpr uint32_t TB = NW * 256;
     __shared__ __align__(16) uint8_t table[TB];
     extern __shared__ __align__(16) uint32_t pq_smem[];
@@ -2582,11 +2598,11 @@ __global__ void __launch_bounds__(RND ? kScanRoundThreads : kScanThreads) pq_sca
     uint32_t* pc = rinfo + 72;    // probe ranks < kRoundPre: cell, first entry, length
     uint32_t* pe0 = pc + kRoundPre;
     uint32_t* plen = pe0 + kRoundPre;
-    if (!HAM) {
+    if (!HAM && !SPLIT) {
         const uint4* src = reinterpret_cast<const uint4*>(Wk.lut + static_cast<uint64_t>(qi) * TB);
         for (uint32_t i = tid; i < TB / 16; i += nt) reinterpret_cast<uint4*>(table)[i] = src[i];
     }
-    if (!HAM && K.pq_pair) {
+    if (!HAM && !SPLIT && K.pq_pair) {
         // entry p*256 + (a | b << 4) = table[2p][a] + table[2p+1][b], two entries per thread per step
         __syncthreads();
         for (uint32_t i = 2 * tid; i < NW * 2048; i += 2 * nt) {
@@ -2612,6 +2628,12 @@ __global__ void __launch_bounds__(RND ? kScanRoundThreads : kScanThreads) pq_sca
                 plen[r] = A.mem_off[c + 1] - e0;
             }
         }
+    }
+    uint32_t* sC = reinterpret_cast<uint32_t*>(stage + kPqStage);  // SPLIT: kSplitCells x bins4
+    uint32_t* sN = sC + kSplitCells * nb4;                         // SPLIT: entry count of each rank
+    uint32_t* sD = sN + ((K.nprobe + 1 + 3) & ~3u);                // SPLIT: tau, kept, stop, flag per rank
+    if constexpr (SPLIT) {
+        for (uint32_t r = tid; r < nch; r += nt) sN[r] = Wk.pqn[static_cast<uint64_t>(qi) * K.nprobe + r];
     }
     const float delta = Wk.delta[qi], bias = Wk.bias[qi];
     // suffix maxima of the reachability bounds (src/index.rs:1466-1489), suffix[nch] = -inf: wave 0,
@@ -2753,7 +2775,104 @@ __global__ void __launch_bounds__(RND ? kScanRoundThreads : kScanThreads) pq_sca
     // both; s_cnt is read only where no admission is in flight: after a cell's barrier, after a
     // compaction)
     uint32_t cum = 0, cnt_prev = 0;
-    if constexpr (RND) {
+    if constexpr (SPLIT) {
+        const uint32_t wv = tid / kWave;
+        const uint64_t qr = static_cast<uint64_t>(qi) * K.nprobe;
+        uint32_t r0 = 0, last = nch;  // ranks below last are scanned
+        while (r0 < nch) {
+            const uint32_t nr = min(nch - r0, kSplitCells), tau0 = s_tau;
+            // C[j][b] = hist[b] + the counts of ranks r0 .. r0 + j, for the bins up to tau0 (the
+            // others no longer count)
+            for (uint32_t b = tid; b <= tau0; b += nt) {
+                uint32_t v[kSplitCells];
+#pragma unroll
+                for (uint32_t j = 0; j < kSplitCells; ++j) v[j] = j < nr ? Wk.pqh[(qr + r0 + j) * nb4 + b] : 0u;
+                uint32_t acc = hist[b];
+#pragma unroll
+                for (uint32_t j = 0; j < kSplitCells; ++j) {
+                    acc += v[j];
+                    if (j < nr) sC[j * nb4 + b] = acc;
+                }
+            }
+            __syncthreads();
+            // each rank's tau and adaptive decision, one wave per rank
+            for (uint32_t j = wv; j < nr; j += nt / kWave) {
+                const uint32_t* cj = sC + j * nb4;
+                uint32_t c = 0;
+                for (uint32_t b = lane; b <= tau0; b += kWave) c += cj[b];
+                c = wave_sum_u32(c);
+                uint32_t t, kept;
+                walk(cj, tau0, c, t, kept);
+                bool flag = false;
+                const bool stp = adaptive_stop(t, kept, suffix[r0 + j + 1], flag);
+                if (lane == 0) {
+                    sD[j] = t;
+                    sD[kSplitCells + j] = kept;
+                    sD[2 * kSplitCells + j] = stp ? 1u : 0u;
+                    sD[3 * kSplitCells + j] = flag ? 1u : 0u;
+                }
+            }
+            __syncthreads();
+            // the first rank that stops is the last one scanned
+            uint32_t js = nr - 1, stp = 0;
+            for (uint32_t j = 0; j < nr; ++j) {
+                if (sD[2 * kSplitCells + j]) {
+                    js = j;
+                    stp = 1;
+                    break;
+                }
+            }
+            if (tid == 0) {
+                for (uint32_t j = 0; j <= js; ++j) flagged = flagged || sD[3 * kSplitCells + j] != 0;
+                s_tau = sD[js];
+                s_stop = stp;
+            }
+            for (uint32_t b = tid; b <= tau0; b += nt) hist[b] = sC[js * nb4 + b];
+            __syncthreads();
+            if (stp) {
+                last = r0 + js + 1;
+                break;
+            }
+            r0 += nr;
+        }
+        // the survivors (h <= tau) of the scanned ranks, a wave per rank with four entries per lane
+        // in flight: into the stage and the candidate buffer
+        const uint32_t tfin = s_tau;
+        if (tid == 0) s_cnt = 0;
+        __syncthreads();
+        for (uint32_t r = wv; r < last; r += nt / kWave) {
+            const uint32_t n_r = sN[r];
+            const uint64_t* src = Wk.pqe + (qr + r) * K.pq_room;
+            for (uint32_t i0 = 0; i0 < n_r; i0 += 4 * kWave) {
+                uint64_t v[4];
+#pragma unroll
+                for (uint32_t u = 0; u < 4; ++u) {
+                    const uint32_t i = i0 + u * kWave + lane;
+                    v[u] = i < n_r ? src[i] : 0ull;
+                }
+#pragma unroll
+                for (uint32_t u = 0; u < 4; ++u) {
+                    const uint32_t i = i0 + u * kWave + lane;
+                    const bool ok = i < n_r && bucket(static_cast<uint32_t>(v[u] >> 32) & 0xFFFFu) <= tfin;
+                    const uint64_t bm = __ballot(ok);
+                    if (!bm) continue;
+                    uint32_t wb = 0;
+                    if (lane == 0) wb = atomicAdd(&s_cnt, static_cast<uint32_t>(__popcll(bm)));
+                    wb = __shfl(wb, 0, kWave);
+                    if (ok) {
+                        const uint32_t pos = wb + lanes_below(bm);
+                        if (pos < kPqStage) stage[pos] = v[u];
+                        if (pos < K.pq_cap) cbuf[pos] = v[u];
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        if (tid == 0 && s_cnt > K.pq_cap) {
+            s_stop = 2;
+            s_over = s_cnt;
+        }
+    } else if constexpr (RND) {
         // ---- rounds of up to kRoundCells cells (cum: #(h <= s_tau) over every admitted entry)
         const uint32_t wv = tid / kWave;
         uint32_t r0 = 0;
@@ -3044,7 +3163,7 @@ __global__ void __launch_bounds__(RND ? kScanRoundThreads : kScanThreads) pq_sca
     }
     __syncthreads();
     if (tid == 0) {
-        if (s_stop == 2) atomicMax(&Wk.ctl->pq_overflow, RND ? s_over : s_cnt + K.pq_room);
+        if (s_stop == 2) atomicMax(&Wk.ctl->pq_overflow, MODE ? s_over : s_cnt + K.pq_room);
     }
     if (tid == 0 && flagged) Wk.flag_prune[atomicAdd(&Wk.ctl->nflag_prune, 1u)] = qi;
     uint2* cand = Wk.cand + static_cast<uint64_t>(qi) * K.cand_cap;
@@ -3065,7 +3184,7 @@ __global__ void __launch_bounds__(RND ? kScanRoundThreads : kScanThreads) pq_sca
     const uint32_t n = s_cnt, t = s_tau;
     // the keys in LDS when they fit (every pass below reads them), with all of a thread's loads in flight
     const bool staged = n <= kPqStage;
-    if (staged) {
+    if (staged && !SPLIT) {  // the split scan gathered its survivors into the stage already
         constexpr uint32_t PER = kPqStage / kScanThreads;
         uint64_t v[PER];
 #pragma unroll
@@ -3179,6 +3298,102 @@ __global__ void __launch_bounds__(RND ? kScanRoundThreads : kScanThreads) pq_sca
         Wk.cand_cnt[qi] = s_w;
         Wk.seed_cnt[qi] = 0;
     }
+}
+
+// The split scan's first kernel (small batches): one workgroup per (probe rank, query) scores
+// the probed cell's members against the query's FastScan table (or by Hamming distance, HAM) and
+// admits those the tag filter and the first-ranked-home rule keep (src/index.rs:1433-1447: a home
+// at a lower probe rank was scanned before), with no threshold. It writes them (d << 32 | slot) at
+// rank * pq_room in the query's region of Wk.pqe, their histogram over the bucket-queue bins to
+// Wk.pqh and their count to Wk.pqn; pq_scan_kernel<NW, HAM, 2> replays the bucket queue from these.
+// The nibble tables serve the lookups: a cell's few hundred members do not repay a pair table.
+// LDS: static table[W*256] | earlier[MW4] (the cells at lower ranks) | hist[bins4].
+template <int NW, bool HAM = false>
+__global__ void __launch_bounds__(kScanThreads) pq_cells_kernel(DevArena A, Work Wk, KParams K) {
+    constexpr uint32_t TB = NW * 256;
+    __shared__ __align__(16) uint8_t table[TB];
+    extern __shared__ __align__(16) uint32_t pc_smem[];
+    __shared__ uint32_t s_n;
+    const uint32_t r = blockIdx.x, qi = blockIdx.y;
+    if (qi >= K.nq) return;
+    const uint32_t nch = Wk.nchosen[qi];
+    if (r >= nch) return;  // uniform over the workgroup
+    const uint32_t tid = threadIdx.x, nt = blockDim.x, lane = lane_id();
+    const uint32_t nbins = pq_bins(A.maxk, NW, HAM), nb4 = (nbins + 3) & ~3u;
+    auto bucket = [](uint32_t dv) { return HAM ? dv : dv >> 6; };
+    const uint32_t* chosen = Wk.chosen + static_cast<uint64_t>(qi) * K.nprobe;
+    const uint32_t c = chosen[r];
+    const uint32_t e0 = A.mem_off[c], len = A.mem_off[c + 1] - e0;
+    uint32_t* earlier = pc_smem;
+    uint32_t* hist = earlier + ((A.MW + 3) & ~3u);
+    // one member's data; the first chunk's is in flight while the tables are set up
+    Code<NW> code;
+    uint32_t slot = 0, alt = 0, tag = 0;
+    auto load = [&](uint32_t i) {
+        if (i < len) {
+            const uint64_t e = static_cast<uint64_t>(e0) + i;
+            code.load(A.codes + e * (2 * NW));
+            slot = A.members[e];
+            alt = A.ma == 2 ? A.entry_alt[e] : 0u;
+            tag = K.filter ? A.entry_tag[e] : 0u;
+        }
+    };
+    load(tid);
+    uint32_t qd[2 * NW];
+    if constexpr (HAM) {
+        const uint32_t* qb = reinterpret_cast<const uint32_t*>(Wk.qbits + static_cast<uint64_t>(qi) * NW);
+#pragma unroll
+        for (int j = 0; j < 2 * NW; ++j) qd[j] = qb[j];
+    } else {
+        const uint4* src = reinterpret_cast<const uint4*>(Wk.lut + static_cast<uint64_t>(qi) * TB);
+        for (uint32_t i = tid; i < TB / 16; i += nt) reinterpret_cast<uint4*>(table)[i] = src[i];
+    }
+    for (uint32_t i = tid; i < A.MW; i += nt) earlier[i] = 0;
+    for (uint32_t i = tid; i < nbins; i += nt) hist[i] = 0;
+    if (tid == 0) s_n = 0;
+    __syncthreads();
+    for (uint32_t i = tid; i < r; i += nt) {
+        const uint32_t h = chosen[i];
+        atomicOr(&earlier[h >> 5], 1u << (h & 31));
+    }
+    __syncthreads();
+    auto seen = [&](uint32_t h) { return h != c && ((earlier[h >> 5] >> (h & 31)) & 1u); };
+    uint64_t* out = Wk.pqe + (static_cast<uint64_t>(qi) * K.nprobe + r) * K.pq_room;
+    for (uint32_t base = 0; base < len; base += nt) {
+        const uint32_t i = base + tid;
+        if (base > 0) load(i);
+        bool ok = false;
+        uint32_t dv = 0;
+        if (i < len) {
+            if constexpr (HAM)
+                dv = code_hamming<NW>(code, qd);
+            else
+                dv = A.maxk - lut_sum1<NW>(code, table);
+            ok = !K.filter || (tag >= K.tag_lo && tag <= K.tag_hi);
+            if (ok && A.ma == 2) {
+                ok = !(alt != kNoAlt && seen(alt));
+            } else if (ok && A.ma > 2) {
+                for (uint32_t hj = 0; hj < A.ma && ok; ++hj) {
+                    const uint32_t h = A.slot_cells[static_cast<uint64_t>(slot) * A.ma + hj];
+                    if (h != kNone && seen(h)) ok = false;
+                }
+            }
+        }
+        const uint64_t bm = __ballot(ok);
+        if (bm) {
+            uint32_t wb = 0;
+            if (lane == 0) wb = atomicAdd(&s_n, static_cast<uint32_t>(__popcll(bm)));
+            wb = __shfl(wb, 0, kWave);
+            if (ok) {
+                out[wb + lanes_below(bm)] = (static_cast<uint64_t>(dv) << 32) | slot;
+                atomicAdd(&hist[bucket(dv)], 1u);
+            }
+        }
+    }
+    __syncthreads();
+    uint32_t* gh = Wk.pqh + (static_cast<uint64_t>(qi) * K.nprobe + r) * nb4;
+    for (uint32_t b = tid; b < nb4; b += nt) gh[b] = b < nbins ? hist[b] : 0u;
+    if (tid == 0) Wk.pqn[static_cast<uint64_t>(qi) * K.nprobe + r] = s_n;
 }
 
 }  // namespace maivs_dev

@@ -293,6 +293,8 @@ int ensure_all(maivs_gpu_ctx* ctx, uint32_t nq, uint32_t nprobe, uint32_t k) {
 
 constexpr uint32_t kPqPairMaxQ = 256;   // batches up to this many queries use the pair tables in the per-query scan
 constexpr uint32_t kPqMaxProbe = 8192;  // probe-list bound of the per-query scan's on-chip suffix array
+constexpr uint32_t kSplitMaxProbe = 256;                // the split per-query scan: probe lists up to this long
+constexpr uint64_t kSplitMaxBytes = 512ull << 20;       // and per-cell entry buffers up to this size
 constexpr uint32_t kPqMaxLevels = 64;
 
 // Tree lists (nq x tcap), scan candidate buffers (nq x pq_cap) and the beams; grow only.
@@ -318,6 +320,33 @@ int ensure_pq(maivs_gpu_ctx* ctx, uint32_t nq, uint32_t tcap, uint32_t pq_cap) {
     ctx->cap_pq_nq = n;
     ctx->cap_tcap = t;
     ctx->cap_pq = c;
+    return 0;
+}
+
+// The split per-query scan's buffers (Work::pqe, pqh, pqn) for nq queries of nprobe cells of up to
+// room entries and nb4 histogram bins each; grow only.
+int ensure_split(maivs_gpu_ctx* ctx, uint32_t nq, uint32_t nprobe, uint32_t room, uint32_t nb4) {
+    const uint64_t cells = static_cast<uint64_t>(nq) * nprobe;
+    const uint64_t ne = cells * room, nh = cells * nb4;
+    if (ne <= ctx->cap_split_e && nh <= ctx->cap_split_h && cells <= ctx->cap_split_n) return 0;
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    drop_graph(ctx);
+    free_all(ctx->split_allocs);
+    const uint64_t e = std::max(ne, ctx->cap_split_e), h = std::max(nh, ctx->cap_split_h),
+                   n = std::max(cells, ctx->cap_split_n);
+    Work& W = ctx->Wk;
+    int rc = 0;
+    rc |= dalloc(ctx, ctx->split_allocs, &W.pqe, e);
+    rc |= dalloc(ctx, ctx->split_allocs, &W.pqh, h);
+    rc |= dalloc(ctx, ctx->split_allocs, &W.pqn, n);
+    if (rc) {
+        free_all(ctx->split_allocs);
+        ctx->cap_split_e = ctx->cap_split_h = ctx->cap_split_n = 0;
+        return rc;
+    }
+    ctx->cap_split_e = e;
+    ctx->cap_split_h = h;
+    ctx->cap_split_n = n;
     return 0;
 }
 
@@ -946,9 +975,10 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
 
 int launch_pq_scan(maivs_gpu_ctx* ctx, const KParams& K) {
     const DevArena& A = ctx->A;
-    const size_t lds = static_cast<size_t>(pq_scan_lds_words(A.MW, A.maxk, K.nprobe, A.W, K.pq_pair != 0,
-                                                             K.pq_ham != 0, K.pq_rounds != 0)) * 4;
-    const uint32_t threads = K.pq_rounds ? kScanRoundThreads : kScanThreads;
+    const uint32_t mode = K.pq_split ? 2u : K.pq_rounds ? 1u : 0u;
+    const size_t lds =
+        static_cast<size_t>(pq_scan_lds_words(A.MW, A.maxk, K.nprobe, A.W, K.pq_pair != 0, K.pq_ham != 0, mode)) * 4;
+    const uint32_t threads = mode ? kScanRoundThreads : kScanThreads;
     if (lds + A.W * 256 + threads * 4 > kLdsBudget)
         return fail(ctx, MAIVS_ERR_UNSUPPORTED, "per-query scan needs %zu bytes of LDS", lds);
     auto go = [&](const void* fn, auto kernel) -> int {
@@ -958,7 +988,20 @@ int launch_pq_scan(maivs_gpu_ctx* ctx, const KParams& K) {
         return 0;
     };
     int rc = 0;
-    if (K.pq_ham && K.pq_rounds) {
+    if (K.pq_split) {
+        // every probed cell by its own workgroup, then the bucket queue replayed per query
+        const size_t lds1 = static_cast<size_t>(pq_cells_lds_words(A.MW, A.maxk, A.W, K.pq_ham != 0)) * 4;
+        auto cells = [&](auto kernel) {
+            hipLaunchKernelGGL(kernel, dim3(K.nprobe, K.nq), dim3(kScanThreads), lds1, ctx->stream, A, ctx->Wk, K);
+        };
+        if (K.pq_ham) {
+            DISPATCH_NW(A.W, cells(pq_cells_kernel<NW, true>));
+            DISPATCH_NW(A.W, rc = go(reinterpret_cast<const void*>(pq_scan_kernel<NW, true, 2>), pq_scan_kernel<NW, true, 2>));
+        } else {
+            DISPATCH_NW(A.W, cells(pq_cells_kernel<NW, false>));
+            DISPATCH_NW(A.W, rc = go(reinterpret_cast<const void*>(pq_scan_kernel<NW, false, 2>), pq_scan_kernel<NW, false, 2>));
+        }
+    } else if (K.pq_ham && K.pq_rounds) {
         DISPATCH_NW(A.W, rc = go(reinterpret_cast<const void*>(pq_scan_kernel<NW, true, true>), pq_scan_kernel<NW, true, true>));
     } else if (K.pq_ham) {
         DISPATCH_NW(A.W, rc = go(reinterpret_cast<const void*>(pq_scan_kernel<NW, true>), pq_scan_kernel<NW, true>));
@@ -1009,13 +1052,22 @@ int run_search_pq(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs
     K.pq_noflag = 0;
     // without FastScan blocks: search_one's Hamming branch (src/index.rs:1694-1760)
     K.pq_ham = A.fs ? 0u : 1u;
-    if (K.pq_rounds && pq_scan_lds_words(A.MW, A.maxk, K.nprobe, A.W, false, K.pq_ham != 0, true) * 4 + A.W * 256 +
+    if (K.pq_rounds && pq_scan_lds_words(A.MW, A.maxk, K.nprobe, A.W, false, K.pq_ham != 0, 1) * 4 + A.W * 256 +
                                kScanRoundThreads * 4 >
                            kLdsBudget)
         K.pq_rounds = 0;
+    // the split scan: small batches of at most kSplitMaxProbe probes whose per-cell buffers stay modest
+    K.pq_split = 0;
+    if (nq <= ctx->pq_split_max_q && A.W <= 8 && p->nprobe <= kSplitMaxProbe &&
+        static_cast<uint64_t>(nq) * p->nprobe * K.pq_room * 8 <= kSplitMaxBytes &&
+        pq_scan_lds_words(A.MW, A.maxk, K.nprobe, A.W, false, K.pq_ham != 0, 2) * 4 + A.W * 256 + kScanRoundThreads * 4 <=
+            kLdsBudget) {
+        K.pq_split = 1;
+        if ((rc = ensure_split(ctx, nq, K.nprobe, K.pq_room, (pq_bins(A.maxk, A.W, K.pq_ham != 0) + 3) & ~3u))) return rc;
+    }
     // small batches (at most one workgroup per CU) look up position pairs: half the LDS lookups
     K.pq_pair = !K.pq_ham && nq <= kPqPairMaxQ &&
-                        pq_scan_lds_words(A.MW, A.maxk, K.nprobe, A.W, true, false, K.pq_rounds != 0) * 4 + A.W * 256 +
+                        pq_scan_lds_words(A.MW, A.maxk, K.nprobe, A.W, true, false, K.pq_rounds ? 1u : 0u) * 4 + A.W * 256 +
                                 (K.pq_rounds ? kScanRoundThreads : kScanThreads) * 4 <=
                             kLdsBudget
                     ? 1u
@@ -1194,6 +1246,8 @@ int maivs_gpu_create(int device, maivs_gpu_ctx** out) {
     if (const char* t = std::getenv("MAIVS_GPU_PQ_TREE_BLOCK")) ctx->pq_tree_block_max_q = static_cast<uint32_t>(std::max(0, std::atoi(t)));
     // the per-query scan in rounds of cells (a 1024-thread workgroup per query) up to this many queries
     if (const char* r = std::getenv("MAIVS_GPU_PQ_ROUNDS")) ctx->pq_rounds_max_q = static_cast<uint32_t>(std::max(0, std::atoi(r)));
+    // the split per-query scan (a workgroup per probed cell, then the bucket queue replayed) up to this many queries
+    if (const char* sp = std::getenv("MAIVS_GPU_PQ_SPLIT")) ctx->pq_split_max_q = static_cast<uint32_t>(std::max(0, std::atoi(sp)));
     // the matrix-core scan's items in cell order, a contiguous chunk per XCD: 1 (default) or 0
     if (const char* x = std::getenv("MAIVS_GPU_XCD_ORDER")) ctx->xcd_order = std::strcmp(x, "0") != 0;
     if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
@@ -1233,6 +1287,7 @@ void maivs_gpu_destroy(maivs_gpu_ctx* ctx) {
     free_all(ctx->work_allocs);
     free_all(ctx->cand_allocs);
     free_all(ctx->pq_allocs);
+    free_all(ctx->split_allocs);
     free_all(ctx->arena_allocs);
     free_all(ctx->store.allocs);
     for (auto& e : ctx->ev)
@@ -1282,9 +1337,11 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
     free_all(ctx->work_allocs);
     free_all(ctx->cand_allocs);
     free_all(ctx->pq_allocs);
+    free_all(ctx->split_allocs);
     free_all(ctx->arena_allocs);
     ctx->cap_nq = ctx->cap_nprobe = ctx->cap_k = ctx->cap_cand = ctx->cap_seed = ctx->cand_nq = 0;
     ctx->cap_pq_nq = ctx->cap_tcap = ctx->cap_pq = ctx->pq_cap_min = 0;
+    ctx->cap_split_e = ctx->cap_split_h = ctx->cap_split_n = 0;
     ctx->d_beams = nullptr;
     ctx->beams_on_device.clear();
     ctx->uploaded = false;

@@ -133,6 +133,11 @@ struct Work {
     uint32_t* tlist;       // nq x tcap: the centroid tree's leaf cells for each query
     uint32_t* tcount;      // nq
     uint64_t* pqc;         // nq x pq_cap: scanned candidates (d << 32 | slot)
+    // the split per-query scan (small batches): each probed cell's admitted entries (nq x nprobe x
+    // pq_room, d << 32 | slot), their bucket-queue histogram (nq x nprobe x bins4) and count (nq x nprobe)
+    uint64_t* pqe;
+    uint32_t* pqh;
+    uint32_t* pqn;
     // The cell-major scans' running cut of each query: starts at tau, and drops to the upper edge of
     // the d >> 8 bin holding the target-th smallest d among the entries counted so far in dhist
     // (the seed's scored members, then every appended candidate). Those are entries of the query's
@@ -161,6 +166,8 @@ struct KParams {
     uint32_t pq_ham;
     // per-query scan: probed cells in rounds scanned together (small batches)
     uint32_t pq_rounds;
+    // per-query scan: every probed cell scored by its own workgroup, then the bucket queue replayed
+    uint32_t pq_split;
     // matrix-core scan: items in cell order, a contiguous chunk per XCD (else arrival order)
     uint32_t xcd_order;
     // routing: every live cell is rescored (no tree, no two-stage shortlist)

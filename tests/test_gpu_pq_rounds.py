@@ -1,9 +1,11 @@
-"""The per-query scan's two forms on the GPU, each against the oracle's search_one
-(src/index.rs:1381-1864): cell by cell (MAIVS_GPU_PQ_ROUNDS=0, what batches above 64 queries run)
-and in rounds of up to eight probed cells scanned together (forced for every batch size here; the
-default for small batches). Slots and score bits identical, query by query, for FastScan and the
-Hamming branch, adaptive stops inside a round, multi-home vectors, the tag filter, nucleus probe
-lists and candidate buffers that overflow and grow.
+"""The per-query scan's three forms on the GPU, each against the oracle's search_one
+(src/index.rs:1381-1864): cell by cell (what batches above 64 queries run), in rounds of up to
+eight probed cells scanned together by one workgroup, and split (every probed cell scored by its
+own workgroup, then the bucket queue replayed from the cells' histograms; the default for batches
+of up to 64 queries and 256 probes). Each form is forced for every batch size here. Slots and
+score bits identical, query by query, for FastScan and the Hamming branch, adaptive stops inside a
+round, multi-home vectors, the tag filter, nucleus probe lists and candidate buffers that overflow
+and grow.
 """
 import numpy as np
 import pytest
@@ -15,16 +17,18 @@ from .test_oracle_pq import churned_uncompacted, tight_uncompacted, tree40k  # n
 
 pytestmark = pytest.mark.gpu
 
-MODES = ["0", "1000000"]
+# (MAIVS_GPU_PQ_ROUNDS, MAIVS_GPU_PQ_SPLIT): the largest batch each form serves
+MODES = [("0", "0"), ("1000000", "0"), ("0", "1000000")]
 
 
 def _params(ix, k, nprobe, tc=1.0, beta=8.0):
     return capi.params_from_bytes(ix._search_params(k, nprobe, tc, beta))
 
 
-@pytest.fixture(params=MODES, ids=["cell_by_cell", "rounds"])
+@pytest.fixture(params=MODES, ids=["cell_by_cell", "rounds", "split"])
 def ctx(request, monkeypatch):
-    monkeypatch.setenv("MAIVS_GPU_PQ_ROUNDS", request.param)
+    monkeypatch.setenv("MAIVS_GPU_PQ_ROUNDS", request.param[0])
+    monkeypatch.setenv("MAIVS_GPU_PQ_SPLIT", request.param[1])
     c = capi.Context(0)
     yield c
     c.close()
@@ -94,14 +98,15 @@ def test_rounds_hamming_branch(ctx, churned_uncompacted, tight_uncompacted, mix5
 
 
 def test_rounds_candidate_buffer_grows(ctx, quality50k, mix50k):
-    """No adaptive stop, every cell, k * rf > N: the candidate lists outgrow the scan's buffer
-    (the host grows it and runs the scan again) and the on-chip staging."""
+    """No adaptive stop, (nearly) every cell, k * rf > N: the candidate lists outgrow the scan's
+    buffer (the host grows it and runs the scan again) and the on-chip staging."""
     _, queries, _ = mix50k
     ix = quality50k
     ix.set_adaptive(False, 0.02)
     ix.set_rerank_factor(5001)
     try:
         _compare(ctx, ix, queries[:12], _params(ix, 10, 390))
+        _compare(ctx, ix, queries[12:20], _params(ix, 10, 256))
     finally:
         ix.set_adaptive(True, 0.02)
         ix.set_rerank_factor(32)
