@@ -51,6 +51,7 @@ struct maivs_gpu_ctx {
     uint32_t pq_tree_block_max_q = 1000000;  // the block-wide tree descent up to this many queries
     uint32_t pq_rounds_max_q = 64;           // the per-query scan in rounds of cells up to this many queries
     uint32_t pq_split_max_q = 64;            // the split per-query scan up to this many queries
+    uint32_t finish_wide_max_q = 64;         // the finish with kFinishWideThreads threads up to this many queries
     Ctl* h_ctl = nullptr;  // pinned host copy of the control block (read after each pass)
     hipEvent_t ev[8] = {};
     // last call, for maivs_gpu_last_candidates / maivs_gpu_last_counters

@@ -19,20 +19,85 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
                                      __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
 }
 
+// The value of lane (lane ^ M) for M a power of two below 64, without the LDS crossbar where the
+// wave's DPP row permutations reach: M = 1, 2 a quad permutation; 4 = half-row mirror then quad
+// reversal (i ^ 7 ^ 3); 8 = row mirror then half-row mirror (i ^ 15 ^ 7); 16 a swizzle within 32
+// lanes (xor mask 16); 32 a permute. Every lane of the wave must be active.
+template <int M>
+__device__ __forceinline__ float xor_lanes(float x) {
+    static_assert(M >= 1 && M <= 32 && (M & (M - 1)) == 0, "a lane distance of 1, 2, 4, 8, 16 or 32");
+    const int v = __float_as_int(x);
+    int r;
+    if constexpr (M == 1)
+        r = __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true);
+    else if constexpr (M == 2)
+        r = __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, true);
+    else if constexpr (M == 4)
+        r = __builtin_amdgcn_mov_dpp(__builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, true), 0x1B, 0xF, 0xF, true);
+    else if constexpr (M == 8)
+        r = __builtin_amdgcn_mov_dpp(__builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, true), 0x141, 0xF, 0xF, true);
+    else if constexpr (M == 16)
+        r = __builtin_amdgcn_ds_swizzle(v, 0x401F);
+    else
+        r = __shfl_xor(v, 32, kWave);
+    return __int_as_float(r);
+}
+
+// Inclusive prefix sum over the wave's 64 lanes without the LDS crossbar: row shifts by 1, 2, 4
+// and 8 lanes scan each row of 16, then row 15's total is broadcast into rows 1 and 3 and lane
+// 31's into rows 2 and 3. Every lane of the wave must be active.
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t x) {
+    int v = static_cast<int>(x);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, true);   // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, true);   // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true);   // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, true);   // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31
+    return static_cast<uint32_t>(v);
+}
+
+// lane ^ M's value of a 32-bit integer (xor_lanes)
+template <int M>
+__device__ __forceinline__ uint32_t xor_lanes_u32(uint32_t x) {
+    return __float_as_uint(xor_lanes<M>(__uint_as_float(x)));
+}
+
+// Whole-wave reductions by lane exchanges at distances 32 .. 1 (every lane active)
 __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    v += xor_lanes_u32<32>(v);
+    v += xor_lanes_u32<16>(v);
+    v += xor_lanes_u32<8>(v);
+    v += xor_lanes_u32<4>(v);
+    v += xor_lanes_u32<2>(v);
+    v += xor_lanes_u32<1>(v);
     return v;
 }
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
-    for (int o = 32; o > 0; o >>= 1) v = min(v, static_cast<uint32_t>(__shfl_xor(v, o, kWave)));
+    v = min(v, xor_lanes_u32<32>(v));
+    v = min(v, xor_lanes_u32<16>(v));
+    v = min(v, xor_lanes_u32<8>(v));
+    v = min(v, xor_lanes_u32<4>(v));
+    v = min(v, xor_lanes_u32<2>(v));
+    v = min(v, xor_lanes_u32<1>(v));
     return v;
 }
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-    for (int o = 32; o > 0; o >>= 1) v = max(v, static_cast<uint32_t>(__shfl_xor(v, o, kWave)));
+    v = max(v, xor_lanes_u32<32>(v));
+    v = max(v, xor_lanes_u32<16>(v));
+    v = max(v, xor_lanes_u32<8>(v));
+    v = max(v, xor_lanes_u32<4>(v));
+    v = max(v, xor_lanes_u32<2>(v));
+    v = max(v, xor_lanes_u32<1>(v));
     return v;
 }
 __device__ __forceinline__ float wave_max_f32(float v) {
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    v = fmaxf(v, xor_lanes<32>(v));
+    v = fmaxf(v, xor_lanes<16>(v));
+    v = fmaxf(v, xor_lanes<8>(v));
+    v = fmaxf(v, xor_lanes<4>(v));
+    v = fmaxf(v, xor_lanes<2>(v));
+    v = fmaxf(v, xor_lanes<1>(v));
     return v;
 }
 
@@ -74,11 +139,7 @@ __device__ __forceinline__ float block_max_f32(float v, float* scratch) {
 // Exclusive prefix sum of one value per thread, block-wide; returns the total in *total.
 __device__ __forceinline__ uint32_t block_excl_scan_u32(uint32_t v, uint32_t* scratch, uint32_t* total) {
     const uint32_t lane = lane_id(), w = threadIdx.x / kWave, nw = (blockDim.x + kWave - 1) / kWave;
-    uint32_t x = v;
-    for (int o = 1; o < kWave; o <<= 1) {
-        uint32_t y = __shfl_up(x, o, kWave);
-        if (lane >= static_cast<uint32_t>(o)) x += y;
-    }
+    const uint32_t x = wave_incl_scan_u32(v);
     __syncthreads();
     if (lane == kWave - 1) scratch[w] = x;
     __syncthreads();

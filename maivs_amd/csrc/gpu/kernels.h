@@ -74,10 +74,10 @@ __device__ __forceinline__ float dot_cm_f32(const float* __restrict__ row, const
         acc = __builtin_fmaf(q(8 * (t + 3) + l), v.w, acc);
     }
     for (; t < C.T; ++t) acc = __builtin_fmaf(q(8 * t + l), p[t], acc);
-    float s = acc + __shfl_xor(acc, 4, 8);
-    float s2 = __shfl_xor(s, 2, 8);
+    float s = acc + xor_lanes<4>(acc);
+    float s2 = xor_lanes<2>(s);
     float u = s + s2;
-    float r = u + __shfl_xor(u, 1, 8);
+    float r = u + xor_lanes<1>(u);
     const float* tp = row + 8 * C.Tp;
     for (uint32_t i = 0; i < C.tail; ++i) r += q(8 * C.T + i) * tp[i];
     return r;
@@ -111,10 +111,10 @@ __device__ __forceinline__ float dot_cm_u8(const uint8_t* __restrict__ row, cons
             acc = __builtin_fmaf(q(8 * (t + j) + l), static_cast<float>((w[j >> 2] >> (8 * (j & 3))) & 0xFFu), acc);
     }
     for (; t < C.T; ++t) acc = __builtin_fmaf(q(8 * t + l), static_cast<float>(p[t]), acc);
-    float s = acc + __shfl_xor(acc, 4, 8);
-    float s2 = __shfl_xor(s, 2, 8);
+    float s = acc + xor_lanes<4>(acc);
+    float s2 = xor_lanes<2>(s);
     float u = s + s2;
-    float r = u + __shfl_xor(u, 1, 8);
+    float r = u + xor_lanes<1>(u);
     const uint8_t* tp = row + 8 * C.Tp;
     for (uint32_t i = 0; i < C.tail; ++i) r += q(8 * C.T + i) * static_cast<float>(tp[i]);
     return r;
@@ -564,15 +564,21 @@ __device__ __forceinline__ void prep_wave_codes(const DevArena& A, const Work& W
                 }
             }
         }
-#pragma unroll
-        for (uint32_t m = 1; m < kWave; m <<= 1) {
+        auto across = [&](auto mc) {
+            constexpr int m = decltype(mc)::value;
             const bool upper = (lane & m) != 0;
 #pragma unroll
             for (int e = 0; e < EPL; ++e) {
-                const float v = __shfl_xor(x[e], static_cast<int>(m), kWave);
+                const float v = xor_lanes<m>(x[e]);
                 x[e] = upper ? v - x[e] : x[e] + v;
             }
-        }
+        };
+        across(std::integral_constant<int, 1>{});
+        across(std::integral_constant<int, 2>{});
+        across(std::integral_constant<int, 4>{});
+        across(std::integral_constant<int, 8>{});
+        across(std::integral_constant<int, 16>{});
+        across(std::integral_constant<int, 32>{});
 #pragma unroll
         for (int e = 0; e < EPL; ++e) x[e] *= A.fht_scale;
     }
@@ -651,33 +657,36 @@ __device__ __forceinline__ void prep_wave_tables(const DevArena& A, const Work& 
     // lane 1 the rescore base sum(q * csq_min) from 0.0, lane 2 the SQ8 rerank base
     // sum(q * sq_min) from 0.0
     if (lane < 3) {
-        // whole 16-element chunks with the next chunk's LDS reads in flight, then the tail
+        // whole 32-element chunks in two alternating buffers, each chunk's LDS reads in flight
+        // while the one before is added, then the tail
         const uint32_t n = lane == 0 ? npos : lane == 1 ? (sq8 ? d : 0u) : (rsq8 ? d : 0u);
         const float* src = lane == 0 ? mins : lane == 1 ? cqp : rqp;
         const float4* src4 = reinterpret_cast<const float4*>(src);
         float s = lane == 0 ? -0.0f : 0.0f;
-        const uint32_t nfull = n / 16;
-        float4 cur[4], nxt[4];
-        if (nfull > 0) {
+        const uint32_t nfull = n / 32;
+        float4 ba[8], bb[8];
+        auto fetch = [&](float4 (&buf)[8], uint32_t c) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) cur[j] = src4[j];
-        }
-        for (uint32_t c = 0; c < nfull; ++c) {
-            if (c + 1 < nfull) {
+            for (int j = 0; j < 8; ++j) buf[j] = src4[8 * c + j];
+        };
+        auto add = [&](const float4 (&buf)[8]) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) nxt[j] = src4[4 * (c + 1) + j];
+            for (int j = 0; j < 8; ++j) {
+                s += buf[j].x;
+                s += buf[j].y;
+                s += buf[j].z;
+                s += buf[j].w;
             }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                s += cur[j].x;
-                s += cur[j].y;
-                s += cur[j].z;
-                s += cur[j].w;
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) cur[j] = nxt[j];
+        };
+        if (nfull > 0) fetch(ba, 0);
+        for (uint32_t c = 0; c < nfull; c += 2) {
+            if (c + 1 < nfull) fetch(bb, c + 1);
+            add(ba);
+            if (c + 1 >= nfull) break;
+            if (c + 2 < nfull) fetch(ba, c + 2);
+            add(bb);
         }
-        for (uint32_t i = nfull * 16; i < n; ++i) s += src[i];
+        for (uint32_t i = nfull * 32; i < n; ++i) s += src[i];
         if (lane == 0) {
             Wk.bias[qi] = s;
             Wk.delta[qi] = delta;
@@ -888,12 +897,7 @@ __device__ __forceinline__ void route_phase(const DevArena& A, const Work& Wk, c
         const uint32_t lane = tid, per = (nbins + kWave - 1) / kWave, b0 = lane * per, b1 = min(b0 + per, nbins);
         uint32_t loc = 0;
         for (uint32_t i = b0; i < b1; ++i) loc += hist[i];
-        uint32_t x = loc;
-#pragma unroll
-        for (int o = 1; o < kWave; o <<= 1) {
-            const uint32_t y = __shfl_up(x, o, kWave);
-            if (lane >= static_cast<uint32_t>(o)) x += y;
-        }
+        uint32_t x = wave_incl_scan_u32(loc);
         uint32_t cand = kNone, cum = x - loc;
         if (cum < K.want_c && x >= K.want_c) {
             for (uint32_t i = b0; i < b1; ++i) {
@@ -1157,12 +1161,7 @@ __device__ __forceinline__ void seed_phase(const DevArena& A, const Work& Wk, co
             e0 = A.mem_off[c];
             len = A.mem_off[c + 1] - e0;
         }
-        uint32_t x = len;
-#pragma unroll
-        for (int o = 1; o < static_cast<int>(kSeedCells); o <<= 1) {
-            const uint32_t y = __shfl_up(x, o, kWave);
-            if (tid >= static_cast<uint32_t>(o)) x += y;
-        }
+        uint32_t x = wave_incl_scan_u32(len);
         if (tid < ns) {
             misc[kOff + tid + 1] = x;
             misc[kCell + tid] = c;
@@ -1266,12 +1265,7 @@ __device__ __forceinline__ void seed_phase(const DevArena& A, const Work& Wk, co
                 v[k] = h[4 * lane + k];
                 s4 += v[k];
             }
-            uint32_t x = s4;
-#pragma unroll
-            for (int o = 1; o < kWave; o <<= 1) {
-                const uint32_t y = __shfl_up(x, o, kWave);
-                if (lane >= static_cast<uint32_t>(o)) x += y;
-            }
+            uint32_t x = wave_incl_scan_u32(s4);
             uint32_t cum = x - s4;
             if (cum < want && x >= want) {
 #pragma unroll
@@ -1380,12 +1374,7 @@ __device__ __forceinline__ void seed_phase(const DevArena& A, const Work& Wk, co
                 e0 = A.mem_off[c];
                 len = A.mem_off[c + 1] - e0;
             }
-            uint32_t x = len;
-#pragma unroll
-            for (int o = 1; o < static_cast<int>(kFrontRestMax); o <<= 1) {
-                const uint32_t y = __shfl_up(x, o, kWave);
-                if (tid >= static_cast<uint32_t>(o)) x += y;
-            }
+            uint32_t x = wave_incl_scan_u32(len);
             if (tid < nr) {
                 misc[kOff + tid + 1] = x;
                 misc[kCell + tid] = c;
@@ -2351,7 +2340,10 @@ __device__ __forceinline__ void pass_epilogue(const Work& Wk, uint32_t M, uint32
     if (t == 0) *Wk.done = 0;
 }
 
-__global__ void __launch_bounds__(kFinishThreads, 4)
+// NT threads per query: kFinishThreads, or kFinishWideThreads for small batches (one round of
+// rerank gathers for the usual candidate lists instead of several dependent ones).
+template <uint32_t NT>
+__global__ void __launch_bounds__(NT, 1024 / NT)
 finish_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries, uint32_t* __restrict__ out_slots,
               float* __restrict__ out_scores) {
     uint32_t cc = 0;
@@ -2423,18 +2415,21 @@ pq_tree_kernel(DevArena A, Work Wk, KParams K, TreeDev T, const uint32_t* __rest
     if (lane == 0) Wk.tcount[qi] = n;
 }
 
-// The same descent by a whole workgroup per query (block_tree_descent), for small batches: the
-// frontier's code loads and the selections spread over kPqTreeBlock threads instead of one wave.
+// The same descent by a whole workgroup per query (block_tree_descent): the frontier's code loads
+// and the selections spread over kPqTreeBlock threads instead of one wave. The top level's codes
+// are staged in LDS while the query's code is read, when they fit in kTreeTopWords words.
 // LDS: qb[W] u64 | hist[W*64 + 1 (4)] | rbase[cap + 1] | rpre[cap + 2] | knodes[cap] | scratch[32] |
-// hcache[kTreeHCache] u16.
+// hcache[kTreeHCache] u16 | fr[kTreeHCache] | fid[kTreeHCache] | top[top_words] (8-byte aligned).
 constexpr uint32_t kPqTreeBlock = 256;
+constexpr uint32_t kTreeTopWords = 8192;  // 32 KB of top-level codes at most
 
-__host__ __device__ inline uint32_t pq_tree_block_lds_words(uint32_t W, uint32_t cap) {
-    return pq_tree_lds_words(W, cap) + 32;
+__host__ __device__ inline uint32_t pq_tree_block_lds_words(uint32_t W, uint32_t cap, uint32_t top_words) {
+    return ((pq_tree_lds_words(W, cap) + 32 + 2 * kTreeHCache + 1) & ~1u) + top_words;
 }
 
 __global__ void __launch_bounds__(kPqTreeBlock)
-pq_tree_block_kernel(DevArena A, Work Wk, KParams K, TreeDev T, const uint32_t* __restrict__ beams, uint32_t cap) {
+pq_tree_block_kernel(DevArena A, Work Wk, KParams K, TreeDev T, const uint32_t* __restrict__ beams, uint32_t cap,
+                     uint32_t top_words) {
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t qi = blockIdx.x;
     if (qi >= K.nq) return;  // uniform over the workgroup
@@ -2445,10 +2440,19 @@ pq_tree_block_kernel(DevArena A, Work Wk, KParams K, TreeDev T, const uint32_t* 
     uint32_t* knodes = rpre + cap + 2;
     uint32_t* scratch = knodes + cap;
     uint16_t* hcache = reinterpret_cast<uint16_t*>(scratch + 32);
+    uint32_t* fr = scratch + 32 + kTreeHCache / 2;
+    uint32_t* fid = fr + kTreeHCache;
+    uint64_t* top = reinterpret_cast<uint64_t*>(reinterpret_cast<uint32_t*>(smem) +
+                                                pq_tree_block_lds_words(A.W, cap, 0));
     for (uint32_t w = threadIdx.x; w < A.W; w += blockDim.x) qb[w] = Wk.qbits[static_cast<uint64_t>(qi) * A.W + w];
+    if (top_words) {
+        const uint64_t* src = T.lv_codes + static_cast<uint64_t>(T.lv_off[0]) * A.W;
+        for (uint32_t i = threadIdx.x; i < top_words / 2; i += blockDim.x) top[i] = src[i];
+    }
     __syncthreads();
     const uint32_t n = block_tree_descent(T, beams, K.want_c, qb, A.W, hist, rbase, rpre, knodes,
-                                          Wk.tlist + static_cast<uint64_t>(qi) * K.tcap, hcache, kTreeHCache, scratch);
+                                          Wk.tlist + static_cast<uint64_t>(qi) * K.tcap, hcache, kTreeHCache, scratch,
+                                          fr, fid, kTreeHCache, top_words ? top : nullptr);
     if (threadIdx.x == 0) Wk.tcount[qi] = n;
 }
 
@@ -2632,8 +2636,22 @@ __global__ void __launch_bounds__(MODE ? kScanRoundThreads : kScanThreads) pq_sc
     uint32_t* sC = reinterpret_cast<uint32_t*>(stage + kPqStage);  // SPLIT: kSplitCells x bins4
     uint32_t* sN = sC + kSplitCells * nb4;                         // SPLIT: entry count of each rank
     uint32_t* sD = sN + ((K.nprobe + 1 + 3) & ~3u);                // SPLIT: tau, kept, stop, flag per rank
+    // SPLIT: the first kSplitCells ranks' counts of bin tid, and the first entries of rank (wave), in
+    // flight through the setup
+    uint32_t pre_h[kSplitCells];
+    uint64_t pre_e[4];
     if constexpr (SPLIT) {
-        for (uint32_t r = tid; r < nch; r += nt) sN[r] = Wk.pqn[static_cast<uint64_t>(qi) * K.nprobe + r];
+        const uint64_t qr = static_cast<uint64_t>(qi) * K.nprobe;
+        for (uint32_t r = tid; r < nch; r += nt) sN[r] = Wk.pqn[qr + r];
+#pragma unroll
+        for (uint32_t j = 0; j < kSplitCells; ++j)
+            pre_h[j] = j < nch && tid < nbins ? Wk.pqh[(qr + j) * nb4 + tid] : 0u;
+        const uint32_t wv = tid / kWave, room = min(K.pq_room, 4u * kWave);
+#pragma unroll
+        for (uint32_t u = 0; u < 4; ++u) {
+            const uint32_t i = u * kWave + lane;
+            pre_e[u] = wv < nch && i < room ? Wk.pqe[(qr + wv) * K.pq_room + i] : 0ull;
+        }
     }
     const float delta = Wk.delta[qi], bias = Wk.bias[qi];
     // suffix maxima of the reachability bounds (src/index.rs:1466-1489), suffix[nch] = -inf: wave 0,
@@ -2673,11 +2691,7 @@ __global__ void __launch_bounds__(MODE ? kScanRoundThreads : kScanThreads) pq_sc
             for (;;) {
                 const int32_t bi = static_cast<int32_t>(t) - static_cast<int32_t>(lane);
                 const uint32_t hv = bi >= 0 ? h[bi] : 0u;
-                uint32_t incl = hv;
-                for (int o = 1; o < kWave; o <<= 1) {
-                    const uint32_t y = __shfl_up(incl, o, kWave);
-                    if (lane >= static_cast<uint32_t>(o)) incl += y;
-                }
+                uint32_t incl = wave_incl_scan_u32(hv);
                 // the walk stops at the first bin u = t - l whose lower neighbour's count
                 // #(h <= u - 1) falls below the target (bin 0's lower count is 0)
                 const uint64_t stopm = __ballot(bi >= 0 && c - incl < target);
@@ -2782,11 +2796,13 @@ __global__ void __launch_bounds__(MODE ? kScanRoundThreads : kScanThreads) pq_sc
         while (r0 < nch) {
             const uint32_t nr = min(nch - r0, kSplitCells), tau0 = s_tau;
             // C[j][b] = hist[b] + the counts of ranks r0 .. r0 + j, for the bins up to tau0 (the
-            // others no longer count)
-            for (uint32_t b = tid; b <= tau0; b += nt) {
+            // others no longer count); bin b by thread b (nbins <= nt)
+            if (tid <= tau0) {
+                const uint32_t b = tid;
                 uint32_t v[kSplitCells];
 #pragma unroll
-                for (uint32_t j = 0; j < kSplitCells; ++j) v[j] = j < nr ? Wk.pqh[(qr + r0 + j) * nb4 + b] : 0u;
+                for (uint32_t j = 0; j < kSplitCells; ++j)
+                    v[j] = r0 == 0 ? pre_h[j] : j < nr ? Wk.pqh[(qr + r0 + j) * nb4 + b] : 0u;
                 uint32_t acc = hist[b];
 #pragma unroll
                 for (uint32_t j = 0; j < kSplitCells; ++j) {
@@ -2797,12 +2813,35 @@ __global__ void __launch_bounds__(MODE ? kScanRoundThreads : kScanThreads) pq_sc
             __syncthreads();
             // each rank's tau and adaptive decision, one wave per rank
             for (uint32_t j = wv; j < nr; j += nt / kWave) {
+                // tau = min(tau0, the first u with #(h <= u) >= target), by one forward pass: lane l
+                // holds bins [l * bpl, (l + 1) * bpl) up to tau0, an inclusive scan of their sums
+                // finds the lane where the count reaches the target, and that lane walks its bins
                 const uint32_t* cj = sC + j * nb4;
-                uint32_t c = 0;
-                for (uint32_t b = lane; b <= tau0; b += kWave) c += cj[b];
-                c = wave_sum_u32(c);
-                uint32_t t, kept;
-                walk(cj, tau0, c, t, kept);
+                const uint32_t bpl = (tau0 + kWave) / kWave;
+                const uint32_t b0 = min(lane * bpl, tau0 + 1), b1 = min(b0 + bpl, tau0 + 1);
+                uint32_t mine = 0;
+                for (uint32_t b = b0; b < b1; ++b) mine += cj[b];
+                uint32_t incl = wave_incl_scan_u32(mine);
+                const uint32_t c = __shfl(incl, kWave - 1, kWave);
+                uint32_t t = tau0, kept = c;
+                const uint64_t hm = __ballot(incl >= target);
+                if (c >= target) {
+                    const int L = __ffsll(static_cast<long long>(hm)) - 1;
+                    uint32_t tl = 0, kl = 0;
+                    if (lane == static_cast<uint32_t>(L)) {
+                        uint32_t cum = incl - mine;
+                        for (uint32_t b = b0; b < b1; ++b) {
+                            cum += cj[b];
+                            if (cum >= target) {
+                                tl = b;
+                                kl = cum;
+                                break;
+                            }
+                        }
+                    }
+                    t = __shfl(tl, L, kWave);
+                    kept = __shfl(kl, L, kWave);
+                }
                 bool flag = false;
                 const bool stp = adaptive_stop(t, kept, suffix[r0 + j + 1], flag);
                 if (lane == 0) {
@@ -2813,17 +2852,13 @@ __global__ void __launch_bounds__(MODE ? kScanRoundThreads : kScanThreads) pq_sc
                 }
             }
             __syncthreads();
-            // the first rank that stops is the last one scanned
-            uint32_t js = nr - 1, stp = 0;
-            for (uint32_t j = 0; j < nr; ++j) {
-                if (sD[2 * kSplitCells + j]) {
-                    js = j;
-                    stp = 1;
-                    break;
-                }
-            }
+            // the first rank that stops is the last one scanned (every wave finds it by ballot)
+            const uint64_t stopm = __ballot(lane < nr && sD[2 * kSplitCells + lane] != 0);
+            const uint32_t js = stopm ? static_cast<uint32_t>(__ffsll(static_cast<long long>(stopm)) - 1) : nr - 1;
+            const uint32_t stp = stopm ? 1u : 0u;
+            const uint64_t flagm = __ballot(lane <= js && sD[3 * kSplitCells + lane] != 0);
             if (tid == 0) {
-                for (uint32_t j = 0; j <= js; ++j) flagged = flagged || sD[3 * kSplitCells + j] != 0;
+                flagged = flagged || flagm != 0;
                 s_tau = sD[js];
                 s_stop = stp;
             }
@@ -2848,7 +2883,7 @@ __global__ void __launch_bounds__(MODE ? kScanRoundThreads : kScanThreads) pq_sc
 #pragma unroll
                 for (uint32_t u = 0; u < 4; ++u) {
                     const uint32_t i = i0 + u * kWave + lane;
-                    v[u] = i < n_r ? src[i] : 0ull;
+                    v[u] = r == wv && i0 == 0 ? pre_e[u] : i < n_r ? src[i] : 0ull;
                 }
 #pragma unroll
                 for (uint32_t u = 0; u < 4; ++u) {
@@ -2893,11 +2928,7 @@ __global__ void __launch_bounds__(MODE ? kScanRoundThreads : kScanThreads) pq_sc
                         len = A.mem_off[c + 1] - e0;
                     }
                 }
-                uint32_t incl = len;
-                for (int o = 1; o < static_cast<int>(kRoundCells); o <<= 1) {
-                    const uint32_t y = __shfl_up(incl, o, kWave);
-                    if (lane >= static_cast<uint32_t>(o)) incl += y;
-                }
+                uint32_t incl = wave_incl_scan_u32(len);
                 // a prefix of the lanes: have and the running total are both monotone in j
                 const bool fits = have && (j == 0 || incl <= kRoundBudget);
                 const uint32_t nr = static_cast<uint32_t>(__popcll(__ballot(fits)));

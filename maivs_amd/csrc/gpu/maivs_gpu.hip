@@ -366,14 +366,16 @@ int raise_lds_limit(maivs_gpu_ctx* ctx, const void* fn, size_t lds) {
 
 int launch_pq_tree(maivs_gpu_ctx* ctx, const KParams& K, uint32_t cap) {
     if (K.nq <= ctx->pq_tree_block_max_q) {
-        // small batches: a workgroup per query
-        const size_t lds = static_cast<size_t>(pq_tree_block_lds_words(ctx->A.W, cap)) * 4;
+        // a workgroup per query, the top level's codes staged in LDS when they fit
+        const uint32_t top_n = ctx->tree_level_n.empty() ? 0u : ctx->tree_level_n[0];
+        const uint32_t top = top_n * ctx->A.W * 2 <= kTreeTopWords ? top_n * ctx->A.W * 2 : 0u;
+        const size_t lds = static_cast<size_t>(pq_tree_block_lds_words(ctx->A.W, cap, top)) * 4;
         if (lds > kLdsBudget) return fail(ctx, MAIVS_ERR_UNSUPPORTED, "tree descent needs %zu bytes of LDS", lds);
         int rc;
         if (lds > 64 * 1024 && (rc = raise_lds_limit(ctx, reinterpret_cast<const void*>(pq_tree_block_kernel), lds)))
             return rc;
         hipLaunchKernelGGL(pq_tree_block_kernel, dim3(K.nq), dim3(kPqTreeBlock), lds, ctx->stream, ctx->A, ctx->Wk, K,
-                           ctx->tree, ctx->d_beams, cap);
+                           ctx->tree, ctx->d_beams, cap, top);
         HIP_TRY(ctx, hipGetLastError());
         return 0;
     }
@@ -666,8 +668,12 @@ int launch_pad(maivs_gpu_ctx* ctx, uint32_t* d_slots, float* d_scores, uint64_t 
 }
 
 int launch_finish(maivs_gpu_ctx* ctx, const KParams& K, const float* d_q, uint32_t* d_slots, float* d_scores) {
-    hipLaunchKernelGGL(finish_kernel, dim3(K.nq), dim3(kFinishThreads), ctx->lds_finish, ctx->stream, ctx->A, ctx->Wk,
-                       K, d_q, d_slots, d_scores);
+    if (K.nq <= ctx->finish_wide_max_q)
+        hipLaunchKernelGGL(finish_kernel<kFinishWideThreads>, dim3(K.nq), dim3(kFinishWideThreads), ctx->lds_finish,
+                           ctx->stream, ctx->A, ctx->Wk, K, d_q, d_slots, d_scores);
+    else
+        hipLaunchKernelGGL(finish_kernel<kFinishThreads>, dim3(K.nq), dim3(kFinishThreads), ctx->lds_finish,
+                           ctx->stream, ctx->A, ctx->Wk, K, d_q, d_slots, d_scores);
     HIP_TRY(ctx, hipGetLastError());
     return 0;
 }
@@ -1246,6 +1252,8 @@ int maivs_gpu_create(int device, maivs_gpu_ctx** out) {
     if (const char* t = std::getenv("MAIVS_GPU_PQ_TREE_BLOCK")) ctx->pq_tree_block_max_q = static_cast<uint32_t>(std::max(0, std::atoi(t)));
     // the per-query scan in rounds of cells (a 1024-thread workgroup per query) up to this many queries
     if (const char* r = std::getenv("MAIVS_GPU_PQ_ROUNDS")) ctx->pq_rounds_max_q = static_cast<uint32_t>(std::max(0, std::atoi(r)));
+    // the finish with a 1024-thread workgroup per query up to this many queries
+    if (const char* fw = std::getenv("MAIVS_GPU_FINISH_WIDE")) ctx->finish_wide_max_q = static_cast<uint32_t>(std::max(0, std::atoi(fw)));
     // the split per-query scan (a workgroup per probed cell, then the bucket queue replayed) up to this many queries
     if (const char* sp = std::getenv("MAIVS_GPU_PQ_SPLIT")) ctx->pq_split_max_q = static_cast<uint32_t>(std::max(0, std::atoi(sp)));
     // the matrix-core scan's items in cell order, a contiguous chunk per XCD: 1 (default) or 0
@@ -1552,7 +1560,9 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
     // every kernel's dynamic-LDS limit only grows (another context's smaller arena must not lower
     // the limit this one's launches rely on), and a failure is an error
     auto raise = [&](const void* fn, size_t lds) { return raise_lds_limit(ctx, fn, lds); };
-    if ((rc = raise(reinterpret_cast<const void*>(finish_kernel), ctx->lds_finish))) return rc;
+    if ((rc = raise(reinterpret_cast<const void*>(finish_kernel<kFinishThreads>), ctx->lds_finish)) ||
+        (rc = raise(reinterpret_cast<const void*>(finish_kernel<kFinishWideThreads>), ctx->lds_finish)))
+        return rc;
     DISPATCH_EPL(A.P / 64, rc = raise(reinterpret_cast<const void*>(prep_kernel<EPL>), ctx->lds_prep));
     if (rc) return rc;
     DISPATCH_NW(A.W, {

@@ -20,6 +20,7 @@ constexpr uint32_t kRouteThreads = 256;
 constexpr uint32_t kSeedThreads = 256;
 constexpr uint32_t kScanThreads = 256;
 constexpr uint32_t kFinishThreads = 256;
+constexpr uint32_t kFinishWideThreads = 1024;  // the finish of small batches
 constexpr uint32_t kG = 4;               // queries interleaved per cell_scan table pass
 constexpr uint32_t kItemQ = 2 * kG;      // queries per scan work item (two interleaved tables)
 constexpr uint32_t kBucketQ = 32;       // bucket entries per scan work item (one matrix-core query tile)

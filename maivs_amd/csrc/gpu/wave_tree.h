@@ -66,11 +66,7 @@ __device__ uint32_t wave_keep_smallest(uint32_t F, uint32_t keep, uint32_t bits,
     const uint32_t b0 = min(lane * bpl, nb), b1 = min(b0 + bpl, nb);
     uint32_t mine = 0;
     for (uint32_t b = b0; b < b1; ++b) mine += hist[b];
-    uint32_t incl = mine;
-    for (int o = 1; o < kWave; o <<= 1) {
-        const uint32_t y = __shfl_up(incl, o, kWave);
-        if (lane >= static_cast<uint32_t>(o)) incl += y;
-    }
+    uint32_t incl = wave_incl_scan_u32(mine);
     const uint32_t excl = incl - mine;
     const bool here = excl < keep && incl >= keep;
     uint32_t t = 0, below = 0;
@@ -179,11 +175,7 @@ __device__ inline uint32_t tree_descent(const TreeDev& T, const uint32_t* beams,
             const uint32_t k = k0 + lane;
             const uint32_t node = k < nk ? knodes[k] : 0u;
             const uint32_t len = k < nk ? cl[node] : 0u;
-            uint32_t incl = len;
-            for (int o = 1; o < kWave; o <<= 1) {
-                const uint32_t y = __shfl_up(incl, o, kWave);
-                if (lane >= static_cast<uint32_t>(o)) incl += y;
-            }
+            uint32_t incl = wave_incl_scan_u32(len);
             if (k < nk) {
                 rbase[k] = cs[node];
                 rpre[k] = carry + incl - len;
@@ -279,11 +271,14 @@ __device__ uint32_t block_keep_smallest(uint32_t F, uint32_t keep, uint32_t bits
 }
 
 // tree_descent by the whole workgroup (every thread calls it): the same leaves in the same order.
-// LDS as tree_descent's, plus scratch (18 words).
+// LDS as tree_descent's, plus scratch (18 words), fr and fid (fcap words each: the frontier's nodes
+// below the top level, and the leaves' cells, so neither needs a search or a second load), and
+// top: the top level's codes when the caller staged them in LDS (else null).
 __device__ inline uint32_t block_tree_descent(const TreeDev& T, const uint32_t* beams, uint32_t want, const uint64_t* qb,
                                               uint32_t W, uint32_t* hist, uint32_t* rbase, uint32_t* rpre,
                                               uint32_t* knodes, uint32_t* out, uint16_t* hcache, uint32_t hcap,
-                                              uint32_t* scratch) {
+                                              uint32_t* scratch, uint32_t* fr, uint32_t* fid, uint32_t fcap,
+                                              const uint64_t* top) {
     const uint32_t tid = threadIdx.x, nt = blockDim.x, bits = W * 64;
     if (T.n_levels == 0) return 0;
     uint32_t nr = 1;
@@ -294,19 +289,20 @@ __device__ inline uint32_t block_tree_descent(const TreeDev& T, const uint32_t* 
     }
     __syncthreads();
     uint32_t F = T.lv_off[1] - T.lv_off[0];
+    // the node at frontier position p: p itself on the top level, else fr[p] (or the search past fcap)
+    auto node_of = [&](uint32_t li, uint32_t p) {
+        return li == 0 ? p : p < fcap ? fr[p] : frontier_node(rbase, rpre, nr, p);
+    };
     for (uint32_t li = 0; li < T.n_levels; ++li) {
-        const uint64_t* codes = T.lv_codes + static_cast<uint64_t>(T.lv_off[li]) * W;
+        const uint64_t* codes = li == 0 && top ? top : T.lv_codes + static_cast<uint64_t>(T.lv_off[li]) * W;
         const uint32_t keep = min(beams[li], F);
         if (keep == 0) return 0;
         const uint32_t nk = block_keep_smallest(
             F, keep, bits, hist, scratch,
-            [&](uint32_t p) {
-                const uint32_t node = frontier_node(rbase, rpre, nr, p);
-                return hamming_lds(qb, codes + static_cast<uint64_t>(node) * W, W);
-            },
-            [&](uint32_t k, uint32_t p) { knodes[k] = frontier_node(rbase, rpre, nr, p); }, hcache, hcap);
+            [&](uint32_t p) { return hamming_lds(qb, codes + static_cast<uint64_t>(node_of(li, p)) * W, W); },
+            [&](uint32_t k, uint32_t p) { knodes[k] = node_of(li, p); }, hcache, hcap);
         __syncthreads();
-        // children of the kept nodes, in order: the next frontier's ranges
+        // children of the kept nodes, in order: the next frontier's ranges, then its nodes
         const uint32_t* cs = T.lv_cs + T.lv_off[li];
         const uint32_t* cl = T.lv_cl + T.lv_off[li];
         uint32_t carry = 0;
@@ -324,18 +320,27 @@ __device__ inline uint32_t block_tree_descent(const TreeDev& T, const uint32_t* 
         }
         if (tid == 0) rpre[nk] = carry;
         __syncthreads();
+        for (uint32_t k = tid; k < nk; k += nt) {
+            const uint32_t b = rbase[k], p0 = rpre[k], len = rpre[k + 1] - p0;
+            for (uint32_t j = 0; j < len && p0 + j < fcap; ++j) fr[p0 + j] = b + j;
+        }
+        __syncthreads();
         nr = nk;
         F = carry;
     }
     const uint32_t keep = min(want, F);
     if (keep == 0) return 0;
+    const uint32_t ll = T.n_levels;  // the leaves: frontier nodes are leaf indices
+    const bool every = keep >= F;     // kept without a distance pass: fid is not filled
     const uint32_t nout = block_keep_smallest(
         F, keep, bits, hist, scratch,
         [&](uint32_t p) {
-            const uint32_t leaf = frontier_node(rbase, rpre, nr, p);
+            const uint32_t leaf = node_of(ll, p);
+            if (p < fcap) fid[p] = T.leaf_ids[leaf];
             return hamming_lds(qb, T.leaf_codes + static_cast<uint64_t>(leaf) * W, W);
         },
-        [&](uint32_t k, uint32_t p) { out[k] = T.leaf_ids[frontier_node(rbase, rpre, nr, p)]; }, hcache, hcap);
+        [&](uint32_t k, uint32_t p) { out[k] = !every && p < fcap ? fid[p] : T.leaf_ids[node_of(ll, p)]; }, hcache,
+        hcap);
     __syncthreads();
     return nout;
 }
