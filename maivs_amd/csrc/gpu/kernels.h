@@ -27,24 +27,6 @@ __device__ __forceinline__ float acos_f(float x) { return static_cast<float>(aco
 __device__ __forceinline__ float cos_f(float x) { return static_cast<float>(cos(static_cast<double>(x))); }
 __device__ __forceinline__ float exp_f(float x) { return static_cast<float>(exp(static_cast<double>(x))); }
 
-// Sequential f32 sum of n LDS values in index order, starting from `init` (one thread).
-__device__ __forceinline__ float seq_sum_lds(const float* v, uint32_t n, float init) {
-    float s = init;
-    uint32_t i = 0;
-    for (; i + 16 <= n; i += 16) {
-        float4 a = reinterpret_cast<const float4*>(v + i)[0];
-        float4 b = reinterpret_cast<const float4*>(v + i)[1];
-        float4 c = reinterpret_cast<const float4*>(v + i)[2];
-        float4 e = reinterpret_cast<const float4*>(v + i)[3];
-        s += a.x; s += a.y; s += a.z; s += a.w;
-        s += b.x; s += b.y; s += b.z; s += b.w;
-        s += c.x; s += c.y; s += c.z; s += c.w;
-        s += e.x; s += e.y; s += e.z; s += e.w;
-    }
-    for (; i < n; ++i) s += v[i];
-    return s;
-}
-
 // One group of 8 lanes computes one chain-major f32 row's dot with q(j): lane l owns the chain
 // acc_l = fma(q(8t+l), row(8t+l), acc_l) over t ascending; then the hsum order
 // ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)); then the tail sequentially (src/index.rs:136-152).
@@ -602,6 +584,38 @@ __device__ __forceinline__ void prep_wave_codes(const DevArena& A, const Work& W
     (void)mins;
 }
 
+// s + src[0] + ... + src[n - 1] added in index order by one lane, from LDS (16-byte aligned): 32
+// floats at a time in two alternating buffers, each chunk's reads in flight while the one before
+// is added.
+__device__ __forceinline__ float seq_sum_lds(const float* src, uint32_t n, float s) {
+    const float4* src4 = reinterpret_cast<const float4*>(src);
+    const uint32_t nfull = n / 32;
+    float4 ba[8], bb[8];
+    auto fetch = [&](float4 (&buf)[8], uint32_t c) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) buf[j] = src4[8 * c + j];
+    };
+    auto add = [&](const float4 (&buf)[8]) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            s += buf[j].x;
+            s += buf[j].y;
+            s += buf[j].z;
+            s += buf[j].w;
+        }
+    };
+    if (nfull > 0) fetch(ba, 0);
+    for (uint32_t c = 0; c < nfull; c += 2) {
+        if (c + 1 < nfull) fetch(bb, c + 1);
+        add(ba);
+        if (c + 1 >= nfull) break;
+        if (c + 2 < nfull) fetch(ba, c + 2);
+        add(bb);
+    }
+    for (uint32_t i = nfull * 32; i < n; ++i) s += src[i];
+    return s;
+}
+
 // The FastScan table and the sequential sums of one query, by one wave, from prep_wave_codes'
 // LDS region (src/quantize.rs:279-313; src/index.rs:1326-1330,1934-1942).
 __device__ __forceinline__ void prep_wave_tables(const DevArena& A, const Work& Wk, uint32_t qi, uint32_t lane,
@@ -657,36 +671,9 @@ __device__ __forceinline__ void prep_wave_tables(const DevArena& A, const Work& 
     // lane 1 the rescore base sum(q * csq_min) from 0.0, lane 2 the SQ8 rerank base
     // sum(q * sq_min) from 0.0
     if (lane < 3) {
-        // whole 32-element chunks in two alternating buffers, each chunk's LDS reads in flight
-        // while the one before is added, then the tail
         const uint32_t n = lane == 0 ? npos : lane == 1 ? (sq8 ? d : 0u) : (rsq8 ? d : 0u);
         const float* src = lane == 0 ? mins : lane == 1 ? cqp : rqp;
-        const float4* src4 = reinterpret_cast<const float4*>(src);
-        float s = lane == 0 ? -0.0f : 0.0f;
-        const uint32_t nfull = n / 32;
-        float4 ba[8], bb[8];
-        auto fetch = [&](float4 (&buf)[8], uint32_t c) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) buf[j] = src4[8 * c + j];
-        };
-        auto add = [&](const float4 (&buf)[8]) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                s += buf[j].x;
-                s += buf[j].y;
-                s += buf[j].z;
-                s += buf[j].w;
-            }
-        };
-        if (nfull > 0) fetch(ba, 0);
-        for (uint32_t c = 0; c < nfull; c += 2) {
-            if (c + 1 < nfull) fetch(bb, c + 1);
-            add(ba);
-            if (c + 1 >= nfull) break;
-            if (c + 2 < nfull) fetch(ba, c + 2);
-            add(bb);
-        }
-        for (uint32_t i = nfull * 32; i < n; ++i) s += src[i];
+        const float s = seq_sum_lds(src, n, lane == 0 ? -0.0f : 0.0f);
         if (lane == 0) {
             Wk.bias[qi] = s;
             Wk.delta[qi] = delta;
@@ -2454,6 +2441,83 @@ pq_tree_block_kernel(DevArena A, Work Wk, KParams K, TreeDev T, const uint32_t* 
                                           Wk.tlist + static_cast<uint64_t>(qi) * K.tcap, hcache, kTreeHCache, scratch,
                                           fr, fid, kTreeHCache, top_words ? top : nullptr);
     if (threadIdx.x == 0) Wk.tcount[qi] = n;
+}
+
+// LDS of pq_front_kernel's routing workgroup after its prep region (u32 words from there): the
+// tree descent's regions as pq_tree_block_kernel has them (fr, fid and top 16-byte aligned).
+struct PqFrontLds {
+    uint32_t hist, rbase, rpre, knodes, scratch, hcache, fr, fid, top, end;
+};
+__host__ __device__ inline PqFrontLds pq_front_layout(uint32_t W, uint32_t cap, uint32_t top_words) {
+    PqFrontLds L;
+    L.hist = 0;
+    L.rbase = ((W * 64 + 1) + 3) & ~3u;
+    L.rpre = L.rbase + cap + 1;
+    L.knodes = L.rpre + cap + 2;
+    L.scratch = L.knodes + cap;
+    L.hcache = L.scratch + 32;
+    L.fr = (L.hcache + kTreeHCache / 2 + 3) & ~3u;
+    L.fid = L.fr + kTreeHCache;
+    L.top = L.fid + kTreeHCache;
+    L.end = L.top + top_words;
+    return L;
+}
+
+// The per-query path's prep, tree descent and route in one launch for small batches (codes over
+// the whole padded dimension): two workgroups per query run side by side. Workgroup qi (qi < nq)
+// computes the query's rotation and code (wave 0, prep_wave_codes) while wave 1 adds up the
+// rescore base sum(q * csq_min) in index order (prep_wave_tables' order) and the other waves
+// stage the tree's top level in LDS; then it descends the centroid tree (block_tree_descent) and
+// routes the query (route_phase). Workgroup nq + qi computes the rotation again and the FastScan
+// table and sums (prep_wave) for the scan, so the table's sequential sums are off the routing
+// path. Both write the same values to qbits, cqs and cqbase. The per-call counters are clear
+// beforehand (the last pass's epilogue, or a reset launch).
+// LDS: codes[16] u64 | x[P] | mins[npos4] | cqp[d4] | rqp[d4] | pq_front_layout; route_phase's
+// layout from offset 0 once the descent is done.
+template <int NW>
+__global__ void __launch_bounds__(kPqTreeBlock)
+pq_front_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries, TreeDev T,
+                const uint32_t* __restrict__ beams, uint32_t cap, uint32_t top_words) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const uint32_t tid = threadIdx.x, nt = blockDim.x, lane = lane_id(), wv = tid / kWave;
+    uint64_t* qw = reinterpret_cast<uint64_t*>(smem);
+    float* xs = reinterpret_cast<float*>(qw + 16);
+    if (blockIdx.x >= K.nq) {
+        const uint32_t qi = blockIdx.x - K.nq;
+        if (qi < K.nq && wv == 0) prep_wave<NW>(A, Wk, queries, qi, lane, xs, qw);
+        return;
+    }
+    const uint32_t qi = blockIdx.x;
+    const uint32_t prep_words = 32 + A.P + ((A.npos + 3) & ~3u) + 2 * ((A.d + 3) & ~3u);
+    uint32_t* tr = reinterpret_cast<uint32_t*>(smem) + prep_words;
+    const PqFrontLds L = pq_front_layout(NW, cap, top_words);
+    uint64_t* top = reinterpret_cast<uint64_t*>(tr + L.top);
+    if (wv == 0) {
+        prep_wave_codes<NW>(A, Wk, queries, qi, lane, xs, qw);
+    } else if (wv == 1) {
+        float* prod = reinterpret_cast<float*>(tr + L.fr);  // free until the descent
+        float base = 0.0f;
+        if (A.cent_sq8 != nullptr) {
+            const float* q = queries + static_cast<uint64_t>(qi) * A.d;
+            for (uint32_t i = lane; i < A.d; i += kWave) prod[i] = q[i] * A.csq_min[i];
+            wave_sync();
+            base = seq_sum_lds(prod, A.d, 0.0f);
+        }
+        if (lane == 0) Wk.cqbase[qi] = base;
+    } else if (K.tree_list && top_words) {
+        const uint64_t* src = T.lv_codes + static_cast<uint64_t>(T.lv_off[0]) * NW;
+        for (uint32_t i = tid - 2 * kWave; i < top_words / 2; i += nt - 2 * kWave) top[i] = src[i];
+    }
+    __syncthreads();
+    if (K.tree_list) {
+        const uint32_t n = block_tree_descent(T, beams, K.want_c, qw, NW, tr + L.hist, tr + L.rbase, tr + L.rpre,
+                                              tr + L.knodes, Wk.tlist + static_cast<uint64_t>(qi) * K.tcap,
+                                              reinterpret_cast<uint16_t*>(tr + L.hcache), kTreeHCache, tr + L.scratch,
+                                              tr + L.fr, tr + L.fid, kTreeHCache, top_words ? top : nullptr);
+        if (tid == 0) Wk.tcount[qi] = n;
+        __syncthreads();
+    }
+    route_phase<NW>(A, Wk, K, qi);
 }
 
 // want-th smallest (1-based) of the n u32 values get(i), block-wide, four 8-bit radix passes.

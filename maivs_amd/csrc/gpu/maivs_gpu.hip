@@ -391,6 +391,32 @@ int launch_pq_tree(maivs_gpu_ctx* ctx, const KParams& K, uint32_t cap) {
     return 0;
 }
 
+// The per-query path's prep, tree descent and route in one launch (pq_front_kernel), two
+// workgroups per query; the counters must be clear.
+int launch_pq_front(maivs_gpu_ctx* ctx, const KParams& K, const float* d_q, uint32_t cap) {
+    const DevArena& A = ctx->A;
+    uint32_t top = 0;
+    if (K.tree_list) {
+        const uint32_t top_n = ctx->tree_level_n.empty() ? 0u : ctx->tree_level_n[0];
+        top = top_n * A.W * 2 <= kTreeTopWords ? top_n * A.W * 2 : 0u;
+    }
+    const PqFrontLds L = pq_front_layout(A.W, cap, top);
+    const size_t lds = std::max(prep1_lds(A) + static_cast<size_t>(L.end) * 4, route_lds(A, K.sort_cap, K.nprobe));
+    if (lds > kLdsBudget) return fail(ctx, MAIVS_ERR_UNSUPPORTED, "the fused route needs %zu bytes of LDS", lds);
+    int rc = 0;
+    auto go = [&](const void* fn, auto kernel) -> int {
+        int r;
+        if (lds > 64 * 1024 && (r = raise_lds_limit(ctx, fn, lds))) return r;
+        hipLaunchKernelGGL(kernel, dim3(2 * K.nq), dim3(kPqTreeBlock), lds, ctx->stream, A, ctx->Wk, K, d_q, ctx->tree,
+                           ctx->d_beams, cap, top);
+        return 0;
+    };
+    DISPATCH_NW(A.W, rc = go(reinterpret_cast<const void*>(pq_front_kernel<NW>), pq_front_kernel<NW>));
+    if (rc) return rc;
+    HIP_TRY(ctx, hipGetLastError());
+    return 0;
+}
+
 KParams make_params(maivs_gpu_ctx* ctx, uint32_t nq, const maivs_search_params* p) {
     const DevArena& A = ctx->A;
     KParams K{};
@@ -1090,12 +1116,23 @@ int run_search_pq(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs
     Work& W = ctx->Wk;
     // timed only when the caller asks for measurements
     if (st) HIP_TRY(ctx, hipEventRecord(ctx->ev[0], ctx->stream));
-    ctx->counters_clean = false;  // cleared here by the prep, and again by the finish's epilogue
-    if ((rc = launch_prep(ctx, K, d_q, kPrepReset))) return rc;
+    // small batches with codes over the whole padded dimension: prep, descent and route in one
+    // launch (the counters cleared beforehand only when the last pass left them set)
+    const bool fused = nq <= ctx->pq_front_max_q && A.W * 64 == A.P;
+    if (fused) {
+        if (!ctx->counters_clean && (rc = launch_reset(ctx, nq))) return rc;
+    } else if ((rc = launch_prep(ctx, K, d_q, kPrepReset))) {
+        return rc;
+    }
+    ctx->counters_clean = false;  // the finish's epilogue clears them again
     for (;;) {
-        if (tree && (rc = launch_pq_tree(ctx, K, cap))) return rc;
-        if ((rc = launch_route(ctx, K)) || (rc = launch_pq_scan(ctx, K)) || (rc = launch_finish(ctx, K, d_q, d_slots, d_scores)))
-            return rc;
+        if (fused) {
+            if ((rc = launch_pq_front(ctx, K, d_q, cap))) return rc;
+        } else {
+            if (tree && (rc = launch_pq_tree(ctx, K, cap))) return rc;
+            if ((rc = launch_route(ctx, K))) return rc;
+        }
+        if ((rc = launch_pq_scan(ctx, K)) || (rc = launch_finish(ctx, K, d_q, d_slots, d_scores))) return rc;
         Ctl ctl{};
         if ((rc = read_ctl(ctx, &ctl))) return rc;
         if (ctl.err_shortlist && K.sort_cap < ctx->max_sort_cap_route) {
@@ -1252,6 +1289,8 @@ int maivs_gpu_create(int device, maivs_gpu_ctx** out) {
     if (const char* t = std::getenv("MAIVS_GPU_PQ_TREE_BLOCK")) ctx->pq_tree_block_max_q = static_cast<uint32_t>(std::max(0, std::atoi(t)));
     // the per-query scan in rounds of cells (a 1024-thread workgroup per query) up to this many queries
     if (const char* r = std::getenv("MAIVS_GPU_PQ_ROUNDS")) ctx->pq_rounds_max_q = static_cast<uint32_t>(std::max(0, std::atoi(r)));
+    // the per-query path's prep, tree descent and route in one launch up to this many queries
+    if (const char* pf = std::getenv("MAIVS_GPU_PQ_FRONT")) ctx->pq_front_max_q = static_cast<uint32_t>(std::max(0, std::atoi(pf)));
     // the finish with a 1024-thread workgroup per query up to this many queries
     if (const char* fw = std::getenv("MAIVS_GPU_FINISH_WIDE")) ctx->finish_wide_max_q = static_cast<uint32_t>(std::max(0, std::atoi(fw)));
     // the split per-query scan (a workgroup per probed cell, then the bucket queue replayed) up to this many queries

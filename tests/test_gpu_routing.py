@@ -70,16 +70,23 @@ def test_batched_route_mode_1_matches_oracle(ctx, quality50k, tree40k, mix50k, u
         ix.set_rerank_factor(32)
 
 
+@pytest.mark.parametrize("fused", ["0", "1000000"])
 @pytest.mark.parametrize("nprobe", [8, 64])
-def test_per_query_every_live_cell_matches_oracle(ctx, quality50k, memory50k, mix50k, nprobe):
+def test_per_query_every_live_cell_matches_oracle(monkeypatch, quality50k, memory50k, mix50k, nprobe, fused):
+    """Separate prep / route launches and the fused prep + route (MAIVS_GPU_PQ_FRONT)."""
     _, queries, _ = mix50k
-    for ix in (quality50k, memory50k):
-        ctx.upload(ix._arena_desc())
-        p = _params(ix, 10, nprobe)
-        q = queries[:200]
-        slots, scores = ctx.search_queries(q, p)
-        oslots, oscores = oracle.search_one(ix._arena_desc(), q, p, nthreads=8)
-        _same(slots, scores, oslots, oscores)
+    monkeypatch.setenv("MAIVS_GPU_PQ_FRONT", fused)
+    c = capi.Context(0)
+    try:
+        for ix in (quality50k, memory50k):
+            c.upload(ix._arena_desc())
+            p = _params(ix, 10, nprobe)
+            for q in (queries[:200], queries[200:201]):
+                slots, scores = c.search_queries(q, p)
+                oslots, oscores = oracle.search_one(ix._arena_desc(), q, p, nthreads=8)
+                _same(slots, scores, oslots, oscores)
+    finally:
+        c.close()
 
 
 def test_noalloc_tree_route_matches_device_entry(tree40k, mix50k):
