@@ -53,6 +53,7 @@ struct maivs_gpu_ctx {
     uint32_t pq_split_max_q = 64;            // the split per-query scan up to this many queries
     uint32_t finish_wide_max_q = 64;         // the finish with kFinishWideThreads threads up to this many queries
     uint32_t pq_front_max_q = 64;            // the per-query path's fused prep + tree + route up to this many queries
+    uint32_t pq_finish_split_max_q = 64;     // the per-query path's rerank spread over workgroups up to this many queries
     Ctl* h_ctl = nullptr;  // pinned host copy of the control block (read after each pass)
     hipEvent_t ev[8] = {};
     // last call, for maivs_gpu_last_candidates / maivs_gpu_last_counters

@@ -124,6 +124,17 @@ __device__ __forceinline__ uint32_t block_min_u32(uint32_t v, uint32_t* scratch)
     __syncthreads();
     return s;
 }
+__device__ __forceinline__ uint32_t block_max_u32(uint32_t v, uint32_t* scratch) {
+    v = wave_max_u32(v);
+    const uint32_t w = threadIdx.x / kWave, nw = (blockDim.x + kWave - 1) / kWave;
+    __syncthreads();
+    if (lane_id() == 0) scratch[w] = v;
+    __syncthreads();
+    uint32_t s = 0;
+    for (uint32_t i = 0; i < nw; ++i) s = max(s, scratch[i]);
+    __syncthreads();
+    return s;
+}
 __device__ __forceinline__ float block_max_f32(float v, float* scratch) {
     v = wave_max_f32(v);
     const uint32_t w = threadIdx.x / kWave, nw = (blockDim.x + kWave - 1) / kWave;

@@ -2139,6 +2139,44 @@ __device__ __forceinline__ uint32_t wave_select_kth(const uint32_t (&v)[KPL], ui
     return prefix;
 }
 
+// The k best of n unique keys kk (ascending key: descending score, then ascending slot) into query
+// qi's output row, padded with kNone / -inf. Block-wide; a list longer than the block is sorted
+// in place (kk has room for n rounded up to a power of two).
+__device__ __forceinline__ void write_topk(uint64_t* kk, uint32_t n, const KParams& K, uint32_t qi,
+                                           uint32_t* __restrict__ out_slots, float* __restrict__ out_scores) {
+    const uint32_t tid = threadIdx.x, nt = blockDim.x;
+    const uint32_t kout = min(K.k, n);
+    if (n <= nt) {
+        // the rank of each (unique) key among the n places it directly in the output
+        if (tid < n) {
+            const uint64_t mine = kk[tid];
+            uint32_t r = 0;
+#pragma unroll 8
+            for (uint32_t j = 0; j < n; ++j) r += kk[j] < mine;
+            if (r < kout) {
+                out_slots[static_cast<uint64_t>(qi) * K.k + r] = static_cast<uint32_t>(mine);
+                out_scores[static_cast<uint64_t>(qi) * K.k + r] = key_score(mine);
+            }
+        }
+        for (uint32_t i = kout + tid; i < K.k; i += nt) {
+            out_slots[static_cast<uint64_t>(qi) * K.k + i] = kNone;
+            out_scores[static_cast<uint64_t>(qi) * K.k + i] = -INFINITY;
+        }
+    } else {
+        // an LDS list has n <= kFinishLdsCap (a power of two), so n2 fits; longer lists sort in
+        // the global key buffer
+        uint32_t n2 = 1;
+        while (n2 < n) n2 <<= 1;
+        for (uint32_t i = n + tid; i < n2; i += nt) kk[i] = kKeyMax;
+        bitonic_sort_u64(kk, n2);
+        for (uint32_t i = tid; i < K.k; i += nt) {
+            const bool ok = i < kout;
+            out_slots[static_cast<uint64_t>(qi) * K.k + i] = ok ? static_cast<uint32_t>(kk[i]) : kNone;
+            out_scores[static_cast<uint64_t>(qi) * K.k + i] = ok ? key_score(kk[i]) : -INFINITY;
+        }
+    }
+}
+
 // Exact tie-inclusive cut at k*rerank_factor over the seed and scan candidates
 // (src/index.rs:2281-2293), exact rerank (rerank_exact, :1309-1378), top-k by (score desc, slot asc).
 // Up to kFinishLdsCap candidates are staged in LDS once; the cut G is then a one-wave radix
@@ -2255,36 +2293,7 @@ __device__ __forceinline__ uint32_t finish_phase(const DevArena& A, const Work& 
             }
         }
         __syncthreads();
-        const uint32_t kout = min(K.k, n);
-        if (n <= nt) {
-            // the rank of each (unique) key among the n places it directly in the output
-            if (tid < n) {
-                const uint64_t mine = kk[tid];
-                uint32_t r = 0;
-#pragma unroll 8
-                for (uint32_t j = 0; j < n; ++j) r += kk[j] < mine;
-                if (r < kout) {
-                    out_slots[static_cast<uint64_t>(qi) * K.k + r] = static_cast<uint32_t>(mine);
-                    out_scores[static_cast<uint64_t>(qi) * K.k + r] = key_score(mine);
-                }
-            }
-            for (uint32_t i = kout + tid; i < K.k; i += nt) {
-                out_slots[static_cast<uint64_t>(qi) * K.k + i] = kNone;
-                out_scores[static_cast<uint64_t>(qi) * K.k + i] = -INFINITY;
-            }
-        } else {
-            // an LDS list has n <= kFinishLdsCap (a power of two), so n2 fits; longer lists sort in
-            // the global key buffer
-            uint32_t n2 = 1;
-            while (n2 < n) n2 <<= 1;
-            for (uint32_t i = n + tid; i < n2; i += nt) kk[i] = kKeyMax;
-            bitonic_sort_u64(kk, n2);
-            for (uint32_t i = tid; i < K.k; i += nt) {
-                const bool ok = i < kout;
-                out_slots[static_cast<uint64_t>(qi) * K.k + i] = ok ? static_cast<uint32_t>(kk[i]) : kNone;
-                out_scores[static_cast<uint64_t>(qi) * K.k + i] = ok ? key_score(kk[i]) : -INFINITY;
-            }
-        }
+        write_topk(kk, n, K, qi, out_slots, out_scores);
         return n;
     };
     const uint32_t n = total <= kFinishLdsCap ? tail(keys) : tail(Wk.keys + static_cast<uint64_t>(qi) * K.key_cap);
@@ -2335,6 +2344,74 @@ finish_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries,
               float* __restrict__ out_scores) {
     uint32_t cc = 0;
     if (blockIdx.x < K.nq) cc = finish_phase(A, Wk, K, queries, out_slots, out_scores, blockIdx.x);
+    pass_epilogue(Wk, A.M, K.nq, cc > K.cand_cap ? cc : 0u);
+}
+
+// The per-query path's finish for small batches whose candidate lists the scan already cut to the
+// target (the FastScan branch): every candidate is kept (finish_phase's cut keeps them all), so
+// the exact rerank is spread over workgroups of kRerankRows rows, one per CU, and pq_topk_kernel
+// orders each query's keys. Workgroup (g, qi) reranks candidates [g * kRerankRows, ...) of query
+// qi, 8 lanes per row with the finish's dots, into Wk.keys. LDS: qs[d4].
+constexpr uint32_t kRerankRows = 8;
+
+__global__ void __launch_bounds__(kRerankRows * 8)
+pq_rerank_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries) {
+    extern __shared__ __align__(16) float qsm[];
+    const uint32_t g = blockIdx.x, qi = blockIdx.y;
+    if (qi >= K.nq) return;
+    const uint32_t n = min(Wk.cand_cnt[qi], K.cand_cap), i0 = g * kRerankRows;
+    if (i0 >= n) return;  // uniform over the workgroup
+    const uint32_t tid = threadIdx.x, l = tid & 7, i = i0 + (tid >> 3);
+    const bool sq8 = A.rerank_mode == MAIVS_RERANK_SQ8;
+    const uint32_t slot = Wk.cand[static_cast<uint64_t>(qi) * K.cand_cap + (i < n ? i : i0)].y;
+    const float* q = queries + static_cast<uint64_t>(qi) * A.d;
+    for (uint32_t j = tid; j < A.d; j += blockDim.x) qsm[j] = sq8 ? q[j] * A.sq_step[j] : q[j];
+    __syncthreads();
+    auto qf = [&](uint32_t j) { return qsm[j]; };
+    float sc;
+    if (sq8)
+        sc = Wk.rbase[qi] + dot_cm_u8(A.sq8 + static_cast<uint64_t>(slot) * A.cu.stride, A.cu, l, qf);
+    else
+        sc = dot_cm_f32(A.vecs + static_cast<uint64_t>(slot) * A.cf.stride, A.cf, l, qf);
+    if (i < n && l == 0) Wk.keys[static_cast<uint64_t>(qi) * K.key_cap + i] = desc_score_key(sc, slot);
+}
+
+// The end of that finish: one workgroup per query orders its reranked keys into the output
+// (write_topk), records the list, cut and count as finish_phase does (every candidate kept: the
+// cut is the largest d when the list reaches the target, else maxk), then the pass epilogue.
+// LDS: keys[kFinishLdsCap] u64 | scratch[32].
+__global__ void __launch_bounds__(kFinishThreads)
+pq_topk_kernel(DevArena A, Work Wk, KParams K, uint32_t* __restrict__ out_slots, float* __restrict__ out_scores) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    uint64_t* lk = reinterpret_cast<uint64_t*>(smem);
+    uint32_t* scratch = reinterpret_cast<uint32_t*>(lk + kFinishLdsCap);
+    uint32_t cc = 0;
+    if (blockIdx.x < K.nq) {
+        const uint32_t qi = blockIdx.x, tid = threadIdx.x, nt = blockDim.x;
+        cc = Wk.cand_cnt[qi];
+        const uint32_t n = min(cc, K.cand_cap);
+        if (tid == 0) Wk.cand_n[qi] = cc;
+        const uint2* cand = Wk.cand + static_cast<uint64_t>(qi) * K.cand_cap;
+        uint2* fin = Wk.fin + static_cast<uint64_t>(qi) * K.fin_cap;
+        uint64_t* gk = Wk.keys + static_cast<uint64_t>(qi) * K.key_cap;
+        const bool staged = n <= kFinishLdsCap;
+        uint32_t dmax = 0;
+        for (uint32_t i = tid; i < n; i += nt) {
+            const uint2 e = cand[i];
+            fin[i] = e;
+            dmax = max(dmax, e.x);
+            if (staged) lk[i] = gk[i];
+        }
+        dmax = block_max_u32(dmax, scratch);  // ends with a barrier: the staged keys are visible
+        if (staged)
+            write_topk(lk, n, K, qi, out_slots, out_scores);
+        else
+            write_topk(gk, n, K, qi, out_slots, out_scores);
+        if (tid == 0) {
+            Wk.cut[qi] = n >= K.target ? dmax : A.maxk;
+            Wk.ncand[qi] = n;
+        }
+    }
     pass_epilogue(Wk, A.M, K.nq, cc > K.cand_cap ? cc : 0u);
 }
 

@@ -704,6 +704,20 @@ int launch_finish(maivs_gpu_ctx* ctx, const KParams& K, const float* d_q, uint32
     return 0;
 }
 
+// The per-query path's finish: for small batches whose candidate lists the scan cut to the target
+// (the FastScan branch), the rerank over workgroups of kRerankRows rows and then the top k
+// (pq_rerank_kernel, pq_topk_kernel); else finish_kernel.
+int launch_pq_finish(maivs_gpu_ctx* ctx, const KParams& K, const float* d_q, uint32_t* d_slots, float* d_scores) {
+    if (K.nq > ctx->pq_finish_split_max_q || K.pq_ham) return launch_finish(ctx, K, d_q, d_slots, d_scores);
+    const uint32_t groups = (K.target + kRerankRows - 1) / kRerankRows;
+    hipLaunchKernelGGL(pq_rerank_kernel, dim3(groups, K.nq), dim3(kRerankRows * 8), ((ctx->A.d + 3) & ~3u) * 4,
+                       ctx->stream, ctx->A, ctx->Wk, K, d_q);
+    hipLaunchKernelGGL(pq_topk_kernel, dim3(K.nq), dim3(kFinishThreads), kFinishLdsCap * 8 + 32 * 4, ctx->stream,
+                       ctx->A, ctx->Wk, K, d_slots, d_scores);
+    HIP_TRY(ctx, hipGetLastError());
+    return 0;
+}
+
 // Fetch one query's probe list and scores (host check helpers).
 int fetch_probe_list(maivs_gpu_ctx* ctx, uint32_t qi, uint32_t nprobe, std::vector<float>& cs,
                      std::vector<uint32_t>& ch) {
@@ -1132,7 +1146,7 @@ int run_search_pq(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs
             if (tree && (rc = launch_pq_tree(ctx, K, cap))) return rc;
             if ((rc = launch_route(ctx, K))) return rc;
         }
-        if ((rc = launch_pq_scan(ctx, K)) || (rc = launch_finish(ctx, K, d_q, d_slots, d_scores))) return rc;
+        if ((rc = launch_pq_scan(ctx, K)) || (rc = launch_pq_finish(ctx, K, d_q, d_slots, d_scores))) return rc;
         Ctl ctl{};
         if ((rc = read_ctl(ctx, &ctl))) return rc;
         if (ctl.err_shortlist && K.sort_cap < ctx->max_sort_cap_route) {
@@ -1205,7 +1219,7 @@ int run_search_pq(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs
             if (!rerun) break;
             S.reruns++;
             if ((rc = launch_reset(ctx, nq)) || (rc = launch_pq_scan(ctx, K)) ||
-                (rc = launch_finish(ctx, K, d_q, d_slots, d_scores)) || (rc = read_ctl(ctx, &ctl)))
+                (rc = launch_pq_finish(ctx, K, d_q, d_slots, d_scores)) || (rc = read_ctl(ctx, &ctl)))
                 return rc;
             ctl.nflag_route = 0;  // decided above; nucleus flags are raised only by the route
         }
@@ -1291,6 +1305,8 @@ int maivs_gpu_create(int device, maivs_gpu_ctx** out) {
     if (const char* r = std::getenv("MAIVS_GPU_PQ_ROUNDS")) ctx->pq_rounds_max_q = static_cast<uint32_t>(std::max(0, std::atoi(r)));
     // the per-query path's prep, tree descent and route in one launch up to this many queries
     if (const char* pf = std::getenv("MAIVS_GPU_PQ_FRONT")) ctx->pq_front_max_q = static_cast<uint32_t>(std::max(0, std::atoi(pf)));
+    // the per-query path's rerank over workgroups of 8 rows, then the top k, up to this many queries
+    if (const char* fs = std::getenv("MAIVS_GPU_PQ_FINISH_SPLIT")) ctx->pq_finish_split_max_q = static_cast<uint32_t>(std::max(0, std::atoi(fs)));
     // the finish with a 1024-thread workgroup per query up to this many queries
     if (const char* fw = std::getenv("MAIVS_GPU_FINISH_WIDE")) ctx->finish_wide_max_q = static_cast<uint32_t>(std::max(0, std::atoi(fw)));
     // the split per-query scan (a workgroup per probed cell, then the bucket queue replayed) up to this many queries

@@ -5,8 +5,8 @@ own workgroup, then the bucket queue replayed from the cells' histograms; the de
 of up to 64 queries and 256 probes). Each form is forced for every batch size here. Slots and
 score bits identical, query by query, for FastScan and the Hamming branch, adaptive stops inside a
 round, multi-home vectors, the tag filter, nucleus probe lists and candidate buffers that overflow
-and grow; the finish's two workgroup sizes and the fused or separate prep, descent and route
-likewise.
+and grow; the finish's two workgroup sizes, the rerank spread over workgroups and the fused or
+separate prep, descent and route likewise.
 """
 import numpy as np
 import pytest
@@ -18,10 +18,12 @@ from .test_oracle_pq import churned_uncompacted, tight_uncompacted, tree40k  # n
 
 pytestmark = pytest.mark.gpu
 
-# (MAIVS_GPU_PQ_ROUNDS, MAIVS_GPU_PQ_SPLIT, MAIVS_GPU_FINISH_WIDE, MAIVS_GPU_PQ_FRONT): the largest
-# batch each form serves; the split form also runs the 1024-thread finish and the fused prep +
-# descent + route for every batch size, the other two the separate launches
-MODES = [("0", "0", "0", "0"), ("1000000", "0", "0", "0"), ("0", "1000000", "1000000", "1000000")]
+# (MAIVS_GPU_PQ_ROUNDS, MAIVS_GPU_PQ_SPLIT, MAIVS_GPU_FINISH_WIDE, MAIVS_GPU_PQ_FRONT,
+# MAIVS_GPU_PQ_FINISH_SPLIT): the largest batch each form serves; the split form also runs the
+# fused prep + descent + route and the rerank over workgroups for every batch size, the rounds form
+# the 1024-thread finish, the cell-by-cell form the separate launches and the 256-thread finish
+MODES = [("0", "0", "0", "0", "0"), ("1000000", "0", "1000000", "0", "0"),
+         ("0", "1000000", "0", "1000000", "1000000")]
 
 
 def _params(ix, k, nprobe, tc=1.0, beta=8.0):
@@ -34,6 +36,7 @@ def ctx(request, monkeypatch):
     monkeypatch.setenv("MAIVS_GPU_PQ_SPLIT", request.param[1])
     monkeypatch.setenv("MAIVS_GPU_FINISH_WIDE", request.param[2])
     monkeypatch.setenv("MAIVS_GPU_PQ_FRONT", request.param[3])
+    monkeypatch.setenv("MAIVS_GPU_PQ_FINISH_SPLIT", request.param[4])
     c = capi.Context(0)
     yield c
     c.close()
