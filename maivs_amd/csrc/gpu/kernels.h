@@ -1522,6 +1522,110 @@ hamming_kernel(DevArena A, Work Wk, uint32_t nq) {
     }
 }
 
+// The same rows on the matrix cores: h = popc(q) + popc(c) - 2 (q . c), the code bits taken as
+// int8 0/1 values in v_mfma_i32_32x32x32_i8 steps of 32 bits (the i32 sums are exact). A workgroup
+// takes kHamMmaQ queries, 32 per wave, whose bits each wave expands into registers once, and
+// kHamMmaC cells, 32 at a time: the 256 threads expand a tile's codes into LDS in the operand
+// layout (double-buffered, so one barrier per tile), and each wave multiplies it with its queries.
+// Operands of step s (bits 32s .. 32s + 31): lane l holds the 16 bits 32s + 16(l/32) .. + 15 of row
+// (query) or column (cell) l % 32, one byte each; result register r of lane l is query
+// 8(r/4) + 4(l/32) + r%4, cell l % 32.
+typedef int mma_v4 __attribute__((ext_vector_type(4)));
+typedef int mma_v16 __attribute__((ext_vector_type(16)));
+constexpr uint32_t kHamMmaQ = 128, kHamMmaC = 256;
+
+// bits b0..b3 of x to bytes 0..3 (the four shifted copies of x do not overlap, so no carries)
+__device__ __forceinline__ uint32_t spread4(uint32_t x) { return ((x & 0xFu) * 0x00204081u) & 0x01010101u; }
+
+__device__ __forceinline__ mma_v4 spread16(uint32_t b) {
+    const mma_v4 v = {static_cast<int>(spread4(b)), static_cast<int>(spread4(b >> 4)), static_cast<int>(spread4(b >> 8)),
+                      static_cast<int>(spread4(b >> 12))};
+    return v;
+}
+
+template <int NW>
+__global__ void __launch_bounds__(256) hamming_mma_kernel(DevArena A, Work Wk, uint32_t nq) {
+    constexpr uint32_t S = 2 * NW;                         // 32-bit steps
+    constexpr uint32_t PPT = (S * kWave + 255) / 256;      // operand pieces per thread per tile
+    __shared__ mma_v4 bx[2][S][kWave];
+    __shared__ uint32_t pcs[kHamMmaC];
+    const uint32_t tid = threadIdx.x, lane = lane_id(), w = tid / kWave, g = lane >> 5, j = lane & 31;
+    const uint32_t q0 = blockIdx.x * kHamMmaQ + w * 32, cb = blockIdx.y * kHamMmaC;
+    const uint32_t ntile = (min(kHamMmaC, A.Mp > cb ? A.Mp - cb : 0u) + 31) / 32;
+    if (ntile == 0) return;  // uniform over the workgroup
+    // the block's cells' popcounts, one cell per thread
+    {
+        const uint32_t c = cb + tid;
+        uint32_t pc = 0;
+        if (c < A.M) {
+#pragma unroll
+            for (int k = 0; k < NW; ++k) pc += __popcll(A.cent_bits[static_cast<uint64_t>(c) * NW + k]);
+        }
+        pcs[tid] = pc;
+    }
+    // this wave's queries: lane (j, g) holds query q0 + j's bits 32s + 16g .. + 15 for every step
+    mma_v4 a[S];
+    uint32_t pq;
+    {
+        uint64_t qw[NW];
+        const bool in = q0 + j < nq;
+#pragma unroll
+        for (int k = 0; k < NW; ++k) qw[k] = in ? Wk.qbits[static_cast<uint64_t>(q0 + j) * NW + k] : 0ull;
+        pq = 0;
+#pragma unroll
+        for (int k = 0; k < NW; ++k) pq += __popcll(qw[k]);
+#pragma unroll
+        for (uint32_t s = 0; s < S; ++s)
+            a[s] = spread16(static_cast<uint32_t>(qw[s / 2] >> (32 * (s & 1) + 16 * g)) & 0xFFFFu);
+    }
+    uint32_t prow[16];  // popc of the query of each result register
+#pragma unroll
+    for (uint32_t r = 0; r < 16; ++r) prow[r] = __shfl(pq, 8 * (r / 4) + 4 * g + (r % 4), kWave);
+    // a tile's S * 64 operand pieces (step s, half gg, cell jj): their code words, then their bytes
+    uint64_t raw[PPT];
+    auto fetch = [&](uint32_t c0) {
+#pragma unroll
+        for (uint32_t k = 0; k < PPT; ++k) {
+            const uint32_t u = tid + 256 * k, jj = u & 31, s = u >> 6, c = c0 + jj;
+            raw[k] = u < S * kWave && c < A.M ? A.cent_bits[static_cast<uint64_t>(c) * NW + s / 2] : 0ull;
+        }
+    };
+    auto store = [&](uint32_t buf) {
+#pragma unroll
+        for (uint32_t k = 0; k < PPT; ++k) {
+            const uint32_t u = tid + 256 * k, jj = u & 31, gg = (u >> 5) & 1, s = u >> 6;
+            if (u < S * kWave)
+                bx[buf][s][gg * 32 + jj] = spread16(static_cast<uint32_t>(raw[k] >> (32 * (s & 1) + 16 * gg)) & 0xFFFFu);
+        }
+    };
+    fetch(cb);
+    store(0);
+    for (uint32_t t = 0; t < ntile; ++t) {
+        const uint32_t buf = t & 1, c0 = cb + 32 * t;
+        __syncthreads();  // tile t is in bx[buf]; every wave is done with tile t - 1's buffer
+        if (t + 1 < ntile) fetch(c0 + 32);
+        // two independent accumulation chains over the steps
+        mma_v16 acc0 = {}, acc1 = {};
+#pragma unroll
+        for (uint32_t s = 0; s < S; s += 2) {
+            acc0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[s], bx[buf][s][lane], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[s + 1], bx[buf][s + 1][lane], acc1, 0, 0, 0);
+        }
+        if (t + 1 < ntile) store(buf ^ 1);
+        const uint32_t c = c0 + j, pc = pcs[32 * t + j];
+        if (c < A.Mp) {
+#pragma unroll
+            for (uint32_t r = 0; r < 16; ++r) {
+                const uint32_t q = q0 + 8 * (r / 4) + 4 * g + (r % 4);
+                if (q < nq)
+                    Wk.hs[static_cast<uint64_t>(q) * A.Mp + c] =
+                        c < A.M ? static_cast<uint16_t>(prow[r] + pc - 2u * static_cast<uint32_t>(acc0[r] + acc1[r]))
+                                : static_cast<uint16_t>(0xFFFFu);
+            }
+        }
+    }
+}
+
 // Prep, route and seed of one query in one workgroup, for codes over the whole padded dimension
 // (n_words * 64 == dim_pad, so prep's coordinates per lane equal NW). Wave 0 computes the query's
 // rotation and code (prep_wave_codes) while the other waves clear the route's histogram; then wave
@@ -1885,8 +1989,6 @@ cell_scan_kernel(DevArena A, Work Wk, KParams K) {
 
 // ---------------------------------------------------------------- cell-major scan, matrix cores
 
-typedef int mma_v4 __attribute__((ext_vector_type(4)));
-typedef int mma_v16 __attribute__((ext_vector_type(16)));
 
 // The cell-major scan of bucket work items with many queries (at least K.mma_min of kBucketQ) on
 // the matrix cores. A member's FastScan sum is an integer dot product,

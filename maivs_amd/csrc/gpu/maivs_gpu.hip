@@ -621,6 +621,13 @@ int launch_route_seed(maivs_gpu_ctx* ctx, const KParams& K, bool rows_ready = fa
 // The Hamming rows of every query (indexes with more cells than a route keeps in LDS).
 int launch_hamming(maivs_gpu_ctx* ctx, uint32_t nq) {
     const DevArena& A = ctx->A;
+    if (ctx->ham_mma) {
+        // on the matrix cores: 128 queries x 256 cells per workgroup
+        const dim3 grid((nq + kHamMmaQ - 1) / kHamMmaQ, (A.Mp + kHamMmaC - 1) / kHamMmaC);
+        DISPATCH_NW(A.W, hipLaunchKernelGGL(hamming_mma_kernel<NW>, grid, dim3(256), 0, ctx->stream, A, ctx->Wk, nq));
+        HIP_TRY(ctx, hipGetLastError());
+        return 0;
+    }
     const dim3 grid((nq + kHamQ - 1) / kHamQ, (A.Mp + kHamC - 1) / kHamC);
     DISPATCH_NW(A.W, hipLaunchKernelGGL(hamming_kernel<NW>, grid, dim3(kHamC), 0, ctx->stream, A, ctx->Wk, nq));
     HIP_TRY(ctx, hipGetLastError());
@@ -1303,6 +1310,9 @@ int maivs_gpu_create(int device, maivs_gpu_ctx** out) {
     if (const char* t = std::getenv("MAIVS_GPU_PQ_TREE_BLOCK")) ctx->pq_tree_block_max_q = static_cast<uint32_t>(std::max(0, std::atoi(t)));
     // the per-query scan in rounds of cells (a 1024-thread workgroup per query) up to this many queries
     if (const char* r = std::getenv("MAIVS_GPU_PQ_ROUNDS")) ctx->pq_rounds_max_q = static_cast<uint32_t>(std::max(0, std::atoi(r)));
+    // the Hamming rows of indexes with more cells than the route keeps in LDS: by popcounts (0, the
+    // default) or on the matrix cores (1); both write the same rows, and both are bound by writing them
+    if (const char* hm = std::getenv("MAIVS_GPU_HAM_MMA")) ctx->ham_mma = std::strcmp(hm, "0") != 0;
     // the per-query path's prep, tree descent and route in one launch up to this many queries
     if (const char* pf = std::getenv("MAIVS_GPU_PQ_FRONT")) ctx->pq_front_max_q = static_cast<uint32_t>(std::max(0, std::atoi(pf)));
     // the per-query path's rerank over workgroups of 8 rows, then the top k, up to this many queries

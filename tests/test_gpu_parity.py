@@ -292,6 +292,31 @@ def test_global_hamming_rows_match_oracle(ctx, cells9k, mix50k, nprobe):
     _compare_search(ctx, ix, queries, p, gt)
 
 
+@pytest.mark.parametrize("mma", ["1", "0"])
+def test_hamming_rows_both_kernels_match_oracle(cells9k, mix50k, monkeypatch, mma):
+    """The query-tiled Hamming rows on the matrix cores (popc(q) + popc(c) - 2 q.c over int8 bits,
+    MAIVS_GPU_HAM_MMA=1) and by popcounts (0): the routing built from them equals the oracle's, probe
+    lists and score bits, for 1,000 queries (not a multiple of the 128-query tile) and 9,000 cells."""
+    monkeypatch.setenv("MAIVS_GPU_HAM_MMA", mma)
+    _, queries, gt = mix50k
+    ix = cells9k
+    c = capi.Context(0)
+    try:
+        _upload(c, ix)
+        for nprobe in (5, 40):
+            p = _params(ix, 10, nprobe)
+            ch, cs, nch = c.route(queries, p)
+            _, och, ocs, onch = oracle.route_batch(ix._arena_desc(), queries, p, 8)
+            assert np.array_equal(nch, onch)
+            for i in range(len(queries)):
+                n = onch[i]
+                assert np.array_equal(ch[i, :n], och[i, :n]), i
+                assert cs[i, :n].tobytes() == ocs[i, :n].tobytes(), i
+        _compare_search(c, ix, queries[:333], _params(ix, 10, 40), None)
+    finally:
+        c.close()
+
+
 @pytest.mark.parametrize("mode", ["1", "0", "12"])
 def test_scan_paths_match_oracle(quality50k, memory50k, churn50k, mix50k, monkeypatch, mode):
     """The cell-major scan with every bucket work item on the matrix cores (MAIVS_GPU_MMA_MIN=1:
