@@ -65,6 +65,7 @@ struct maivs_gpu_ctx {
     int mma_min_mode = -1;     // matrix-core scan items: -1 by cell sharing, 0 off, else their least query count
     bool xcd_order = true;     // matrix-core scan items in cell order, a contiguous chunk per XCD
     bool ham_mma = false;      // the query-tiled Hamming rows on the matrix cores (else by popcounts)
+    bool rows_pass = false;    // the batched pass by Hamming rows at any cell count
     // the main pass captured as one HIP graph, replayed while its key matches
     struct GraphKey {
         KParams K;

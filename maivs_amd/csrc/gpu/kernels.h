@@ -786,10 +786,11 @@ __device__ __forceinline__ void hamming_row(const DevArena& A, const Work& Wk, u
         run(Wk.hs + static_cast<uint64_t>(qi) * Mp);
 }
 
-// Takes the dead cells (no members) out of hamming_row's histogram and row: h = 0xFFFF.
+// Takes the dead cells (no members) out of hamming_row's histogram and row: h = 0xFFFF. The row
+// is in LDS up to kHdLdsCells cells unless global_row (the rows a Hamming-rows kernel wrote).
 __device__ __forceinline__ void dead_fixup(const DevArena& A, const Work& Wk, uint32_t qi, uint32_t* hist,
-                                           uint16_t* hd_lds, uint32_t t, uint32_t nt) {
-    uint16_t* hd = A.Mp <= kHdLdsCells ? hd_lds : Wk.hs + static_cast<uint64_t>(qi) * A.Mp;
+                                           uint16_t* hd_lds, uint32_t t, uint32_t nt, bool global_row = false) {
+    uint16_t* hd = !global_row && A.Mp <= kHdLdsCells ? hd_lds : Wk.hs + static_cast<uint64_t>(qi) * A.Mp;
     for (uint32_t i = t; i < A.n_dead; i += nt) {
         const uint32_t c = A.dead[i];
         atomicSub(&hist[hd[c]], 1u);
@@ -875,7 +876,7 @@ __device__ __forceinline__ void route_phase(const DevArena& A, const Work& Wk, c
         __syncthreads();
     }
     if (A.n_dead) {
-        dead_fixup(A, Wk, qi, hist, reinterpret_cast<uint16_t*>(scratch + 16), tid, nt);
+        dead_fixup(A, Wk, qi, hist, reinterpret_cast<uint16_t*>(scratch + 16), tid, nt, kRowsReady);
         __syncthreads();
     }
     // cut = smallest t whose cumulative live count reaches want_c (wave 0: a run of bins per lane,
@@ -940,7 +941,7 @@ __device__ __forceinline__ void route_phase(const DevArena& A, const Work& Wk, c
         }
         nsl = tot;
     };
-    if (Mp <= kHdLdsCells)
+    if (!kRowsReady && Mp <= kHdLdsCells)
         shortlist(reinterpret_cast<const uint16_t*>(scratch + 16));
     else
         shortlist(Wk.hs + static_cast<uint64_t>(qi) * Mp);

@@ -149,7 +149,7 @@ struct Carver {
 // The per-query and per-cell work buffers of a batched call of nq queries (everything but the
 // candidate lists). host_io: the staged queries and outputs of the host-buffer entry points.
 void carve_work(const DevArena& A, uint32_t nq, uint32_t nprobe, uint32_t k, uint32_t seed_cap, uint32_t bcap,
-                bool host_io, Carver& c, Work& W) {
+                bool host_io, Carver& c, Work& W, bool rows = false) {
     const uint64_t nql = nq;
     if (host_io) {
         c.take(&W.q, nql * A.d);
@@ -168,7 +168,7 @@ void carve_work(const DevArena& A, uint32_t nq, uint32_t nprobe, uint32_t k, uin
     c.take(&W.cqbase, nql);
     c.take(&W.rbase, nql);
     W.hs = nullptr;
-    if (A.Mp > kHdLdsCells) c.take(&W.hs, nql * A.Mp);
+    if (rows || A.Mp > kHdLdsCells) c.take(&W.hs, nql * A.Mp);
     c.take(&W.bnd, nql * nprobe);
     c.take(&W.chosen, nql * nprobe);
     c.take(&W.cscore, nql * nprobe);
@@ -239,7 +239,7 @@ int ensure_work(maivs_gpu_ctx* ctx, uint32_t nq, uint32_t nprobe, uint32_t k) {
     const uint32_t bcap_all = std::max(bcap, ctx->cap_bucket);
     Carver count{nullptr};
     Work& W = ctx->Wk;
-    carve_work(A, nq, nprobe, k, seed_cap, bcap_all, true, count, W);
+    carve_work(A, nq, nprobe, k, seed_cap, bcap_all, true, count, W, ctx->rows_pass);
     uint8_t* base = nullptr;
     int rc = dalloc(ctx, ctx->work_allocs, &base, count.used);
     ctx->counters_clean = false;  // fresh buffers: the next pass clears them first
@@ -249,7 +249,7 @@ int ensure_work(maivs_gpu_ctx* ctx, uint32_t nq, uint32_t nprobe, uint32_t k) {
         return rc;
     }
     Carver cv{base};
-    carve_work(A, nq, nprobe, k, seed_cap, bcap_all, true, cv, W);
+    carve_work(A, nq, nprobe, k, seed_cap, bcap_all, true, cv, W, ctx->rows_pass);
     ctx->cap_nq = nq;
     ctx->cap_nprobe = nprobe;
     ctx->cap_k = k;
@@ -834,7 +834,7 @@ int run_search(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_se
             if ((r = mark(0)) || (r = launch_prep(ctx, K, d_q, kPrepReset))) return r;
             if (K.tree_list && (r = launch_pq_tree(ctx, K, tree_cap))) return r;
             if ((r = mark(3)) || (r = launch_route_seed(ctx, K)) || (r = mark(2))) return r;
-        } else if (ctx->A.Mp > kHdLdsCells) {
+        } else if (ctx->A.Mp > kHdLdsCells || ctx->rows_pass) {
             // many cells: Hamming rows by query tiles, then route and seed from them
             if ((r = mark(0)) || (r = launch_prep(ctx, K, d_q, 0)) || (r = launch_hamming(ctx, K.nq)) || (r = mark(3)))
                 return r;
@@ -1313,6 +1313,8 @@ int maivs_gpu_create(int device, maivs_gpu_ctx** out) {
     // the Hamming rows of indexes with more cells than the route keeps in LDS: by popcounts (0, the
     // default) or on the matrix cores (1); both write the same rows, and both are bound by writing them
     if (const char* hm = std::getenv("MAIVS_GPU_HAM_MMA")) ctx->ham_mma = std::strcmp(hm, "0") != 0;
+    // the batched pass by Hamming rows (prep, rows, route + seed) at any cell count
+    if (const char* rp = std::getenv("MAIVS_GPU_ROWS")) ctx->rows_pass = std::strcmp(rp, "0") != 0;
     // the per-query path's prep, tree descent and route in one launch up to this many queries
     if (const char* pf = std::getenv("MAIVS_GPU_PQ_FRONT")) ctx->pq_front_max_q = static_cast<uint32_t>(std::max(0, std::atoi(pf)));
     // the per-query path's rerank over workgroups of 8 rows, then the top k, up to this many queries

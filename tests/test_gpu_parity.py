@@ -317,6 +317,24 @@ def test_hamming_rows_both_kernels_match_oracle(cells9k, mix50k, monkeypatch, mm
         c.close()
 
 
+@pytest.mark.parametrize("mma", ["1", "0"])
+def test_rows_pass_at_few_cells_matches_oracle(quality50k, churn50k, mix50k, monkeypatch, mma):
+    """The batched pass by Hamming rows (prep, the rows kernel, route + seed from the rows) forced
+    on indexes whose rows would fit in LDS (MAIVS_GPU_ROWS=1): the shortlist and the dead-cell
+    fix-up read the written rows, and the search equals the oracle's, with both rows kernels."""
+    monkeypatch.setenv("MAIVS_GPU_ROWS", "1")
+    monkeypatch.setenv("MAIVS_GPU_HAM_MMA", mma)
+    _, queries, gt = mix50k
+    c = capi.Context(0)
+    try:
+        for nprobe in (10, 40):
+            _compare_search(c, quality50k, queries, _params(quality50k, 10, nprobe), gt)
+        ix, _, _ = churn50k
+        _compare_search(c, ix, queries[:500], _params(ix, 10, 24))
+    finally:
+        c.close()
+
+
 @pytest.mark.parametrize("mode", ["1", "0", "12"])
 def test_scan_paths_match_oracle(quality50k, memory50k, churn50k, mix50k, monkeypatch, mode):
     """The cell-major scan with every bucket work item on the matrix cores (MAIVS_GPU_MMA_MIN=1:
