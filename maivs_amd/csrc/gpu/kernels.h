@@ -831,7 +831,8 @@ __device__ __forceinline__ void route_phase(const DevArena& A, const Work& Wk, c
         for (uint32_t r0 = 0; r0 < nt_list; r0 += nt) {
             const uint32_t i = r0 + tid;
             const uint32_t c = i < nt_list ? tl[i] : 0u;
-            const bool live = i < nt_list && A.mem_off[c + 1] > A.mem_off[c];
+            // (an index without dead cells has every cell live: no member-range loads)
+            const bool live = i < nt_list && (A.n_dead == 0 || A.mem_off[c + 1] > A.mem_off[c]);
             uint32_t tot;
             const uint32_t pos = nsl + block_excl_scan_u32(live ? 1u : 0u, scratch, &tot);
             if (live && pos < K.sort_cap) keys[pos] = c;
@@ -2626,8 +2627,10 @@ pq_tree_block_kernel(DevArena A, Work Wk, KParams K, TreeDev T, const uint32_t* 
 // LDS of pq_front_kernel's routing workgroup after its prep region (u32 words from there): the
 // tree descent's regions as pq_tree_block_kernel has them (fr, fid and top 16-byte aligned).
 struct PqFrontLds {
-    uint32_t hist, rbase, rpre, knodes, scratch, hcache, fr, fid, top, end;
+    uint32_t hist, rbase, rpre, knodes, scratch, hcache, fr, fid, top, tcs, tcl, end;
 };
+// top_words: the staged top level's codes (top_n * W * 2 words), followed by its child starts and
+// lengths (top_n words each)
 __host__ __device__ inline PqFrontLds pq_front_layout(uint32_t W, uint32_t cap, uint32_t top_words) {
     PqFrontLds L;
     L.hist = 0;
@@ -2639,7 +2642,10 @@ __host__ __device__ inline PqFrontLds pq_front_layout(uint32_t W, uint32_t cap, 
     L.fr = (L.hcache + kTreeHCache / 2 + 3) & ~3u;
     L.fid = L.fr + kTreeHCache;
     L.top = L.fid + kTreeHCache;
-    L.end = L.top + top_words;
+    const uint32_t top_n = W ? top_words / (2 * W) : 0u;
+    L.tcs = L.top + top_words;
+    L.tcl = L.tcs + top_n;
+    L.end = L.tcl + top_n;
     return L;
 }
 
@@ -2687,13 +2693,19 @@ pq_front_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ querie
     } else if (K.tree_list && top_words) {
         const uint64_t* src = T.lv_codes + static_cast<uint64_t>(T.lv_off[0]) * NW;
         for (uint32_t i = tid - 2 * kWave; i < top_words / 2; i += nt - 2 * kWave) top[i] = src[i];
+        const uint32_t top_n = top_words / (2 * NW);
+        for (uint32_t i = tid - 2 * kWave; i < top_n; i += nt - 2 * kWave) {
+            tr[L.tcs + i] = T.lv_cs[T.lv_off[0] + i];
+            tr[L.tcl + i] = T.lv_cl[T.lv_off[0] + i];
+        }
     }
     __syncthreads();
     if (K.tree_list) {
         const uint32_t n = block_tree_descent(T, beams, K.want_c, qw, NW, tr + L.hist, tr + L.rbase, tr + L.rpre,
                                               tr + L.knodes, Wk.tlist + static_cast<uint64_t>(qi) * K.tcap,
                                               reinterpret_cast<uint16_t*>(tr + L.hcache), kTreeHCache, tr + L.scratch,
-                                              tr + L.fr, tr + L.fid, kTreeHCache, top_words ? top : nullptr);
+                                              tr + L.fr, tr + L.fid, kTreeHCache, top_words ? top : nullptr,
+                                              top_words ? tr + L.tcs : nullptr, top_words ? tr + L.tcl : nullptr);
         if (tid == 0) Wk.tcount[qi] = n;
         __syncthreads();
     }

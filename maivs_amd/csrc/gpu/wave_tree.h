@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "device_common.h"
 
 namespace maivs_dev {
@@ -28,6 +30,41 @@ __device__ __forceinline__ uint32_t hamming_lds(const uint64_t* qb, const uint64
 __device__ __forceinline__ uint32_t asc_f32_key(float f) {
     const uint32_t b = __float_as_uint(f == 0.0f ? 0.0f : f);
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// t = the smallest distance with count(h <= t) >= keep and below = count(h < t), on every lane of
+// the calling wave (keep at most the histogram's total). bits = 64 * W with W <= 16: lane l sums
+// bins [l * W, (l + 1) * W) from registers (lane 63 also bin bits), one wave scan, and the lane
+// whose run crosses keep walks its registers.
+__device__ inline void wave_hist_threshold(const uint32_t* hist, uint32_t bits, uint32_t keep, uint32_t lane,
+                                           uint32_t& t, uint32_t& below) {
+    const uint32_t per = bits / kWave;
+    uint32_t v[16], mine = 0;
+#pragma unroll
+    for (uint32_t j = 0; j < 16; ++j) {
+        v[j] = j < per ? hist[lane * per + j] : 0u;
+        mine += v[j];
+    }
+    mine += lane == kWave - 1 ? hist[bits] : 0u;
+    const uint32_t incl = wave_incl_scan_u32(mine), excl = incl - mine;
+    const bool here = excl < keep && incl >= keep;
+    uint32_t b = bits, cum = excl;
+    bool found = false;
+#pragma unroll
+    for (uint32_t j = 0; j < 16; ++j) {
+        if (!found && j < per) {
+            if (cum + v[j] >= keep) {
+                b = lane * per + j;
+                found = true;
+            } else {
+                cum += v[j];
+            }
+        }
+    }
+    // (not found among the registers: lane 63's bin bits, with cum counting all below it)
+    const int src = __ffsll(static_cast<long long>(__ballot(here))) - 1;
+    t = __shfl(b, src, kWave);
+    below = __shfl(cum, src, kWave);
 }
 
 // keep_smallest over the frontier positions [0, F) with distance hd(p): emit(k, p) for the kept
@@ -61,30 +98,8 @@ __device__ uint32_t wave_keep_smallest(uint32_t F, uint32_t keep, uint32_t bits,
         }
     }
     wave_sync();
-    // t = the smallest distance with count(h <= t) >= keep; below = count(h < t)
-    const uint32_t nb = bits + 1, bpl = (nb + kWave - 1) / kWave;
-    const uint32_t b0 = min(lane * bpl, nb), b1 = min(b0 + bpl, nb);
-    uint32_t mine = 0;
-    for (uint32_t b = b0; b < b1; ++b) mine += hist[b];
-    uint32_t incl = wave_incl_scan_u32(mine);
-    const uint32_t excl = incl - mine;
-    const bool here = excl < keep && incl >= keep;
-    uint32_t t = 0, below = 0;
-    if (here) {
-        uint32_t cum = excl;
-        for (uint32_t b = b0; b < b1; ++b) {
-            if (cum + hist[b] >= keep) {
-                t = b;
-                below = cum;
-                break;
-            }
-            cum += hist[b];
-        }
-    }
-    const uint64_t hm = __ballot(here);
-    const int src = __ffsll(static_cast<long long>(hm)) - 1;
-    t = __shfl(t, src, kWave);
-    below = __shfl(below, src, kWave);
+    uint32_t t, below;
+    wave_hist_threshold(hist, bits, keep, lane, t, below);
     const uint32_t need_eq = keep - below;
     uint32_t eq_seen = 0, kept = 0;
     for (uint32_t c0 = 0; c0 < F; c0 += kWave) {
@@ -230,55 +245,71 @@ __device__ uint32_t block_keep_smallest(uint32_t F, uint32_t keep, uint32_t bits
         }
     }
     __syncthreads();
-    // t = the smallest distance with count(h <= t) >= keep; below = count(h < t)
-    const uint32_t nb = bits + 1, bpt = (nb + nt - 1) / nt;
-    const uint32_t b0 = min(tid * bpt, nb), b1 = min(b0 + bpt, nb);
-    uint32_t mine = 0;
-    for (uint32_t b = b0; b < b1; ++b) mine += hist[b];
-    uint32_t total;
-    const uint32_t excl = block_excl_scan_u32(mine, scratch, &total);
-    if (excl < keep && excl + mine >= keep) {
-        uint32_t cum = excl;
-        for (uint32_t b = b0; b < b1; ++b) {
-            if (cum + hist[b] >= keep) {
-                scratch[16] = b;
-                scratch[17] = cum;
-                break;
-            }
-            cum += hist[b];
+    // t = the smallest distance with count(h <= t) >= keep; below = count(h < t): wave 0 alone
+    if (tid < kWave) {
+        uint32_t t, below;
+        wave_hist_threshold(hist, bits, keep, tid, t, below);
+        if (tid == 0) {
+            scratch[16] = t;
+            scratch[17] = below;
         }
     }
     __syncthreads();
     const uint32_t t = scratch[16], below = scratch[17];
     const uint32_t need_eq = keep - below;
-    // encounter order, a chunk of nt positions at a time: one scan counts both the entries below t
-    // (low half) and those at t (high half) before each position
+    // encounter order: thread tid takes positions [tid * PPT, (tid + 1) * PPT) of each chunk of
+    // nt * PPT (PPT by the frontier's size), and one scan counts both the entries below t (low half)
+    // and those at t (high half) before its run; the run then walks its positions in order
     uint32_t eq_seen = 0, kept = 0;
-    for (uint32_t c0 = 0; c0 < F; c0 += nt) {
-        const uint32_t p = c0 + tid;
-        const bool valid = p < F;
-        const uint32_t h = valid ? (p < hcap ? static_cast<uint32_t>(hcache[p]) : hd(p)) : 0xFFFFFFFFu;
-        const bool lt = valid && h < t, eq = valid && h == t;
-        uint32_t tot;
-        const uint32_t ex = block_excl_scan_u32((lt ? 1u : 0u) | (eq ? 0x10000u : 0u), scratch, &tot);
-        const uint32_t rem = need_eq > eq_seen ? need_eq - eq_seen : 0u;
-        const uint32_t eq_before = ex >> 16;
-        if (lt || (eq && eq_before < rem)) emit(kept + (ex & 0xFFFFu) + min(eq_before, rem), p);
-        kept += (tot & 0xFFFFu) + min(tot >> 16, rem);
-        eq_seen += tot >> 16;
-    }
+    auto emit_runs = [&](auto ppt_tag) {
+        constexpr uint32_t PPT = decltype(ppt_tag)::value;
+        for (uint32_t c0 = 0; c0 < F; c0 += nt * PPT) {
+            uint32_t hv[PPT], cnt = 0;
+#pragma unroll
+            for (uint32_t i = 0; i < PPT; ++i) {
+                const uint32_t p = c0 + tid * PPT + i;
+                hv[i] = p < F ? (p < hcap ? static_cast<uint32_t>(hcache[p]) : hd(p)) : 0xFFFFFFFFu;
+                cnt += hv[i] < t ? 1u : hv[i] == t ? 0x10000u : 0u;
+            }
+            uint32_t tot;
+            const uint32_t ex = block_excl_scan_u32(cnt, scratch, &tot);
+            const uint32_t rem = need_eq > eq_seen ? need_eq - eq_seen : 0u;
+            uint32_t lt_before = ex & 0xFFFFu, eq_before = ex >> 16;
+#pragma unroll
+            for (uint32_t i = 0; i < PPT; ++i) {
+                const uint32_t p = c0 + tid * PPT + i;
+                if (hv[i] < t) {
+                    emit(kept + lt_before + min(eq_before, rem), p);
+                    ++lt_before;
+                } else if (hv[i] == t) {
+                    if (eq_before < rem) emit(kept + lt_before + eq_before, p);
+                    ++eq_before;
+                }
+            }
+            kept += (tot & 0xFFFFu) + min(tot >> 16, rem);
+            eq_seen += tot >> 16;
+        }
+    };
+    if (F <= nt)
+        emit_runs(std::integral_constant<uint32_t, 1>{});
+    else if (F <= 2 * nt)
+        emit_runs(std::integral_constant<uint32_t, 2>{});
+    else
+        emit_runs(std::integral_constant<uint32_t, 4>{});
     return kept;
 }
 
 // tree_descent by the whole workgroup (every thread calls it): the same leaves in the same order.
 // LDS as tree_descent's, plus scratch (18 words), fr and fid (fcap words each: the frontier's nodes
 // below the top level, and the leaves' cells, so neither needs a search or a second load), and
-// top: the top level's codes when the caller staged them in LDS (else null).
+// top (top_cs, top_cl): the top level's codes (child ranges) when the caller staged them in LDS
+// (else null).
 __device__ inline uint32_t block_tree_descent(const TreeDev& T, const uint32_t* beams, uint32_t want, const uint64_t* qb,
                                               uint32_t W, uint32_t* hist, uint32_t* rbase, uint32_t* rpre,
                                               uint32_t* knodes, uint32_t* out, uint16_t* hcache, uint32_t hcap,
                                               uint32_t* scratch, uint32_t* fr, uint32_t* fid, uint32_t fcap,
-                                              const uint64_t* top) {
+                                              const uint64_t* top, const uint32_t* top_cs = nullptr,
+                                              const uint32_t* top_cl = nullptr) {
     const uint32_t tid = threadIdx.x, nt = blockDim.x, bits = W * 64;
     if (T.n_levels == 0) return 0;
     uint32_t nr = 1;
@@ -303,8 +334,8 @@ __device__ inline uint32_t block_tree_descent(const TreeDev& T, const uint32_t* 
             [&](uint32_t k, uint32_t p) { knodes[k] = node_of(li, p); }, hcache, hcap);
         __syncthreads();
         // children of the kept nodes, in order: the next frontier's ranges, then its nodes
-        const uint32_t* cs = T.lv_cs + T.lv_off[li];
-        const uint32_t* cl = T.lv_cl + T.lv_off[li];
+        const uint32_t* cs = li == 0 && top_cs ? top_cs : T.lv_cs + T.lv_off[li];
+        const uint32_t* cl = li == 0 && top_cl ? top_cl : T.lv_cl + T.lv_off[li];
         uint32_t carry = 0;
         for (uint32_t k0 = 0; k0 < nk; k0 += nt) {
             const uint32_t k = k0 + tid;
@@ -320,9 +351,10 @@ __device__ inline uint32_t block_tree_descent(const TreeDev& T, const uint32_t* 
         }
         if (tid == 0) rpre[nk] = carry;
         __syncthreads();
-        for (uint32_t k = tid; k < nk; k += nt) {
-            const uint32_t b = rbase[k], p0 = rpre[k], len = rpre[k + 1] - p0;
-            for (uint32_t j = 0; j < len && p0 + j < fcap; ++j) fr[p0 + j] = b + j;
+        // eight threads per kept node, every eighth child each
+        for (uint32_t x = tid; x < nk * 8; x += nt) {
+            const uint32_t k = x >> 3, b = rbase[k], p0 = rpre[k], len = rpre[k + 1] - p0;
+            for (uint32_t j = x & 7; j < len && p0 + j < fcap; j += 8) fr[p0 + j] = b + j;
         }
         __syncthreads();
         nr = nk;
