@@ -444,10 +444,12 @@ __global__ void pad_kernel(uint32_t* __restrict__ slots, float* __restrict__ sco
 // others across lanes (partner l ^ (h / EPL)), in the reference's ascending level order, so every
 // butterfly sees the reference's operands. `xs` is the wave's LDS region (x[P] | mins[npos4] |
 // cqp[d4] | rqp[d4]): it receives the rotated query and the summands q * csq_min (and, for an SQ8
-// rerank store, q * sq_min) that prep_wave_tables adds up; `qw` receives the code words.
+// rerank store, q * sq_min) that prep_wave_tables adds up; `qw` receives the code words. cqs_lds
+// (or null): an LDS copy of the rescore operand cqs (d floats, 16-byte aligned).
 template <int EPL>
 __device__ __forceinline__ void prep_wave_codes(const DevArena& A, const Work& Wk, const float* __restrict__ queries,
-                                                uint32_t qi, uint32_t lane, float* xs, uint64_t* qw) {
+                                                uint32_t qi, uint32_t lane, float* xs, uint64_t* qw,
+                                                float* cqs_lds = nullptr) {
     const uint32_t P = A.P, d = A.d, npos = A.npos;
     const uint32_t np4 = (npos + 3) & ~3u;
     float* mins = xs + P;
@@ -514,6 +516,7 @@ __device__ __forceinline__ void prep_wave_codes(const DevArena& A, const Work& W
             m.z = sq8 ? x[e + 2] * mn[2] : 0.0f;
             m.w = sq8 ? x[e + 3] * mn[3] : 0.0f;
             *reinterpret_cast<float4*>(cqs_out + base + e) = o;
+            if (cqs_lds) *reinterpret_cast<float4*>(cqs_lds + base + e) = o;
             *reinterpret_cast<float4*>(cqp + base + e) = m;
         }
     } else {
@@ -522,7 +525,9 @@ __device__ __forceinline__ void prep_wave_codes(const DevArena& A, const Work& W
             const uint32_t i = base + e;
             if (i < d) {
                 const float v = x[e];
-                cqs_out[i] = sq8 ? v * A.csq_step[i] : v;
+                const float o = sq8 ? v * A.csq_step[i] : v;
+                cqs_out[i] = o;
+                if (cqs_lds) cqs_lds[i] = o;
                 cqp[i] = sq8 ? v * A.csq_min[i] : 0.0f;
             }
         }
@@ -800,12 +805,17 @@ __device__ __forceinline__ void dead_fixup(const DevArena& A, const Work& Wk, ui
 
 // kFront: the caller (front_kernel) already cleared the histogram, staged cqs and ran hamming_row,
 // and K.tree_list and K.flat_route are 0. kRowsReady: hamming_kernel already wrote the query's row of Wk.hs (more
-// cells than the LDS row holds); the histogram is built from it.
+// cells than the LDS row holds); the histogram is built from it. Callers that hold them on chip
+// pass (else null): cqs_src, the query's cqs in LDS; tl_lds and n_tl, the tree's leaf list in LDS
+// and its length; aux, nt floats of LDS that carry each shortlisted cell's r_bound through the
+// sort (loaded beside its centroid row at the rescore).
 template <class Get>
 __device__ uint32_t select_kth_u32(uint32_t n, uint32_t want, Get get, uint32_t* hist, uint32_t* scratch);
 
 template <int NW, bool kFront = false, bool kRowsReady = false>
-__device__ __forceinline__ void route_phase(const DevArena& A, const Work& Wk, const KParams& K, uint32_t qi) {
+__device__ __forceinline__ void route_phase(const DevArena& A, const Work& Wk, const KParams& K, uint32_t qi,
+                                            const float* cqs_src = nullptr, const uint32_t* tl_lds = nullptr,
+                                            uint32_t n_tl = 0, float* aux = nullptr) {
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t tid = threadIdx.x, nt = blockDim.x;
     const uint32_t d = A.d, M = A.M, Mp = A.Mp;
@@ -820,19 +830,23 @@ __device__ __forceinline__ void route_phase(const DevArena& A, const Work& Wk, c
 
     if constexpr (!kFront) {
         for (uint32_t i = tid; i < nbins; i += nt) hist[i] = 0;
-        for (uint32_t i = tid; i < d; i += nt) cqs[i] = Wk.cqs[static_cast<uint64_t>(qi) * d + i];
+        for (uint32_t i = tid; i < d; i += nt) cqs[i] = cqs_src ? cqs_src[i] : Wk.cqs[static_cast<uint64_t>(qi) * d + i];
         __syncthreads();
     }
     uint32_t nsl = 0;
-    if (!kFront && K.tree_list) {
+    if (!kFront && K.tree_list && tl_lds && A.n_dead == 0) {
+        // the centroid tree's leaves, every one live (route_query, src/index.rs:1193-1204)
+        for (uint32_t i = tid; i < min(n_tl, K.sort_cap); i += nt) keys[i] = tl_lds[i];
+        nsl = n_tl;
+    } else if (!kFront && K.tree_list) {
         // the centroid tree's leaves, live cells only (route_query, src/index.rs:1193-1204)
-        const uint32_t* tl = Wk.tlist + static_cast<uint64_t>(qi) * K.tcap;
-        const uint32_t nt_list = Wk.tcount[qi];
+        const uint32_t* tl = tl_lds ? tl_lds : Wk.tlist + static_cast<uint64_t>(qi) * K.tcap;
+        const uint32_t nt_list = tl_lds ? n_tl : Wk.tcount[qi];
         for (uint32_t r0 = 0; r0 < nt_list; r0 += nt) {
             const uint32_t i = r0 + tid;
             const uint32_t c = i < nt_list ? tl[i] : 0u;
             // (an index without dead cells has every cell live: no member-range loads)
-            const bool live = i < nt_list && (A.n_dead == 0 || A.mem_off[c + 1] > A.mem_off[c]);
+            const bool live = i < nt_list && A.mem_off[c + 1] > A.mem_off[c];
             uint32_t tot;
             const uint32_t pos = nsl + block_excl_scan_u32(live ? 1u : 0u, scratch, &tot);
             if (live && pos < K.sort_cap) keys[pos] = c;
@@ -961,12 +975,16 @@ __device__ __forceinline__ void route_phase(const DevArena& A, const Work& Wk, c
     // ---- exact rescore, 8 lanes per cell in the reference's FMA order (:777-800)
     const bool sq8 = A.cent_sq8 != nullptr;
     const float cqbase = sq8 ? Wk.cqbase[qi] : 0.0f;
+    // (the adaptive stop's bound of a probed cell needs its r_bound: with aux, loaded at the
+    // rescore and carried through the rank sort)
+    const bool carry = aux != nullptr && K.adaptive && nsl <= nt;
     {
         const uint32_t l = tid & 7, grp = tid >> 3, ngrp = nt >> 3;
         const uint32_t rounds = (nsl + ngrp - 1) / ngrp;
         for (uint32_t rr = 0; rr < rounds; ++rr) {
             const uint32_t i = rr * ngrp + grp;
             const uint32_t c = i < nsl ? static_cast<uint32_t>(keys[i]) : static_cast<uint32_t>(keys[0]);
+            const float rb = carry && l == 0 ? A.r_bound[c] : 0.0f;
             float s;
             if (sq8)
                 s = dot_cm_u8(A.cent_sq8 + static_cast<uint64_t>(c) * A.cu.stride, A.cu, l,
@@ -975,7 +993,11 @@ __device__ __forceinline__ void route_phase(const DevArena& A, const Work& Wk, c
                 s = dot_cm_f32(A.cents + static_cast<uint64_t>(c) * A.cf.stride, A.cf, l,
                                [&](uint32_t j) { return cqs[j]; });
             __syncthreads();  // every read of keys[] in this round precedes the writes
-            if (i < nsl && l == 0) keys[i] = desc_score_key(s, c);
+            if (i < nsl && l == 0) {
+                const uint64_t key = desc_score_key(s, c);
+                keys[i] = key;
+                if (carry) aux[i] = rb;
+            }
         }
     }
     __syncthreads();
@@ -985,12 +1007,18 @@ __device__ __forceinline__ void route_phase(const DevArena& A, const Work& Wk, c
         // keys are unique: each one's rank among the nsl places it (read all, then write)
         uint64_t mine = 0;
         uint32_t r = 0;
+        float mb = 0.0f;
         if (tid < nsl) {
             mine = keys[tid];
+            if (carry) mb = aux[tid];
+#pragma unroll 8
             for (uint32_t j = 0; j < nsl; ++j) r += keys[j] < mine;
         }
         __syncthreads();
-        if (tid < nsl) keys[r] = mine;
+        if (tid < nsl) {
+            keys[r] = mine;
+            if (carry) aux[r] = mb;
+        }
     } else {
         uint32_t n2 = 1;
         while (n2 < nsl) n2 <<= 1;
@@ -1027,9 +1055,10 @@ __device__ __forceinline__ void route_phase(const DevArena& A, const Work& Wk, c
         const float s = ok ? key_score(keys[i]) : __uint_as_float(0x7fc00000u);
         chosen[i] = c;
         cscore[i] = s;
+        // the adaptive stop's bound of a probed cell (src/index.rs:1484-1485, 2178-2179)
         if (K.adaptive && ok && i >= K.bnd_from)
             Wk.bnd[static_cast<uint64_t>(qi) * K.nprobe + i] =
-                cos_f(fmaxf(acos_f(fminf(fmaxf(s, -1.0f), 1.0f)) - A.r_bound[c], 0.0f));
+                cos_f(fmaxf(acos_f(fminf(fmaxf(s, -1.0f), 1.0f)) - (carry ? aux[i] : A.r_bound[c]), 0.0f));
     }
     // ---- nucleus over the capped list (:1960-1973); tc >= 1 keeps all cap cells
     uint32_t nch = cap;
@@ -2649,6 +2678,20 @@ __host__ __device__ inline PqFrontLds pq_front_layout(uint32_t W, uint32_t cap, 
     return L;
 }
 
+// Byte offset of pq_front_kernel's LDS kept across its phases: cqs[d4] | leaves[tcap4] |
+// bounds[kPqTreeBlock] (pq_front_keep_bytes), past both the prep + descent layout and route_phase's.
+__host__ __device__ inline uint32_t pq_front_keep_off(uint32_t P, uint32_t npos, uint32_t d, uint32_t W, uint32_t Mp,
+                                                      uint32_t sort_cap, uint32_t nprobe, uint32_t cap,
+                                                      uint32_t top_words) {
+    const uint32_t prep = 4 * (32 + P + ((npos + 3) & ~3u) + 2 * ((d + 3) & ~3u));
+    const uint32_t a = prep + 4 * pq_front_layout(W, cap, top_words).end;
+    const uint32_t b = static_cast<uint32_t>(route_lds_bytes(d, W, Mp, sort_cap, nprobe));
+    return ((a > b ? a : b) + 15) & ~15u;
+}
+__host__ __device__ inline uint32_t pq_front_keep_bytes(uint32_t d, uint32_t tcap) {
+    return 4 * (((d + 3) & ~3u) + ((tcap + 3) & ~3u) + kPqTreeBlock);
+}
+
 // The per-query path's prep, tree descent and route in one launch for small batches (codes over
 // the whole padded dimension): two workgroups per query run side by side. Workgroup qi (qi < nq)
 // computes the query's rotation and code (wave 0, prep_wave_codes) while wave 1 adds up the
@@ -2659,11 +2702,13 @@ __host__ __device__ inline PqFrontLds pq_front_layout(uint32_t W, uint32_t cap, 
 // path. Both write the same values to qbits, cqs and cqbase. The per-call counters are clear
 // beforehand (the last pass's epilogue, or a reset launch).
 // LDS: codes[16] u64 | x[P] | mins[npos4] | cqp[d4] | rqp[d4] | pq_front_layout; route_phase's
-// layout from offset 0 once the descent is done.
+// layout from offset 0 once the descent is done; past both, the query's cqs, the descent's leaf
+// list and the route's bounds (pq_front_keep_off), so the route reads none of them from memory
+// (keep = 0: no such region, the route reads them from memory).
 template <int NW>
 __global__ void __launch_bounds__(kPqTreeBlock)
 pq_front_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries, TreeDev T,
-                const uint32_t* __restrict__ beams, uint32_t cap, uint32_t top_words) {
+                const uint32_t* __restrict__ beams, uint32_t cap, uint32_t top_words, uint32_t keep) {
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t tid = threadIdx.x, nt = blockDim.x, lane = lane_id(), wv = tid / kWave;
     uint64_t* qw = reinterpret_cast<uint64_t*>(smem);
@@ -2678,8 +2723,13 @@ pq_front_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ querie
     uint32_t* tr = reinterpret_cast<uint32_t*>(smem) + prep_words;
     const PqFrontLds L = pq_front_layout(NW, cap, top_words);
     uint64_t* top = reinterpret_cast<uint64_t*>(tr + L.top);
+    float* cqs_l = keep ? reinterpret_cast<float*>(smem + pq_front_keep_off(A.P, A.npos, A.d, NW, A.Mp, K.sort_cap,
+                                                                             K.nprobe, cap, top_words))
+                        : nullptr;
+    uint32_t* leaves = keep ? reinterpret_cast<uint32_t*>(cqs_l + ((A.d + 3) & ~3u)) : nullptr;
+    float* bounds = keep ? reinterpret_cast<float*>(leaves + ((K.tcap + 3) & ~3u)) : nullptr;
     if (wv == 0) {
-        prep_wave_codes<NW>(A, Wk, queries, qi, lane, xs, qw);
+        prep_wave_codes<NW>(A, Wk, queries, qi, lane, xs, qw, cqs_l);
     } else if (wv == 1) {
         float* prod = reinterpret_cast<float*>(tr + L.fr);  // free until the descent
         float base = 0.0f;
@@ -2700,16 +2750,16 @@ pq_front_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ querie
         }
     }
     __syncthreads();
+    uint32_t n = 0;
     if (K.tree_list) {
-        const uint32_t n = block_tree_descent(T, beams, K.want_c, qw, NW, tr + L.hist, tr + L.rbase, tr + L.rpre,
-                                              tr + L.knodes, Wk.tlist + static_cast<uint64_t>(qi) * K.tcap,
-                                              reinterpret_cast<uint16_t*>(tr + L.hcache), kTreeHCache, tr + L.scratch,
-                                              tr + L.fr, tr + L.fid, kTreeHCache, top_words ? top : nullptr,
-                                              top_words ? tr + L.tcs : nullptr, top_words ? tr + L.tcl : nullptr);
+        n = block_tree_descent(T, beams, K.want_c, qw, NW, tr + L.hist, tr + L.rbase, tr + L.rpre, tr + L.knodes,
+                               Wk.tlist + static_cast<uint64_t>(qi) * K.tcap, reinterpret_cast<uint16_t*>(tr + L.hcache),
+                               kTreeHCache, tr + L.scratch, tr + L.fr, tr + L.fid, kTreeHCache, top_words ? top : nullptr,
+                               top_words ? tr + L.tcs : nullptr, top_words ? tr + L.tcl : nullptr, leaves);
         if (tid == 0) Wk.tcount[qi] = n;
         __syncthreads();
     }
-    route_phase<NW>(A, Wk, K, qi);
+    route_phase<NW>(A, Wk, K, qi, cqs_l, K.tree_list && keep ? leaves : nullptr, n, bounds);
 }
 
 // want-th smallest (1-based) of the n u32 values get(i), block-wide, four 8-bit radix passes.

@@ -400,15 +400,17 @@ int launch_pq_front(maivs_gpu_ctx* ctx, const KParams& K, const float* d_q, uint
         const uint32_t top_n = ctx->tree_level_n.empty() ? 0u : ctx->tree_level_n[0];
         top = top_n * A.W * 2 <= kTreeTopWords ? top_n * A.W * 2 : 0u;
     }
-    const PqFrontLds L = pq_front_layout(A.W, cap, top);
-    const size_t lds = std::max(prep1_lds(A) + static_cast<size_t>(L.end) * 4, route_lds(A, K.sort_cap, K.nprobe));
+    // the region kept across the phases (cqs, leaves, bounds) when it fits beside the rest
+    const size_t base = pq_front_keep_off(A.P, A.npos, A.d, A.W, A.Mp, K.sort_cap, K.nprobe, cap, top);
+    const uint32_t keep = base + pq_front_keep_bytes(A.d, K.tcap) <= kLdsBudget ? 1u : 0u;
+    const size_t lds = keep ? base + pq_front_keep_bytes(A.d, K.tcap) : base;
     if (lds > kLdsBudget) return fail(ctx, MAIVS_ERR_UNSUPPORTED, "the fused route needs %zu bytes of LDS", lds);
     int rc = 0;
     auto go = [&](const void* fn, auto kernel) -> int {
         int r;
         if (lds > 64 * 1024 && (r = raise_lds_limit(ctx, fn, lds))) return r;
         hipLaunchKernelGGL(kernel, dim3(2 * K.nq), dim3(kPqTreeBlock), lds, ctx->stream, A, ctx->Wk, K, d_q, ctx->tree,
-                           ctx->d_beams, cap, top);
+                           ctx->d_beams, cap, top, keep);
         return 0;
     };
     DISPATCH_NW(A.W, rc = go(reinterpret_cast<const void*>(pq_front_kernel<NW>), pq_front_kernel<NW>));

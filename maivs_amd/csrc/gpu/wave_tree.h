@@ -303,13 +303,13 @@ __device__ uint32_t block_keep_smallest(uint32_t F, uint32_t keep, uint32_t bits
 // LDS as tree_descent's, plus scratch (18 words), fr and fid (fcap words each: the frontier's nodes
 // below the top level, and the leaves' cells, so neither needs a search or a second load), and
 // top (top_cs, top_cl): the top level's codes (child ranges) when the caller staged them in LDS
-// (else null).
+// (else null); out_lds: an LDS copy of out (want words), or null.
 __device__ inline uint32_t block_tree_descent(const TreeDev& T, const uint32_t* beams, uint32_t want, const uint64_t* qb,
                                               uint32_t W, uint32_t* hist, uint32_t* rbase, uint32_t* rpre,
                                               uint32_t* knodes, uint32_t* out, uint16_t* hcache, uint32_t hcap,
                                               uint32_t* scratch, uint32_t* fr, uint32_t* fid, uint32_t fcap,
                                               const uint64_t* top, const uint32_t* top_cs = nullptr,
-                                              const uint32_t* top_cl = nullptr) {
+                                              const uint32_t* top_cl = nullptr, uint32_t* out_lds = nullptr) {
     const uint32_t tid = threadIdx.x, nt = blockDim.x, bits = W * 64;
     if (T.n_levels == 0) return 0;
     uint32_t nr = 1;
@@ -371,8 +371,12 @@ __device__ inline uint32_t block_tree_descent(const TreeDev& T, const uint32_t* 
             if (p < fcap) fid[p] = T.leaf_ids[leaf];
             return hamming_lds(qb, T.leaf_codes + static_cast<uint64_t>(leaf) * W, W);
         },
-        [&](uint32_t k, uint32_t p) { out[k] = !every && p < fcap ? fid[p] : T.leaf_ids[node_of(ll, p)]; }, hcache,
-        hcap);
+        [&](uint32_t k, uint32_t p) {
+            const uint32_t c = !every && p < fcap ? fid[p] : T.leaf_ids[node_of(ll, p)];
+            out[k] = c;
+            if (out_lds) out_lds[k] = c;
+        },
+        hcache, hcap);
     __syncthreads();
     return nout;
 }
