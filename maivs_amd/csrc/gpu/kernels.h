@@ -734,41 +734,57 @@ prep_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries, u
 // (NW = 1: one lane, the whole 8-byte code), so that one load instruction reads a contiguous run
 // of codes; the partial counts meet by lane exchange. Rounds of U codes per lane are double
 // buffered: the next round's loads are in flight while this round is counted. The loop bounds are
-// uniform: every lane takes part in the exchanges.
-template <int NW>
+// uniform: every lane takes part in the exchanges. The query's code comes from q_lds (LDS) or else
+// from Wk.qbits; before reading it the threads call wait() (the caller's barrier after which the
+// code and the cleared histogram are ready), with the first round's code loads already in flight.
+struct NoWait {
+    __device__ void operator()() const {}
+};
+template <int NW, class Wait = NoWait>
 __device__ __forceinline__ void hamming_row(const DevArena& A, const Work& Wk, uint32_t qi, uint32_t* hist,
-                                            uint16_t* hd_lds, uint32_t t, uint32_t nt) {
+                                            uint16_t* hd_lds, uint32_t t, uint32_t nt,
+                                            const uint64_t* q_lds = nullptr, Wait wait = Wait{}) {
     const uint32_t M = A.M, Mp = A.Mp;
     auto run = [&](auto* out) {
         constexpr uint32_t L = NW >= 2 ? NW / 2 : 1;
         constexpr uint32_t U = 8;
         const uint32_t sub = t % L, cpr = nt / L, cl = t / L, step = U * cpr;
-        const uint64_t* qg = Wk.qbits + static_cast<uint64_t>(qi) * NW;
-        const uint64_t q0 = qg[NW >= 2 ? 2 * sub : 0];
-        const uint64_t q1 = NW >= 2 ? qg[2 * sub + 1] : 0ull;
+        uint64_t q0 = 0, q1 = 0;  // the query's code words of this lane, read after wait()
+        // (32-bit byte offsets from the codes' base, M * NW * 8 < 2^32: one offset register per load.
+        // A lane's cells of a round are stepped one from the last, each step behind an empty asm
+        // statement, so the compiler keeps no per-u offsets live across the loop.)
+        const char* cb = reinterpret_cast<const char*>(A.cent_bits);
         auto load = [&](uint32_t base, uint64_t (&w0)[U], uint64_t (&w1)[U]) {
+            uint32_t c = base + cl;
 #pragma unroll
             for (uint32_t u = 0; u < U; ++u) {
-                const uint32_t c = base + u * cpr + cl;
-                const uint64_t* src = A.cent_bits + static_cast<uint64_t>(c < M ? c : 0u) * NW;
+                if (u) {
+                    c += cpr;
+                    asm volatile("" : "+v"(c));
+                }
+                const uint32_t off = (c < M ? c : 0u) * (NW * 8u) + (NW >= 2 ? sub * 16u : 0u);
                 if constexpr (NW == 1) {
-                    w0[u] = src[0];
+                    w0[u] = *reinterpret_cast<const uint64_t*>(cb + off);
                     w1[u] = 0ull;
                 } else {
-                    const uint4 v = reinterpret_cast<const uint4*>(src)[sub];
+                    const uint4 v = *reinterpret_cast<const uint4*>(cb + off);
                     w0[u] = (static_cast<uint64_t>(v.y) << 32) | v.x;
                     w1[u] = (static_cast<uint64_t>(v.w) << 32) | v.z;
                 }
             }
         };
         auto count = [&](uint32_t base, const uint64_t (&w0)[U], const uint64_t (&w1)[U]) {
+            uint32_t c = base + cl;
 #pragma unroll
             for (uint32_t u = 0; u < U; ++u) {
+                if (u) {
+                    c += cpr;
+                    asm volatile("" : "+v"(c));
+                }
                 uint32_t h = __popcll(q0 ^ w0[u]) + (NW >= 2 ? __popcll(q1 ^ w1[u]) : 0u);
                 if constexpr (L >= 2) h += static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(h), 0xB1, 0xF, 0xF, true));
                 if constexpr (L >= 4) h += static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(h), 0x4E, 0xF, 0xF, true));
                 if constexpr (L >= 8) h += __shfl_xor(h, 4, kWave);
-                const uint32_t c = base + u * cpr + cl;
                 if (sub == 0 && c < Mp) {
                     out[c] = c < M ? static_cast<uint16_t>(h) : static_cast<uint16_t>(0xFFFFu);
                     if (c < M) atomicAdd(&hist[h], 1u);
@@ -777,11 +793,18 @@ __device__ __forceinline__ void hamming_row(const DevArena& A, const Work& Wk, u
         };
         uint64_t a0[U], a1[U], b0[U], b1[U];
         load(0, a0, a1);
+        wait();
+        const uint64_t* qg = q_lds ? q_lds : Wk.qbits + static_cast<uint64_t>(qi) * NW;
+        q0 = qg[NW >= 2 ? 2 * sub : 0];
+        q1 = NW >= 2 ? qg[2 * sub + 1] : 0ull;
+        // (the loads are unconditional, cells past M read cell 0's code and are not counted: with no
+        // branch around them the compiler's wait counts let a round's loads stay in flight while the
+        // round before it is counted)
         for (uint32_t base = 0; base < Mp; base += 2 * step) {
-            if (base + step < Mp) load(base + step, b0, b1);
+            load(base + step, b0, b1);
             count(base, a0, a1);
             if (base + step >= Mp) break;
-            if (base + 2 * step < Mp) load(base + 2 * step, a0, a1);
+            load(base + 2 * step, a0, a1);
             count(base + step, b0, b1);
         }
     };
@@ -1139,7 +1162,7 @@ __device__ __forceinline__ uint32_t lut_sum_pair(const Code<NW>& c, const uint16
 // (src/index.rs:2150-2154); tau is their exact target-th smallest d (:2155-2160) and only
 // d <= tau is kept; then the adaptive cut (:2166-2188) from the route's bounds, and the per-cell
 // probe counts for the inversion.
-// LDS: static table[TB] at offset 0; dynamic probed[MW4] | coarse[256] | fine[256] | misc[32] |
+// LDS: static table[TB] at offset 0; dynamic probed[MW4] | coarse[256] | fine[256] | misc[64] |
 // sbuf[seed_cap4] u16 (d by item index).
 // The seed stage's FastScan table in static LDS: the kernel's largest static LDS variable, at
 // address 0, so the table lookups need no base add.
@@ -1156,16 +1179,19 @@ __device__ __forceinline__ void seed_phase(const DevArena& A, const Work& Wk, co
     const uint32_t tid = threadIdx.x, nt = blockDim.x, lane = lane_id();
     constexpr uint32_t TB = NW * 256;
     constexpr uint32_t kOff = 0, kCell = 9, kE0 = 17, kCnt = 25, kKeep = 26, kTau = 27, kRe = 28, kHb = 29, kBelow = 30;
+    // the first rest cells (ranks ns .. ns + nr_max - 1): member offsets, cells and first entries
+    constexpr uint32_t kROff = 32, kRCell = 41, kRE0 = 49;
     uint8_t* const table = seed_table<NW>();
     uint32_t* probed = reinterpret_cast<uint32_t*>(smem);
     uint32_t* coarse = probed + ((A.MW + 3) & ~3u);
     uint32_t* fine = coarse + 256;
     uint32_t* misc = fine + 256;
-    uint16_t* sbuf = reinterpret_cast<uint16_t*>(misc + 32);
+    uint16_t* sbuf = reinterpret_cast<uint16_t*>(misc + 64);
 
     const uint32_t nch = Wk.nchosen[qi];
     const uint32_t* chosen = Wk.chosen + static_cast<uint64_t>(qi) * K.nprobe;
     const uint32_t ns = min(kSeedCells, nch);
+    const uint32_t nr_max = nch > ns ? min(nch - ns, K.front_rest) : 0u;
     if constexpr (!kTableReady) {
         const uint4* src = reinterpret_cast<const uint4*>(Wk.lut + static_cast<uint64_t>(qi) * TB);
         for (uint32_t i = tid; i < TB / 16; i += nt) reinterpret_cast<uint4*>(table)[i] = src[i];
@@ -1173,20 +1199,29 @@ __device__ __forceinline__ void seed_phase(const DevArena& A, const Work& Wk, co
     for (uint32_t i = tid; i < A.MW; i += nt) probed[i] = 0;
     for (uint32_t i = tid; i < 512; i += nt) coarse[i] = 0;  // coarse and fine
     if (tid < kWave) {
+        // the seed cells, and with the same loads the rest cells that the seed stage may scan
         uint32_t c = 0, e0 = 0, len = 0;
-        if (tid < ns) {
+        if (tid < ns + nr_max) {
             c = chosen[tid];
             e0 = A.mem_off[c];
             len = A.mem_off[c + 1] - e0;
         }
-        uint32_t x = wave_incl_scan_u32(len);
+        const bool rest = tid >= ns && tid < ns + nr_max;
+        const uint32_t x = wave_incl_scan_u32(tid < ns ? len : 0u);
+        const uint32_t xr = wave_incl_scan_u32(rest ? len : 0u);
         if (tid < ns) {
             misc[kOff + tid + 1] = x;
             misc[kCell + tid] = c;
             misc[kE0 + tid] = e0;
         }
+        if (rest) {
+            misc[kROff + tid - ns + 1] = xr;
+            misc[kRCell + tid - ns] = c;
+            misc[kRE0 + tid - ns] = e0;
+        }
         if (tid == 0) {
             misc[kOff] = 0;
+            misc[kROff] = 0;
             misc[kCnt] = 0;
             misc[kKeep] = 0;
         }
@@ -1273,6 +1308,41 @@ __device__ __forceinline__ void seed_phase(const DevArena& A, const Work& Wk, co
     }
     __syncthreads();
     const uint32_t cnt = misc[kCnt];
+    // ---- each thread's first two members of the first rest cells, loaded now so that their
+    // latency passes under tau, the keep and the adaptive cut. Which of the cells are scanned
+    // depends on those (ranks [ns, r_in) below): members past them are loaded but not kept.
+    const bool filt = K.filter != 0;
+    struct RMem {
+        Code<NW> code;
+        uint64_t e;
+        uint32_t c, alt, tag, slot;
+    };
+    // member it (< tot) of the rest cells whose offsets are roff (roff[k] = offset of cell k)
+    auto rfetch = [&](uint32_t it, uint32_t tot, const uint32_t (&roff)[kFrontRestMax], RMem& m) {
+        const uint32_t j = min(it, tot - 1);
+        uint32_t s = 0;
+#pragma unroll
+        for (uint32_t k = 1; k < kFrontRestMax; ++k) s += j >= roff[k];
+        m.c = misc[kRCell + s];
+        m.e = static_cast<uint64_t>(misc[kRE0 + s]) + (j - misc[kROff + s]);
+        m.code.load(A.codes + m.e * (2 * NW));
+        m.alt = A.ma == 2 ? A.entry_alt[m.e] : kNoAlt;
+        m.tag = filt ? A.entry_tag[m.e] : 0u;
+        m.slot = A.members[m.e];
+    };
+    auto rest_offsets = [&](uint32_t nr, uint32_t (&roff)[kFrontRestMax]) {
+#pragma unroll
+        for (uint32_t k = 1; k < kFrontRestMax; ++k)
+            roff[k] = k < nr ? __builtin_amdgcn_readfirstlane(misc[kROff + k]) : 0xFFFFFFFFu;
+    };
+    const uint32_t rtot_max = misc[kROff + nr_max];
+    RMem ra, rb;
+    if (rtot_max > 0) {
+        uint32_t roff[kFrontRestMax];
+        rest_offsets(nr_max, roff);
+        rfetch(tid, rtot_max, roff, ra);
+        rfetch(tid + nt, rtot_max, roff, rb);
+    }
     // ---- tau = target-th smallest seed d (two 256-bin passes, scanned by wave 0)
     uint32_t tau = A.maxk;
     if (cnt >= K.target) {
@@ -1384,50 +1454,15 @@ __device__ __forceinline__ void seed_phase(const DevArena& A, const Work& Wk, co
     // candidates, as the cell-major scan would emit them (src/index.rs:2231-2275)
     const uint32_t r_in = min(rest_end, ns + K.front_rest);
     if (r_in > ns) {
-        const uint32_t nr = r_in - ns;
-        if (tid < kWave) {
-            uint32_t c = 0, e0 = 0, len = 0;
-            if (tid < nr) {
-                c = chosen[ns + tid];
-                e0 = A.mem_off[c];
-                len = A.mem_off[c + 1] - e0;
-            }
-            uint32_t x = wave_incl_scan_u32(len);
-            if (tid < nr) {
-                misc[kOff + tid + 1] = x;
-                misc[kCell + tid] = c;
-                misc[kE0 + tid] = e0;
-            }
-            if (tid == 0) {
-                misc[kOff] = 0;
-                misc[kCnt] = 0;
-            }
-        }
+        const uint32_t nr = r_in - ns;  // <= nr_max
+        if (tid == 0) misc[kCnt] = 0;
         __syncthreads();
-        const uint32_t rtotal = misc[kOff + nr];
+        const uint32_t rtotal = misc[kROff + nr];
         uint32_t roff[kFrontRestMax];
-#pragma unroll
-        for (uint32_t k = 1; k < kFrontRestMax; ++k)
-            roff[k] = k < nr ? __builtin_amdgcn_readfirstlane(misc[kOff + k]) : 0xFFFFFFFFu;
+        rest_offsets(nr, roff);
         if (rtotal > 0) {
-            const bool filt = K.filter != 0;
-            struct RMem {
-                Code<NW> code;
-                uint64_t e;
-                uint32_t c, alt, tag, slot;
-            };
-            auto fetch = [&](uint32_t it, RMem& m) {
-                const uint32_t j = min(it, rtotal - 1);
-                uint32_t s = 0;
-#pragma unroll
-                for (uint32_t k = 1; k < kFrontRestMax; ++k) s += j >= roff[k];
-                m.c = misc[kCell + s];
-                m.e = static_cast<uint64_t>(misc[kE0 + s]) + (j - misc[kOff + s]);
-                m.code.load(A.codes + m.e * (2 * NW));
-                m.alt = A.ma == 2 ? A.entry_alt[m.e] : kNoAlt;
-                m.tag = filt ? A.entry_tag[m.e] : 0u;
-                m.slot = A.members[m.e];
-            };
+            // (the members below rtotal are the same under nr_max's offsets as under nr's)
+            auto fetch = [&](uint32_t it, RMem& m) { rfetch(it, rtotal, roff, m); };
             auto keep = [&](const RMem& m, bool have, uint32_t& dv) {
                 dv = A.maxk - lut_sum1<NW>(m.code, table);
                 if (!have || dv > tau) return false;
@@ -1439,9 +1474,7 @@ __device__ __forceinline__ void seed_phase(const DevArena& A, const Work& Wk, co
                 return pass && (!filt || (m.tag >= K.tag_lo && m.tag <= K.tag_hi));
             };
             uint2* cand = Wk.cand + static_cast<uint64_t>(qi) * K.cand_cap;
-            RMem a, b;
-            fetch(tid, a);
-            fetch(tid + nt, b);
+            RMem a = ra, b = rb;
             for (uint32_t r = 0; r < rtotal; r += 2 * nt) {
                 const bool more = r + 2 * nt < rtotal;
                 RMem na, nb;
@@ -1659,12 +1692,12 @@ __global__ void __launch_bounds__(256) hamming_mma_kernel(DevArena A, Work Wk, u
 
 // Prep, route and seed of one query in one workgroup, for codes over the whole padded dimension
 // (n_words * 64 == dim_pad, so prep's coordinates per lane equal NW). Wave 0 computes the query's
-// rotation and code (prep_wave_codes) while the other waves clear the route's histogram; then wave
-// 0 builds the FastScan table and sums (prep_wave_tables) while the others compute the Hamming row
-// and stage the rescore operand; then every wave routes and seeds the query. Each phase reads what
-// the previous ones wrote to global memory after the barrier between them. LDS: the route's
-// regions (route_phase's layout) | the prep region (codes[16] u64 | x[P] | mins | cqp | rqp); the
-// seed phase reuses all of it.
+// rotation, code and rescore operand (prep_wave_codes, the operand straight into the route's LDS)
+// while the other waves clear the route's histogram and load their first cell codes; then wave 0
+// builds the FastScan table and sums (prep_wave_tables) while the others compute the Hamming row
+// from the code in LDS; then every wave routes and seeds the query. LDS: the route's regions
+// (route_phase's layout) | the prep region (codes[16] u64 | x[P] | mins | cqp | rqp); the seed
+// phase reuses all of it.
 template <int NW>
 __global__ void __launch_bounds__(kSeedThreads, NW >= 16 ? 3 : 4)
 front_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries) {
@@ -1679,20 +1712,20 @@ front_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ queries) 
     uint32_t* scratch = hist + ((nbins + 3) & ~3u);
     uint8_t* prep = smem + route_lds_bytes(d, NW, A.Mp, K.sort_cap, K.nprobe);
     float* xs = reinterpret_cast<float*>(prep + 16 * 8);
+    // (waves 1-3 clear the histogram and put their first Hamming loads in flight before the barrier
+    // that waits for the code; the rescore operand goes straight to the route's LDS)
     if (tid < kWave) {
-        prep_wave_codes<NW>(A, Wk, queries, qi, lane_id(), xs, reinterpret_cast<uint64_t*>(prep));
-    } else {
-        for (uint32_t i = tid - kWave; i < nbins; i += nt - kWave) hist[i] = 0;
-    }
-    __syncthreads();
-    if (tid < kWave) {
+        prep_wave_codes<NW>(A, Wk, queries, qi, lane_id(), xs, reinterpret_cast<uint64_t*>(prep), cqs);
+        __syncthreads();
         prep_wave_tables(A, Wk, qi, lane_id(), xs, seed_table<NW>());
     } else {
-        for (uint32_t i = tid - kWave; i < d; i += nt - kWave) cqs[i] = Wk.cqs[static_cast<uint64_t>(qi) * d + i];
-        hamming_row<NW>(A, Wk, qi, hist, reinterpret_cast<uint16_t*>(scratch + 16), tid - kWave, nt - kWave);
+        for (uint32_t i = tid - kWave; i < nbins; i += nt - kWave) hist[i] = 0;
+        hamming_row<NW>(A, Wk, qi, hist, reinterpret_cast<uint16_t*>(scratch + 16), tid - kWave, nt - kWave,
+                        reinterpret_cast<const uint64_t*>(prep), [] { __syncthreads(); });
     }
     __syncthreads();
-    route_phase<NW, true>(A, Wk, K, qi);
+    // (the rotated query x[P] is free once the table is built: it carries the route's bounds)
+    route_phase<NW, true>(A, Wk, K, qi, nullptr, nullptr, 0, A.P >= nt ? xs : nullptr);
     __syncthreads();
     seed_phase<NW, true>(A, Wk, K, qi);
 }

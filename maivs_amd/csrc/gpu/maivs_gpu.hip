@@ -103,10 +103,10 @@ size_t prep1_lds(const DevArena& A) {
 // The fused front kernel runs when the code covers the whole padded dimension.
 bool fused_front(const DevArena& A) { return static_cast<uint64_t>(A.W) * 64 == A.P; }
 
-// Dynamic LDS of seed: probed[MW4] | coarse[256] | fine[256] | misc[32] | sbuf[seed_cap8] u16
+// Dynamic LDS of seed: probed[MW4] | coarse[256] | fine[256] | misc[64] | sbuf[seed_cap8] u16
 // (plus its static table of W*256 bytes)
 size_t seed_lds(const DevArena& A, uint32_t seed_cap) {
-    return ((A.MW + 3) & ~3u) * 4 + 512 * 4 + 32 * 4 + static_cast<size_t>((seed_cap + 7) & ~7u) * 2;
+    return ((A.MW + 3) & ~3u) * 4 + 512 * 4 + 64 * 4 + static_cast<size_t>((seed_cap + 7) & ~7u) * 2;
 }
 
 // LDS of finish: hist[256] | scratch[32] | qs[d4] | ent[kFinishLdsCap] (d, slot) | keys[kFinishLdsCap] u64
