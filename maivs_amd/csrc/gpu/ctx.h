@@ -55,6 +55,10 @@ struct maivs_gpu_ctx {
     uint32_t pq_front_max_q = 64;            // the per-query path's fused prep + tree + route up to this many queries
     uint32_t pq_finish_split_max_q = 64;     // the per-query path's rerank spread over workgroups up to this many queries
     Ctl* h_ctl = nullptr;  // pinned host copy of the control block (read after each pass)
+    // pinned staging of the host-buffer entry points (queries in, slots and scores out), grown on
+    // demand and kept for the context's life
+    void* h_stage = nullptr;
+    size_t h_stage_bytes = 0;
     hipEvent_t ev[8] = {};
     // last call, for maivs_gpu_last_candidates / maivs_gpu_last_counters
     uint32_t last_nq = 0, last_fin_cap = 0;

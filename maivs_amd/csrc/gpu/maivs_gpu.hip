@@ -1370,6 +1370,7 @@ void maivs_gpu_destroy(maivs_gpu_ctx* ctx) {
     for (auto& e : ctx->ev)
         if (e) (void)hipEventDestroy(e);
     if (ctx->h_ctl) (void)hipHostFree(ctx->h_ctl);
+    if (ctx->h_stage) (void)hipHostFree(ctx->h_stage);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
 }
@@ -1790,6 +1791,38 @@ int maivs_gpu_search_batch_device_noalloc(maivs_gpu_ctx* ctx, const float* d_q, 
     return 0;
 }
 
+// The host-buffer entry points' copies: the queries through the context's pinned staging buffer to
+// the device, `run` on them, and the slots and scores back through the same buffer (a pinned copy
+// runs at the link's rate; a pageable one goes through the runtime's own staging in pieces).
+extern "C++" template <class Run>
+static int staged_search(maivs_gpu_ctx* ctx, const float* q, uint32_t nq, uint32_t k, uint32_t* out_slots,
+                         float* out_scores, Run run) {
+    const size_t qb = static_cast<size_t>(nq) * ctx->A.d * 4, ob = static_cast<size_t>(nq) * k * 4;
+    const size_t need = std::max(qb, 2 * ob);
+    if (need > ctx->h_stage_bytes) {
+        if (ctx->h_stage) HIP_TRY(ctx, hipHostFree(ctx->h_stage));
+        ctx->h_stage = nullptr;
+        ctx->h_stage_bytes = 0;
+        if (hipHostMalloc(&ctx->h_stage, need, hipHostMallocDefault) != hipSuccess) {
+            ctx->h_stage = nullptr;
+            return fail(ctx, MAIVS_ERR_OOM, "pinned staging of %zu bytes", need);
+        }
+        ctx->h_stage_bytes = need;
+    }
+    uint8_t* h = static_cast<uint8_t*>(ctx->h_stage);
+    std::memcpy(h, q, qb);
+    HIP_TRY(ctx, hipMemcpyAsync(ctx->Wk.q, h, qb, hipMemcpyHostToDevice, ctx->stream));
+    int rc = run();
+    if (rc) return rc;
+    // (the queries' copy has finished before the kernels that read them, so the buffer is free)
+    HIP_TRY(ctx, hipMemcpyAsync(h, ctx->Wk.out_slots, ob, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(ctx, hipMemcpyAsync(h + ob, ctx->Wk.out_scores, ob, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    std::memcpy(out_slots, h, ob);
+    std::memcpy(out_scores, h + ob, ob);
+    return 0;
+}
+
 int maivs_gpu_search_batch(maivs_gpu_ctx* ctx, const float* q, uint32_t nq, const maivs_search_params* p,
                            uint32_t* out_slots, float* out_scores, maivs_gpu_stats* st) {
     if (!ctx || !p || (nq && (!q || !out_slots || !out_scores))) return MAIVS_ERR_ARG;
@@ -1799,15 +1832,9 @@ int maivs_gpu_search_batch(maivs_gpu_ctx* ctx, const float* q, uint32_t nq, cons
     if (nq == 0) return 0;
     int rc = ensure_all(ctx, nq, p->nprobe, p->k);
     if (rc) return rc;
-    HIP_TRY(ctx, hipMemcpyAsync(ctx->Wk.q, q, static_cast<size_t>(nq) * ctx->A.d * 4, hipMemcpyHostToDevice, ctx->stream));
-    rc = run_search(ctx, ctx->Wk.q, nq, p, ctx->Wk.out_slots, ctx->Wk.out_scores, st);
-    if (rc) return rc;
-    HIP_TRY(ctx, hipMemcpyAsync(out_slots, ctx->Wk.out_slots, static_cast<size_t>(nq) * p->k * 4, hipMemcpyDeviceToHost,
-                                ctx->stream));
-    HIP_TRY(ctx, hipMemcpyAsync(out_scores, ctx->Wk.out_scores, static_cast<size_t>(nq) * p->k * 4,
-                                hipMemcpyDeviceToHost, ctx->stream));
-    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
-    return 0;
+    return staged_search(ctx, q, nq, p->k, out_slots, out_scores, [&] {
+        return run_search(ctx, ctx->Wk.q, nq, p, ctx->Wk.out_slots, ctx->Wk.out_scores, st);
+    });
 }
 
 int maivs_gpu_search_queries_device(maivs_gpu_ctx* ctx, const float* d_q, uint32_t nq, const maivs_search_params* p,
@@ -1827,15 +1854,9 @@ int maivs_gpu_search_queries(maivs_gpu_ctx* ctx, const float* q, uint32_t nq, co
     if (nq == 0) return 0;
     int rc = ensure_all(ctx, nq, p->nprobe, p->k);
     if (rc) return rc;
-    HIP_TRY(ctx, hipMemcpyAsync(ctx->Wk.q, q, static_cast<size_t>(nq) * ctx->A.d * 4, hipMemcpyHostToDevice, ctx->stream));
-    rc = run_search_pq(ctx, ctx->Wk.q, nq, p, ctx->Wk.out_slots, ctx->Wk.out_scores, st);
-    if (rc) return rc;
-    HIP_TRY(ctx, hipMemcpyAsync(out_slots, ctx->Wk.out_slots, static_cast<size_t>(nq) * p->k * 4, hipMemcpyDeviceToHost,
-                                ctx->stream));
-    HIP_TRY(ctx, hipMemcpyAsync(out_scores, ctx->Wk.out_scores, static_cast<size_t>(nq) * p->k * 4,
-                                hipMemcpyDeviceToHost, ctx->stream));
-    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
-    return 0;
+    return staged_search(ctx, q, nq, p->k, out_slots, out_scores, [&] {
+        return run_search_pq(ctx, ctx->Wk.q, nq, p, ctx->Wk.out_slots, ctx->Wk.out_scores, st);
+    });
 }
 
 int maivs_gpu_query_prep(maivs_gpu_ctx* ctx, const float* q, uint32_t nq, uint64_t* out_bits, uint8_t* out_lut,

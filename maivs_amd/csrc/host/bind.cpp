@@ -34,6 +34,35 @@ F32Rows as_rows(const py::array& a, const char* what, const char* contig_msg) {
     return {static_cast<const float*>(a.data()), static_cast<size_t>(a.shape(0)), static_cast<size_t>(a.shape(1))};
 }
 
+// Flat Python lists of the results, as the reference returns them: one allocation for the list and
+// one object per entry (the C API directly, without the generic caster's per-element checks).
+py::list ids_list(const std::vector<uint64_t>& v) {
+    PyObject* l = PyList_New(static_cast<Py_ssize_t>(v.size()));
+    if (!l) throw py::error_already_set();
+    for (size_t i = 0; i < v.size(); ++i) {
+        PyObject* o = PyLong_FromUnsignedLongLong(v[i]);
+        if (!o) {
+            Py_DECREF(l);
+            throw py::error_already_set();
+        }
+        PyList_SET_ITEM(l, static_cast<Py_ssize_t>(i), o);
+    }
+    return py::reinterpret_steal<py::list>(l);
+}
+py::list scores_list(const std::vector<float>& v) {
+    PyObject* l = PyList_New(static_cast<Py_ssize_t>(v.size()));
+    if (!l) throw py::error_already_set();
+    for (size_t i = 0; i < v.size(); ++i) {
+        PyObject* o = PyFloat_FromDouble(static_cast<double>(v[i]));
+        if (!o) {
+            Py_DECREF(l);
+            throw py::error_already_set();
+        }
+        PyList_SET_ITEM(l, static_cast<Py_ssize_t>(i), o);
+    }
+    return py::reinterpret_steal<py::list>(l);
+}
+
 // Index errors cross into Python through a registered translator (it runs with the GIL held,
 // so C++ code may throw them from regions that released the GIL).
 template <class F>
@@ -201,7 +230,7 @@ PYBIND11_MODULE(_maivs, m) {
                     py::gil_scoped_release nogil;
                     translate([&] { s.ix.search(qc.data(), k, nprobe, tc, beta, ids, scores); });
                 }
-                return py::make_tuple(py::cast(ids), py::cast(scores));
+                return py::make_tuple(ids_list(ids), scores_list(scores));
             },
             py::arg("query"), py::arg("k"), py::arg("nprobe") = 16, py::arg("target_confidence") = 0.95f,
             py::arg("beta") = 8.0f)
@@ -223,7 +252,7 @@ PYBIND11_MODULE(_maivs, m) {
                     py::gil_scoped_release nogil;
                     translate([&] { s.ix.search_batch(q, nq, k, nprobe, tc, beta, cell_major, ids, scores, &s.last); });
                 }
-                return py::make_tuple(py::cast(ids), py::cast(scores));
+                return py::make_tuple(ids_list(ids), scores_list(scores));
             },
             py::arg("queries"), py::arg("k"), py::arg("nprobe") = 16, py::arg("target_confidence") = 0.95f,
             py::arg("beta") = 8.0f, py::arg("cell_major") = true)
