@@ -1392,7 +1392,12 @@ int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* a) {
     if (!(fs_arena || a->slot_codes || from_store) || !a->mem_off || !a->members || !a->rot_signs || !a->r_bound)
         return fail(ctx, MAIVS_ERR_ARG, "arena is missing its codes (FastScan blocks or per-slot codes), members, "
                                         "rotation or radii");
+    if (a->n_cells == 0) return fail(ctx, MAIVS_ERR_ARG, "the arena has no cells");
     if (!supported_nw(a->n_words)) return fail(ctx, MAIVS_ERR_UNSUPPORTED, "n_words %u not in {1,2,4,8,16}", a->n_words);
+    // (the Hamming rows address the cell codes with 32-bit byte offsets)
+    if (static_cast<uint64_t>(a->n_cells) * a->n_words * 8 >= (1ull << 32))
+        return fail(ctx, MAIVS_ERR_UNSUPPORTED, "%u cells of %u-word codes exceed 4 GiB of cell codes", a->n_cells,
+                    a->n_words);
     if (a->max_assign > 1 && !a->slot_cells) return fail(ctx, MAIVS_ERR_ARG, "slot_cells missing");
     if (a->max_assign > 1) {
         // homes index per-cell bitsets on the device: every one must name a cell
