@@ -461,3 +461,24 @@ def test_small_arena_upload_keeps_larger_lds_limits(mix50k):
     finally:
         ca.close()
         cb.close()
+
+
+def test_upload_refuses_an_arena_without_cells(quality50k, mix50k):
+    """An arena description with no cells is refused at upload with an argument error (every kernel
+    indexes cell 0's code), and the context still uploads and searches a good arena afterwards."""
+    import ctypes as C
+    _, queries, _ = mix50k
+    ix = quality50k
+    bad = capi.ArenaDesc.from_buffer_copy(capi.ArenaDesc.from_address(ix._arena_desc()))
+    bad.n_cells = 0
+    c = capi.Context(0)
+    try:
+        with pytest.raises(capi.GpuError, match="no cells"):
+            c.upload(C.addressof(bad))
+        c.upload(ix._arena_desc())
+        p = _params(ix, 10, 8)
+        s, v = c.search(queries[:64], p)
+        o_s, o_v = oracle.search_batch(ix._arena_desc(), queries[:64], p, 8)
+        assert np.array_equal(s, o_s) and v.tobytes() == o_v.tobytes()
+    finally:
+        c.close()
