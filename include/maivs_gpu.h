@@ -168,13 +168,16 @@ int maivs_gpu_create(int device, maivs_gpu_ctx** out);
 void maivs_gpu_destroy(maivs_gpu_ctx* ctx);
 const char* maivs_gpu_last_error(const maivs_gpu_ctx* ctx);
 
-/* Copy the compacted arena to HBM (replaces any previous one). */
+/* Copy the compacted arena to HBM (replaces any previous one). An arena without cells is refused
+ * (MAIVS_ERR_ARG), and so is one whose cell codes exceed 4 GiB (MAIVS_ERR_UNSUPPORTED). */
 int maivs_gpu_upload_arena(maivs_gpu_ctx* ctx, const maivs_arena_desc* arena);
 
 /*
  * Batched cell-major search. Host buffers: queries nq x dim (f32, row-major), outputs nq x k.
  * out_slots[q*k + i] is the arena slot of the i-th best result of query q, best first, ties by
- * ascending slot; rows with fewer than k results are padded with UINT32_MAX / -inf.
+ * ascending slot; rows with fewer than k results are padded with UINT32_MAX / -inf. The copies
+ * go through a pinned staging buffer the context allocates on first use and keeps (grown to the
+ * largest call).
  */
 int maivs_gpu_search_batch(maivs_gpu_ctx* ctx, const float* queries, uint32_t nq,
                            const maivs_search_params* params, uint32_t* out_slots,
