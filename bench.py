@@ -91,8 +91,8 @@ def main() -> int:
     args = ap.parse_args()
 
     if args.gpus != 1:
-        print(f"bench.py runs on one GPU; --gpus {args.gpus} is not supported by this build "
-              f"(the multi-GPU sharding is a design, see the design notes)", file=sys.stderr)
+        print(f"bench.py runs on one GPU; --gpus {args.gpus} is not supported "
+              f"(the search's sharding across GPUs is designed but not built)", file=sys.stderr)
         return 2
 
     if args.workload == "churn400k":

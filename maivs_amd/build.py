@@ -3,8 +3,8 @@
 * ``libmaivs_gpu.so`` - the HIP kernels and the C ABI (``include/maivs_gpu.h``), hipcc for gfx950.
 * ``_maivs*.so``      - the host index (build path) and the Python binding, g++ + pybind11.
 
-Both land next to this file so the package (and a GPU box snapshot of the tree) loads them
-without installation. Run ``python -m maivs_amd.build``.
+Both land next to this file, so the package loads them from the source tree without
+installation. Run ``python -m maivs_amd.build``.
 """
 from __future__ import annotations
 

@@ -177,7 +177,7 @@ void FlatCellIndex::set_tree_route(bool on, size_t min_cells, size_t fanout, flo
 }
 
 void FlatCellIndex::set_graph_route(bool on, size_t min_cells) {  // :2860-2866
-    // The centroid HNSW itself is not part of this build; only whether the reference would hold
+    // The centroid HNSW itself is not implemented by this library; only whether the reference would hold
     // one (rebuild_centroid_graph, :625-636) is tracked, so that searches it would route refuse.
     graph_route_ = on;
     if (min_cells > 0) graph_min_cells_ = min_cells;
@@ -217,7 +217,7 @@ void FlatCellIndex::set_per_dim_sq(bool on) {  // :2908-2915
 }
 
 void FlatCellIndex::set_f16_rerank(bool on) {  // :2922-2928
-    if (on) throw Unsupported("the f16 rerank store is not part of this build (f32 or per-dimension SQ8 only)");
+    if (on) throw Unsupported("the f16 rerank store is not implemented by this library (f32 or per-dimension SQ8 only)");
     f16_rerank_ = false;
 }
 
@@ -1057,14 +1057,14 @@ void FlatCellIndex::compact_arena() {  // src/index.rs:929-1112
 
 std::string FlatCellIndex::cellmajor_blocker(bool cell_major) const {
     // the cm_ok gate of src/index.rs:3343-3348, plus what the MI355X path needs
-    if (!cell_major) return "cell_major=False selects the per-query path, which is not part of this build";
+    if (!cell_major) return "cell_major=False selects the per-query path";
     if (scan_mode_ != ScanMode::Binary) return "the batched path needs scan_mode='binary'";
     if (!compacted_) return "the index is not compacted (call compact() after add_batch/remove)";
     if (!(max_assign_ == 1 || !rep_off_.empty())) return "polysemic runs are missing (compact() again)";
     if (!fastscan_ || fs_off_.empty()) return "the MI355X scan needs set_fastscan(True) before compact()";
     if (!(two_stage_ && !cent_bits_.empty()) && !tree_ && graph_built_)
-        return "the centroid-graph router is not part of this build (set_graph_route(False, ...))";
-    if (f16_rerank_) return "the f16 rerank store is not part of this build";
+        return "the centroid-graph router is not implemented by this library (set_graph_route(False, ...))";
+    if (f16_rerank_) return "the f16 rerank store is not implemented by this library";
     if (!per_dim_sq_ && (!keep_f32_ || vecs_f32_.empty()))
         return "the rerank needs the f32 rows or the per-dimension SQ8 store";
     if (n_words_ * 64 > 65536) return "codes longer than 65536 bits";
@@ -1161,15 +1161,15 @@ std::string FlatCellIndex::perquery_blocker() const {
     if (scan_mode_ != ScanMode::Binary) return "the per-query path needs scan_mode='binary'";
     if (!(fastscan_ && compacted_ && !fs_off_.empty())) {
         // the Hamming branch (src/index.rs:1694-1760)
-        if (asym_cascade_ > 0) return "the asymmetric cascade (set_asym_cascade) is not part of this build";
+        if (asym_cascade_ > 0) return "the asymmetric cascade (set_asym_cascade) is not implemented by this library";
         if (bits_.size() < ext_ids_.size() * n_words_ || bits_.empty())
             return "the Hamming scan needs the per-slot sign codes";
     }
     if (!tree_ && graph_built_)
-        return "the centroid-graph router is not part of this build (set_graph_route(False, ...))";
+        return "the centroid-graph router is not implemented by this library (set_graph_route(False, ...))";
     if (par_scan_ && !adaptive_ && max_assign_ <= 1)
-        return "set_parallel_scan's within-query parallel scan is not part of this build";
-    if (f16_rerank_) return "the f16 rerank store is not part of this build";
+        return "set_parallel_scan's within-query parallel scan is not implemented by this library";
+    if (f16_rerank_) return "the f16 rerank store is not implemented by this library";
     if (!per_dim_sq_ && (!keep_f32_ || vecs_f32_.empty()))
         return "the rerank needs the f32 rows or the per-dimension SQ8 store";
     if (n_words_ * 64 > 65536) return "codes longer than 65536 bits";

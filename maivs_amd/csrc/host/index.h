@@ -4,7 +4,7 @@
 //
 // Reference: the pyo3 class FlatCellIndex, src/index.rs:431-566 (state) and :2670-3603
 // (methods). Only the state the batched cell-major search, its build and persistence need is
-// kept; the per-query path, HNSW routing and split/merge are not part of this build.
+// kept; HNSW routing and split/merge are not implemented by this library.
 #pragma once
 
 #include <cstdint>

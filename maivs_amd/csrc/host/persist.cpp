@@ -130,7 +130,7 @@ void FlatCellIndex::save(const std::string& path) const {  // src/persist.rs:80-
     w.f32(tree_beam_frac_);
     w.pod(bits_);
     w.pod(scan_i8_);
-    w.pod(std::vector<uint16_t>{});  // rr_f16: this build keeps no f16 rerank store
+    w.pod(std::vector<uint16_t>{});  // rr_f16: this library keeps no f16 rerank store
     w.pod(sq_min_);
     w.pod(sq_step_);
     w.pod(vecs_f32_);
@@ -200,7 +200,7 @@ void FlatCellIndex::load_file(const std::string& path) {  // src/persist.rs:145-
             for (uint64_t& v : ext) v = r.u64();
         }
     }
-    if (!rr_f16.empty()) throw Unsupported("the index file holds an f16 rerank store, which this build does not keep");
+    if (!rr_f16.empty()) throw Unsupported("the index file holds an f16 rerank store, which this library does not keep");
 
     // The reference trusts the file; the arena is uploaded to the GPU, so the sizes are checked.
     const uint64_t dim = h[0], dim_pad = h[3], nw = h[4], ma = h[7];

@@ -1,7 +1,7 @@
 /*
  * The oracle: a CPU restatement of MAIVS's batched cell-major search, used only by the tests,
- * by __graft_entry__.smoke() and by bench.py's cpu_baseline leg, as the checker and as the
- * timed CPU baseline. Never linked into or called by the product library.
+ * by __graft_entry__.smoke() and by bench.py's cpu_baseline leg, to check the GPU's results and as
+ * the timed CPU baseline. Never linked into or called by the product library.
  *
  * Every function cites the reference file:line (V47VANSH/MAIVS) it restates. The arena and
  * parameters are the same POD structs the GPU library takes (include/maivs_gpu.h).

@@ -147,7 +147,7 @@ def test_binding_errors_and_padding():
     p = np.frombuffer(ix._search_params(5, 8, 1.0, 1.0), np.uint32)
     assert p[-1] == 1  # route_mode 1: route_query's routing
     # a centroid graph exists once graph routing is on past min_cells live cells (src/index.rs:625-636);
-    # the graph router is not part of this build, so a search it would route refuses
+    # the graph router is not implemented by this library, so a search it would route refuses
     ix.set_graph_route(True, 8)
     assert "graph" in ix.perquery_blocker()
     ix.set_graph_route(False, 0)

@@ -4,7 +4,7 @@ The reference's own checks (tests/test_index.py:184-217, 490-512) are restated h
 quant_scale and the cell count survive a reload; deleted ids stay deleted; with no mutation in
 between, save -> load (-> set_fastscan(True); compact()) is an identity. The byte layout is pinned
 by an independent reader written from src/persist.rs:145-199, which must consume exactly the
-reference's blocks and stop at this build's extension trailer. A file without the trailer (what
+reference's blocks and stop at this library's extension trailer. A file without the trailer (what
 the reference writes) loads with the reference's defaults.
 """
 import os
@@ -110,7 +110,7 @@ def test_file_layout_is_the_reference_format(small_index, tmp_path):
     cent = np.stack([c[2] for c in cells])
     assert np.array_equal(cent.reshape(-1), a["centroids"])
     assert np.array_equal(np.array([c[3] for c in cells], np.float32), a["r_bound"])
-    # the reference stops here; the rest is this build's trailer
+    # the reference stops here; the rest is this library's trailer
     assert buf[end:end + 8] == TRAILER
     (nf,) = struct.unpack_from("<Q", buf, end + 8)
     assert len(buf) == end + 16 + 8 * nf
