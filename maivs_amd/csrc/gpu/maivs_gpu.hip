@@ -1805,6 +1805,8 @@ static int staged_search(maivs_gpu_ctx* ctx, const float* q, uint32_t nq, uint32
     const size_t qb = static_cast<size_t>(nq) * ctx->A.d * 4, ob = static_cast<size_t>(nq) * k * 4;
     const size_t need = std::max(qb, 2 * ob);
     if (need > ctx->h_stage_bytes) {
+        // (no copy of an earlier call may still read the old buffer)
+        if (ctx->h_stage) HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
         if (ctx->h_stage) HIP_TRY(ctx, hipHostFree(ctx->h_stage));
         ctx->h_stage = nullptr;
         ctx->h_stage_bytes = 0;
@@ -1818,7 +1820,10 @@ static int staged_search(maivs_gpu_ctx* ctx, const float* q, uint32_t nq, uint32
     std::memcpy(h, q, qb);
     HIP_TRY(ctx, hipMemcpyAsync(ctx->Wk.q, h, qb, hipMemcpyHostToDevice, ctx->stream));
     int rc = run();
-    if (rc) return rc;
+    if (rc) {
+        (void)hipStreamSynchronize(ctx->stream);  // the queries' copy out of the buffer is done
+        return rc;
+    }
     // (the queries' copy has finished before the kernels that read them, so the buffer is free)
     HIP_TRY(ctx, hipMemcpyAsync(h, ctx->Wk.out_slots, ob, hipMemcpyDeviceToHost, ctx->stream));
     HIP_TRY(ctx, hipMemcpyAsync(h + ob, ctx->Wk.out_scores, ob, hipMemcpyDeviceToHost, ctx->stream));
