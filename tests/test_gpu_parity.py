@@ -482,3 +482,25 @@ def test_upload_refuses_an_arena_without_cells(quality50k, mix50k):
         assert np.array_equal(s, o_s) and v.tobytes() == o_v.tobytes()
     finally:
         c.close()
+
+
+def test_host_buffer_calls_grow_the_staging(quality50k, mix50k):
+    """The host-buffer entry points stage queries and results through one pinned buffer that grows
+    with the call: batches of rising and falling size on one context, through both entry points,
+    each equal to the oracle."""
+    _, queries, _ = mix50k
+    ix = quality50k
+    c = capi.Context(0)
+    try:
+        c.upload(ix._arena_desc())
+        p = _params(ix, 10, 8)
+        for n in (3, 64, 700, 5, 1000, 2):
+            q = np.ascontiguousarray(queries[:n])
+            s, v = c.search(q, p)
+            o_s, o_v = oracle.search_batch(ix._arena_desc(), q, p, 8)
+            assert np.array_equal(s, o_s) and v.tobytes() == o_v.tobytes(), n
+            s, v = c.search_queries(q, p)
+            o_s, o_v = oracle.search_one(ix._arena_desc(), q, p, nthreads=8)
+            assert np.array_equal(s, o_s) and v.tobytes() == o_v.tobytes(), n
+    finally:
+        c.close()
