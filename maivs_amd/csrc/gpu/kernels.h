@@ -2177,20 +2177,22 @@ cell_mma_kernel(DevArena A, Work Wk, KParams K) {
         // every wave reads the item's bucket entries itself (lane j: query j), so its table loads
         // follow the bucket read directly; wave 0 also publishes them for the settle
         const uint32_t qj = j < nqi ? Wk.qbuck[static_cast<uint64_t>(c) * K.bucket_cap + g0 + j] : kNone;
-        // B operands: this wave's quarter of query j's table, 128 subtracted from every byte
+        // B operands: this wave's quarter of query j's table, 128 subtracted from every byte. The
+        // loads are unconditional (an empty column j reads query 0's table; its sums are never
+        // kept), so all SPW of them are in flight together instead of one round trip each.
         mma_v4 bq[SPW];
         {
             const uint4* lut = reinterpret_cast<const uint4*>(Wk.lut + static_cast<uint64_t>(qj != kNone ? qj : 0u) * TB);
+            uint4 v[SPW];
 #pragma unroll
-            for (uint32_t s = 0; s < SPW; ++s) {
-                const uint4 v = qj != kNone ? lut[2 * (w * SPW + s) + g] : make_uint4(0u, 0u, 0u, 0u);
-                bq[s] = mma_v4{static_cast<int>(v.x ^ 0x80808080u), static_cast<int>(v.y ^ 0x80808080u),
-                               static_cast<int>(v.z ^ 0x80808080u), static_cast<int>(v.w ^ 0x80808080u)};
-            }
+            for (uint32_t s = 0; s < SPW; ++s) v[s] = lut[2 * (w * SPW + s) + g];
+#pragma unroll
+            for (uint32_t s = 0; s < SPW; ++s)
+                bq[s] = mma_v4{static_cast<int>(v[s].x ^ 0x80808080u), static_cast<int>(v[s].y ^ 0x80808080u),
+                               static_cast<int>(v[s].z ^ 0x80808080u), static_cast<int>(v[s].w ^ 0x80808080u)};
         }
-        const uint32_t tj = qj != kNone ? scan_cut(Wk, K, qj, w == 0) : 0u;  // wave 0 lowers the cuts
-        if (tid < kBucketQ) s_q[tid] = qj;
-        // this wave's code dwords of member t*32 + j (zero past the cell's end)
+        // this wave's code dwords of member t*32 + j (member 0's past the cell's end: the sums of
+        // those rows are never kept, and no select waits for the load)
         auto load_codes = [&](uint32_t t, uint32_t (&dw)[CDW]) {
             const uint32_t mi = t * 32 + j;
             const uint32_t* src = A.codes + static_cast<uint64_t>(e0 + (mi < len ? mi : 0u)) * (2 * NW) + dw_lo;
@@ -2207,22 +2209,24 @@ cell_mma_kernel(DevArena A, Work Wk, KParams K) {
 #pragma unroll
                 for (uint32_t k = 0; k < CDW; ++k) dw[k] = src[k];
             }
-            if (mi >= len) {
-#pragma unroll
-                for (uint32_t k = 0; k < CDW; ++k) dw[k] = 0u;
-            }
         };
         const uint32_t ntile = (len + 31) / 32;
-        uint32_t cur[CDW], nx1[CDW], nx2[CDW];
-        load_codes(0, cur);
-        if (ntile > 1) load_codes(1, nx1);
+        // three code buffers in turn, each loaded two tiles ahead (unconditionally: past the cell's
+        // end the loads read member 0), so a tile waits only for its own codes: with the roles
+        // rotating in code rather than by register copies, the wait counts stay exact
+        uint32_t ca[CDW], cb[CDW], cc[CDW];
+        load_codes(0, ca);
+        load_codes(1, cb);
+        // the query's cut after the tables' and codes' loads: its reads wait for those in flight
+        // (the counter is in order) rather than putting a round trip between them
+        const uint32_t tj = qj != kNone ? scan_cut(Wk, K, qj, w == 0) : 0u;  // wave 0 lowers the cuts
+        if (tid < kBucketQ) s_q[tid] = qj;
         uint32_t n = 0;  // queued survivors (the same in every thread)
-        for (uint32_t t = 0; t < ntile; ++t) {
-            if (t + 2 < ntile) load_codes(t + 2, nx2);
+        auto tile = [&](uint32_t t, const uint32_t (&cd)[CDW]) {
             // nibble * 8 of each of this lane's positions, one per byte
             uint32_t cw8[CDW];
 #pragma unroll
-            for (uint32_t k = 0; k < CDW; ++k) cw8[k] = ((cur[k] >> (4 * g)) & 0x0F0F0F0Fu) << 3;
+            for (uint32_t k = 0; k < CDW; ++k) cw8[k] = ((cd[k] >> (4 * g)) & 0x0F0F0F0Fu) << 3;
             mma_v16 acc = {};
 #pragma unroll
             for (uint32_t s = 0; s < SPW; ++s) {
@@ -2269,11 +2273,16 @@ cell_mma_kernel(DevArena A, Work Wk, KParams K) {
                 }
             }
             n += t0 + t1 + t2 + t3;
-#pragma unroll
-            for (uint32_t k = 0; k < CDW; ++k) {
-                cur[k] = nx1[k];
-                nx1[k] = nx2[k];
-            }
+        };
+        for (uint32_t t = 0; t < ntile; t += 3) {
+            load_codes(t + 2, cc);
+            tile(t, ca);
+            if (t + 1 >= ntile) break;
+            load_codes(t + 3, ca);
+            tile(t + 1, cb);
+            if (t + 2 >= ntile) break;
+            load_codes(t + 4, cb);
+            tile(t + 2, cc);
         }
         __syncthreads();  // the last tile's queue entries are written
         if (n) settle(n, c, e0);
