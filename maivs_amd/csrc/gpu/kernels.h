@@ -533,9 +533,13 @@ __device__ __forceinline__ void prep_wave_codes(const DevArena& A, const Work& W
         }
     }
     if (rsq8) {
+        // (the loads unconditional, past d from the last coordinate, so they are in flight together)
+        float mn[EPL];
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) mn[e] = A.sq_min[min(base + e, d - 1)];
 #pragma unroll
         for (int e = 0; e < EPL; ++e)
-            if (base + e < d) rqp[base + e] = x[e] * A.sq_min[base + e];
+            if (base + e < d) rqp[base + e] = x[e] * mn[e];
     }
     for (int r = 0; r < 2; ++r) {
 #pragma unroll
@@ -2777,7 +2781,19 @@ pq_front_kernel(DevArena A, Work Wk, KParams K, const float* __restrict__ querie
         float base = 0.0f;
         if (A.cent_sq8 != nullptr) {
             const float* q = queries + static_cast<uint64_t>(qi) * A.d;
-            for (uint32_t i = lane; i < A.d; i += kWave) prod[i] = q[i] * A.csq_min[i];
+            // four rounds of loads in flight together (indices past d read the last coordinate)
+            for (uint32_t i0 = 0; i0 < A.d; i0 += 4 * kWave) {
+                float qv[4], mv[4];
+#pragma unroll
+                for (uint32_t u = 0; u < 4; ++u) {
+                    const uint32_t i = min(i0 + u * kWave + lane, A.d - 1);
+                    qv[u] = q[i];
+                    mv[u] = A.csq_min[i];
+                }
+#pragma unroll
+                for (uint32_t u = 0; u < 4; ++u)
+                    if (i0 + u * kWave + lane < A.d) prod[i0 + u * kWave + lane] = qv[u] * mv[u];
+            }
             wave_sync();
             base = seq_sum_lds(prod, A.d, 0.0f);
         }
